@@ -1,0 +1,254 @@
+#!/usr/bin/env python3
+"""Decode benchmark: µs per decode step + effective HBM GB/s on one MI355X.
+
+Default workload (BASELINE.json metric): GQA-16 decode, B=1, H_q=32, H_kv=2,
+D=256, MLX-affine 4-bit gs=32, fp16, N=131072 keys.  Synthetic data: K/V and
+q ~ N(0,1) (torch, seeded) quantized on the GPU by the library's own
+quantize kernel; no checkpoint or dataset is involved.
+
+A "step" is one fused decode (all its launches) over one KV set.  The timed
+loop cycles over enough distinct KV sets (>= --kv-bytes, default 1.2 GB) that
+the 256 MB Infinity Cache cannot hold them, so every step streams its K/V
+from HBM.  Inputs are resident in HBM before timing starts.
+
+Printed JSON line (rank 0, N=1):
+  value            µs per decode step (wall time of K steps / K)
+  roofline         achieved GB/s of the main decode kernel: algorithmic bytes
+                   (q + packed K/V + scales + biases + out, the reference's
+                   formula) / that kernel's mean duration, timed with HIP
+                   events recorded by the library around the kernel launch
+  cpu_baseline     the oracle's float32 dequantize + attention (the
+                   reference's CPU-capable path) on a bounded sample
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT, ROOT / "mlx-qsdpa_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+METRIC = "µs/decode step + effective HBM GB/s (% peak), GQA-16 D=256 4-bit N=128K"
+HBM_PEAK_GBPS = 8000.0
+# Reference's published fused decode time for this exact config on an Apple
+# M2 Ultra (README.md:89): 2431 µs at N=128K.
+REFERENCE_US = {131072: 2431.0, 65536: 1438.0, 32768: 882.0, 16384: 588.0}
+
+CONFIGS = {
+    # name: (B, H_q, H_kv, D, bits, group_size, dtype, N, outlier_frac)
+    "c1": (1, 8, 2, 128, 4, 64, "f16", 4096, 0.0),
+    "c2": (1, 2, 2, 256, 8, 64, "bf16", 131072, 0.01),
+    "c3": (1, 32, 2, 256, 4, 32, "f16", 131072, 0.0),
+    "c5": (4, 16, 4, 128, 8, 128, "bf16", 4096, 0.0),
+}
+
+
+def parse_args(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=300)
+    ap.add_argument("--warmup", type=int, default=30)
+    ap.add_argument("--config", default="c3", choices=sorted(CONFIGS))
+    ap.add_argument("--n", type=int, default=None, help="override the key count N")
+    ap.add_argument("--kv-bytes", type=float, default=1.2e9,
+                    help="distinct KV bytes cycled through (defeats the MALL)")
+    ap.add_argument("--splits", type=int, default=0, help="0 = library heuristic")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="time budget of the CPU baseline sample (0 = skip)")
+    ap.add_argument("--seed", type=int, default=0)
+    return ap.parse_args(argv)
+
+
+class HipEvents:
+    """hipEvent_t helpers through the HIP runtime torch already loaded."""
+
+    def __init__(self):
+        self.lib = ctypes.CDLL("libamdhip64.so.7")
+        self.lib.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.lib.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p,
+                                                 ctypes.c_void_p]
+        self.lib.hipEventDestroy.argtypes = [ctypes.c_void_p]
+
+    def create(self, n):
+        evs = []
+        for _ in range(n):
+            e = ctypes.c_void_p()
+            rc = self.lib.hipEventCreate(ctypes.byref(e))
+            if rc != 0:
+                raise RuntimeError(f"hipEventCreate failed ({rc})")
+            evs.append(e.value)
+        return evs
+
+    def elapsed_ms(self, a, b):
+        ms = ctypes.c_float()
+        rc = self.lib.hipEventElapsedTime(ctypes.byref(ms), a, b)
+        if rc != 0:
+            raise RuntimeError(f"hipEventElapsedTime failed ({rc})")
+        return ms.value
+
+    def destroy(self, evs):
+        for e in evs:
+            self.lib.hipEventDestroy(e)
+
+
+def make_sets(cfg, N, n_sets, device, seed):
+    import torch
+
+    from mlx_qsdpa_amd import kernels
+
+    B, Hq, Hkv, D, bits, gs, dt, _, outl = cfg
+    T = torch.float16 if dt == "f16" else torch.bfloat16
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    sets = []
+    for _ in range(n_sets):
+        kv = []
+        for _ in range(2):
+            w = torch.randn((B, Hkv, N, D), generator=g, device=device, dtype=torch.float32)
+            if outl > 0:
+                n_out = max(1, int(round(outl * D)))
+                ch = torch.randperm(D, generator=g, device=device)[:n_out]
+                w[..., ch] *= 8.0
+            kv.append(kernels.quantize(w.to(T), gs, bits))
+            del w
+        q = torch.randn((B, Hq, 1, D), generator=g, device=device, dtype=torch.float32).to(T)
+        sets.append((q, kv[0], kv[1]))
+    torch.cuda.synchronize()
+    return sets
+
+
+def cpu_baseline(cfg, N, host_set, budget_s):
+    """Oracle float32 decode (1 thread) on the first KV set, repeated within budget."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+
+    from oracle import attention
+
+    B, Hq, Hkv, D, bits, gs, dt, _, _ = cfg
+    q, kq, vq = host_set
+    with threadpool_limits(limits=1):
+        times = []
+        t_end = time.perf_counter() + budget_s
+        while True:
+            t0 = time.perf_counter()
+            attention.decode_fp32(q, kq[0], vq[0], kq[1], vq[1], kq[2], vq[2], bits=bits,
+                                  group_size=gs)
+            times.append(time.perf_counter() - t0)
+            if time.perf_counter() > t_end or len(times) >= 50:
+                break
+    us = float(np.median(times)) * 1e6
+    return {"value": round(us, 1), "unit": "us/step", "cores": 1, "kind": "port",
+            "sample": (f"{len(times)} full decode steps of the same workload (N={N}) on one "
+                       f"host core, numpy float32 dequantize + attention "
+                       f"(oracle.attention.decode_fp32), median")}
+
+
+def main(argv=None) -> int:
+    args = parse_args(argv)
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the decode path is "
+              "single-GPU in this build, see DESIGN.md for how it would shard.", file=sys.stderr)
+        return 2
+    import numpy as np
+    import torch
+
+    from mlx_qsdpa_amd import kernels, metric
+
+    cfg = CONFIGS[args.config]
+    B, Hq, Hkv, D, bits, gs, dt, N0, _ = cfg
+    N = args.n or N0
+    device = torch.device("cuda:0")
+    kv_set_bytes = B * N * metric.kv_bytes_per_token(Hkv, D, bits, gs)
+    n_sets = max(2, math.ceil(args.kv_bytes / kv_set_bytes))
+    print(f"bench: config={args.config} N={N} sets={n_sets} ({kv_set_bytes / 1e6:.1f} MB each)",
+          file=sys.stderr, flush=True)
+    sets = make_sets(cfg, N, n_sets, device, args.seed)
+    plans = [kernels.DecodePlan(q, kq[0], vq[0], kq[1], vq[1], kq[2], vq[2], scale=D ** -0.5,
+                                bits=bits, group_size=gs, num_splits=args.splits)
+             for q, kq, vq in sets]
+    splits = plans[0].num_splits
+
+    hip = HipEvents()
+    ev_b = hip.create(args.steps)
+    ev_e = hip.create(args.steps)
+    for i in range(args.warmup):
+        plans[i % n_sets]()
+    torch.cuda.synchronize()
+
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        plans[i % n_sets]((ev_b[i], ev_e[i]))
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    kern_ms = [hip.elapsed_ms(ev_b[i], ev_e[i]) for i in range(args.steps)]
+    hip.destroy(ev_b + ev_e)
+
+    us_step = wall / args.steps * 1e6
+    kern_us = float(np.mean(kern_ms)) * 1e3
+    alg_bytes = metric.decode_bytes(B, Hq, Hkv, D, bits, gs, B * N)
+    step_gbps = alg_bytes / (us_step * 1e-6) / 1e9
+    kern_gbps = alg_bytes / (kern_us * 1e-6) / 1e9
+    print(f"bench: {us_step:.2f} us/step wall, main kernel {kern_us:.2f} us "
+          f"({kern_gbps:.0f} GB/s), splits={splits}", file=sys.stderr, flush=True)
+
+    cpu = None
+    if args.cpu_seconds > 0:
+        host = tuple(x.cpu().numpy() if x.dtype == torch.uint32 else x.float().cpu().numpy()
+                     for x in (sets[0][0],))
+        kq = tuple(x.cpu().numpy() if x.dtype == torch.uint32 else x.float().cpu().numpy()
+                   for x in sets[0][1])
+        vq = tuple(x.cpu().numpy() if x.dtype == torch.uint32 else x.float().cpu().numpy()
+                   for x in sets[0][2])
+        cpu = cpu_baseline(cfg, N, (host[0], kq, vq), args.cpu_seconds)
+
+    ref_us = REFERENCE_US.get(N) if args.config == "c3" else None
+    line = {
+        "metric": METRIC,
+        "value": round(us_step, 3),
+        "unit": "us/step",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(us_step / 1e3, 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": round(us_step / ref_us, 5) if ref_us else None,
+        "vs_baseline_ref": (f"M2 Ultra fused decode {ref_us} us (mlx-qsdpa README.md:89)"
+                            if ref_us else None),
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": (f"{args.config}: decode B={B} H_q={Hq} H_kv={Hkv} D={D} {bits}-bit "
+                         f"gs={gs} {dt} N={N}"),
+            "B": B, "H_q": Hq, "H_kv": Hkv, "D": D, "N": N, "bits": bits, "group_size": gs,
+            "kv_dtype": dt, "num_splits": splits, "kv_sets": n_sets,
+        },
+        "effective_gbps": round(step_gbps, 1),
+        "pct_hbm_peak": round(100.0 * step_gbps / HBM_PEAK_GBPS, 2),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(kern_gbps, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(kern_gbps / HBM_PEAK_GBPS, 4),
+            "traffic": None,
+            "kernel_us": round(kern_us, 3),
+            "algorithmic_bytes": alg_bytes,
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,174 @@
+/*
+ * qsdpa.h -- C ABI of the MI355X (gfx950) fused quantized SDPA decode library.
+ *
+ * Everything crossing this boundary is a plain C type: device pointers,
+ * 64-bit element strides, int32 shape fields and an opaque stream handle
+ * (a hipStream_t passed as void*; NULL = the null stream).  The library never
+ * allocates or frees caller memory, keeps no pointer after a call returns and
+ * never throws.  Every entry point returns QSDPA_OK (0) or a negative
+ * QSDPA_ERR_* code; qsdpa_last_error() then holds a thread-local message.
+ * All launches are stream-ordered; no entry point synchronizes the device.
+ *
+ * Data format (the MLX affine format of mx.quantize, bits in {4, 8}):
+ *   packed : uint32 [.., N, D*bits/32]; element j of a word occupies bits
+ *            [j*bits, (j+1)*bits), element index d = word*(32/bits) + j
+ *            (reference: mlx_qsdpa/kernels.py:101-105).
+ *   scales, biases : T [.., N, D/group_size], T in {fp16, bf16}; the value
+ *            of element d of a token is scale[g]*q[d] + bias[g], g=d/group_size.
+ *
+ * Reference interfaces replaced (paths relative to the mlx-qsdpa repo):
+ *   qsdpa_decode     <- the three mx.fast.metal_kernel launches of
+ *                       mlx_qsdpa/dispatch.py:158-171 (single pass, kernel
+ *                       built at kernels.py:182-191) and dispatch.py:225-265
+ *                       (split-K pass 1 + pass 2, kernels.py:452-473).
+ *   qsdpa_quantize   <- mx.quantize(keys, group_size, bits) followed by the
+ *                       slice assignment into the cache buffers
+ *                       (mlx_qsdpa/cache.py:186-192, 314-318, 576-581,
+ *                       610-614, 798-804, 830-834).
+ *   qsdpa_dequantize <- mx.dequantize(...) (mlx_qsdpa/dispatch.py:69-78,
+ *                       mlx_qsdpa/__init__.py:50-57) and the dequantize +
+ *                       temporal reorder of cache.py:622-634, 842-857.
+ */
+#ifndef QSDPA_H_
+#define QSDPA_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QSDPA_ABI_VERSION 1
+
+enum {
+  QSDPA_OK = 0,
+  QSDPA_ERR_INVALID = -1,     /* bad argument (shape, stride, pointer) */
+  QSDPA_ERR_UNSUPPORTED = -2, /* valid but not compiled (e.g. D=96)    */
+  QSDPA_ERR_WORKSPACE = -3,   /* workspace missing or too small        */
+  QSDPA_ERR_LAUNCH = -4       /* HIP launch error                      */
+};
+
+/* Element types. */
+enum {
+  QSDPA_F16 = 0,
+  QSDPA_BF16 = 1,
+  QSDPA_F32 = 2,
+  QSDPA_BOOL = 3 /* one byte per element, nonzero = attend */
+};
+
+/*
+ * A strided view of a 4-D tensor [B, H, N, inner] whose innermost dimension
+ * is contiguous.  Strides are in ELEMENTS of the tensor's own type.  A stride
+ * of 0 broadcasts that dimension.  ptr == NULL means "absent".
+ */
+typedef struct {
+  const void* ptr;
+  int64_t stride_b;
+  int64_t stride_h;
+  int64_t stride_n;
+} qsdpa_view;
+
+/*
+ * Decode attention: out[b, h, 0, :] = softmax(scale * q[b,h] . K[b, h/G]^T
+ * + mask) V[b, h/G] with G = H_q / H_kv, K/V dequantized on the fly.
+ */
+typedef struct {
+  int32_t B, H_q, H_kv, N, D;
+  int32_t bits;       /* 4 or 8 */
+  int32_t group_size; /* 32, 64 or 128 */
+  int32_t dtype;      /* QSDPA_F16 or QSDPA_BF16: q, scales, biases, out */
+  float scale;        /* softmax scale applied to q.k */
+
+  qsdpa_view q;        /* [B, H_q, 1, D]          (stride_n unused)     */
+  qsdpa_view k_packed; /* [B, H_kv, N, D*bits/32] uint32                 */
+  qsdpa_view v_packed;
+  qsdpa_view k_scales; /* [B, H_kv, N, D/group_size] dtype               */
+  qsdpa_view v_scales;
+  qsdpa_view k_biases; /* ptr NULL => zero biases (symmetric format)     */
+  qsdpa_view v_biases;
+  qsdpa_view out;      /* [B, H_q, 1, D] dtype     (stride_n unused)     */
+
+  /* Optional mask over keys, broadcastable [B|1, H_q|1, 1, N]: a stride of
+   * 0 broadcasts.  QSDPA_BOOL: nonzero keeps the key; QSDPA_F16/BF16/F32:
+   * additive (added to the scaled score).  ptr NULL = no mask.            */
+  qsdpa_view mask;
+  int32_t mask_dtype;
+
+  /* Optional int32 [B]: keys with index < kv_start[b] are skipped (never
+   * read).  Expresses left padding without a mask.  NULL = all keys.      */
+  const int32_t* kv_start;
+
+  /* 0 = choose automatically, 1 = single pass, >1 = split-K with this many
+   * splits per (batch, kv head).                                          */
+  int32_t num_splits;
+
+  /* Scratch for split-K partials, from qsdpa_decode_workspace_size().    */
+  void* workspace;
+  size_t workspace_bytes;
+
+  /* Optional profiling hook: two hipEvent_t handles (or NULL).  When set,
+   * the library records prof_begin on `stream` right before the main decode
+   * kernel and prof_end right after it (before any merge kernel), so a
+   * caller can time that kernel alone with hipEventElapsedTime.          */
+  void* prof_begin;
+  void* prof_end;
+} qsdpa_decode_args;
+
+/* Bytes of workspace qsdpa_decode needs for these args (0 for a single
+ * pass).  If num_splits_out is not NULL it receives the split count that
+ * qsdpa_decode will use.  Returns a negative QSDPA_ERR_* on bad args.     */
+int64_t qsdpa_decode_workspace_size(const qsdpa_decode_args* args,
+                                    int32_t* num_splits_out);
+
+/* Launch the decode on `stream`. */
+int qsdpa_decode(const qsdpa_decode_args* args, void* stream);
+
+/*
+ * Quantize rows of T values into the affine format and store them at token
+ * positions [t0, t0 + S) of the destination buffers:
+ *   dst[b, h, t0 + s, :] = quantize(src[b, h, s, :]).
+ * The per-group rule is the contract restated in oracle/affine.py.
+ */
+typedef struct {
+  int32_t B, H, S, D;
+  int32_t bits, group_size, dtype;
+  int32_t t0;              /* first destination token index            */
+  qsdpa_view src;          /* [B, H, S, D] dtype                        */
+  qsdpa_view dst_packed;   /* [B, H, cap, D*bits/32] uint32 (writable)  */
+  qsdpa_view dst_scales;   /* [B, H, cap, D/group_size] dtype           */
+  qsdpa_view dst_biases;   /* [B, H, cap, D/group_size] dtype           */
+} qsdpa_quantize_args;
+
+int qsdpa_quantize(const qsdpa_quantize_args* args, void* stream);
+
+/*
+ * Dequantize N tokens to T:  dst[b, h, t, :] = dequant(src[b, h, u(t), :])
+ * with u(t) = t for t < keep, else keep + (t - keep + rot) % (N - keep).
+ * rot = 0 is a plain dequantize; rot > 0 turns a ring buffer whose oldest
+ * ring slot is keep + rot into temporal order.  Each element is
+ * round_to_T(fmaf(scale, q, bias)).  Biases may be absent (zero).
+ */
+typedef struct {
+  int32_t B, H, N, D;
+  int32_t bits, group_size, dtype;
+  int32_t keep, rot;
+  qsdpa_view src_packed;
+  qsdpa_view src_scales;
+  qsdpa_view src_biases;
+  qsdpa_view dst;          /* [B, H, N, D] dtype (writable) */
+} qsdpa_dequantize_args;
+
+int qsdpa_dequantize(const qsdpa_dequantize_args* args, void* stream);
+
+/* Thread-local message describing the last error ("" if none). */
+const char* qsdpa_last_error(void);
+
+/* QSDPA_ABI_VERSION of the loaded library. */
+int qsdpa_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QSDPA_H_ */

@@ -1,0 +1,240 @@
+// C-ABI entry points: argument validation (the reference's ValueError set,
+// mlx_qsdpa/dispatch.py:42-65, re-checked here so a direct FFI caller gets
+// an error code instead of a fault), the split-count heuristic, workspace
+// sizing and kernel dispatch.  No entry point allocates, frees or
+// synchronizes.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <algorithm>
+#include <mutex>
+
+#include "abi_internal.h"
+
+namespace qsdpa {
+
+static thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+void clear_error() { g_err[0] = '\0'; }
+
+int check_launch(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(QSDPA_ERR_LAUNCH, "%s launch failed: %s", what, hipGetErrorString(e));
+  return QSDPA_OK;
+}
+
+// Defined in decode_valu.hip / decode_mfma.hip.
+int valu_heads_per_block(int G);
+int launch_decode_valu(const qsdpa_decode_args* a, int num_splits, float* part_acc, float* part_ml,
+                       hipStream_t stream);
+int launch_merge(const qsdpa_decode_args* a, int num_splits, const float* part_acc,
+                 const float* part_ml, hipStream_t stream);
+bool mfma_supports(const qsdpa_decode_args* a);
+int mfma_num_splits(const qsdpa_decode_args* a, int cus);
+int launch_decode_mfma(const qsdpa_decode_args* a, int num_splits, float* part_acc, float* part_ml,
+                       hipStream_t stream);
+
+namespace {
+
+constexpr int kMaxSplits = 1024;
+
+int compute_units() {
+  static int cus = 0;
+  static std::once_flag once;
+  std::call_once(once, [] {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+      cus = n;
+    else
+      cus = 256;
+  });
+  return cus;
+}
+
+bool valid_dtype(int d) { return d == QSDPA_F16 || d == QSDPA_BF16; }
+
+int check_view(const qsdpa_view& v, const char* name, int align_bytes, int64_t stride_mult,
+               bool required) {
+  if (!v.ptr) {
+    if (required) return fail(QSDPA_ERR_INVALID, "%s: null pointer", name);
+    return QSDPA_OK;
+  }
+  if (!aligned(v.ptr, align_bytes))
+    return fail(QSDPA_ERR_INVALID, "%s: pointer not %d-byte aligned", name, align_bytes);
+  if (v.stride_b % stride_mult || v.stride_h % stride_mult || v.stride_n % stride_mult)
+    return fail(QSDPA_ERR_INVALID, "%s: strides must be multiples of %lld elements", name,
+                static_cast<long long>(stride_mult));
+  return QSDPA_OK;
+}
+
+int validate_decode(const qsdpa_decode_args* a) {
+  if (!a) return fail(QSDPA_ERR_INVALID, "null args");
+  if (a->B < 1 || a->H_q < 1 || a->H_kv < 1 || a->N < 1)
+    return fail(QSDPA_ERR_INVALID, "B, H_q, H_kv, N must be >= 1 (got %d, %d, %d, %d)", a->B,
+                a->H_q, a->H_kv, a->N);
+  if (a->bits != 4 && a->bits != 8) return fail(QSDPA_ERR_INVALID, "bits must be 4 or 8, got %d", a->bits);
+  if (a->D % 32 != 0) return fail(QSDPA_ERR_INVALID, "D must be multiple of 32, got %d", a->D);
+  if (a->D != 64 && a->D != 128 && a->D != 256)
+    return fail(QSDPA_ERR_UNSUPPORTED, "D=%d not compiled (64, 128, 256)", a->D);
+  if (a->group_size != 32 && a->group_size != 64 && a->group_size != 128)
+    return fail(QSDPA_ERR_UNSUPPORTED, "group_size=%d not supported (32, 64, 128)", a->group_size);
+  if (a->D % a->group_size != 0)
+    return fail(QSDPA_ERR_INVALID, "D=%d not a multiple of group_size=%d", a->D, a->group_size);
+  if (a->H_q % a->H_kv != 0)
+    return fail(QSDPA_ERR_INVALID, "H_q (%d) must be divisible by H_kv (%d)", a->H_q, a->H_kv);
+  if (!valid_dtype(a->dtype)) return fail(QSDPA_ERR_INVALID, "dtype must be F16 or BF16");
+  if (a->num_splits < 0 || a->num_splits > kMaxSplits)
+    return fail(QSDPA_ERR_INVALID, "num_splits must be in [0, %d]", kMaxSplits);
+  int rc;
+  if ((rc = check_view(a->q, "q", 2, 1, true))) return rc;
+  if ((rc = check_view(a->out, "out", 2, 1, true))) return rc;
+  if ((rc = check_view(a->k_packed, "k_packed", 16, 4, true))) return rc;
+  if ((rc = check_view(a->v_packed, "v_packed", 16, 4, true))) return rc;
+  if ((rc = check_view(a->k_scales, "k_scales", 2, 1, true))) return rc;
+  if ((rc = check_view(a->v_scales, "v_scales", 2, 1, true))) return rc;
+  if ((rc = check_view(a->k_biases, "k_biases", 2, 1, false))) return rc;
+  if ((rc = check_view(a->v_biases, "v_biases", 2, 1, false))) return rc;
+  if ((a->k_biases.ptr == nullptr) != (a->v_biases.ptr == nullptr))
+    return fail(QSDPA_ERR_INVALID, "k_biases and v_biases must both be given or both be NULL");
+  if (a->mask.ptr) {
+    const int md = a->mask_dtype;
+    if (md != QSDPA_F16 && md != QSDPA_BF16 && md != QSDPA_F32 && md != QSDPA_BOOL)
+      return fail(QSDPA_ERR_INVALID, "mask_dtype %d invalid", md);
+    const int al = md == QSDPA_F32 ? 4 : (md == QSDPA_BOOL ? 1 : 2);
+    if ((rc = check_view(a->mask, "mask", al, 1, true))) return rc;
+  }
+  return QSDPA_OK;
+}
+
+}  // namespace
+
+// Split count: enough workgroups to cover every CU twice, but never fewer
+// than 64 keys per split, and no more than kMaxSplits.
+int decode_plan(const qsdpa_decode_args* a, int* num_splits, int64_t* workspace_bytes) {
+  int splits = a->num_splits;
+  const bool mfma = mfma_supports(a);
+  if (splits == 0) {
+    if (mfma) {
+      splits = mfma_num_splits(a, compute_units());
+    } else {
+      const int G = a->H_q / a->H_kv;
+      const int64_t units = static_cast<int64_t>(a->B) * a->H_kv * (G / valu_heads_per_block(G));
+      const int64_t target = 2LL * compute_units();
+      int64_t s = (target + units - 1) / units;
+      const int64_t max_by_len = std::max<int64_t>(1, a->N / 64);
+      s = std::min<int64_t>(std::min<int64_t>(s, max_by_len), kMaxSplits);
+      splits = static_cast<int>(std::max<int64_t>(s, 1));
+    }
+  }
+  splits = std::min(splits, std::max(1, a->N));
+  *num_splits = splits;
+  *workspace_bytes =
+      splits > 1 ? static_cast<int64_t>(a->B) * a->H_q * splits * (a->D + 2) * 4 + 256 : 0;
+  return QSDPA_OK;
+}
+
+}  // namespace qsdpa
+
+using namespace qsdpa;
+
+extern "C" {
+
+int qsdpa_abi_version(void) { return QSDPA_ABI_VERSION; }
+
+const char* qsdpa_last_error(void) { return g_err; }
+
+int64_t qsdpa_decode_workspace_size(const qsdpa_decode_args* args, int32_t* num_splits_out) {
+  clear_error();
+  int rc = validate_decode(args);
+  if (rc) return rc;
+  int splits = 1;
+  int64_t ws = 0;
+  rc = decode_plan(args, &splits, &ws);
+  if (rc) return rc;
+  if (num_splits_out) *num_splits_out = splits;
+  return ws;
+}
+
+int qsdpa_decode(const qsdpa_decode_args* args, void* stream) {
+  clear_error();
+  int rc = validate_decode(args);
+  if (rc) return rc;
+  int splits = 1;
+  int64_t ws = 0;
+  rc = decode_plan(args, &splits, &ws);
+  if (rc) return rc;
+  float* part_acc = nullptr;
+  float* part_ml = nullptr;
+  if (splits > 1) {
+    if (!args->workspace || static_cast<int64_t>(args->workspace_bytes) < ws)
+      return fail(QSDPA_ERR_WORKSPACE, "workspace of %lld bytes required, got %lld",
+                  static_cast<long long>(ws), static_cast<long long>(args->workspace_bytes));
+    if (!aligned(args->workspace, 16)) return fail(QSDPA_ERR_INVALID, "workspace not 16-byte aligned");
+    part_acc = static_cast<float*>(args->workspace);
+    part_ml = part_acc + static_cast<int64_t>(args->B) * args->H_q * splits * args->D;
+  }
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (args->prof_begin) {
+    const hipError_t e = hipEventRecord(static_cast<hipEvent_t>(args->prof_begin), s);
+    if (e != hipSuccess) return fail(QSDPA_ERR_LAUNCH, "hipEventRecord: %s", hipGetErrorString(e));
+  }
+  if (mfma_supports(args)) rc = launch_decode_mfma(args, splits, part_acc, part_ml, s);
+  else rc = launch_decode_valu(args, splits, part_acc, part_ml, s);
+  if (rc) return rc;
+  if (args->prof_end) {
+    const hipError_t e = hipEventRecord(static_cast<hipEvent_t>(args->prof_end), s);
+    if (e != hipSuccess) return fail(QSDPA_ERR_LAUNCH, "hipEventRecord: %s", hipGetErrorString(e));
+  }
+  if (splits > 1) rc = launch_merge(args, splits, part_acc, part_ml, s);
+  return rc;
+}
+
+int qsdpa_quantize(const qsdpa_quantize_args* a, void* stream) {
+  clear_error();
+  if (!a) return fail(QSDPA_ERR_INVALID, "null args");
+  if (a->bits != 4 && a->bits != 8) return fail(QSDPA_ERR_INVALID, "bits must be 4 or 8, got %d", a->bits);
+  if (a->group_size != 32 && a->group_size != 64 && a->group_size != 128)
+    return fail(QSDPA_ERR_UNSUPPORTED, "group_size=%d not supported (32, 64, 128)", a->group_size);
+  if (a->B < 0 || a->H < 0 || a->S < 0 || a->D <= 0 || a->D % a->group_size != 0)
+    return fail(QSDPA_ERR_INVALID, "bad shape B=%d H=%d S=%d D=%d gs=%d", a->B, a->H, a->S, a->D,
+                a->group_size);
+  if (a->t0 < 0) return fail(QSDPA_ERR_INVALID, "t0 must be >= 0");
+  if (!valid_dtype(a->dtype)) return fail(QSDPA_ERR_INVALID, "dtype must be F16 or BF16");
+  int rc;
+  if ((rc = check_view(a->src, "src", 2, 1, true))) return rc;
+  if ((rc = check_view(a->dst_packed, "dst_packed", 4, 1, true))) return rc;
+  if ((rc = check_view(a->dst_scales, "dst_scales", 2, 1, true))) return rc;
+  if ((rc = check_view(a->dst_biases, "dst_biases", 2, 1, true))) return rc;
+  return launch_quantize(a, static_cast<hipStream_t>(stream));
+}
+
+int qsdpa_dequantize(const qsdpa_dequantize_args* a, void* stream) {
+  clear_error();
+  if (!a) return fail(QSDPA_ERR_INVALID, "null args");
+  if (a->bits != 4 && a->bits != 8) return fail(QSDPA_ERR_INVALID, "bits must be 4 or 8, got %d", a->bits);
+  if (a->group_size != 32 && a->group_size != 64 && a->group_size != 128)
+    return fail(QSDPA_ERR_UNSUPPORTED, "group_size=%d not supported (32, 64, 128)", a->group_size);
+  if (a->B < 0 || a->H < 0 || a->N < 0 || a->D <= 0 || a->D % a->group_size != 0)
+    return fail(QSDPA_ERR_INVALID, "bad shape B=%d H=%d N=%d D=%d gs=%d", a->B, a->H, a->N, a->D,
+                a->group_size);
+  if (a->keep < 0 || a->rot < 0 || (a->N > 0 && a->keep >= a->N && a->rot > 0))
+    return fail(QSDPA_ERR_INVALID, "bad keep/rot (keep=%d rot=%d N=%d)", a->keep, a->rot, a->N);
+  if (!valid_dtype(a->dtype)) return fail(QSDPA_ERR_INVALID, "dtype must be F16 or BF16");
+  int rc;
+  if ((rc = check_view(a->src_packed, "src_packed", 4, 1, true))) return rc;
+  if ((rc = check_view(a->src_scales, "src_scales", 2, 1, true))) return rc;
+  if ((rc = check_view(a->src_biases, "src_biases", 2, 1, false))) return rc;
+  if ((rc = check_view(a->dst, "dst", 2, 1, true))) return rc;
+  return launch_dequantize(a, static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,34 @@
+// Host-side helpers shared by the C-ABI entry points.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/qsdpa.h"
+
+namespace qsdpa {
+
+// Record a thread-local error message and return `code`.
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+void clear_error();
+// Map hipGetLastError() after a launch to QSDPA_OK / QSDPA_ERR_LAUNCH.
+int check_launch(const char* what);
+
+inline bool aligned(const void* p, int bytes) {
+  return (reinterpret_cast<uintptr_t>(p) % static_cast<uintptr_t>(bytes)) == 0;
+}
+
+// Dispatch-time description of one strided operand.
+struct View {
+  const void* ptr;
+  int64_t sb, sh, sn;
+};
+inline View view_of(const qsdpa_view& v) { return View{v.ptr, v.stride_b, v.stride_h, v.stride_n}; }
+
+// Launch hooks implemented in the kernel translation units.
+int launch_quantize(const qsdpa_quantize_args* a, hipStream_t stream);
+int launch_dequantize(const qsdpa_dequantize_args* a, hipStream_t stream);
+int launch_decode(const qsdpa_decode_args* a, int num_splits, hipStream_t stream);
+int decode_plan(const qsdpa_decode_args* a, int* num_splits, int64_t* workspace_bytes);
+
+}  // namespace qsdpa

@@ -1,0 +1,92 @@
+// Shared device helpers for the gfx950 quantized SDPA kernels.
+//
+// Storage types are handled as raw 16-bit patterns so the float16 and
+// bfloat16 paths share one code shape: `Tag` selects the conversion.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/qsdpa.h"
+
+namespace qsdpa {
+
+struct F16 {
+  static constexpr int kId = QSDPA_F16;
+};
+struct BF16 {
+  static constexpr int kId = QSDPA_BF16;
+};
+
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t h) {
+  return __builtin_bit_cast(float, static_cast<uint32_t>(h) << 16);
+}
+// float -> float16, round to nearest even (v_cvt_f16_f32 in the default mode).
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float x) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
+}
+// float -> bfloat16, round to nearest even; NaN stays NaN (quiet).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float x) {
+  uint32_t u = __builtin_bit_cast(uint32_t, x);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+template <typename Tag>
+__device__ __forceinline__ float to_f32(uint16_t h) {
+  if constexpr (Tag::kId == QSDPA_F16) return f16_bits_to_f32(h);
+  else return bf16_bits_to_f32(h);
+}
+template <typename Tag>
+__device__ __forceinline__ uint16_t from_f32(float x) {
+  if constexpr (Tag::kId == QSDPA_F16) return f32_to_f16_bits(x);
+  else return f32_to_bf16_bits(x);
+}
+// Round a float to the nearest T value and return it as float.
+template <typename Tag>
+__device__ __forceinline__ float round_T(float x) {
+  return to_f32<Tag>(from_f32<Tag>(x));
+}
+
+// ---------------------------------------------------------------------------
+// Cross-lane helpers (wave64).
+// DPP controls: quad_perm [1,0,3,2] = 0xB1, quad_perm [2,3,0,1] = 0x4E,
+// row_half_mirror = 0x141, row_mirror = 0x140.
+// ---------------------------------------------------------------------------
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float x) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float shfl_xor_f32(float x, int mask) {
+  const int lane = __lane_id();
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_ds_bpermute((lane ^ mask) << 2, __builtin_bit_cast(int, x)));
+}
+
+// Sum over aligned groups of G consecutive lanes; every lane of a group gets
+// the bitwise-identical total (each step adds symmetric partners).
+template <int G>
+__device__ __forceinline__ float group_sum(float x) {
+  if constexpr (G >= 2) x += dpp_f32<0xB1>(x);
+  if constexpr (G >= 4) x += dpp_f32<0x4E>(x);
+  if constexpr (G >= 8) x += dpp_f32<0x141>(x);
+  if constexpr (G >= 16) x += dpp_f32<0x140>(x);
+  if constexpr (G >= 32) x += shfl_xor_f32(x, 16);
+  if constexpr (G >= 64) x += shfl_xor_f32(x, 32);
+  return x;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Strided 4-D addressing (element strides).
+__device__ __forceinline__ int64_t off3(int b, int h, int n, int64_t sb, int64_t sh, int64_t sn) {
+  return static_cast<int64_t>(b) * sb + static_cast<int64_t>(h) * sh + static_cast<int64_t>(n) * sn;
+}
+
+}  // namespace qsdpa

@@ -1,0 +1,173 @@
+// Quantize-on-append and dequantize kernels (MLX affine format).
+//
+// quantize: one thread per (row, group).  The per-group rule is the float32
+// edge-snapped affine quantizer (see oracle/affine.py for the written
+// contract); every operation is spelled with an explicitly rounded intrinsic
+// so the compiler can neither contract nor reassociate it, which keeps the
+// output bit-identical to the numpy restatement.
+//
+// dequantize: one thread per packed word; value = round_T(fmaf(s, q, b)).
+// Replaces mx.quantize + slice assignment (mlx_qsdpa/cache.py:186-192) and
+// mx.dequantize (mlx_qsdpa/dispatch.py:69-78, cache.py:628-633).
+#include "abi_internal.h"
+#include "common.h"
+
+namespace qsdpa {
+namespace {
+
+struct QuantParams {
+  int B, H, S, D, gs, t0;
+  const uint16_t* src;
+  int64_t s_sb, s_sh, s_sn;
+  uint32_t* dp;
+  int64_t p_sb, p_sh, p_sn;
+  uint16_t* ds;
+  int64_t c_sb, c_sh, c_sn;
+  uint16_t* db;
+  int64_t z_sb, z_sh, z_sn;
+};
+
+template <typename Tag, int BITS>
+__global__ __launch_bounds__(256) void quantize_kernel(QuantParams p) {
+  constexpr int PER = 32 / BITS;
+  constexpr float kBins = static_cast<float>((1 << BITS) - 1);
+  const int ng = p.D / p.gs;
+  const int64_t total = static_cast<int64_t>(p.B) * p.H * p.S * ng;
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (gid >= total) return;
+  const int g = static_cast<int>(gid % ng);
+  int64_t row = gid / ng;
+  const int s = static_cast<int>(row % p.S);
+  row /= p.S;
+  const int h = static_cast<int>(row % p.H);
+  const int b = static_cast<int>(row / p.H);
+
+  const uint16_t* src = p.src + off3(b, h, s, p.s_sb, p.s_sh, p.s_sn) + g * p.gs;
+
+  float w_min = __builtin_huge_valf(), w_max = -__builtin_huge_valf();
+  for (int i = 0; i < p.gs; ++i) {
+    const float v = to_f32<Tag>(src[i]);
+    w_min = fminf(w_min, v);
+    w_max = fmaxf(w_max, v);
+  }
+  float scale = fmaxf(__fdiv_rn(__fsub_rn(w_max, w_min), kBins), 1e-7f);
+  const bool side = fabsf(w_min) > fabsf(w_max);
+  scale = side ? scale : -scale;
+  const float edge = side ? w_min : w_max;
+  const float q0 = rintf(__fdiv_rn(edge, scale));
+  const bool nz = q0 != 0.0f;
+  if (nz) scale = __fdiv_rn(edge, q0);
+  const float bias = nz ? edge : 0.0f;
+
+  const int t = p.t0 + s;
+  uint32_t* dst = p.dp + off3(b, h, t, p.p_sb, p.p_sh, p.p_sn) + (g * p.gs) / PER;
+  for (int w = 0; w < p.gs / PER; ++w) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const float v = to_f32<Tag>(src[w * PER + j]);
+      float q = rintf(__fdiv_rn(__fsub_rn(v, bias), scale));
+      q = fminf(fmaxf(q, 0.0f), kBins);
+      word |= static_cast<uint32_t>(q) << (j * BITS);
+    }
+    dst[w] = word;
+  }
+  p.ds[off3(b, h, t, p.c_sb, p.c_sh, p.c_sn) + g] = from_f32<Tag>(scale);
+  p.db[off3(b, h, t, p.z_sb, p.z_sh, p.z_sn) + g] = from_f32<Tag>(bias);
+}
+
+struct DequantParams {
+  int B, H, N, D, gs, keep, rot;
+  const uint32_t* sp;
+  int64_t p_sb, p_sh, p_sn;
+  const uint16_t* ss;
+  int64_t c_sb, c_sh, c_sn;
+  const uint16_t* sbias;  // may be null
+  int64_t z_sb, z_sh, z_sn;
+  uint16_t* dst;
+  int64_t d_sb, d_sh, d_sn;
+};
+
+template <typename Tag, int BITS>
+__global__ __launch_bounds__(256) void dequantize_kernel(DequantParams p) {
+  constexpr int PER = 32 / BITS;
+  constexpr uint32_t kMask = (1u << BITS) - 1u;
+  const int words = p.D / PER;
+  const int64_t total = static_cast<int64_t>(p.B) * p.H * p.N * words;
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (gid >= total) return;
+  const int w = static_cast<int>(gid % words);
+  int64_t row = gid / words;
+  const int t = static_cast<int>(row % p.N);
+  row /= p.N;
+  const int h = static_cast<int>(row % p.H);
+  const int b = static_cast<int>(row / p.H);
+  const int u = (t < p.keep) ? t : p.keep + (t - p.keep + p.rot) % (p.N - p.keep);
+
+  const uint32_t word = p.sp[off3(b, h, u, p.p_sb, p.p_sh, p.p_sn) + w];
+  const int g = (w * PER) / p.gs;
+  const float s = to_f32<Tag>(p.ss[off3(b, h, u, p.c_sb, p.c_sh, p.c_sn) + g]);
+  const float bi = p.sbias ? to_f32<Tag>(p.sbias[off3(b, h, u, p.z_sb, p.z_sh, p.z_sn) + g]) : 0.0f;
+  uint16_t* out = p.dst + off3(b, h, t, p.d_sb, p.d_sh, p.d_sn) + w * PER;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const float q = static_cast<float>((word >> (j * BITS)) & kMask);
+    out[j] = from_f32<Tag>(__fmaf_rn(s, q, bi));
+  }
+}
+
+}  // namespace
+
+int launch_quantize(const qsdpa_quantize_args* a, hipStream_t stream) {
+  QuantParams p;
+  p.B = a->B; p.H = a->H; p.S = a->S; p.D = a->D; p.gs = a->group_size; p.t0 = a->t0;
+  p.src = static_cast<const uint16_t*>(a->src.ptr);
+  p.s_sb = a->src.stride_b; p.s_sh = a->src.stride_h; p.s_sn = a->src.stride_n;
+  p.dp = static_cast<uint32_t*>(const_cast<void*>(a->dst_packed.ptr));
+  p.p_sb = a->dst_packed.stride_b; p.p_sh = a->dst_packed.stride_h; p.p_sn = a->dst_packed.stride_n;
+  p.ds = static_cast<uint16_t*>(const_cast<void*>(a->dst_scales.ptr));
+  p.c_sb = a->dst_scales.stride_b; p.c_sh = a->dst_scales.stride_h; p.c_sn = a->dst_scales.stride_n;
+  p.db = static_cast<uint16_t*>(const_cast<void*>(a->dst_biases.ptr));
+  p.z_sb = a->dst_biases.stride_b; p.z_sh = a->dst_biases.stride_h; p.z_sn = a->dst_biases.stride_n;
+  const int64_t total = static_cast<int64_t>(a->B) * a->H * a->S * (a->D / a->group_size);
+  if (total == 0) return QSDPA_OK;
+  const dim3 block(256);
+  const dim3 grid(static_cast<unsigned>((total + 255) / 256));
+  if (a->dtype == QSDPA_F16) {
+    if (a->bits == 4) quantize_kernel<F16, 4><<<grid, block, 0, stream>>>(p);
+    else quantize_kernel<F16, 8><<<grid, block, 0, stream>>>(p);
+  } else {
+    if (a->bits == 4) quantize_kernel<BF16, 4><<<grid, block, 0, stream>>>(p);
+    else quantize_kernel<BF16, 8><<<grid, block, 0, stream>>>(p);
+  }
+  return check_launch("quantize");
+}
+
+int launch_dequantize(const qsdpa_dequantize_args* a, hipStream_t stream) {
+  DequantParams p;
+  p.B = a->B; p.H = a->H; p.N = a->N; p.D = a->D; p.gs = a->group_size;
+  p.keep = a->keep; p.rot = a->rot;
+  p.sp = static_cast<const uint32_t*>(a->src_packed.ptr);
+  p.p_sb = a->src_packed.stride_b; p.p_sh = a->src_packed.stride_h; p.p_sn = a->src_packed.stride_n;
+  p.ss = static_cast<const uint16_t*>(a->src_scales.ptr);
+  p.c_sb = a->src_scales.stride_b; p.c_sh = a->src_scales.stride_h; p.c_sn = a->src_scales.stride_n;
+  p.sbias = static_cast<const uint16_t*>(a->src_biases.ptr);
+  p.z_sb = a->src_biases.stride_b; p.z_sh = a->src_biases.stride_h; p.z_sn = a->src_biases.stride_n;
+  p.dst = static_cast<uint16_t*>(const_cast<void*>(a->dst.ptr));
+  p.d_sb = a->dst.stride_b; p.d_sh = a->dst.stride_h; p.d_sn = a->dst.stride_n;
+  const int per = 32 / a->bits;
+  const int64_t total = static_cast<int64_t>(a->B) * a->H * a->N * (a->D / per);
+  if (total == 0) return QSDPA_OK;
+  const dim3 block(256);
+  const dim3 grid(static_cast<unsigned>((total + 255) / 256));
+  if (a->dtype == QSDPA_F16) {
+    if (a->bits == 4) dequantize_kernel<F16, 4><<<grid, block, 0, stream>>>(p);
+    else dequantize_kernel<F16, 8><<<grid, block, 0, stream>>>(p);
+  } else {
+    if (a->bits == 4) dequantize_kernel<BF16, 4><<<grid, block, 0, stream>>>(p);
+    else dequantize_kernel<BF16, 8><<<grid, block, 0, stream>>>(p);
+  }
+  return check_launch("dequantize");
+}
+
+}  // namespace qsdpa

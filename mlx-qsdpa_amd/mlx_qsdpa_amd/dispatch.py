@@ -1,0 +1,177 @@
+"""quantized_sdpa: validation and routing onto the HIP decode kernels.
+
+Mirrors mlx_qsdpa/dispatch.py:8-111 (same signature, same ValueError set,
+same defaults for ``scale`` and for missing biases), with three MI355X
+choices:
+
+* Masked decode runs in-kernel (bool keep-mask or additive mask), where the
+  reference falls back to dequantize + SDPA (dispatch.py:68-83).
+* ``threshold`` keeps its meaning when given (N <= threshold: single pass,
+  else split-K); the default ``None`` lets the library pick the split count
+  for 256 CUs.
+* ``kv_start`` (extension) skips keys before a per-sequence start index, the
+  left padding of a batched cache, without reading them.
+
+Prefill (qL > 1) dequantizes with the HIP kernel and runs float32 attention
+with torch on the GPU (the reference's fallback, dispatch.py:68-83).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import kernels
+
+
+def _validate(q, packed_k, packed_v, bits, group_size):
+    """dispatch.py:42-65."""
+    if q.dim() != 4:
+        raise ValueError(f"q must be 4D (B, H_q, qL, D), got ndim={q.dim()}")
+    B, H_q, qL, D = q.shape
+    if bits not in (4, 8):
+        raise ValueError(f"bits must be 4 or 8, got {bits}")
+    if D % 32 != 0:
+        raise ValueError(f"D must be multiple of 32, got {D}")
+    elems_per_int = 32 // bits
+    pack_D = D // elems_per_int
+    if packed_k.dim() != 4 or packed_v.dim() != 4:
+        raise ValueError("packed_k and packed_v must be 4D (B, H_kv, N, pack_D)")
+    _, H_kv, N, actual_pack_D = packed_k.shape
+    if actual_pack_D != pack_D:
+        raise ValueError(
+            f"packed_k last dim {actual_pack_D} != expected pack_D={pack_D} "
+            f"for bits={bits}, D={D}")
+    if H_q % H_kv != 0:
+        raise ValueError(f"H_q ({H_q}) must be divisible by H_kv ({H_kv})")
+    return B, H_q, qL, D, H_kv, N
+
+
+def attention_fp32(q, k, v, scale, mask=None):
+    """float32 SDPA on the GPU with MLX mask conventions.
+
+    q [B,Hq,L,D], k/v [B,Hkv,N,D] (dequantized T).  Bool masks keep True,
+    float masks are added, "causal" is lower-right aligned; rows with every
+    key masked return 0.  Output has q's dtype.
+    """
+    B, Hq, L, D = q.shape
+    Hkv, N = k.shape[1], k.shape[2]
+    G = Hq // Hkv
+    qf = q.float().reshape(B, Hkv, G * L, D)
+    kt = k.float().transpose(-1, -2).contiguous()
+    s = torch.matmul(qf, kt).reshape(B, Hkv, G, L, N) * float(scale)
+    s = s.reshape(B, Hq, L, N)
+    if isinstance(mask, str):
+        if mask != "causal":
+            raise ValueError(f"unknown mask {mask!r}")
+        qi = torch.arange(L, device=q.device)[:, None] + (N - L)
+        kj = torch.arange(N, device=q.device)[None, :]
+        s = s.masked_fill(qi < kj, float("-inf"))
+    elif mask is not None:
+        m = mask.to(q.device)
+        if m.dtype == torch.bool:
+            s = s.masked_fill(~m, float("-inf"))
+        else:
+            s = s + m.float()
+    p = torch.softmax(s, dim=-1)
+    p = torch.nan_to_num(p, nan=0.0)
+    o = torch.matmul(p.reshape(B, Hkv, G * L, N), v.float().contiguous())
+    return o.reshape(B, Hq, L, D).to(q.dtype)
+
+
+def dequantize_attention(q, k_quant, v_quant, *, bits, group_size, scale, mask):
+    """The reference's dequantize + SDPA path (dispatch.py:68-83)."""
+    k = kernels.dequantize(*k_quant, group_size=group_size, bits=bits)
+    v = kernels.dequantize(*v_quant, group_size=group_size, bits=bits)
+    return attention_fp32(q, k, v, scale, mask)
+
+
+def fallback_sdpa(q, k_quant, v_quant, *, bits, group_size, scale, mask=None, kv_start=None):
+    """Dequantize (HIP) + float32 attention: the path of dispatch.py:68-83.
+
+    Missing biases are zeros (dispatch.py:71, 76); ``kv_start`` is folded
+    into the mask as "keys before kv_start[b] are masked".
+    """
+    B, _, qL, _ = q.shape
+    N = k_quant[0].shape[2]
+    if kv_start is not None:
+        keep = torch.arange(N, device=q.device)[None, :] >= kv_start.to(q.device)[:, None]
+        keep = keep[:, None, None, :]
+        if mask is None:
+            mask = keep
+        elif isinstance(mask, str):
+            qi = torch.arange(qL, device=q.device)[:, None] + (N - qL)
+            mask = keep & (qi >= torch.arange(N, device=q.device)[None, :])
+        elif mask.dtype == torch.bool:
+            mask = mask.to(q.device) & keep
+        else:
+            mask = mask.to(q.device).masked_fill(~keep, float("-inf"))
+    kb = k_quant[2] if k_quant[2] is not None else torch.zeros_like(k_quant[1])
+    vb = v_quant[2] if v_quant[2] is not None else torch.zeros_like(v_quant[1])
+    return dequantize_attention(q, (k_quant[0], k_quant[1], kb), (v_quant[0], v_quant[1], vb),
+                                bits=bits, group_size=group_size, scale=scale, mask=mask)
+
+
+def quantized_sdpa(
+    q,
+    packed_k,
+    packed_v,
+    k_scales,
+    v_scales,
+    k_biases=None,
+    v_biases=None,
+    scale=None,
+    mask=None,
+    bits=4,
+    group_size=32,
+    threshold=None,
+    *,
+    kv_start=None,
+    num_splits=None,
+):
+    """Quantized scaled dot-product attention for decode (qL = 1).
+
+    Args (as mlx_qsdpa.quantized_sdpa, dispatch.py:22-40):
+        q:          (B, H_q, qL, D) float16/bfloat16
+        packed_k/v: (B, H_kv, N, D*bits/32) uint32
+        k/v_scales: (B, H_kv, N, D/group_size) q.dtype
+        k/v_biases: same shape, or None for the symmetric format
+        scale:      softmax scale (default D**-0.5)
+        mask:       None, bool keep-mask or additive mask broadcastable to
+                    (B, H_q, 1, N); "causal" (no-op for qL = 1)
+        bits:       4 or 8;  group_size: 32, 64 or 128
+        threshold:  N <= threshold -> single pass, else split-K;
+                    None -> choose for the GPU
+        kv_start:   optional (B,) int tensor: keys before it are ignored
+        num_splits: optional explicit split count (overrides threshold)
+    Returns (B, H_q, qL, D) in q's dtype.
+    """
+    B, H_q, qL, D, H_kv, N = _validate(q, packed_k, packed_v, bits, group_size)
+    if scale is None:
+        scale = D ** -0.5                                          # dispatch.py:86-87
+
+    if qL > 1:                                                     # dispatch.py:68-83
+        return fallback_sdpa(q, (packed_k, k_scales, k_biases), (packed_v, v_scales, v_biases),
+                             bits=bits, group_size=group_size, scale=scale, mask=mask,
+                             kv_start=kv_start)
+
+    has_biases = k_biases is not None and v_biases is not None     # dispatch.py:89-94
+    if not has_biases:
+        k_biases = v_biases = None
+    if isinstance(mask, str):
+        if mask != "causal":
+            raise ValueError(f"unknown mask {mask!r}")
+        mask = None                                                # qL == 1: sees every key
+
+    if num_splits is None:
+        if threshold is None:
+            num_splits = 0
+        elif N <= threshold:                                       # dispatch.py:98
+            num_splits = 1
+        else:
+            auto, _ = kernels.decode_plan(q, packed_k, packed_v, k_scales, v_scales, k_biases,
+                                          v_biases, scale=scale, bits=bits,
+                                          group_size=group_size)
+            num_splits = max(2, auto)
+    return kernels.decode(q, packed_k, packed_v, k_scales, v_scales, k_biases, v_biases,
+                          scale=scale, bits=bits, group_size=group_size, mask=mask,
+                          kv_start=kv_start, num_splits=num_splits)

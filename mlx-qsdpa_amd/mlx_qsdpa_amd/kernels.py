@@ -1,0 +1,280 @@
+"""torch-facing wrappers of the HIP kernels (C ABI: include/qsdpa.h).
+
+Every function here launches on the tensor's device, on torch's current
+stream, and never synchronizes.  Tensors must live on a ROCm device; CPU
+tensors raise (the library has no CPU implementation).
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+_DTYPE_CODE = {torch.float16: _lib.QSDPA_F16, torch.bfloat16: _lib.QSDPA_BF16}
+_MASK_CODE = {torch.float16: _lib.QSDPA_F16, torch.bfloat16: _lib.QSDPA_BF16,
+              torch.float32: _lib.QSDPA_F32, torch.bool: _lib.QSDPA_BOOL}
+
+
+def _require_device(*tensors):
+    for t in tensors:
+        if t is not None and t.device.type != "cuda":
+            raise RuntimeError(
+                "mlx_qsdpa_amd kernels run on a ROCm GPU only; got a tensor on "
+                f"{t.device} (there is no CPU implementation)")
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return _DTYPE_CODE[dtype]
+    except KeyError:
+        raise ValueError(f"dtype must be float16 or bfloat16, got {dtype}") from None
+
+
+def _view(t: torch.Tensor | None) -> _lib.View:
+    """View of a [B, H, N, inner] tensor (innermost stride must be 1)."""
+    if t is None:
+        return _lib.View(None, 0, 0, 0)
+    if t.dim() != 4:
+        raise ValueError(f"expected a 4-D tensor, got shape {tuple(t.shape)}")
+    if t.shape[-1] > 1 and t.stride(-1) != 1:
+        raise ValueError("innermost dimension must be contiguous")
+    s = t.stride()
+    return _lib.View(t.data_ptr(), s[0], s[1], s[2])
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _inner_contig(t: torch.Tensor) -> torch.Tensor:
+    return t if (t.shape[-1] <= 1 or t.stride(-1) == 1) else t.contiguous()
+
+
+# ---------------------------------------------------------------------------
+# quantize / dequantize
+# ---------------------------------------------------------------------------
+def _expect_shape(name, t, shape):
+    if t is not None and tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name}: expected shape {tuple(shape)}, got {tuple(t.shape)}")
+
+
+def quantize_into(src: torch.Tensor, dst: tuple, t0: int, bits: int, group_size: int) -> None:
+    """dst[b, h, t0 + s, :] = quantize(src[b, h, s, :]) for the 3 dst tensors."""
+    _require_device(src, *dst)
+    src = _inner_contig(src)
+    B, H, S, D = src.shape
+    if bits not in (4, 8) or D % group_size:
+        raise ValueError(f"bad bits={bits} / group_size={group_size} for D={D}")
+    cap = dst[0].shape[2]
+    if t0 < 0 or t0 + S > cap:
+        raise ValueError(f"tokens [{t0}, {t0 + S}) do not fit a buffer of {cap}")
+    _expect_shape("dst_packed", dst[0], (B, H, cap, D * bits // 32))
+    _expect_shape("dst_scales", dst[1], (B, H, cap, D // group_size))
+    _expect_shape("dst_biases", dst[2], (B, H, cap, D // group_size))
+    if dst[0].dtype != torch.uint32 or dst[1].dtype != src.dtype or dst[2].dtype != src.dtype:
+        raise ValueError("destination dtypes must be (uint32, src.dtype, src.dtype)")
+    a = _lib.QuantizeArgs(B, H, S, D, bits, group_size, dtype_code(src.dtype), int(t0),
+                          _view(src), _view(dst[0]), _view(dst[1]), _view(dst[2]))
+    lib = _lib.load()
+    _lib.check(lib.qsdpa_quantize(ctypes.byref(a), _stream(src)))
+
+
+def quantize(w: torch.Tensor, group_size: int = 64, bits: int = 4):
+    """mx.quantize for [..., D] float16/bfloat16 tensors -> (packed, scales, biases)."""
+    if w.dim() < 1:
+        raise ValueError("w must have at least one dimension")
+    shape = w.shape
+    D = shape[-1]
+    if D % group_size:
+        raise ValueError(f"last dim {D} not divisible by group_size {group_size}")
+    if bits not in (4, 8):
+        raise ValueError(f"bits must be 4 or 8, got {bits}")
+    w4 = w.reshape(1, 1, -1, D)
+    rows = w4.shape[2]
+    packed = torch.empty((1, 1, rows, D * bits // 32), dtype=torch.uint32, device=w.device)
+    scales = torch.empty((1, 1, rows, D // group_size), dtype=w.dtype, device=w.device)
+    biases = torch.empty_like(scales)
+    quantize_into(w4, (packed, scales, biases), 0, bits, group_size)
+    return (packed.reshape(*shape[:-1], -1), scales.reshape(*shape[:-1], -1),
+            biases.reshape(*shape[:-1], -1))
+
+
+def dequantize_into(src: tuple, dst: torch.Tensor, bits: int, group_size: int,
+                    keep: int = 0, rot: int = 0) -> None:
+    """dst = dequantize(src) with the ring reorder described in qsdpa.h."""
+    packed, scales, biases = src
+    _require_device(packed, scales, biases, dst)
+    B, H, N, W = packed.shape
+    D = dst.shape[-1]
+    if bits not in (4, 8) or W * (32 // bits) != D or D % group_size:
+        raise ValueError(f"packed width {W} does not match D={D}, bits={bits}, gs={group_size}")
+    if packed.dtype != torch.uint32:
+        raise ValueError("packed must be uint32")
+    _expect_shape("scales", scales, (B, H, N, D // group_size))
+    _expect_shape("biases", biases, (B, H, N, D // group_size))
+    _expect_shape("dst", dst, (B, H, N, D))
+    if not 0 <= keep <= N or rot < 0 or (rot > 0 and keep >= N):
+        raise ValueError(f"bad keep={keep} / rot={rot} for N={N}")
+    a = _lib.DequantizeArgs(B, H, N, D, bits, group_size, dtype_code(dst.dtype), int(keep),
+                            int(rot), _view(packed), _view(scales), _view(biases), _view(dst))
+    _lib.check(_lib.load().qsdpa_dequantize(ctypes.byref(a), _stream(dst)))
+
+
+def dequantize(packed: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor | None = None,
+               group_size: int = 64, bits: int = 4, keep: int = 0, rot: int = 0):
+    """mx.dequantize for [..., N, W] packed tensors (biases None = zero)."""
+    lead = packed.shape[:-1]
+    D = packed.shape[-1] * (32 // bits)
+    p4 = packed.reshape(-1, 1, packed.shape[-2] if packed.dim() > 1 else 1, packed.shape[-1])
+    s4 = scales.reshape(p4.shape[0], 1, p4.shape[2], scales.shape[-1])
+    b4 = None if biases is None else biases.reshape(p4.shape[0], 1, p4.shape[2], biases.shape[-1])
+    out = torch.empty((p4.shape[0], 1, p4.shape[2], D), dtype=scales.dtype, device=packed.device)
+    dequantize_into((p4, s4, b4), out, bits, group_size, keep, rot)
+    return out.reshape(*lead, D)
+
+
+# ---------------------------------------------------------------------------
+# decode
+# ---------------------------------------------------------------------------
+def _decode_args(q, pk, pv, ks, vs, kb, vb, out, scale, bits, group_size, mask, kv_start,
+                 num_splits):
+    B, Hq, qL, D = q.shape
+    _, Hkv, N, _ = pk.shape
+    if qL != 1:
+        raise ValueError("the fused decode takes one query position (qL == 1)")
+    if bits not in (4, 8) or D % group_size:
+        raise ValueError(f"bad bits={bits} / group_size={group_size} for D={D}")
+    for name, t, inner, dt in (("packed_k", pk, D * bits // 32, torch.uint32),
+                               ("packed_v", pv, D * bits // 32, torch.uint32),
+                               ("k_scales", ks, D // group_size, q.dtype),
+                               ("v_scales", vs, D // group_size, q.dtype),
+                               ("k_biases", kb, D // group_size, q.dtype),
+                               ("v_biases", vb, D // group_size, q.dtype)):
+        _expect_shape(name, t, (B, Hkv, N, inner))
+        if t is not None and t.dtype != dt:
+            raise ValueError(f"{name}: dtype {t.dtype}, expected {dt}")
+    _expect_shape("out", out, (B, Hq, 1, D))
+    if kv_start is not None and tuple(kv_start.shape) != (B,):
+        raise ValueError(f"kv_start must have shape ({B},)")
+    mview = _lib.View(None, 0, 0, 0)
+    mcode = 0
+    if mask is not None:
+        if mask.dtype not in _MASK_CODE:
+            raise ValueError(f"unsupported mask dtype {mask.dtype}")
+        m = mask
+        while m.dim() < 4:
+            m = m.unsqueeze(0)
+        if m.shape[-1] != N:
+            raise ValueError(f"mask last dim {m.shape[-1]} != number of keys {N}")
+        if m.shape[-2] != 1:
+            raise ValueError("decode mask must have a query dim of 1")
+        m = m.expand(B, Hq, 1, N)
+        if m.stride(-1) != 1:
+            m = m.contiguous()
+        if m.dtype == torch.bool:
+            m = m.view(torch.uint8)
+        s = m.stride()
+        mview = _lib.View(m.data_ptr(), s[0], s[1], s[3])
+        mcode = _MASK_CODE[mask.dtype]
+        mask = m
+    ks_ptr = None
+    if kv_start is not None:
+        ks_t = kv_start
+        ks_ptr = ks_t.data_ptr()
+    a = _lib.DecodeArgs()
+    a.B, a.H_q, a.H_kv, a.N, a.D = B, Hq, Hkv, N, D
+    a.bits, a.group_size, a.dtype = bits, group_size, dtype_code(q.dtype)
+    a.scale = float(scale)
+    a.q = _view(q)
+    a.k_packed, a.v_packed = _view(pk), _view(pv)
+    a.k_scales, a.v_scales = _view(ks), _view(vs)
+    a.k_biases, a.v_biases = _view(kb), _view(vb)
+    a.out = _view(out)
+    a.mask, a.mask_dtype = mview, mcode
+    a.kv_start = ks_ptr
+    a.num_splits = int(num_splits)
+    return a, mask
+
+
+def decode_plan(q, pk, pv, ks, vs, kb, vb, *, scale, bits, group_size, num_splits=0):
+    """(num_splits, workspace_bytes) the library would use for these inputs."""
+    out = torch.empty_like(q)
+    a, _ = _decode_args(q, pk, pv, ks, vs, kb, vb, out, scale, bits, group_size, None, None,
+                        num_splits)
+    n = ctypes.c_int32(0)
+    ws = _lib.check(_lib.load().qsdpa_decode_workspace_size(ctypes.byref(a), ctypes.byref(n)))
+    return int(n.value), int(ws)
+
+
+class DecodePlan:
+    """A decode whose argument block is built once and re-launched cheaply.
+
+    For tight decode loops (and the benchmark): the output and workspace are
+    allocated at construction; each call re-issues the same launch on the
+    current stream of the inputs' device with one ctypes call.  The caller
+    updates the input tensors in place between calls.
+    """
+
+    def __init__(self, q, pk, pv, ks, vs, kb, vb, *, scale, bits, group_size, mask=None,
+                 kv_start=None, num_splits=0):
+        _require_device(q, pk, pv, ks, vs, kb, vb, mask, kv_start)
+        self.q = _inner_contig(q)
+        self.out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+        if kv_start is not None:
+            kv_start = kv_start.to(device=q.device, dtype=torch.int32).contiguous()
+        self._refs = (pk, pv, ks, vs, kb, vb, kv_start)
+        self.args, self._mask = _decode_args(self.q, pk, pv, ks, vs, kb, vb, self.out, scale, bits,
+                                             group_size, mask, kv_start, num_splits)
+        self.lib = _lib.load()
+        n = ctypes.c_int32(0)
+        ws = _lib.check(self.lib.qsdpa_decode_workspace_size(ctypes.byref(self.args),
+                                                             ctypes.byref(n)))
+        self.num_splits = int(n.value)
+        self.workspace = None
+        if ws > 0:
+            self.workspace = torch.empty(ws, dtype=torch.uint8, device=q.device)
+            self.args.workspace = self.workspace.data_ptr()
+            self.args.workspace_bytes = ws
+        self._args_ref = ctypes.byref(self.args)
+        self.device = q.device
+
+    def __call__(self, prof_events=None):
+        if prof_events is not None:
+            self.args.prof_begin, self.args.prof_end = prof_events
+        else:
+            self.args.prof_begin = self.args.prof_end = None
+        _lib.check(self.lib.qsdpa_decode(self._args_ref, _stream(self.q)))
+        return self.out
+
+
+def decode(q, pk, pv, ks, vs, kb, vb, *, scale, bits, group_size, mask=None, kv_start=None,
+           num_splits=0, out=None, workspace=None, prof_events=None):
+    """Fused quantized decode; returns out [B, H_q, 1, D] (dtype of q).
+
+    ``prof_events``: optional (begin, end) raw hipEvent_t handles recorded
+    around the main decode kernel (see qsdpa_decode_args.prof_begin).
+    """
+    _require_device(q, pk, pv, ks, vs, kb, vb, mask, kv_start)
+    q = _inner_contig(q)
+    if out is None:
+        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    if kv_start is not None:
+        kv_start = kv_start.to(device=q.device, dtype=torch.int32).contiguous()
+    a, keep_alive = _decode_args(q, pk, pv, ks, vs, kb, vb, out, scale, bits, group_size, mask,
+                                 kv_start, num_splits)
+    lib = _lib.load()
+    n = ctypes.c_int32(0)
+    ws = _lib.check(lib.qsdpa_decode_workspace_size(ctypes.byref(a), ctypes.byref(n)))
+    if ws > 0:
+        if workspace is None or workspace.numel() < ws:
+            workspace = torch.empty(ws, dtype=torch.uint8, device=q.device)
+        a.workspace = workspace.data_ptr()
+        a.workspace_bytes = ws
+    if prof_events is not None:
+        a.prof_begin, a.prof_end = prof_events
+    _lib.check(lib.qsdpa_decode(ctypes.byref(a), _stream(q)))
+    del keep_alive
+    return out

@@ -1,0 +1,114 @@
+"""Shared test setup.
+
+* Registers the ``gpu`` marker (tests that need an MI355X).
+* Puts the repo root (for ``oracle``) and ``mlx-qsdpa_amd`` (for the
+  ``mlx_qsdpa_amd`` package) on sys.path.
+* ``cpu_kernels``: replaces the library's kernel wrappers with oracle-backed
+  CPU versions so the cache state machines (host logic) run on CPU tensors.
+  The shipped package never does this; only these tests patch it.
+"""
+
+from __future__ import annotations
+
+import os
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+for p in (ROOT, ROOT / "mlx-qsdpa_amd"):
+    if str(p) not in sys.path:
+        sys.path.insert(0, str(p))
+
+import torch  # noqa: E402
+
+from oracle import affine  # noqa: E402
+
+GOLDEN = ROOT / "tests" / "golden"
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs a ROCm GPU (MI355X) and the built HIP library")
+
+
+def has_gpu() -> bool:
+    return torch.cuda.is_available()
+
+
+@pytest.fixture(scope="session")
+def device():
+    if not has_gpu():
+        pytest.skip("no ROCm GPU in this environment")
+    from mlx_qsdpa_amd import _lib
+    _lib.load()  # fail loudly if the HIP library is missing
+    return torch.device("cuda:0")
+
+
+def dtype_name(dt: torch.dtype) -> str:
+    return {torch.float16: "f16", torch.bfloat16: "bf16"}[dt]
+
+
+def torch_dtype(name: str) -> torch.dtype:
+    return {"f16": torch.float16, "bf16": torch.bfloat16}[name]
+
+
+def to_np(t: torch.Tensor) -> np.ndarray:
+    """Exact host copy: uint32 stays uint32, T -> float32 values."""
+    t = t.detach().cpu()
+    if t.dtype == torch.uint32:
+        return t.numpy()
+    return t.float().numpy()
+
+
+def from_np(x: np.ndarray, dtype: torch.dtype, device=None) -> torch.Tensor:
+    if x.dtype == np.uint32:
+        t = torch.from_numpy(np.ascontiguousarray(x))
+    else:
+        t = torch.from_numpy(np.ascontiguousarray(x, dtype=np.float32)).to(dtype)
+    return t if device is None else t.to(device)
+
+
+# ---------------------------------------------------------------------------
+# oracle-backed CPU stand-ins for the kernel wrappers (tests only)
+# ---------------------------------------------------------------------------
+def _cpu_quantize_into(src, dst, t0, bits, group_size):
+    name = dtype_name(src.dtype)
+    p, s, b = affine.quantize(to_np(src), group_size, bits, name)
+    S = src.shape[2]
+    dst[0][:, :, t0:t0 + S] = torch.from_numpy(p)
+    dst[1][:, :, t0:t0 + S] = from_np(s, src.dtype)
+    dst[2][:, :, t0:t0 + S] = from_np(b, src.dtype)
+
+
+def _cpu_dequantize(packed, scales, biases=None, group_size=64, bits=4, keep=0, rot=0):
+    name = dtype_name(scales.dtype)
+    out = affine.dequantize(to_np(packed), to_np(scales),
+                            None if biases is None else to_np(biases), group_size, bits, name)
+    n = out.shape[-2]
+    if rot:
+        idx = np.arange(n)
+        u = np.where(idx < keep, idx, keep + (idx - keep + rot) % (n - keep))
+        out = np.take(out, u, axis=-2)
+    return from_np(out, scales.dtype)
+
+
+@pytest.fixture
+def cpu_kernels(monkeypatch):
+    from mlx_qsdpa_amd import kernels
+    monkeypatch.setattr(kernels, "quantize_into", _cpu_quantize_into)
+    monkeypatch.setattr(kernels, "dequantize", _cpu_dequantize)
+    return kernels
+
+
+def rand_T(rng, shape, name, **kw):
+    return affine.random_T(rng, shape, name, **kw)
+
+
+@pytest.fixture
+def rng():
+    return np.random.default_rng(42)
+
+
+os.environ.setdefault("PYTHONHASHSEED", "0")

@@ -1,0 +1,93 @@
+"""The C-ABI boundary (CPU only: no kernel is launched here).
+
+* every function include/qsdpa.h declares is exported by libqsdpa_hip.so;
+* the ctypes structs of the Python binding have the header's layout
+  (sizeof/offsetof printed by a gcc-compiled probe of the header);
+* argument errors come back as negative codes with a message, before any
+  HIP call.
+"""
+
+import ctypes
+import re
+import shutil
+import subprocess
+
+import pytest
+
+from conftest import ROOT
+from mlx_qsdpa_amd import _lib
+
+HEADER = ROOT / "include" / "qsdpa.h"
+
+
+def _declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(qsdpa_[a-z_]+)\s*\(", text)))
+
+
+def test_header_functions_match_binding():
+    assert _declared_functions() == sorted(_lib.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_symbol():
+    lib = _lib.load()
+    for name in _declared_functions():
+        assert hasattr(lib, name), f"{name} not exported"
+    assert lib.qsdpa_abi_version() == _lib.ABI_VERSION
+
+
+_STRUCTS = {
+    "qsdpa_view": _lib.View,
+    "qsdpa_decode_args": _lib.DecodeArgs,
+    "qsdpa_quantize_args": _lib.QuantizeArgs,
+    "qsdpa_dequantize_args": _lib.DequantizeArgs,
+}
+
+
+@pytest.mark.skipif(shutil.which("gcc") is None, reason="gcc not available")
+def test_struct_layout_matches_header(tmp_path):
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void){"]
+    for cname, cls in _STRUCTS.items():
+        lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
+        for fname, _ in cls._fields_:
+            lines.append(f'printf("{cname} {fname} %zu\\n", offsetof({cname}, {fname}));')
+    lines.append("return 0;}")
+    src = tmp_path / "probe.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "probe"
+    subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout
+    got = {}
+    for line in out.splitlines():
+        s, f, v = line.split()
+        got[(s, f)] = int(v)
+    for cname, cls in _STRUCTS.items():
+        assert got[(cname, "size")] == ctypes.sizeof(cls), cname
+        for fname, _ in cls._fields_:
+            assert got[(cname, fname)] == getattr(cls, fname).offset, f"{cname}.{fname}"
+
+
+def test_invalid_arguments_return_codes():
+    lib = _lib.load()
+    q = _lib.QuantizeArgs()
+    q.bits = 3
+    q.group_size = 32
+    assert lib.qsdpa_quantize(ctypes.byref(q), None) == _lib.QSDPA_ERR_INVALID
+    assert b"bits" in lib.qsdpa_last_error()
+    d = _lib.DequantizeArgs()
+    d.bits, d.group_size, d.D = 4, 48, 96
+    assert lib.qsdpa_dequantize(ctypes.byref(d), None) == _lib.QSDPA_ERR_UNSUPPORTED
+    a = _lib.DecodeArgs()
+    a.B = a.H_q = a.H_kv = a.N = 1
+    a.D, a.bits, a.group_size = 100, 4, 32
+    assert lib.qsdpa_decode(ctypes.byref(a), None) == _lib.QSDPA_ERR_INVALID
+    assert b"multiple of 32" in lib.qsdpa_last_error()
+    a.D = 128
+    a.H_q, a.H_kv = 3, 2
+    assert lib.qsdpa_decode_workspace_size(ctypes.byref(a), None) == _lib.QSDPA_ERR_INVALID
+    assert b"divisible" in lib.qsdpa_last_error()
+    a.H_q = 2
+    assert lib.qsdpa_decode(ctypes.byref(a), None) == _lib.QSDPA_ERR_INVALID  # null pointers
+    with pytest.raises(_lib.QsdpaError):
+        _lib.check(lib.qsdpa_decode(ctypes.byref(a), None))

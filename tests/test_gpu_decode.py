@@ -1,0 +1,269 @@
+"""Decode parity on the GPU: HIP kernels (through the C ABI) vs the oracle.
+
+Tolerance (north star): |out - ref| <= 2e-3 + 1e-2 * |ref| with ref the
+float64 dequantize + SDPA oracle on the same seeded, oracle-quantized inputs.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import from_np, to_np, torch_dtype
+from oracle import affine, attention
+
+import mlx_qsdpa_amd as mq
+from mlx_qsdpa_amd import kernels
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 2e-3, 1e-2
+
+
+def make_inputs(rng, B, Hq, Hkv, N, D, bits, gs, dtype="f16", outliers=0.0, symmetric=False):
+    q = affine.random_T(rng, (B, Hq, 1, D), dtype)
+    kw = affine.random_T(rng, (B, Hkv, N, D), dtype, outlier_frac=outliers)
+    vw = affine.random_T(rng, (B, Hkv, N, D), dtype, outlier_frac=outliers)
+    kp, ks, kb = affine.quantize(kw, gs, bits, dtype)
+    vp, vs, vb = affine.quantize(vw, gs, bits, dtype)
+    if symmetric:
+        kb = vb = None
+    return dict(q=q, kp=kp, vp=vp, ks=ks, vs=vs, kb=kb, vb=vb, bits=bits, gs=gs, dtype=dtype)
+
+
+def to_dev(inp, device):
+    t = torch_dtype(inp["dtype"])
+    g = {k: (None if inp[k] is None else from_np(inp[k], t, device))
+         for k in ("q", "kp", "vp", "ks", "vs", "kb", "vb")}
+    return g
+
+
+def oracle_out(inp, mask=None, scale=None):
+    return attention.quantized_sdpa_reference(
+        inp["q"], inp["kp"], inp["vp"], inp["ks"], inp["vs"], inp["kb"], inp["vb"],
+        bits=inp["bits"], group_size=inp["gs"], dtype=inp["dtype"], scale=scale, mask=mask)
+
+
+def run(inp, device, **kw):
+    g = to_dev(inp, device)
+    out = mq.quantized_sdpa(g["q"], g["kp"], g["vp"], g["ks"], g["vs"], g["kb"], g["vb"],
+                            bits=inp["bits"], group_size=inp["gs"], **kw)
+    torch.cuda.synchronize()
+    return to_np(out)
+
+
+def assert_close(got, want, ctx=""):
+    err = np.abs(got - want)
+    bound = ATOL + RTOL * np.abs(want)
+    bad = err > bound
+    assert not bad.any(), (f"{ctx}: {bad.sum()} of {bad.size} outside tolerance, "
+                           f"max abs err {err.max():.3e}")
+    assert np.isfinite(got).all(), ctx
+
+
+# B, Hq, Hkv, N, D, bits, gs, dtype -- the reference's test shapes
+# (tests/test_correctness.py, test_2pass.py, test_formats.py, test_shapes.py,
+# test_long_context.py) and BASELINE configs at oracle-sized N.
+CASES = [
+    (1, 1, 1, 32, 128, 4, 32, "f16"),
+    (1, 16, 2, 64, 256, 4, 32, "f16"),
+    (1, 16, 2, 1024, 256, 4, 32, "f16"),
+    (1, 4, 1, 1, 128, 4, 32, "f16"),
+    (1, 16, 2, 128, 256, 8, 32, "f16"),
+    (1, 16, 2, 128, 256, 4, 64, "f16"),
+    (1, 16, 2, 128, 256, 4, 128, "f16"),
+    (1, 4, 4, 64, 128, 4, 32, "f16"),
+    (1, 4, 2, 64, 256, 4, 32, "f16"),
+    (1, 4, 2, 32, 128, 4, 32, "f16"),
+    (2, 4, 2, 64, 128, 4, 32, "f16"),
+    (1, 16, 2, 4096, 256, 4, 32, "f16"),
+    (1, 16, 2, 8192, 256, 4, 32, "f16"),
+    (1, 32, 2, 64, 256, 4, 32, "f16"),
+    (1, 2, 2, 64, 256, 8, 32, "f16"),
+    (1, 8, 2, 4096, 128, 4, 64, "f16"),      # C1
+    (1, 2, 2, 8192, 256, 8, 64, "bf16"),     # C2 (small N)
+    (1, 32, 2, 16384, 256, 4, 32, "f16"),    # C3 (small N)
+    (4, 32, 8, 1024, 128, 4, 64, "f16"),     # C4 shape
+    (4, 16, 4, 4096, 128, 8, 128, "bf16"),   # C5 decode window
+    (1, 8, 1, 300, 64, 4, 32, "bf16"),
+    (3, 6, 3, 77, 64, 8, 64, "f16"),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: "B{}_Hq{}_Hkv{}_N{}_D{}_b{}_g{}_{}".format(*c))
+def test_decode_matches_oracle(device, case):
+    B, Hq, Hkv, N, D, bits, gs, dt = case
+    rng = np.random.default_rng(1000 + N + D + Hq)
+    inp = make_inputs(rng, B, Hq, Hkv, N, D, bits, gs, dt, outliers=0.01 if dt == "bf16" else 0)
+    want = oracle_out(inp)
+    for splits in (None, 1, 7):
+        got = run(inp, device, num_splits=splits)
+        assert_close(got, want, f"{case} splits={splits}")
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_symmetric_format(device, bits):
+    rng = np.random.default_rng(7)
+    inp = make_inputs(rng, 1, 16, 2, 128, 256, bits, 32, symmetric=True)
+    assert_close(run(inp, device), oracle_out(inp), "symmetric")
+
+
+def test_one_bias_missing_means_zero_biases(device):
+    """dispatch.py:89-94: unless both biases are given, both are zero."""
+    rng = np.random.default_rng(8)
+    inp = make_inputs(rng, 1, 4, 2, 64, 128, 4, 32)
+    g = to_dev(inp, device)
+    out = mq.quantized_sdpa(g["q"], g["kp"], g["vp"], g["ks"], g["vs"], g["kb"], None)
+    want = oracle_out(dict(inp, kb=None, vb=None))
+    assert_close(to_np(out), want, "one bias")
+
+
+def test_threshold_semantics(device):
+    """tests/test_long_context.py:30-67: threshold N+1 -> single, N-1 -> split."""
+    rng = np.random.default_rng(9)
+    N = 4096
+    inp = make_inputs(rng, 1, 16, 2, N, 256, 4, 32)
+    want = oracle_out(inp)
+    a = run(inp, device, threshold=N + 1)
+    b = run(inp, device, threshold=N - 1)
+    c = run(inp, device, threshold=0)
+    for x in (a, b, c):
+        assert_close(x, want, "threshold")
+    assert np.abs(a - b).max() < 2e-3
+
+
+def test_single_key_returns_value_row(device):
+    rng = np.random.default_rng(10)
+    inp = make_inputs(rng, 1, 4, 2, 1, 128, 4, 32)
+    got = run(inp, device)
+    v = affine.dequantize(inp["vp"], inp["vs"], inp["vb"], 32, 4, "f16")
+    want = np.repeat(v[:, :, 0:1], 2, axis=1)
+    assert_close(got, want, "N=1")
+
+
+def test_zero_scales_no_nan(device):
+    """tests/test_shapes.py:89-101."""
+    rng = np.random.default_rng(11)
+    inp = make_inputs(rng, 1, 4, 2, 32, 128, 4, 32)
+    for k in ("ks", "vs", "kb", "vb"):
+        inp[k] = np.zeros_like(inp[k])
+    got = run(inp, device)
+    assert np.isfinite(got).all() and np.all(got == 0)
+
+
+@pytest.mark.parametrize("mdtype", ["bool", "f16", "f32", "per_head"])
+def test_masked_decode_in_kernel(device, mdtype):
+    rng = np.random.default_rng(12)
+    B, Hq, Hkv, N = 2, 8, 2, 700
+    inp = make_inputs(rng, B, Hq, Hkv, N, 128, 4, 32)
+    if mdtype == "per_head":
+        keep = rng.random((B, Hq, 1, N)) > 0.5
+    else:
+        keep = rng.random((B, 1, 1, N)) > 0.3
+    keep[..., 5] = True
+    if mdtype == "bool" or mdtype == "per_head":
+        m_np, m_t = keep, torch.from_numpy(keep).to(device)
+    else:
+        add = np.where(keep, rng.standard_normal(keep.shape) * 0.5, -np.inf).astype(np.float32)
+        if mdtype == "f16":
+            add = add.astype(np.float16).astype(np.float32)
+        m_np = add
+        m_t = torch.from_numpy(add).to(device, torch.float16 if mdtype == "f16" else torch.float32)
+    want = oracle_out(inp, mask=m_np)
+    for splits in (None, 1, 5):
+        assert_close(run(inp, device, mask=m_t, num_splits=splits), want, f"mask {mdtype}")
+
+
+def test_kv_start_left_padding(device):
+    """Keys before kv_start[b] are skipped == additive -inf mask on them (C4 semantics)."""
+    rng = np.random.default_rng(13)
+    B, Hq, Hkv, N = 4, 32, 8, 2000
+    inp = make_inputs(rng, B, Hq, Hkv, N, 128, 4, 64)
+    starts = np.array([0, 1500, 37, 1999])
+    add = np.where(np.arange(N)[None, :] >= starts[:, None], 0.0, -np.inf)[:, None, None, :]
+    want = oracle_out(inp, mask=add)
+    ks = torch.tensor(starts, dtype=torch.int32, device=device)
+    for splits in (None, 1, 9):
+        assert_close(run(inp, device, kv_start=ks, num_splits=splits), want, "kv_start")
+    m = torch.from_numpy(add.astype(np.float32)).to(device, torch.float16)
+    assert_close(run(inp, device, mask=m), want, "additive left padding")
+
+
+def test_fully_masked_row_is_zero(device):
+    rng = np.random.default_rng(14)
+    inp = make_inputs(rng, 2, 4, 2, 64, 128, 4, 32)
+    keep = np.ones((2, 1, 1, 64), bool)
+    keep[1] = False
+    got = run(inp, device, mask=torch.from_numpy(keep).to(device))
+    assert np.all(got[1] == 0) and np.isfinite(got).all()
+    assert_close(got[0], oracle_out(inp, mask=keep)[0], "masked")
+
+
+def test_strided_cache_views(device):
+    """Views of capacity-padded buffers are read by stride (no copy)."""
+    rng = np.random.default_rng(15)
+    B, Hq, Hkv, N, cap, D = 2, 8, 2, 300, 512, 128
+    inp = make_inputs(rng, B, Hq, Hkv, N, D, 4, 32)
+    g = to_dev(inp, device)
+    views = {}
+    for k in ("kp", "vp", "ks", "vs", "kb", "vb"):
+        t = g[k]
+        buf = torch.zeros((B, Hkv, cap, t.shape[-1]), dtype=t.dtype, device=device)
+        buf[:, :, :N] = t
+        views[k] = buf[:, :, :N]
+        assert not views[k].is_contiguous()
+    out = mq.quantized_sdpa(g["q"], views["kp"], views["vp"], views["ks"], views["vs"],
+                            views["kb"], views["vb"], bits=4, group_size=32)
+    assert_close(to_np(out), oracle_out(inp), "strided")
+
+
+def test_prefill_fallback(device):
+    """qL > 1 -> dequantize + attention (dispatch.py:68-83), causal and bool masks."""
+    rng = np.random.default_rng(16)
+    inp = make_inputs(rng, 1, 4, 2, 64, 128, 4, 32)
+    q = affine.random_T(rng, (1, 4, 8, 128), "f16")
+    inp8 = dict(inp, q=q)
+    g = to_dev(inp8, device)
+    for mask in (None, "causal"):
+        out = mq.quantized_sdpa(g["q"], g["kp"], g["vp"], g["ks"], g["vs"], g["kb"], g["vb"],
+                                mask=mask)
+        assert_close(to_np(out), oracle_out(inp8, mask=mask), f"prefill {mask}")
+
+
+def _torch_dequant(p, s, b, bits, gs, T):
+    """Independent float32 dequantize with torch integer ops (shift / mask)."""
+    per = 32 // bits
+    shifts = torch.arange(per, device=p.device, dtype=torch.int64) * bits
+    codes = ((p.view(torch.int32).to(torch.int64) & 0xFFFFFFFF)[..., None] >> shifts) & ((1 << bits) - 1)
+    codes = codes.reshape(*p.shape[:-1], -1).float()
+    sf = s.float().repeat_interleave(gs, dim=-1)
+    bf = b.float().repeat_interleave(gs, dim=-1)
+    return torch.addcmul(bf, codes, sf).to(T)
+
+
+@pytest.mark.parametrize("N", [65536, 131072])
+def test_headline_full_size_properties(device, N):
+    """C3 at full N: vs an independent torch float32 reference, split-K vs single
+    pass, and invariance to a token permutation."""
+    torch.manual_seed(0)
+    B, Hq, Hkv, D, bits, gs = 1, 32, 2, 256, 4, 32
+    T = torch.float16
+    kw = torch.randn((B, Hkv, N, D), device=device).to(T)
+    vw = torch.randn((B, Hkv, N, D), device=device).to(T)
+    q = torch.randn((B, Hq, 1, D), device=device).to(T)
+    kq = kernels.quantize(kw, gs, bits)
+    vq = kernels.quantize(vw, gs, bits)
+    out = mq.quantized_sdpa(q, kq[0], vq[0], kq[1], vq[1], kq[2], vq[2], bits=bits, group_size=gs)
+    k = _torch_dequant(*kq, bits, gs, T)
+    v = _torch_dequant(*vq, bits, gs, T)
+    from mlx_qsdpa_amd.dispatch import attention_fp32
+    ref = attention_fp32(q, k, v, D ** -0.5).float()
+    err = (out.float() - ref).abs()
+    assert bool((err <= ATOL + RTOL * ref.abs()).all()), f"max err {err.max().item():.3e}"
+    single = mq.quantized_sdpa(q, kq[0], vq[0], kq[1], vq[1], kq[2], vq[2], bits=bits,
+                               group_size=gs, num_splits=1)
+    assert (single.float() - out.float()).abs().max().item() < 2e-3
+    perm = torch.randperm(N, device=device)
+    pq = [t[:, :, perm].contiguous() for t in kq], [t[:, :, perm].contiguous() for t in vq]
+    outp = mq.quantized_sdpa(q, pq[0][0], pq[1][0], pq[0][1], pq[1][1], pq[0][2], pq[1][2],
+                             bits=bits, group_size=gs)
+    assert (outp.float() - out.float()).abs().max().item() < 2e-3

@@ -1,0 +1,119 @@
+"""Quantize-on-append and dequantize kernels vs the oracle: bit-exact."""
+
+import json
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import GOLDEN, from_np, to_np, torch_dtype
+from oracle import affine
+
+from mlx_qsdpa_amd import kernels
+
+pytestmark = pytest.mark.gpu
+
+KAT = json.loads((GOLDEN / "affine_known_answers.json").read_text())
+
+
+def _bits_equal(a, b, dtype):
+    return np.array_equal(affine.T_bits(a, dtype), affine.T_bits(b, dtype))
+
+
+@pytest.mark.parametrize("case", KAT["quantize"], ids=lambda c: c["name"])
+def test_quantize_kernel_known_answers(device, case):
+    dt = torch_dtype(case["dtype"])
+    w = from_np(np.array(case["w"], np.float32)[None], dt, device)
+    p, s, b = kernels.quantize(w, case["group_size"], case["bits"])
+    p = to_np(p)
+    assert affine.unpack(p, case["bits"])[0].tolist() == case["codes"]
+    if "words" in case:
+        assert p[0].tolist() == [int(x, 16) for x in case["words"]]
+    assert affine.T_bits(to_np(b), case["dtype"])[0, 0] == int(case["bias_bits"], 16)
+    if "scale_bits" in case:
+        assert affine.T_bits(to_np(s), case["dtype"])[0, 0] == int(case["scale_bits"], 16)
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("bits,gs,D", [(4, 32, 256), (4, 64, 128), (4, 128, 128),
+                                       (8, 32, 64), (8, 64, 256), (8, 128, 128)])
+def test_quantize_kernel_matches_oracle(device, dtype, bits, gs, D):
+    rng = np.random.default_rng(bits * 1000 + gs + D)
+    w = affine.random_T(rng, (3, 4, 257, D), dtype, outlier_frac=0.02)
+    w[0, 0, 0] = 0.0                      # all-zero row
+    w[0, 0, 1] = w[0, 0, 1, :1]           # constant row
+    w[0, 0, 2] = -np.abs(w[0, 0, 2])      # all-negative row
+    want = affine.quantize(w, gs, bits, dtype)
+    got = kernels.quantize(from_np(w, torch_dtype(dtype), device), gs, bits)
+    assert np.array_equal(to_np(got[0]), want[0])
+    assert _bits_equal(to_np(got[1]), want[1], dtype)
+    assert _bits_equal(to_np(got[2]), want[2], dtype)
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_quantize_into_strided_destination(device, dtype):
+    """Writes land at [t0, t0+S) of a capacity-padded buffer; nothing else changes."""
+    rng = np.random.default_rng(3)
+    B, H, S, D, cap, t0, gs, bits = 2, 3, 5, 128, 40, 17, 64, 4
+    T = torch_dtype(dtype)
+    src = affine.random_T(rng, (B, H, S, D), dtype)
+    dst = (torch.full((B, H, cap, D * bits // 32), 0xDEAD, dtype=torch.int32, device=device)
+           .view(torch.uint32),
+           torch.full((B, H, cap, D // gs), 7.0, dtype=T, device=device),
+           torch.full((B, H, cap, D // gs), 7.0, dtype=T, device=device))
+    # a transposed (non-contiguous) source view
+    src_t = from_np(np.ascontiguousarray(src.transpose(1, 0, 2, 3)), T, device).transpose(0, 1)
+    kernels.quantize_into(src_t, dst, t0, bits, gs)
+    want = affine.quantize(src, gs, bits, dtype)
+    p = to_np(dst[0])
+    assert np.array_equal(p[:, :, t0:t0 + S], want[0])
+    assert np.all(p[:, :, :t0] == 0xDEAD) and np.all(p[:, :, t0 + S:] == 0xDEAD)
+    assert _bits_equal(to_np(dst[1])[:, :, t0:t0 + S], want[1], dtype)
+    assert np.all(to_np(dst[2])[:, :, :t0] == 7.0)
+
+
+def _scalar_T(bits_hex, dt, device):
+    v = int(bits_hex, 16)
+    v = v - (1 << 16) if v >= 1 << 15 else v
+    return torch.tensor([[v]], dtype=torch.int16).view(dt).to(device)
+
+
+@pytest.mark.parametrize("case", KAT["dequantize"], ids=lambda c: c["name"])
+def test_dequantize_kernel_known_answers(device, case):
+    dt = torch_dtype(case["dtype"])
+    q = np.zeros((1, case["group_size"]), np.uint32)
+    q[0, 0] = case["code"]
+    p = torch.from_numpy(affine.pack(q, case["bits"])).to(device)
+    s = _scalar_T(case["scale_bits"], dt, device)
+    b = _scalar_T(case["bias_bits"], dt, device)
+    v = kernels.dequantize(p, s, b, case["group_size"], case["bits"])
+    assert affine.T_bits(to_np(v)[:, :1], case["dtype"])[0, 0] == int(case["value_bits"], 16)
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("bits,gs", [(4, 32), (4, 128), (8, 64)])
+def test_dequantize_kernel_matches_oracle(device, dtype, bits, gs):
+    rng = np.random.default_rng(bits + gs)
+    w = affine.random_T(rng, (2, 3, 100, 128), dtype)
+    p, s, b = affine.quantize(w, gs, bits, dtype)
+    T = torch_dtype(dtype)
+    got = kernels.dequantize(torch.from_numpy(p).to(device), from_np(s, T, device),
+                             from_np(b, T, device), gs, bits)
+    want = affine.dequantize(p, s, b, gs, bits, dtype)
+    assert _bits_equal(to_np(got), want, dtype)
+    got0 = kernels.dequantize(torch.from_numpy(p).to(device), from_np(s, T, device), None, gs, bits)
+    assert _bits_equal(to_np(got0), affine.dequantize(p, s, None, gs, bits, dtype), dtype)
+
+
+@pytest.mark.parametrize("keep,rot", [(0, 0), (0, 5), (3, 4), (2, 9)])
+def test_dequantize_ring_reorder(device, keep, rot):
+    rng = np.random.default_rng(keep * 10 + rot)
+    N = 12
+    w = affine.random_T(rng, (1, 2, N, 64), "f16")
+    p, s, b = affine.quantize(w, 32, 4, "f16")
+    T = torch.float16
+    got = kernels.dequantize(torch.from_numpy(p).to(device), from_np(s, T, device),
+                             from_np(b, T, device), 32, 4, keep=keep, rot=rot)
+    full = affine.dequantize(p, s, b, 32, 4, "f16")
+    idx = [t if t < keep else keep + (t - keep + rot) % (N - keep) for t in range(N)]
+    assert _bits_equal(to_np(got), full[:, :, idx], "f16")
