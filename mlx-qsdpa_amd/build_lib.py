@@ -43,15 +43,17 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found")
 
 
-def build(jobs: int = 4, verbose: bool = False) -> Path:
+def build(jobs: int = 4, verbose: bool = False, extra_flags=(), out: Path | None = None) -> Path:
+    """Compile csrc/*.hip and link the library (to `out`, default in-tree)."""
     cc = hipcc()
     srcs = sorted(CSRC.glob("*.hip"))
-    objdir = HERE / "_build"
-    objdir.mkdir(exist_ok=True)
+    lib = Path(out) if out is not None else LIB
+    objdir = HERE / "_build" / (lib.stem if out is not None else "default")
+    objdir.mkdir(parents=True, exist_ok=True)
 
     def compile_one(src: Path) -> Path:
         obj = objdir / (src.stem + ".o")
-        cmd = [cc, *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+        cmd = [cc, *HIPCC_FLAGS, *extra_flags, "-c", str(src), "-o", str(obj)]
         if verbose:
             print(" ".join(cmd), flush=True)
         r = subprocess.run(cmd, capture_output=True, text=True)
@@ -61,21 +63,24 @@ def build(jobs: int = 4, verbose: bool = False) -> Path:
 
     with cf.ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
         objs = list(ex.map(compile_one, srcs))
-    tmp = LIB.with_suffix(".so.tmp")
+    tmp = lib.with_suffix(".so.tmp")
     cmd = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, lib)
+    return lib
 
 
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=4)
     ap.add_argument("-v", "--verbose", action="store_true")
+    ap.add_argument("--out", default=None, help="output library path (default: in-tree)")
+    ap.add_argument("-D", dest="defines", action="append", default=[],
+                    help="extra preprocessor define for the kernels (NAME=VALUE)")
     args = ap.parse_args(argv)
-    lib = build(args.jobs, args.verbose)
+    lib = build(args.jobs, args.verbose, [f"-D{d}" for d in args.defines], args.out)
     print(f"built {lib}")
     return 0
 

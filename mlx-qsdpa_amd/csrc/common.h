@@ -84,6 +84,39 @@ __device__ __forceinline__ float group_sum(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// ---------------------------------------------------------------------------
+// Packed T pairs (two 16-bit values in one 32-bit register).
+// ---------------------------------------------------------------------------
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// Round two floats to T (nearest even) and pack: v_cvt_pk_{f16,bf16}_f32.
+template <typename Tag>
+__device__ __forceinline__ uint32_t pack_T2(float lo, float hi) {
+  const f32x2 v = {lo, hi};
+  if constexpr (Tag::kId == QSDPA_F16) return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
+  else return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+}
+template <typename Tag>
+__device__ __forceinline__ float unpack_T2_lo(uint32_t p) {
+  return to_f32<Tag>(static_cast<uint16_t>(p & 0xFFFFu));
+}
+template <typename Tag>
+__device__ __forceinline__ float unpack_T2_hi(uint32_t p) {
+  if constexpr (Tag::kId == QSDPA_F16) return f16_bits_to_f32(static_cast<uint16_t>(p >> 16));
+  else return __builtin_bit_cast(float, p & 0xFFFF0000u);
+}
+// a.x*b.x + a.y*b.y + c with float accumulation (v_dot2c_f32_{f16,bf16}).
+template <typename Tag>
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  if constexpr (Tag::kId == QSDPA_F16)
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), c, false);
+  else
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c,
+                                           false);
+}
+
 // Strided 4-D addressing (element strides).
 __device__ __forceinline__ int64_t off3(int b, int h, int n, int64_t sb, int64_t sh, int64_t sn) {
   return static_cast<int64_t>(b) * sb + static_cast<int64_t>(h) * sh + static_cast<int64_t>(n) * sn;

@@ -13,9 +13,9 @@
 //   Inside a wave, L = D/E lanes cover one token row (E dims per lane, one
 //   16/8/4-byte load each), so 64/L tokens are in flight per wave step and
 //   every K/V row is read with one coalesced vector load per lane.
-//   Dequantization is folded into the dot products (all E dims of a lane
-//   share one scale/bias):  q.k = s * sum(q * code) + b * sum(q)  and
-//   acc += (p*s) * code  with the bias term p*b accumulated once per lane.
+//   Every K/V element is dequantized as the reference's mx.dequantize does
+//   (scale*code + bias, rounded to T with v_cvt_pk_{f16,bf16}_f32); q.k runs
+//   on T pairs with v_dot2c_f32_{f16,bf16} and p*v accumulates in float.
 //   Softmax is online in the log2 domain with a lazy rescale: the running
 //   max only moves when a score exceeds it by more than 8 (so p <= 256).
 // Partials are float32: acc[D], m, l per (batch, head, split); the merge
@@ -151,26 +151,22 @@ __global__ __launch_bounds__(256) void decode_valu_kernel(DecodeParams p) {
   const int n0 = s0 + split * chunk;
   const int n1 = min(n0 + chunk, p.N);
 
-  float qv[HB][E];
-  float qsum[HB];
+  // q stays in T (exact) as packed pairs; the softmax scale is applied to
+  // the float dot product.
+  uint32_t q2[HB][E / 2];
 #pragma unroll
   for (int h = 0; h < HB; ++h) {
     const uint16_t* qp = p.q + static_cast<int64_t>(b) * p.q_sb + static_cast<int64_t>(h0 + h) * p.q_sh + d0;
-    float s = 0.0f;
 #pragma unroll
-    for (int e = 0; e < E; ++e) {
-      qv[h][e] = to_f32<Tag>(qp[e]) * p.qscale;
-      s += qv[h][e];
-    }
-    qsum[h] = s;
+    for (int e = 0; e < E / 2; ++e)
+      q2[h][e] = static_cast<uint32_t>(qp[2 * e]) | (static_cast<uint32_t>(qp[2 * e + 1]) << 16);
   }
 
-  float m[HB], l[HB], acc[HB][E], bacc[HB];
+  float m[HB], l[HB], acc[HB][E];
 #pragma unroll
   for (int h = 0; h < HB; ++h) {
     m[h] = kNegBig;
     l[h] = 0.0f;
-    bacc[h] = 0.0f;
 #pragma unroll
     for (int e = 0; e < E; ++e) acc[h][e] = 0.0f;
   }
@@ -193,15 +189,21 @@ __global__ __launch_bounds__(256) void decode_valu_kernel(DecodeParams p) {
     const float kbf = kbb ? to_f32<Tag>(kbb[static_cast<int64_t>(tc) * p.kb_sn]) : 0.0f;
     const float vbf = vbb ? to_f32<Tag>(vbb[static_cast<int64_t>(tc) * p.vb_sn]) : 0.0f;
 
+    // K: dequantize each element exactly as the reference's mx.dequantize
+    // (scale*q + bias, rounded to T), then dot with q in T pairs.
     float code[E];
     unpack_codes<BITS, E>(kw.w, code);
+    uint32_t k2[E / 2];
+#pragma unroll
+    for (int e = 0; e < E / 2; ++e)
+      k2[e] = pack_T2<Tag>(fmaf(ksf, code[2 * e], kbf), fmaf(ksf, code[2 * e + 1], kbf));
     float sc[HB];
 #pragma unroll
     for (int h = 0; h < HB; ++h) {
       float dot = 0.0f;
 #pragma unroll
-      for (int e = 0; e < E; ++e) dot = fmaf(qv[h][e], code[e], dot);
-      sc[h] = fmaf(ksf, dot, kbf * qsum[h]);
+      for (int e = 0; e < E / 2; ++e) dot = dot2<Tag>(q2[h][e], k2[e], dot);
+      sc[h] = dot * p.qscale;
     }
 #pragma unroll
     for (int h = 0; h < HB; ++h) sc[h] = group_sum<L>(sc[h]);
@@ -210,7 +212,14 @@ __global__ __launch_bounds__(256) void decode_valu_kernel(DecodeParams p) {
       for (int h = 0; h < HB; ++h) sc[h] += valid ? mask_value<Tag>(p, b, h0 + h, tc) : 0.0f;
     }
 
+    // V: dequantize + round to T, back to float for the accumulation.
     unpack_codes<BITS, E>(vw.w, code);
+#pragma unroll
+    for (int e = 0; e < E / 2; ++e) {
+      const uint32_t v2 = pack_T2<Tag>(fmaf(vsf, code[2 * e], vbf), fmaf(vsf, code[2 * e + 1], vbf));
+      code[2 * e] = unpack_T2_lo<Tag>(v2);
+      code[2 * e + 1] = unpack_T2_hi<Tag>(v2);
+    }
 #pragma unroll
     for (int h = 0; h < HB; ++h) {
       const float s = valid ? sc[h] : -__builtin_huge_valf();
@@ -218,24 +227,19 @@ __global__ __launch_bounds__(256) void decode_valu_kernel(DecodeParams p) {
         const float f = fast_exp2(m[h] - s);
         m[h] = s;
         l[h] *= f;
-        bacc[h] *= f;
 #pragma unroll
         for (int e = 0; e < E; ++e) acc[h][e] *= f;
       }
       const float pr = fast_exp2(s - m[h]);
       l[h] += pr;
-      const float ps = pr * vsf;
-      bacc[h] = fmaf(pr, vbf, bacc[h]);
 #pragma unroll
-      for (int e = 0; e < E; ++e) acc[h][e] = fmaf(ps, code[e], acc[h][e]);
+      for (int e = 0; e < E; ++e) acc[h][e] = fmaf(pr, code[e], acc[h][e]);
     }
   }
 
   // ---- combine the TPW token streams of this wave (lanes with equal part) ----
 #pragma unroll
   for (int h = 0; h < HB; ++h) {
-#pragma unroll
-    for (int e = 0; e < E; ++e) acc[h][e] += bacc[h];
     float mm = m[h];
 #pragma unroll
     for (int x = L; x < 64; x <<= 1) mm = fmaxf(mm, shfl_xor_f32(mm, x));
@@ -299,9 +303,13 @@ __global__ __launch_bounds__(256) void decode_valu_kernel(DecodeParams p) {
   }
 }
 
-// LSE merge of split partials: one workgroup per (batch, q head), one thread
-// per output dim.  Reference: kernels.py:342-418 (online merge 369-386, zero
-// guard 408).
+// LSE merge of split partials.  Reference: kernels.py:342-418 (online merge
+// 369-386, zero guard 408).  One workgroup per (batch, q head, 64-dim chunk):
+// the split weights exp2(m_s - M) / L are computed once into LDS, then each
+// of the 4 waves sums a quarter of the splits for its 64 dims (lane = dim)
+// and the waves are added through LDS.
+constexpr int kMergeMaxSplits = 1024;
+
 template <typename Tag>
 __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ part_acc,
                                                     const float* __restrict__ part_ml, int Hq,
@@ -309,41 +317,60 @@ __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ pa
                                                     int64_t o_sh) {
   const int bh = blockIdx.x;
   const int b = bh / Hq, h = bh % Hq;
+  const int d = blockIdx.y * 64 + (threadIdx.x & 63);
+  const int wave = threadIdx.x >> 6;
   const float* ml = part_ml + static_cast<int64_t>(bh) * splits * 2;
   const float* pa = part_acc + static_cast<int64_t>(bh) * splits * D;
-  __shared__ float s_w[1024];
-  __shared__ float s_inv;
-  // weights exp2(m_s - M) / L computed once per split
-  float mloc = kNegBig;
-  for (int s = threadIdx.x; s < splits; s += blockDim.x) mloc = fmaxf(mloc, ml[2 * s]);
+  __shared__ float s_w[kMergeMaxSplits];
   __shared__ float red[256];
+  __shared__ float s_part[4][64];
+
+  float mloc = kNegBig;
+  for (int s = threadIdx.x; s < splits; s += 256) mloc = fmaxf(mloc, ml[2 * s]);
   red[threadIdx.x] = mloc;
   __syncthreads();
-  for (int st = blockDim.x / 2; st > 0; st >>= 1) {
+  for (int st = 128; st > 0; st >>= 1) {
     if (threadIdx.x < st) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + st]);
     __syncthreads();
   }
   const float M = red[0];
   __syncthreads();
   float lloc = 0.0f;
-  for (int s = threadIdx.x; s < splits; s += blockDim.x) {
+  for (int s = threadIdx.x; s < splits; s += 256) {
     const float w = fast_exp2(ml[2 * s] - M);
     s_w[s] = w;
     lloc = fmaf(ml[2 * s + 1], w, lloc);
   }
   red[threadIdx.x] = lloc;
   __syncthreads();
-  for (int st = blockDim.x / 2; st > 0; st >>= 1) {
+  for (int st = 128; st > 0; st >>= 1) {
     if (threadIdx.x < st) red[threadIdx.x] += red[threadIdx.x + st];
     __syncthreads();
   }
-  if (threadIdx.x == 0) s_inv = red[0] > 0.0f ? 1.0f / red[0] : 0.0f;
+  const float L = red[0];
+  const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+
+  float a = 0.0f;
+  if (d < D) {
+    int s = wave;
+    for (; s + 12 < splits; s += 16) {
+      const float x0 = pa[static_cast<int64_t>(s) * D + d];
+      const float x1 = pa[static_cast<int64_t>(s + 4) * D + d];
+      const float x2 = pa[static_cast<int64_t>(s + 8) * D + d];
+      const float x3 = pa[static_cast<int64_t>(s + 12) * D + d];
+      a = fmaf(x0, s_w[s], a);
+      a = fmaf(x1, s_w[s + 4], a);
+      a = fmaf(x2, s_w[s + 8], a);
+      a = fmaf(x3, s_w[s + 12], a);
+    }
+    for (; s < splits; s += 4) a = fmaf(pa[static_cast<int64_t>(s) * D + d], s_w[s], a);
+  }
+  s_part[wave][threadIdx.x & 63] = a;
   __syncthreads();
-  const float inv = s_inv;
-  for (int d = threadIdx.x; d < D; d += blockDim.x) {
-    float a = 0.0f;
-    for (int s = 0; s < splits; ++s) a = fmaf(pa[static_cast<int64_t>(s) * D + d], s_w[s], a);
-    out[static_cast<int64_t>(b) * o_sb + static_cast<int64_t>(h) * o_sh + d] = from_f32<Tag>(a * inv);
+  if (wave == 0 && d < D) {
+    const float t = (s_part[0][threadIdx.x] + s_part[1][threadIdx.x]) +
+                    (s_part[2][threadIdx.x] + s_part[3][threadIdx.x]);
+    out[static_cast<int64_t>(b) * o_sb + static_cast<int64_t>(h) * o_sh + d] = from_f32<Tag>(t * inv);
   }
 }
 
@@ -425,7 +452,7 @@ int launch_decode_valu(const qsdpa_decode_args* a, int num_splits, float* part_a
 int launch_merge(const qsdpa_decode_args* a, int num_splits, const float* part_acc,
                  const float* part_ml, hipStream_t stream) {
   uint16_t* out = static_cast<uint16_t*>(const_cast<void*>(a->out.ptr));
-  const dim3 grid(a->B * a->H_q);
+  const dim3 grid(a->B * a->H_q, (a->D + 63) / 64);
   if (a->dtype == QSDPA_F16)
     merge_kernel<F16><<<grid, dim3(256), 0, stream>>>(part_acc, part_ml, a->H_q, a->D, num_splits,
                                                       out, a->out.stride_b, a->out.stride_h);

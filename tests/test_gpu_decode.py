@@ -86,6 +86,14 @@ CASES = [
     (4, 16, 4, 4096, 128, 8, 128, "bf16"),   # C5 decode window
     (1, 8, 1, 300, 64, 4, 32, "bf16"),
     (3, 6, 3, 77, 64, 8, 64, "f16"),
+    # head groups of 16 / 32 (MFMA kernel) across D, bits, dtypes, ragged N
+    (2, 32, 2, 777, 256, 8, 64, "bf16"),
+    (1, 16, 1, 300, 128, 4, 32, "bf16"),
+    (1, 32, 1, 1000, 64, 8, 32, "f16"),
+    (3, 16, 1, 129, 128, 8, 128, "f16"),
+    (1, 32, 2, 5000, 256, 4, 64, "bf16"),
+    (1, 16, 1, 31, 256, 4, 128, "f16"),
+    (2, 64, 4, 2049, 64, 4, 32, "bf16"),
 ]
 
 
@@ -150,10 +158,11 @@ def test_zero_scales_no_nan(device):
     assert np.isfinite(got).all() and np.all(got == 0)
 
 
+@pytest.mark.parametrize("heads", [(8, 2), (32, 2)], ids=["G4", "G16"])
 @pytest.mark.parametrize("mdtype", ["bool", "f16", "f32", "per_head"])
-def test_masked_decode_in_kernel(device, mdtype):
+def test_masked_decode_in_kernel(device, mdtype, heads):
     rng = np.random.default_rng(12)
-    B, Hq, Hkv, N = 2, 8, 2, 700
+    (Hq, Hkv), B, N = heads, 2, 700
     inp = make_inputs(rng, B, Hq, Hkv, N, 128, 4, 32)
     if mdtype == "per_head":
         keep = rng.random((B, Hq, 1, N)) > 0.5
@@ -173,10 +182,11 @@ def test_masked_decode_in_kernel(device, mdtype):
         assert_close(run(inp, device, mask=m_t, num_splits=splits), want, f"mask {mdtype}")
 
 
-def test_kv_start_left_padding(device):
+@pytest.mark.parametrize("heads", [(32, 8), (32, 2)], ids=["G4", "G16"])
+def test_kv_start_left_padding(device, heads):
     """Keys before kv_start[b] are skipped == additive -inf mask on them (C4 semantics)."""
     rng = np.random.default_rng(13)
-    B, Hq, Hkv, N = 4, 32, 8, 2000
+    (Hq, Hkv), B, N = heads, 4, 2000
     inp = make_inputs(rng, B, Hq, Hkv, N, 128, 4, 64)
     starts = np.array([0, 1500, 37, 1999])
     add = np.where(np.arange(N)[None, :] >= starts[:, None], 0.0, -np.inf)[:, None, None, :]
@@ -263,7 +273,13 @@ def test_headline_full_size_properties(device, N):
                                group_size=gs, num_splits=1)
     assert (single.float() - out.float()).abs().max().item() < 2e-3
     perm = torch.randperm(N, device=device)
-    pq = [t[:, :, perm].contiguous() for t in kq], [t[:, :, perm].contiguous() for t in vq]
+
+    def take(t):
+        src = t.view(torch.int32) if t.dtype == torch.uint32 else t
+        out = src.index_select(2, perm).contiguous()
+        return out.view(torch.uint32) if t.dtype == torch.uint32 else out
+
+    pq = [take(t) for t in kq], [take(t) for t in vq]
     outp = mq.quantized_sdpa(q, pq[0][0], pq[1][0], pq[0][1], pq[1][1], pq[0][2], pq[1][2],
                              bits=bits, group_size=gs)
     assert (outp.float() - out.float()).abs().max().item() < 2e-3
