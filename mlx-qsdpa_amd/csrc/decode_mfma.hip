@@ -1,37 +1,49 @@
 // Head-grouped split-K quantized decode on the gfx950 matrix cores.
 //
-// Used when the GQA group is a multiple of 16 query heads (BASELINE config
-// 3: 16 query heads per KV head), where the 16 heads sharing a KV head form
-// a dense 16-wide MFMA tile.  Reference: kernels.py:224-318 (split-K pass 1),
-// which instead runs one simdgroup per query head and re-dequantizes every
-// K/V row once per head (kernels.py:241, 265-305).
+// Reference: mlx_qsdpa/kernels.py:224-318 (split-K pass 1) and 42-160 (the
+// single pass).  The reference runs one simdgroup per query head and
+// re-dequantizes every K/V row once per head (kernels.py:241, 265-305); here
+// the query heads that share a KV head (up to 16, padded when the group is
+// narrower) form the N side of 16x16x32 MFMA tiles, so each K/V element is
+// read from HBM and dequantized exactly once per workgroup.
 //
-// One workgroup = 8 waves = one (batch, kv head, 16-head block, token chunk).
-// Each wave streams its own 32-token tiles of the chunk; every global load of
-// a tile is issued one tile ahead (two register sets used alternately):
+// Workgroup = 8 waves = one (batch, kv head, block of 16 query heads, token
+// chunk).  Wave w streams the 32-token tiles w, w + 8, w + 16, ... of the
+// chunk with one register set: the next tile's K loads are issued as soon as
+// the current K has been consumed, its V loads once the current V has been
+// re-arranged for the PV operands.  All K / V / scale / bias reads are raw
+// buffer loads through per-workgroup descriptors that end at the chunk's
+// last row (hardware range checking; out-of-range rows read as zero, and a
+// missing bias is a zero-size descriptor).  Per 32-token tile:
 //
-//   S^T[t, h] = K[t, :] . Q[h, :]   v_mfma_f32_16x16x32_{f16,bf16}: A = K
-//       rows (a lane loads a contiguous quarter row of one token, 128-bit
-//       loads), B = Q^T held in registers for the whole chunk.  K is
-//       dequantized in registers exactly as mx.dequantize (T-rounded).
-//   online softmax in the log2 domain on the C fragment: a lane owns one head
-//       and 4 tokens per 16-token tile; the running max moves only when a
-//       tile max exceeds it by more than 8 (p <= 256).
-//   out^T[d, h] += V^T[d, t] P^T[t, h]   MFMA with A = V^T and B = P^T, where
-//       P^T is exactly the lane's own softmax fragment (the k order of the
-//       token axis is chosen to match the S^T C layout, so P never moves).
-//       V is dequantized in registers, stored token-major to a wave-private
-//       LDS tile and read back transposed with ds_read_b64_tr_b16.
+//   S^T[t, h] = K[t, :] . Q[h, :]       v_mfma_f32_16x16x32_{f16,bf16}, two
+//       16-token halves.  A = K rows: lane (quad, r) holds token r of the half
+//       and the quad's quarter of the row (one contiguous 16/32/64-byte load);
+//       B = Q^T, loaded once.  K is dequantized in registers (value =
+//       scale * code + bias rounded to T, as mx.dequantize).
+//   online softmax in the log2 domain on the S^T C fragment: a lane owns one
+//       head and 8 tokens of the tile; the running max moves only when a tile
+//       max exceeds it by more than 8 (so p <= 256).
+//   out^T[d, h] += V^T[d, t] P^T[t, h]   A = V^T, B = P^T.  P^T is the lane's
+//       own softmax fragment (token k-order = the S^T C layout).  V is loaded
+//       already transposed: lane (quad, r) loads, for each of its 8 tokens,
+//       the 8/16-byte piece of the row holding dims [r*D/16, (r+1)*D/16); each
+//       load instruction reads 4 complete rows.  MFMA nb then takes dim
+//       r*D/16 + nb of the 8 tokens as its A row r, so no LDS transpose is
+//       needed.  Token pairs are interleaved with v_perm_b32 and dequantized
+//       with the per-token scale / bias pairs.
 //
-// Float16: the fp16 dequantize is one v_pk_fma_f16 per pair (the "1024 + q"
-// exponent trick makes the 4-bit codes exact fp16 without a conversion), P
-// goes to fp16.  Bfloat16: the dequantize runs in fp32 and is rounded with
+// Float16: codes become exact fp16 values through the "1024 + code" exponent
+// trick (v_bitop3_b32 / v_perm_b32), then v_pk_fma_f16 applies scale and
+// bias.  Bfloat16: dequantization runs in fp32 and is rounded with
 // v_cvt_pk_bf16_f32; P is split into two bf16 terms (hi + lo) so the P.V
 // product keeps 16 significant bits.
 //
-// The four waves' (m, l, acc) states merge through LDS; a single split
-// writes the normalised output, otherwise float32 partials for the LSE merge
-// kernel in decode_valu.hip.
+// Split boundaries are multiples of 32 tokens from the sequence start, so
+// only the sequence's last tile is partial; its rows past the end read as
+// zero and their scores are set to -inf.  Q^T is staged once per workgroup in
+// LDS.  The 8 waves merge through LDS; one split writes the normalised
+// output, otherwise float32 partials for the merge kernel (merge.hip).
 #include <algorithm>
 
 #include "abi_internal.h"
@@ -44,21 +56,9 @@ int launch_merge(const qsdpa_decode_args* a, int num_splits, const float* part_a
 
 namespace {
 
-#ifndef QSDPA_MFMA_WAVES
-#define QSDPA_MFMA_WAVES 8
-#endif
-constexpr int kWaves = QSDPA_MFMA_WAVES;  // waves per workgroup
+constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * 64;
-// Scheduling fence between the phases of a tile: keeps the compiler from
-// hoisting one phase's loads / dequantization into another, which would
-// raise register pressure past the 2-waves-per-SIMD budget.
-#ifndef QSDPA_PHASE_FENCE
-#define QSDPA_PHASE_FENCE 1
-#endif
-#define PHASE_FENCE()                                   \
-  do {                                                  \
-    if constexpr (QSDPA_PHASE_FENCE) __builtin_amdgcn_sched_barrier(0); \
-  } while (0)
+constexpr int kTile = 32;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegBig = -1.0e30f;
 constexpr float kRescale = 8.0f;
@@ -66,13 +66,11 @@ constexpr float kRescale = 8.0f;
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef __bf16 b8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
-typedef short s4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) s4 lds_s4;
-typedef __attribute__((address_space(3))) uint8_t lds_u8;
 
 struct MfmaParams {
-  int B, Hq, Hkv, N, gs, G, hb_count, num_splits;
+  int B, Hq, Hkv, N, G, hb_count, num_splits, chunk;
   float qscale;  // softmax scale * log2(e)
+  int has_bias;
   const uint16_t* q;
   int64_t q_sb, q_sh;
   const uint32_t* kp;
@@ -83,7 +81,7 @@ struct MfmaParams {
   int64_t ks_sb, ks_sh, ks_sn;
   const uint16_t* vs;
   int64_t vs_sb, vs_sh, vs_sn;
-  const uint16_t* kb;  // null => zero biases
+  const uint16_t* kb;
   int64_t kb_sb, kb_sh, kb_sn;
   const uint16_t* vb;
   int64_t vb_sb, vb_sh, vb_sn;
@@ -97,7 +95,33 @@ struct MfmaParams {
   float* part_ml;
 };
 
-// Order of the 8 dims of one MFMA k-slice as the dequantizer produces them:
+__device__ __forceinline__ uint32_t bitop_and_or(uint32_t a, uint32_t mask, uint32_t c) {
+  return __builtin_amdgcn_bitop3_b32(a, mask, c, 0xEA);  // (a & mask) | c
+}
+__device__ __forceinline__ uint32_t perm(uint32_t hi_src, uint32_t lo_src, uint32_t sel) {
+  return __builtin_amdgcn_perm(hi_src, lo_src, sel);
+}
+
+constexpr uint32_t kNib = 0x000F000Fu;     // nibble of each 16-bit half
+constexpr uint32_t kMagic = 0x64006400u;   // fp16 1024.0 in both halves
+constexpr uint32_t kMagic8 = 0x64646464u;  // byte source for v_perm_b32
+constexpr uint32_t kSelB01 = 0x04010400u;  // [src.b0, 0x64, src.b1, 0x64]
+constexpr uint32_t kSelB23 = 0x04030402u;  // [src.b2, 0x64, src.b3, 0x64]
+
+__device__ __forceinline__ uint32_t f16x2_sub1024(uint32_t t) {
+  const f16x2 k1024 = {static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, t) - k1024);
+}
+__device__ __forceinline__ uint32_t f16x2_fma(uint32_t c, uint32_t s, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(f16x2, c),
+                                                                __builtin_bit_cast(f16x2, s),
+                                                                __builtin_bit_cast(f16x2, b)));
+}
+// Both halves = the low (sel 0x01000100) or high (0x03020302) half of x.
+__device__ __forceinline__ uint32_t splat_lo(uint32_t x) { return perm(x, x, 0x01000100u); }
+__device__ __forceinline__ uint32_t splat_hi(uint32_t x) { return perm(x, x, 0x03020302u); }
+
+// Order of the 8 dims of one QK k-slice as the K dequantizer produces them:
 // slot j holds dim perm8(j) of the slice.
 template <typename Tag, int BITS>
 __device__ __forceinline__ constexpr int perm8(int j) {
@@ -105,36 +129,29 @@ __device__ __forceinline__ constexpr int perm8(int j) {
   else return j;
 }
 
-// Dequantize one 8-dim slice (BITS/4 packed words) to four T pairs,
-// value = round_T(scale * code + bias), in perm8 order.
+// K slice (8 dims of one token, BITS/4 packed words) -> A operand (4 pairs).
+// f16: s2 / b2 hold the group's scale / bias in both halves.  bf16: sf / bf
+// are the float scale / bias.
 template <typename Tag, int BITS>
-__device__ __forceinline__ void dequant8(const uint32_t* w, uint16_t s_bits, uint16_t b_bits,
-                                         uint32_t out[4]) {
+__device__ __forceinline__ void dequant_k(const uint32_t* w, uint32_t s2, uint32_t b2, float sf,
+                                          float bf, uint32_t out[4]) {
   if constexpr (Tag::kId == QSDPA_F16) {
-    const f16x2 s2 = __builtin_bit_cast(f16x2, static_cast<uint32_t>(s_bits) * 0x10001u);
-    const f16x2 b2 = __builtin_bit_cast(f16x2, static_cast<uint32_t>(b_bits) * 0x10001u);
-    const f16x2 k1024 = {static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};
     uint32_t t[4];
     if constexpr (BITS == 4) {
       const uint32_t x = w[0];
-      t[0] = (x & 0x000F000Fu) | 0x64006400u;          // codes 0, 4
-      t[1] = ((x >> 4) & 0x000F000Fu) | 0x64006400u;   // codes 1, 5
-      t[2] = ((x >> 8) & 0x000F000Fu) | 0x64006400u;   // codes 2, 6
-      t[3] = ((x >> 12) & 0x000F000Fu) | 0x64006400u;  // codes 3, 7
+      t[0] = bitop_and_or(x, kNib, kMagic);        // codes 0, 4
+      t[1] = bitop_and_or(x >> 4, kNib, kMagic);   // codes 1, 5
+      t[2] = bitop_and_or(x >> 8, kNib, kMagic);   // codes 2, 6
+      t[3] = bitop_and_or(x >> 12, kNib, kMagic);  // codes 3, 7
     } else {
-      t[0] = __builtin_amdgcn_perm(0x64646464u, w[0], 0x04010400u);  // codes 0, 1
-      t[1] = __builtin_amdgcn_perm(0x64646464u, w[0], 0x04030402u);  // codes 2, 3
-      t[2] = __builtin_amdgcn_perm(0x64646464u, w[1], 0x04010400u);
-      t[3] = __builtin_amdgcn_perm(0x64646464u, w[1], 0x04030402u);
+      t[0] = perm(kMagic8, w[0], kSelB01);
+      t[1] = perm(kMagic8, w[0], kSelB23);
+      t[2] = perm(kMagic8, w[1], kSelB01);
+      t[3] = perm(kMagic8, w[1], kSelB23);
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const f16x2 c = __builtin_bit_cast(f16x2, t[i]) - k1024;  // exact codes
-      out[i] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(c, s2, b2));
-    }
+    for (int i = 0; i < 4; ++i) out[i] = f16x2_fma(f16x2_sub1024(t[i]), s2, b2);
   } else {
-    const float sf = bf16_bits_to_f32(s_bits);
-    const float bf = bf16_bits_to_f32(b_bits);
     float c[8];
     if constexpr (BITS == 4) {
       const uint32_t lo = w[0] & 0x0F0F0F0Fu;
@@ -181,8 +198,12 @@ __device__ __forceinline__ void load_words(const uint32_t* p, uint32_t* w) {
   }
 }
 
-__device__ __forceinline__ float mask_value(const MfmaParams& p, int b, int h, int t) {
-  const int64_t o = off3(b, h, t, p.m_sb, p.m_sh, p.m_sn);
+template <typename T>
+__device__ __forceinline__ const T* add_bytes(const T* p, int64_t bytes) {
+  return reinterpret_cast<const T*>(reinterpret_cast<const uint8_t*>(p) + bytes);
+}
+
+__device__ __forceinline__ float mask_value(const MfmaParams& p, int64_t o) {
   switch (p.mask_kind) {
     case QSDPA_BOOL:
       return static_cast<const uint8_t*>(p.mask)[o] ? 0.0f : -__builtin_huge_valf();
@@ -195,186 +216,206 @@ __device__ __forceinline__ float mask_value(const MfmaParams& p, int b, int h, i
   }
 }
 
-// Per-tile loads of one lane: two 16-token halves of K and V (the lane's
-// quarter row of token tb + 16u + r16) plus their scales / biases for the
-// (at most two) quantization groups the quarter row touches.
-template <int WPL>
-struct TileRegs {
-  uint32_t kw[2][WPL];
-  uint32_t vw[2][WPL];
-  uint32_t ks[2], kb[2], vs[2], vb[2];  // low half: group g0, high half: g0 + 1
+// Geometry of one (D, BITS, GS) instantiation.
+template <int D, int BITS, int GS>
+struct Geo {
+  static constexpr int NM = D / 32;             // QK MFMAs per 16-token half
+  static constexpr int NB = D / 16;             // PV MFMAs (dims per lane row)
+  static constexpr int QD = D / 4;              // K dims per lane (quarter row)
+  static constexpr int KW = QD * BITS / 32;     // K words per lane per half
+  static constexpr int WPS = BITS / 4;          // words per 8-dim slice
+  static constexpr int KG = QD >= GS ? QD / GS : 1;  // groups per K quarter (1 or 2)
+  static constexpr int VW = NB * BITS / 32;     // V words per lane per token
+  static constexpr int RW = D * BITS / 32;      // words per row
+  static constexpr int NG = D / GS;             // groups (scales) per row
+  static constexpr int ND = NG >= 2 ? NG / 2 : 1;  // 32-bit meta words per row
+  static_assert(KG == 1 || KG == 2, "groups per quarter");
+  static_assert(VW >= 1, "V piece");
 };
 
-// Load the 16-bit (one group) or 2 x 16-bit (two groups) metadata of a row.
-template <int NGL>
-__device__ __forceinline__ uint32_t load_meta(const uint16_t* p) {
-  if constexpr (NGL == 2) return *reinterpret_cast<const uint32_t*>(p);
-  else return static_cast<uint32_t>(p[0]);
+// Registers of one tile: K (A layout, two halves), V (transposed pieces of the
+// lane's 8 tokens) and their scales / biases.
+template <int D, int BITS, int GS>
+struct TileRegs {
+  using G = Geo<D, BITS, GS>;
+  uint32_t kw[2][G::KW];
+  uint32_t ks[2], kb[2];     // KG == 2: both groups (16-bit each); else low half
+  uint32_t vw[8][G::VW];
+  uint32_t vs[2], vb[2];     // V scale / bias row words (A layout, per half)
+};
+
+// Per-lane constant byte offsets of a lane's loads relative to the tile's
+// first row: its row within the tile plus its piece of that row.
+struct LaneOffsets {
+  uint32_t k_r, ks_r, kb_r, v_r, vs_r, vb_r;
+};
+
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+// Buffer descriptors of one workgroup's rows and the token strides in bytes.
+struct Rsrcs {
+  rsrc_t k, ks, kb, v, vs, vb;
+  uint32_t k_sn, ks_sn, kb_sn, v_sn, vs_sn, vb_sn;
+};
+
+// Raw buffer descriptor (gfx9 dword3: 32-bit data format, no swizzle).
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), 0x00020000);
 }
 
-template <typename Tag, int D, int BITS, bool HAS_BIAS>
-__global__ __launch_bounds__(kThreads) void decode_mfma_kernel(MfmaParams p) {
-  constexpr int NM = D / 32;           // QK MFMAs (32 dims each)
-  constexpr int NB = D / 16;           // PV MFMAs (16 output dims each)
-  constexpr int QD = D / 4;            // dims per lane quarter row
-  constexpr int NS = QD / 8;           // 8-dim slices per quarter row (= NM)
-  constexpr int WPS = BITS / 4;        // packed words per slice
-  constexpr int WPL = NS * WPS;        // packed words per quarter row
-  constexpr int ROWB = D * 2 + 32;     // LDS bytes per V row (padded)
-  static_assert(NS == NM, "slice count");
-  constexpr int kTileBytes = 32 * ROWB;
-  constexpr int kMergeBytes = kWaves * (D * 16 + 32) * 4;
-  constexpr int kLdsBytes = kWaves * kTileBytes > kMergeBytes ? kWaves * kTileBytes : kMergeBytes;
-  __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
-
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int quad = lane >> 4;
-  const int r16 = lane & 15;
-  const int split = blockIdx.x;
-  const int hblk = blockIdx.y % p.hb_count;
-  const int kvh = blockIdx.y / p.hb_count;
-  const int b = blockIdx.z;
-  const int hq = kvh * p.G + hblk * 16 + r16;  // this lane's query head
-
-  const int s0 = p.kv_start ? min(max(p.kv_start[b], 0), p.N) : 0;
-  const int len = p.N - s0;
-  const int chunk = (len + p.num_splits - 1) / p.num_splits;
-  const int n0 = s0 + split * chunk;
-  const int n1 = min(n0 + chunk, p.N);
-
-  // Groups of the quarter row: g0 (and g0 + 1 when the row spans two).
-  const int g0 = (quad * QD) / p.gs;
-  const bool two_groups = QD > p.gs;  // uniform
-
-  // Q^T as the B operand of the QK MFMAs (head r16, this quad's dims).
-  uint32_t qb[NM][4];
-  {
-    const uint16_t* qp = p.q + static_cast<int64_t>(b) * p.q_sb + static_cast<int64_t>(hq) * p.q_sh;
+template <int WORDS>
+__device__ __forceinline__ void buffer_words(rsrc_t rs, uint32_t off, uint32_t* w) {
+  typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+  typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+  if constexpr (WORDS % 4 == 0) {
 #pragma unroll
-    for (int m = 0; m < NM; ++m) {
-      const int base = quad * QD + 8 * m;
+    for (int i = 0; i < WORDS / 4; ++i) {
+      const u4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16 * i, 0, 0);
+      w[4 * i] = v[0]; w[4 * i + 1] = v[1]; w[4 * i + 2] = v[2]; w[4 * i + 3] = v[3];
+    }
+  } else if constexpr (WORDS == 2) {
+    const u2 v = __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0);
+    w[0] = v[0]; w[1] = v[1];
+  } else {
+    w[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0);
+  }
+}
+
+// Where a lane finds the V scale / bias of its group for its tokens:
+// ds_bpermute byte addresses of the source lanes for token slots j & 3, the
+// v_perm_b32 selector taking the right 16-bit half of two words, and the
+// shift that moves that half to the top (bf16 -> f32).
+struct VMetaLane {
+  int src[4];
+  uint32_t sel;
+  uint32_t shift;
+};
+
+template <typename Tag, int D, int BITS, int GS>
+struct Kernel {
+  using G = Geo<D, BITS, GS>;
+  using Regs = TileRegs<D, BITS, GS>;
+
+  // Token of slot j (0..7) of quad q within a 32-token tile (the S^T C layout).
+  static __device__ __forceinline__ int tau(int q, int j) { return 16 * (j >> 2) + 4 * q + (j & 3); }
+
+  // Issue the K (load_k) or V (load_v) loads of the tile whose first token is
+  // `rel0` rows past the workgroup's first token.  Rows past the chunk end
+  // fall outside the buffer descriptors and read as zero (only the
+  // sequence's last tile has such rows; their scores are set to -inf).
+  static __device__ __forceinline__ void load_k(Regs& R, const Rsrcs& rs, const LaneOffsets& L, int rel0) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        qb[m][i] = static_cast<uint32_t>(qp[base + perm8<Tag, BITS>(2 * i)]) |
-                   (static_cast<uint32_t>(qp[base + perm8<Tag, BITS>(2 * i + 1)]) << 16);
+    for (int u = 0; u < 2; ++u) {
+      const uint32_t row = static_cast<uint32_t>(rel0 + 16 * u);
+      buffer_words<G::KW>(rs.k, row * rs.k_sn + L.k_r, R.kw[u]);
+      if constexpr (G::KG == 2) {
+        R.ks[u] = __builtin_amdgcn_raw_buffer_load_b32(rs.ks, row * rs.ks_sn + L.ks_r, 0, 0);
+        R.kb[u] = __builtin_amdgcn_raw_buffer_load_b32(rs.kb, row * rs.kb_sn + L.kb_r, 0, 0);
+      } else {
+        R.ks[u] = __builtin_amdgcn_raw_buffer_load_b16(rs.ks, row * rs.ks_sn + L.ks_r, 0, 0);
+        R.kb[u] = __builtin_amdgcn_raw_buffer_load_b16(rs.kb, row * rs.kb_sn + L.kb_r, 0, 0);
+      }
     }
   }
 
-  f4 acc[NB];
-#pragma unroll
-  for (int i = 0; i < NB; ++i) acc[i] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-  float mrun = kNegBig;
-  float lrun = 0.0f;
-
-  const uint32_t* kbase = p.kp + off3(b, kvh, 0, p.kp_sb, p.kp_sh, 0) + quad * WPL;
-  const uint32_t* vbase = p.vp + off3(b, kvh, 0, p.vp_sb, p.vp_sh, 0) + quad * WPL;
-  const uint16_t* ksb = p.ks + off3(b, kvh, 0, p.ks_sb, p.ks_sh, 0) + g0;
-  const uint16_t* vsb = p.vs + off3(b, kvh, 0, p.vs_sb, p.vs_sh, 0) + g0;
-  const uint16_t* kbb = HAS_BIAS ? p.kb + off3(b, kvh, 0, p.kb_sb, p.kb_sh, 0) + g0 : nullptr;
-  const uint16_t* vbb = HAS_BIAS ? p.vb + off3(b, kvh, 0, p.vb_sb, p.vb_sh, 0) + g0 : nullptr;
-
-  uint8_t* vt = lds + wave * kTileBytes;
-  lds_u8* vl = (lds_u8*)vt;  // generic -> LDS address space
-  const int rsel = 4 * quad + (r16 >> 2);
-  const int csel = 4 * (r16 & 3) * 2;
-
-  // Issue every global load of the tile starting at tb (no waits here).
-  auto load_tile = [&](TileRegs<WPL>& R, int tb) {
+  static __device__ __forceinline__ void load_v(Regs& R, const Rsrcs& rs, const LaneOffsets& L, int rel0) {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      const int64_t tc = min(tb + 16 * u + r16, n1 - 1);
-      load_words<WPL>(kbase + tc * p.kp_sn, R.kw[u]);
-      load_words<WPL>(vbase + tc * p.vp_sn, R.vw[u]);
-      if (two_groups) {
-        R.ks[u] = load_meta<2>(ksb + tc * p.ks_sn);
-        R.vs[u] = load_meta<2>(vsb + tc * p.vs_sn);
-        if constexpr (HAS_BIAS) {
-          R.kb[u] = load_meta<2>(kbb + tc * p.kb_sn);
-          R.vb[u] = load_meta<2>(vbb + tc * p.vb_sn);
-        }
+      const uint32_t row = static_cast<uint32_t>(rel0 + 16 * u);
+      if constexpr (G::NG >= 2) {
+        R.vs[u] = __builtin_amdgcn_raw_buffer_load_b32(rs.vs, row * rs.vs_sn + L.vs_r, 0, 0);
+        R.vb[u] = __builtin_amdgcn_raw_buffer_load_b32(rs.vb, row * rs.vb_sn + L.vb_r, 0, 0);
       } else {
-        R.ks[u] = load_meta<1>(ksb + tc * p.ks_sn);
-        R.vs[u] = load_meta<1>(vsb + tc * p.vs_sn);
-        if constexpr (HAS_BIAS) {
-          R.kb[u] = load_meta<1>(kbb + tc * p.kb_sn);
-          R.vb[u] = load_meta<1>(vbb + tc * p.vb_sn);
-        }
-      }
-      if constexpr (!HAS_BIAS) {
-        R.kb[u] = 0;
-        R.vb[u] = 0;
+        R.vs[u] = __builtin_amdgcn_raw_buffer_load_b16(rs.vs, row * rs.vs_sn + L.vs_r, 0, 0);
+        R.vb[u] = __builtin_amdgcn_raw_buffer_load_b16(rs.vb, row * rs.vb_sn + L.vb_r, 0, 0);
       }
     }
-  };
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t row = static_cast<uint32_t>(rel0 + 16 * (j >> 2) + (j & 3));
+      buffer_words<G::VW>(rs.v, row * rs.v_sn + L.v_r, R.vw[j]);
+    }
+  }
 
-  // Scale / bias bits of slice m (its group is g0 or g0 + 1).
-  auto meta_of = [&](uint32_t packed, int m) -> uint16_t {
-    const bool hi = two_groups && (8 * m >= p.gs);
-    return static_cast<uint16_t>(hi ? (packed >> 16) : (packed & 0xFFFFu));
-  };
-
-  auto compute_tile = [&](const TileRegs<WPL>& R, int tb) {
-    // ---- S^T = K Q^T for the two 16-token halves ----
-    f4 S[2];
+  // One tile: QK, online softmax, PV.
+  // The next tile's K loads are issued (issue_k) as soon as this tile's K
+  // has been consumed, and its V loads (issue_v) once V is in the PV
+  // operands' pre-permuted form, so one register set suffices.
+  template <typename IK, typename IV>
+  static __device__ __forceinline__ void compute_tile(Regs& R, const MfmaParams& p, const uint8_t* lds_q,
+                                                      f4 (&acc)[G::NB], float& mrun, float& lrun, int tb,
+                                                      int n1, int quad, int b, int hq_lane, const VMetaLane& vm,
+                                                      IK&& issue_k, IV&& issue_v) {
+    // ---- S^T = K Q^T (Q^T operand m read from LDS: 16 B per lane) ----
+    f4 S[2] = {f4{0.0f, 0.0f, 0.0f, 0.0f}, f4{0.0f, 0.0f, 0.0f, 0.0f}};
+    uint32_t s2[2][2], b2[2][2];
+    float sf[2][2], bf[2][2];
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      S[u] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+      if constexpr (G::KG == 2) {
+        s2[u][0] = splat_lo(R.ks[u]); s2[u][1] = splat_hi(R.ks[u]);
+        b2[u][0] = splat_lo(R.kb[u]); b2[u][1] = splat_hi(R.kb[u]);
+        sf[u][0] = to_f32<Tag>(static_cast<uint16_t>(R.ks[u]));
+        sf[u][1] = to_f32<Tag>(static_cast<uint16_t>(R.ks[u] >> 16));
+        bf[u][0] = to_f32<Tag>(static_cast<uint16_t>(R.kb[u]));
+        bf[u][1] = to_f32<Tag>(static_cast<uint16_t>(R.kb[u] >> 16));
+      } else {
+        s2[u][0] = s2[u][1] = splat_lo(R.ks[u]);
+        b2[u][0] = b2[u][1] = splat_lo(R.kb[u]);
+        sf[u][0] = sf[u][1] = to_f32<Tag>(static_cast<uint16_t>(R.ks[u]));
+        bf[u][0] = bf[u][1] = to_f32<Tag>(static_cast<uint16_t>(R.kb[u]));
+      }
+    }
 #pragma unroll
-      for (int m = 0; m < NM; ++m) {
+    for (int m = 0; m < G::NM; ++m) {
+      const uint4 qv = *reinterpret_cast<const uint4*>(lds_q + m * 1024);
+      const uint32_t qb[4] = {qv.x, qv.y, qv.z, qv.w};
+      const int gsel = (G::KG == 2 && m >= G::NM / 2) ? 1 : 0;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
         uint32_t a[4];
-        dequant8<Tag, BITS>(R.kw[u] + m * WPS, meta_of(R.ks[u], m), meta_of(R.kb[u], m), a);
-        S[u] = mfma<Tag>(a, qb[m], S[u]);
+        dequant_k<Tag, BITS>(R.kw[u] + m * G::WPS, s2[u][gsel], b2[u][gsel], sf[u][gsel], bf[u][gsel], a);
+        S[u] = mfma<Tag>(a, qb, S[u]);
       }
     }
-    PHASE_FENCE();
-    // ---- V: dequantize to T, token-major into the wave's LDS tile ----
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      uint8_t* row = vt + (16 * u + r16) * ROWB + quad * QD * 2;
-#pragma unroll
-      for (int m = 0; m < NS; ++m) {
-        uint32_t v[4];
-        dequant8<Tag, BITS>(R.vw[u] + m * WPS, meta_of(R.vs[u], m), meta_of(R.vb[u], m), v);
-        *reinterpret_cast<uint4*>(row + m * 16) = uint4{v[0], v[1], v[2], v[3]};
-      }
-    }
-    PHASE_FENCE();
-    // ---- scores (head r16, tokens tb + 16u + 4*quad + i), online softmax ----
+    issue_k(R);
+
+    // ---- scores of (head hq_lane, tokens tau(quad, j)), online softmax ----
     float sc[8];
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) sc[4 * u + i] = S[u][i] * p.qscale;
+    for (int j = 0; j < 8; ++j) sc[j] = S[j >> 2][j & 3] * p.qscale;
     if (p.mask) {
+      const int64_t mrow = static_cast<int64_t>(b) * p.m_sb + static_cast<int64_t>(hq_lane) * p.m_sh;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const int t = min(tb + 16 * (j >> 2) + 4 * quad + (j & 3), n1 - 1);
-        sc[j] += mask_value(p, b, hq, t);
+        const int t = min(tb + tau(quad, j), n1 - 1);
+        sc[j] += mask_value(p, mrow + static_cast<int64_t>(t) * p.m_sn);
       }
     }
+    if (tb + kTile > n1) {  // the sequence's last, partial tile
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (tb + 16 * (j >> 2) + 4 * quad + (j & 3) >= n1) sc[j] = -__builtin_huge_valf();
-    float tmax = sc[0];
-#pragma unroll
-    for (int i = 1; i < 8; ++i) tmax = fmaxf(tmax, sc[i]);
+      for (int j = 0; j < 8; ++j)
+        if (tb + tau(quad, j) >= n1) sc[j] = -__builtin_huge_valf();
+    }
+    float tmax = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])),
+                       fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
     tmax = fmaxf(tmax, shfl_xor_f32(tmax, 16));
     tmax = fmaxf(tmax, shfl_xor_f32(tmax, 32));
-    if (tmax > mrun + kRescale) {
-      const float f = fast_exp2(mrun - tmax);
-      mrun = tmax;
+    const bool grow = tmax > mrun + kRescale;
+    if (__builtin_amdgcn_ballot_w64(grow)) {
+      const float mnew = grow ? tmax : mrun;
+      const float f = fast_exp2(mrun - mnew);
+      mrun = mnew;
       lrun *= f;
 #pragma unroll
-      for (int i = 0; i < NB; ++i) acc[i] *= f;
+      for (int i = 0; i < G::NB; ++i) acc[i] *= f;
     }
     float pr[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      pr[i] = fast_exp2(sc[i] - mrun);
-      lrun += pr[i];
-    }
-    // ---- P^T operand (k order = tokens 4q..4q+3 of half 0, then of half 1) ----
+    for (int j = 0; j < 8; ++j) pr[j] = fast_exp2(sc[j] - mrun);
+    lrun += ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
+
+    // ---- P^T operand: k slot 2i, 2i+1 = tokens tau(quad, 2i), tau(quad, 2i+1) ----
     uint32_t pb[4], pb_lo[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) pb[i] = pack_T2<Tag>(pr[2 * i], pr[2 * i + 1]);
@@ -384,142 +425,373 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(MfmaParams p) {
         pb_lo[i] = pack_T2<Tag>(pr[2 * i] - unpack_T2_lo<Tag>(pb[i]),
                                 pr[2 * i + 1] - unpack_T2_hi<Tag>(pb[i]));
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // ---- out^T += V^T P^T (V^T rows read transposed from the LDS tile) ----
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      const s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(vl + rsel * ROWB + nb * 32 + csel));
-      const s4 hi =
-          __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(vl + (16 + rsel) * ROWB + nb * 32 + csel));
-      const uint2 l2 = __builtin_bit_cast(uint2, lo);
-      const uint2 h2 = __builtin_bit_cast(uint2, hi);
-      const uint32_t a[4] = {l2.x, l2.y, h2.x, h2.y};
-      acc[nb] = mfma<Tag>(a, pb, acc[nb]);
-      if constexpr (Tag::kId == QSDPA_BF16) acc[nb] = mfma<Tag>(a, pb_lo, acc[nb]);
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  };
 
-  // Software pipeline: the next tile's loads are in flight while the current
-  // tile computes.  One loop body (the prefetched set is copied over), which
-  // keeps the compiler from interleaving two inlined tile bodies.
-  constexpr int kStride = kWaves * 32;
-  TileRegs<WPL> A, Bt;
-  int tb = n0 + wave * 32;
-  if (tb < n1) load_tile(A, tb);
-  while (tb < n1) {
-    const int tb2 = tb + kStride;
-    if (tb2 < n1) load_tile(Bt, tb2);
-    compute_tile(A, tb);
-    A = Bt;
-    tb = tb2;
+    // ---- out^T += V^T P^T: MFMA nb takes dim r*NB + nb of the lane's tokens ----
+    // V scale / bias words of the lane's 8 tokens, gathered from the lanes
+    // that loaded those rows (A layout: token 16u + r, word quad % ND).
+    uint32_t dS[8], dB[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      dS[j] = __builtin_amdgcn_ds_bpermute(vm.src[j & 3], static_cast<int>(R.vs[j >> 2]));
+      dB[j] = __builtin_amdgcn_ds_bpermute(vm.src[j & 3], static_cast<int>(R.vb[j >> 2]));
+    }
+    if constexpr (Tag::kId == QSDPA_F16) {
+      uint32_t sv2[4], bv2[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sv2[i] = perm(dS[2 * i + 1], dS[2 * i], vm.sel);
+        bv2[i] = perm(dB[2 * i + 1], dB[2 * i], vm.sel);
+      }
+      if constexpr (BITS == 4) {
+        // X: nibbles 0-3 of tokens (2i, 2i+1), Y: nibbles 4-7.
+        uint32_t X[4][G::VW], Y[4][G::VW];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int w = 0; w < G::VW; ++w) {
+            X[i][w] = perm(R.vw[2 * i + 1][w], R.vw[2 * i][w], 0x05040100u);
+            Y[i][w] = perm(R.vw[2 * i + 1][w], R.vw[2 * i][w], 0x07060302u);
+          }
+        issue_v(R);
+#pragma unroll
+        for (int nb = 0; nb < G::NB; ++nb) {
+          const int w = nb >> 3, k = nb & 7;
+          uint32_t a[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const uint32_t src = (k < 4 ? X[i][w] : Y[i][w]) >> (4 * (k & 3));
+            a[i] = f16x2_fma(f16x2_sub1024(bitop_and_or(src, kNib, kMagic)), sv2[i], bv2[i]);
+          }
+          acc[nb] = mfma<Tag>(a, pb, acc[nb]);
+        }
+      } else {
+        // Z0: bytes 0-1 of tokens (2i, 2i+1) interleaved, Z1: bytes 2-3.
+        uint32_t Z[4][G::VW][2];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int w = 0; w < G::VW; ++w) {
+            Z[i][w][0] = perm(R.vw[2 * i + 1][w], R.vw[2 * i][w], 0x05010400u);
+            Z[i][w][1] = perm(R.vw[2 * i + 1][w], R.vw[2 * i][w], 0x07030602u);
+          }
+        issue_v(R);
+#pragma unroll
+        for (int nb = 0; nb < G::NB; ++nb) {
+          const int w = nb >> 2, k = nb & 3;
+          uint32_t a[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const uint32_t t = perm(kMagic8, Z[i][w][k >> 1], (k & 1) ? kSelB23 : kSelB01);
+            a[i] = f16x2_fma(f16x2_sub1024(t), sv2[i], bv2[i]);
+          }
+          acc[nb] = mfma<Tag>(a, pb, acc[nb]);
+        }
+      }
+    } else {
+      float svf[8], bvf[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        svf[j] = __builtin_bit_cast(float, (dS[j] << vm.shift) & 0xFFFF0000u);
+        bvf[j] = __builtin_bit_cast(float, (dB[j] << vm.shift) & 0xFFFF0000u);
+      }
+      uint32_t lo[8][G::VW], hi[8][G::VW];
+      if constexpr (BITS == 4) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+          for (int w = 0; w < G::VW; ++w) {
+            lo[j][w] = R.vw[j][w] & 0x0F0F0F0Fu;         // nibbles 0, 2, 4, 6 as bytes
+            hi[j][w] = (R.vw[j][w] >> 4) & 0x0F0F0F0Fu;  // nibbles 1, 3, 5, 7
+          }
+      }
+#pragma unroll
+      for (int nb = 0; nb < G::NB; ++nb) {
+        uint32_t a[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float c[2];
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            const int j = 2 * i + e;
+            if constexpr (BITS == 4) {
+              const int w = nb >> 3, k = nb & 7;
+              const uint32_t src = (k & 1) ? hi[j][w] : lo[j][w];
+              c[e] = static_cast<float>((src >> (8 * (k >> 1))) & 0xFFu);
+            } else {
+              const int w = nb >> 2, k = nb & 3;
+              c[e] = static_cast<float>((R.vw[j][w] >> (8 * k)) & 0xFFu);
+            }
+            c[e] = fmaf(svf[j], c[e], bvf[j]);
+          }
+          a[i] = pack_T2<Tag>(c[0], c[1]);
+        }
+        acc[nb] = mfma<Tag>(a, pb, acc[nb]);
+        acc[nb] = mfma<Tag>(a, pb_lo, acc[nb]);
+      }
+      issue_v(R);
+    }
+  }
+};
+
+template <typename Tag, int D, int BITS, int GS>
+__global__ __launch_bounds__(kThreads) void decode_mfma_kernel(MfmaParams p) {
+  using G = Geo<D, BITS, GS>;
+  using K = Kernel<Tag, D, BITS, GS>;
+  constexpr int kRowF = D + 4;  // LDS floats per (wave, head) row
+  __shared__ __attribute__((aligned(16))) float s_acc[kWaves * 16 * kRowF];
+  __shared__ float s_ml[kWaves][16][2];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int quad = lane >> 4;
+  const int r = lane & 15;
+  const int split = blockIdx.x;
+  const int hblk = blockIdx.y % p.hb_count;
+  const int kvh = blockIdx.y / p.hb_count;
+  const int b = blockIdx.z;
+  const int h0 = kvh * p.G + hblk * 16;        // first query head of the block
+  const int nh = min(16, p.G - hblk * 16);     // real heads in the block
+  const int hq_lane = h0 + min(r, nh - 1);     // this lane's head (clamped)
+
+  const int s0 = p.kv_start ? min(max(p.kv_start[b], 0), p.N) : 0;
+  const int n0 = min(s0 + split * p.chunk, p.N);
+  const int n1 = min(n0 + p.chunk, p.N);
+
+  // Q^T B operands in LDS, [m][lane] x 16 B: head r, dims quad*QD + 8m +
+  // perm8(j), zero for padding heads.  Written by wave 0, read by all.  The
+  // area is reused by the wave merge after the main loop.
+  uint8_t* lds_q = reinterpret_cast<uint8_t*>(s_acc);
+  if (wave == 0) {
+    const uint16_t* qp = p.q + static_cast<int64_t>(b) * p.q_sb + static_cast<int64_t>(hq_lane) * p.q_sh +
+                         quad * G::QD;
+#pragma unroll
+    for (int m = 0; m < G::NM; ++m) {
+      const uint32_t* q32 = reinterpret_cast<const uint32_t*>(qp + 8 * m);
+      const uint32_t d0 = q32[0], d1 = q32[1], d2 = q32[2], d3 = q32[3];
+      uint4 v;
+      if constexpr (Tag::kId == QSDPA_F16 && BITS == 4) {
+        v = uint4{perm(d2, d0, 0x05040100u),   // dims 0, 4
+                  perm(d2, d0, 0x07060302u),   // dims 1, 5
+                  perm(d3, d1, 0x05040100u),   // dims 2, 6
+                  perm(d3, d1, 0x07060302u)};  // dims 3, 7
+      } else {
+        v = uint4{d0, d1, d2, d3};
+      }
+      if (r >= nh) v = uint4{0u, 0u, 0u, 0u};
+      *reinterpret_cast<uint4*>(lds_q + m * 1024 + lane * 16) = v;
+    }
+  }
+  __syncthreads();
+  const uint8_t* lds_q_lane = lds_q + lane * 16;
+
+  f4 acc[G::NB];
+#pragma unroll
+  for (int i = 0; i < G::NB; ++i) acc[i] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  float mrun = kNegBig;
+  float lrun = 0.0f;
+
+  // Buffer descriptors over rows [n0, n1) of this (batch, kv head).
+  Rsrcs rs;
+  {
+    const int rows = n1 - n0;
+    const int64_t tok0 = n0;
+    auto rsrc = [&](const void* base, int64_t sb, int64_t sh, int64_t sn, int esz, int row_bytes,
+                    bool present) {
+      const uint8_t* p0 = static_cast<const uint8_t*>(base) +
+                          (static_cast<int64_t>(b) * sb + static_cast<int64_t>(kvh) * sh + tok0 * sn) * esz;
+      const uint32_t bytes =
+          (present && rows > 0) ? static_cast<uint32_t>((rows - 1) * sn * esz + row_bytes) : 0u;
+      return make_rsrc(p0, bytes);
+    };
+    constexpr int kRow = D * BITS / 8;
+    constexpr int kMeta = G::NG * 2;
+    rs.k = rsrc(p.kp, p.kp_sb, p.kp_sh, p.kp_sn, 4, kRow, true);
+    rs.v = rsrc(p.vp, p.vp_sb, p.vp_sh, p.vp_sn, 4, kRow, true);
+    rs.ks = rsrc(p.ks, p.ks_sb, p.ks_sh, p.ks_sn, 2, kMeta, true);
+    rs.vs = rsrc(p.vs, p.vs_sb, p.vs_sh, p.vs_sn, 2, kMeta, true);
+    rs.kb = rsrc(p.has_bias ? p.kb : p.ks, p.kb_sb, p.kb_sh, p.kb_sn, 2, kMeta, p.has_bias);
+    rs.vb = rsrc(p.has_bias ? p.vb : p.vs, p.vb_sb, p.vb_sh, p.vb_sn, 2, kMeta, p.has_bias);
+    rs.k_sn = static_cast<uint32_t>(p.kp_sn * 4);
+    rs.v_sn = static_cast<uint32_t>(p.vp_sn * 4);
+    rs.ks_sn = static_cast<uint32_t>(p.ks_sn * 2);
+    rs.vs_sn = static_cast<uint32_t>(p.vs_sn * 2);
+    rs.kb_sn = static_cast<uint32_t>(p.kb_sn * 2);
+    rs.vb_sn = static_cast<uint32_t>(p.vb_sn * 2);
+  }
+
+  // Per-lane byte offsets.
+  const int kg0 = (quad * G::QD) / GS;  // first group of the lane's K quarter
+  const int gv = (r * G::NB) / GS;      // group of the lane's V dims
+  const int vword = G::NG >= 2 ? quad % G::ND : 0;  // V meta word this lane loads
+  LaneOffsets L;
+  L.k_r = quad * G::KW * 4 + r * rs.k_sn;
+  L.ks_r = kg0 * 2 + r * rs.ks_sn;
+  L.kb_r = kg0 * 2 + r * rs.kb_sn;
+  L.v_r = r * G::VW * 4 + 4 * quad * rs.v_sn;
+  L.vs_r = vword * 4 + r * rs.vs_sn;
+  L.vb_r = vword * 4 + r * rs.vb_sn;
+  // Token tau(quad, j) of a half sits in row 4*quad + (j & 3); its meta word
+  // gv / 2 was loaded by quad gv / 2.
+  VMetaLane vm;
+  {
+    const int dw = G::NG >= 2 ? gv / 2 : 0;
+    const int half = G::NG >= 2 ? gv % 2 : 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) vm.src[k] = (16 * dw + 4 * quad + k) * 4;
+    vm.sel = half ? 0x07060302u : 0x05040100u;
+    vm.shift = half ? 0u : 16u;
+  }
+
+  constexpr int kStride = kWaves * kTile;
+  typename K::Regs R;
+  int tb = n0 + wave * kTile;
+  if (tb < n1) {
+    K::load_k(R, rs, L, tb - n0);
+    K::load_v(R, rs, L, tb - n0);
+  }
+  for (; tb < n1; tb += kStride) {
+    const int nt = tb + kStride;
+    const bool more = nt < n1;
+    auto ik = [&](typename K::Regs& X) { if (more) K::load_k(X, rs, L, nt - n0); };
+    auto iv = [&](typename K::Regs& X) { if (more) K::load_v(X, rs, L, nt - n0); };
+    K::compute_tile(R, p, lds_q_lane, acc, mrun, lrun, tb, n1, quad, b, hq_lane, vm, ik, iv);
   }
 
   // ---- per-head totals over the four quads ----
   lrun += shfl_xor_f32(lrun, 16);
   lrun += shfl_xor_f32(lrun, 32);
 
-  // ---- merge the waves through LDS: acc[w][h][d] in natural dim order ----
-  __syncthreads();
-  float* sm = reinterpret_cast<float*>(lds);
-  float* sacc = sm + wave * (D * 16 + 32);
-  float* sml = sacc + D * 16;  // [16 heads][2]
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int dp = 16 * nb + 4 * quad + r;               // slot (physical) dim
-      const int d = (dp & ~7) + perm8<Tag, BITS>(dp & 7);  // real dim
-      sacc[r16 * D + d] = acc[nb][r];
-    }
-  }
+  // ---- merge the waves through LDS ----
   if (quad == 0) {
-    sml[2 * r16] = mrun;
-    sml[2 * r16 + 1] = lrun;
+    s_ml[wave][r][0] = mrun;
+    s_ml[wave][r][1] = lrun;
+  }
+  __syncthreads();
+  float M = s_ml[0][r][0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) M = fmaxf(M, s_ml[w][r][0]);
+  const float f = fast_exp2(mrun - M);
+  // acc[nb][i] is out^T[dim (4*quad + i)*NB + nb][head r]: 4 runs of NB dims.
+  float* row = s_acc + (wave * 16 + r) * kRowF;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float* dst = row + (4 * quad + i) * G::NB;
+#pragma unroll
+    for (int nb = 0; nb < G::NB; nb += 4)
+      *reinterpret_cast<f4*>(dst + nb) =
+          f4{acc[nb][i] * f, acc[nb + 1][i] * f, acc[nb + 2][i] * f, acc[nb + 3][i] * f};
   }
   __syncthreads();
 
-  for (int i = threadIdx.x; i < 16 * D; i += kThreads) {
-    const int h = i / D;
-    const int d = i % D;
-    float mm = kNegBig;
+  // 16 heads x D dims; thread -> (head, 8 consecutive dims).
+  constexpr int kPer = 8;
+  for (int idx = threadIdx.x; idx < 16 * (D / kPer); idx += kThreads) {
+    const int h = idx / (D / kPer);
+    const int d = (idx % (D / kPer)) * kPer;
+    if (h >= nh) continue;
+    float Mh = s_ml[0][h][0];
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) mm = fmaxf(mm, sm[w * (D * 16 + 32) + D * 16 + 2 * h]);
-    float a = 0.0f, ll = 0.0f;
+    for (int w = 1; w < kWaves; ++w) Mh = fmaxf(Mh, s_ml[w][h][0]);
+    float L = 0.0f;
+    float v[kPer];
+#pragma unroll
+    for (int e = 0; e < kPer; ++e) v[e] = 0.0f;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) {
-      const float* base = sm + w * (D * 16 + 32);
-      const float f = fast_exp2(base[D * 16 + 2 * h] - mm);
-      a = fmaf(base[h * D + d], f, a);
-      ll = fmaf(base[D * 16 + 2 * h + 1], f, ll);
+      L = fmaf(s_ml[w][h][1], fast_exp2(s_ml[w][h][0] - Mh), L);
+      const float* src = s_acc + (w * 16 + h) * kRowF + d;
+      const f4 a0 = *reinterpret_cast<const f4*>(src);
+      const f4 a1 = *reinterpret_cast<const f4*>(src + 4);
+      v[0] += a0[0]; v[1] += a0[1]; v[2] += a0[2]; v[3] += a0[3];
+      v[4] += a1[0]; v[5] += a1[1]; v[6] += a1[2]; v[7] += a1[3];
     }
-    const int hh = kvh * p.G + hblk * 16 + h;
+    const int hh = h0 + h;
     if (p.num_splits == 1) {
-      const float o = ll > 0.0f ? a / ll : 0.0f;
-      p.out[static_cast<int64_t>(b) * p.o_sb + static_cast<int64_t>(hh) * p.o_sh + d] = from_f32<Tag>(o);
+      const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+      uint32_t pk[kPer / 2];
+#pragma unroll
+      for (int e = 0; e < kPer / 2; ++e) pk[e] = pack_T2<Tag>(v[2 * e] * inv, v[2 * e + 1] * inv);
+      uint16_t* dst = p.out + static_cast<int64_t>(b) * p.o_sb + static_cast<int64_t>(hh) * p.o_sh + d;
+      // out rows are only 2-byte aligned in general: store pairs.
+#pragma unroll
+      for (int e = 0; e < kPer / 2; ++e) {
+        dst[2 * e] = static_cast<uint16_t>(pk[e]);
+        dst[2 * e + 1] = static_cast<uint16_t>(pk[e] >> 16);
+      }
     } else {
       const int64_t slot = (static_cast<int64_t>(b) * p.Hq + hh) * p.num_splits + split;
-      p.part_acc[slot * D + d] = a;
+      float* dst = p.part_acc + slot * D + d;
+      *reinterpret_cast<f4*>(dst) = f4{v[0], v[1], v[2], v[3]};
+      *reinterpret_cast<f4*>(dst + 4) = f4{v[4], v[5], v[6], v[7]};
       if (d == 0) {
-        p.part_ml[slot * 2] = mm;
-        p.part_ml[slot * 2 + 1] = ll;
+        p.part_ml[slot * 2] = Mh;
+        p.part_ml[slot * 2 + 1] = L;
       }
     }
   }
 }
 
 template <typename Tag, int D, int BITS>
-void launch_b(const MfmaParams& p, bool has_bias, hipStream_t stream) {
+void launch_gs(const MfmaParams& p, int gs, hipStream_t stream) {
   const dim3 grid(p.num_splits, p.Hkv * p.hb_count, p.B);
-  if (has_bias) decode_mfma_kernel<Tag, D, BITS, true><<<grid, dim3(kThreads), 0, stream>>>(p);
-  else decode_mfma_kernel<Tag, D, BITS, false><<<grid, dim3(kThreads), 0, stream>>>(p);
+  switch (gs) {
+    case 32: decode_mfma_kernel<Tag, D, BITS, 32><<<grid, dim3(kThreads), 0, stream>>>(p); break;
+    case 64: decode_mfma_kernel<Tag, D, BITS, 64><<<grid, dim3(kThreads), 0, stream>>>(p); break;
+    default: decode_mfma_kernel<Tag, D, BITS, 128><<<grid, dim3(kThreads), 0, stream>>>(p); break;
+  }
 }
 
 template <typename Tag, int D>
-void launch_d(const MfmaParams& p, int bits, bool has_bias, hipStream_t stream) {
-  if (bits == 4) launch_b<Tag, D, 4>(p, has_bias, stream);
-  else launch_b<Tag, D, 8>(p, has_bias, stream);
+void launch_bits(const MfmaParams& p, int bits, int gs, hipStream_t stream) {
+  if (bits == 4) launch_gs<Tag, D, 4>(p, gs, stream);
+  else launch_gs<Tag, D, 8>(p, gs, stream);
 }
 
-// LDS bytes one workgroup of the MFMA kernel uses for head dimension D.
-constexpr int mfma_lds_bytes(int D) {
-  return kWaves * 32 * (D * 2 + 32) > kWaves * (D * 16 + 32) * 4 ? kWaves * 32 * (D * 2 + 32)
-                                                                  : kWaves * (D * 16 + 32) * 4;
-}
-
-bool meta_aligned4(const qsdpa_view& v) {
-  return v.ptr == nullptr || ((reinterpret_cast<uintptr_t>(v.ptr) & 3) == 0 && v.stride_b % 2 == 0 &&
-                              v.stride_h % 2 == 0 && v.stride_n % 2 == 0);
+bool aligned_view(const qsdpa_view& v, int bytes, int64_t elem_bytes) {
+  if (v.ptr == nullptr) return true;
+  if (reinterpret_cast<uintptr_t>(v.ptr) % bytes) return false;
+  const int64_t m = bytes / elem_bytes;
+  return m <= 1 || (v.stride_b % m == 0 && v.stride_h % m == 0 && v.stride_n % m == 0);
 }
 
 }  // namespace
 
-// MFMA path: head groups that are a multiple of 16 wide.  When a lane's
-// quarter row spans two quantization groups their scales are read as one
-// 32-bit word, which needs 4-byte aligned scale / bias rows.
+// The MFMA path covers D in {128, 256} for any GQA factor (heads padded to
+// blocks of 16).  Its vector loads need: q rows 4-byte aligned; K / V rows
+// aligned to the per-lane piece (16 B for the K quarter when it is >= 16 B,
+// the V piece size otherwise); scale / bias rows 4-byte aligned when a K
+// quarter spans two groups (D = 256, group_size = 32).
 bool mfma_supports(const qsdpa_decode_args* a) {
-  const int G = a->H_q / a->H_kv;
-  if (G < 16 || G % 16 != 0) return false;
-  if (a->D != 64 && a->D != 128 && a->D != 256) return false;
-  if (a->D / 4 > a->group_size)
-    return meta_aligned4(a->k_scales) && meta_aligned4(a->v_scales) && meta_aligned4(a->k_biases) &&
-           meta_aligned4(a->v_biases);
+  if (a->D != 128 && a->D != 256) return false;
+  if (a->group_size != 32 && a->group_size != 64 && a->group_size != 128) return false;
+  if (!aligned_view(a->q, 4, 2)) return false;
+  const int kq_bytes = a->D / 4 * a->bits / 8;             // K quarter row
+  const int vp_bytes = a->D / 16 * a->bits / 8;            // V piece per token
+  if (!aligned_view(a->k_packed, std::min(kq_bytes, 16), 4)) return false;
+  if (!aligned_view(a->v_packed, std::min(vp_bytes, 16), 4)) return false;
+  if (a->D / 4 / a->group_size == 2) {
+    if (!aligned_view(a->k_scales, 4, 2) || !aligned_view(a->k_biases, 4, 2)) return false;
+  }
+  // V scales / biases are read as 32-bit words when a row holds >= 2 groups.
+  if (a->D / a->group_size >= 2) {
+    if (!aligned_view(a->v_scales, 4, 2) || !aligned_view(a->v_biases, 4, 2)) return false;
+  }
+  // Lane offsets inside a tile are 32-bit.
+  const int64_t max_sn = std::max({a->k_packed.stride_n * 4, a->v_packed.stride_n * 4,
+                                   a->k_scales.stride_n * 2, a->v_scales.stride_n * 2,
+                                   a->k_biases.stride_n * 2, a->v_biases.stride_n * 2});
+  if (max_sn < 0 || max_sn * kTile >= (int64_t(1) << 30)) return false;
   return true;
 }
 
-// As many workgroups as fit on the GPU at once (LDS-limited), but at least
-// two 32-token tiles per wave.
+// Splits per (batch, kv head, head block): one workgroup per CU in total
+// (LDS and registers allow one 8-wave group per CU), each split at least one
+// tile per wave.  Chunks are whole tiles.
 int mfma_num_splits(const qsdpa_decode_args* a, int cus) {
-  const int G = a->H_q / a->H_kv;
-  const int64_t units = static_cast<int64_t>(a->B) * a->H_kv * (G / 16);
-  const int per_cu = std::max(1, std::min(2, (160 * 1024) / mfma_lds_bytes(a->D)));
-  const int64_t target = static_cast<int64_t>(per_cu) * cus;
-  int64_t s = (target + units - 1) / units;
-  s = std::min<int64_t>(s, std::max<int64_t>(1, a->N / (kWaves * 64)));
+  const int hb = (a->H_q / a->H_kv + 15) / 16;
+  const int64_t units = static_cast<int64_t>(a->B) * a->H_kv * hb;
+  int64_t s = (cus + units - 1) / units;
+  s = std::min<int64_t>(s, std::max<int64_t>(1, a->N / (kWaves * kTile)));
   s = std::min<int64_t>(s, 1024);
   return static_cast<int>(std::max<int64_t>(s, 1));
 }
@@ -527,11 +799,15 @@ int mfma_num_splits(const qsdpa_decode_args* a, int cus) {
 int launch_decode_mfma(const qsdpa_decode_args* a, int num_splits, float* part_acc, float* part_ml,
                        hipStream_t stream) {
   MfmaParams p;
-  p.B = a->B; p.Hq = a->H_q; p.Hkv = a->H_kv; p.N = a->N; p.gs = a->group_size;
+  p.B = a->B; p.Hq = a->H_q; p.Hkv = a->H_kv; p.N = a->N;
   p.G = a->H_q / a->H_kv;
-  p.hb_count = p.G / 16;
+  p.hb_count = (p.G + 15) / 16;
   p.num_splits = num_splits;
+  // Whole tiles per split; the last split absorbs the remainder.
+  const int64_t per = (static_cast<int64_t>(a->N) + num_splits - 1) / num_splits;
+  p.chunk = static_cast<int>(((per + kTile - 1) / kTile) * kTile);
   p.qscale = a->scale * kLog2e;
+  p.has_bias = a->k_biases.ptr != nullptr;
   p.q = static_cast<const uint16_t*>(a->q.ptr); p.q_sb = a->q.stride_b; p.q_sh = a->q.stride_h;
   p.kp = static_cast<const uint32_t*>(a->k_packed.ptr);
   p.kp_sb = a->k_packed.stride_b; p.kp_sh = a->k_packed.stride_h; p.kp_sn = a->k_packed.stride_n;
@@ -545,6 +821,10 @@ int launch_decode_mfma(const qsdpa_decode_args* a, int num_splits, float* part_a
   p.kb_sb = a->k_biases.stride_b; p.kb_sh = a->k_biases.stride_h; p.kb_sn = a->k_biases.stride_n;
   p.vb = static_cast<const uint16_t*>(a->v_biases.ptr);
   p.vb_sb = a->v_biases.stride_b; p.vb_sh = a->v_biases.stride_h; p.vb_sn = a->v_biases.stride_n;
+  if (!p.has_bias) {
+    p.kb_sb = p.ks_sb; p.kb_sh = p.ks_sh; p.kb_sn = p.ks_sn;
+    p.vb_sb = p.vs_sb; p.vb_sh = p.vs_sh; p.vb_sn = p.vs_sn;
+  }
   p.out = static_cast<uint16_t*>(const_cast<void*>(a->out.ptr));
   p.o_sb = a->out.stride_b; p.o_sh = a->out.stride_h;
   p.mask = a->mask.ptr; p.mask_kind = a->mask_dtype;
@@ -553,11 +833,12 @@ int launch_decode_mfma(const qsdpa_decode_args* a, int num_splits, float* part_a
   p.part_acc = part_acc;
   p.part_ml = part_ml;
   const bool f16 = a->dtype == QSDPA_F16;
-  const bool hb = a->k_biases.ptr != nullptr;
-  switch (a->D) {
-    case 64: if (f16) launch_d<F16, 64>(p, a->bits, hb, stream); else launch_d<BF16, 64>(p, a->bits, hb, stream); break;
-    case 128: if (f16) launch_d<F16, 128>(p, a->bits, hb, stream); else launch_d<BF16, 128>(p, a->bits, hb, stream); break;
-    default: if (f16) launch_d<F16, 256>(p, a->bits, hb, stream); else launch_d<BF16, 256>(p, a->bits, hb, stream); break;
+  if (a->D == 128) {
+    if (f16) launch_bits<F16, 128>(p, a->bits, a->group_size, stream);
+    else launch_bits<BF16, 128>(p, a->bits, a->group_size, stream);
+  } else {
+    if (f16) launch_bits<F16, 256>(p, a->bits, a->group_size, stream);
+    else launch_bits<BF16, 256>(p, a->bits, a->group_size, stream);
   }
   return check_launch("decode_mfma");
 }

@@ -303,77 +303,6 @@ __global__ __launch_bounds__(256) void decode_valu_kernel(DecodeParams p) {
   }
 }
 
-// LSE merge of split partials.  Reference: kernels.py:342-418 (online merge
-// 369-386, zero guard 408).  One workgroup per (batch, q head, 64-dim chunk):
-// the split weights exp2(m_s - M) / L are computed once into LDS, then each
-// of the 4 waves sums a quarter of the splits for its 64 dims (lane = dim)
-// and the waves are added through LDS.
-constexpr int kMergeMaxSplits = 1024;
-
-template <typename Tag>
-__global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ part_acc,
-                                                    const float* __restrict__ part_ml, int Hq,
-                                                    int D, int splits, uint16_t* out, int64_t o_sb,
-                                                    int64_t o_sh) {
-  const int bh = blockIdx.x;
-  const int b = bh / Hq, h = bh % Hq;
-  const int d = blockIdx.y * 64 + (threadIdx.x & 63);
-  const int wave = threadIdx.x >> 6;
-  const float* ml = part_ml + static_cast<int64_t>(bh) * splits * 2;
-  const float* pa = part_acc + static_cast<int64_t>(bh) * splits * D;
-  __shared__ float s_w[kMergeMaxSplits];
-  __shared__ float red[256];
-  __shared__ float s_part[4][64];
-
-  float mloc = kNegBig;
-  for (int s = threadIdx.x; s < splits; s += 256) mloc = fmaxf(mloc, ml[2 * s]);
-  red[threadIdx.x] = mloc;
-  __syncthreads();
-  for (int st = 128; st > 0; st >>= 1) {
-    if (threadIdx.x < st) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + st]);
-    __syncthreads();
-  }
-  const float M = red[0];
-  __syncthreads();
-  float lloc = 0.0f;
-  for (int s = threadIdx.x; s < splits; s += 256) {
-    const float w = fast_exp2(ml[2 * s] - M);
-    s_w[s] = w;
-    lloc = fmaf(ml[2 * s + 1], w, lloc);
-  }
-  red[threadIdx.x] = lloc;
-  __syncthreads();
-  for (int st = 128; st > 0; st >>= 1) {
-    if (threadIdx.x < st) red[threadIdx.x] += red[threadIdx.x + st];
-    __syncthreads();
-  }
-  const float L = red[0];
-  const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-
-  float a = 0.0f;
-  if (d < D) {
-    int s = wave;
-    for (; s + 12 < splits; s += 16) {
-      const float x0 = pa[static_cast<int64_t>(s) * D + d];
-      const float x1 = pa[static_cast<int64_t>(s + 4) * D + d];
-      const float x2 = pa[static_cast<int64_t>(s + 8) * D + d];
-      const float x3 = pa[static_cast<int64_t>(s + 12) * D + d];
-      a = fmaf(x0, s_w[s], a);
-      a = fmaf(x1, s_w[s + 4], a);
-      a = fmaf(x2, s_w[s + 8], a);
-      a = fmaf(x3, s_w[s + 12], a);
-    }
-    for (; s < splits; s += 4) a = fmaf(pa[static_cast<int64_t>(s) * D + d], s_w[s], a);
-  }
-  s_part[wave][threadIdx.x & 63] = a;
-  __syncthreads();
-  if (wave == 0 && d < D) {
-    const float t = (s_part[0][threadIdx.x] + s_part[1][threadIdx.x]) +
-                    (s_part[2][threadIdx.x] + s_part[3][threadIdx.x]);
-    out[static_cast<int64_t>(b) * o_sb + static_cast<int64_t>(h) * o_sh + d] = from_f32<Tag>(t * inv);
-  }
-}
-
 template <typename Tag, int D, int BITS, int HB>
 void launch_valu(const DecodeParams& p, hipStream_t stream) {
   constexpr int E = (HB == 1) ? 32 : (HB <= 4 ? 16 : 8);
@@ -447,19 +376,6 @@ int launch_decode_valu(const qsdpa_decode_args* a, int num_splits, float* part_a
   if (a->dtype == QSDPA_F16) dispatch_shape<F16>(p, a->bits, hb, stream);
   else dispatch_shape<BF16>(p, a->bits, hb, stream);
   return check_launch("decode_valu");
-}
-
-int launch_merge(const qsdpa_decode_args* a, int num_splits, const float* part_acc,
-                 const float* part_ml, hipStream_t stream) {
-  uint16_t* out = static_cast<uint16_t*>(const_cast<void*>(a->out.ptr));
-  const dim3 grid(a->B * a->H_q, (a->D + 63) / 64);
-  if (a->dtype == QSDPA_F16)
-    merge_kernel<F16><<<grid, dim3(256), 0, stream>>>(part_acc, part_ml, a->H_q, a->D, num_splits,
-                                                      out, a->out.stride_b, a->out.stride_h);
-  else
-    merge_kernel<BF16><<<grid, dim3(256), 0, stream>>>(part_acc, part_ml, a->H_q, a->D, num_splits,
-                                                       out, a->out.stride_b, a->out.stride_h);
-  return check_launch("merge");
 }
 
 }  // namespace qsdpa
