@@ -16,7 +16,11 @@ Printed JSON line (rank 0, N=1):
   roofline         achieved GB/s of the main decode kernel: algorithmic bytes
                    (q + packed K/V + scales + biases + out, the reference's
                    formula) / that kernel's mean duration, timed with HIP
-                   events recorded by the library around the kernel launch
+                   events that the library attaches to the kernel's own
+                   dispatch (hipExtLaunchKernel start / stop events);
+                   traffic = HBM bytes per launch from the committed
+                   rocprofv3 FETCH_SIZE / WRITE_SIZE summary
+                   (profiles/traffic.txt) when it covers this workload
   cpu_baseline     the oracle's float32 dequantize + attention (the
                    reference's CPU-capable path) on a bounded sample
 """
@@ -65,7 +69,32 @@ def parse_args(argv=None):
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="time budget of the CPU baseline sample (0 = skip)")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="before warmup, run one device-to-device copy of this many MiB (the "
+                         "known-size reference for rocprofv3 FETCH_SIZE / WRITE_SIZE scaling)")
     return ap.parse_args(argv)
+
+
+TRAFFIC_FILE = ROOT / "profiles" / "traffic.txt"
+
+
+def measured_traffic(workload: str):
+    """HBM bytes per launch of the main decode kernel for `workload`, from the
+    committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary (None if absent).
+
+    Lines look like ``<workload> | fetch_bytes=<int> | write_bytes=<int>``.
+    """
+    if not TRAFFIC_FILE.exists():
+        return None
+    for line in TRAFFIC_FILE.read_text().splitlines():
+        if line.startswith("#") or "|" not in line:
+            continue
+        parts = [x.strip() for x in line.split("|")]
+        if parts[0] != workload:
+            continue
+        kv = dict(x.split("=", 1) for x in parts[1:] if "=" in x)
+        return int(kv["fetch_bytes"]) + int(kv["write_bytes"])
+    return None
 
 
 class HipEvents:
@@ -177,6 +206,16 @@ def main(argv=None) -> int:
              for q, kq, vq in sets]
     splits = plans[0].num_splits
 
+    if args.calib_copy_mib > 0:
+        nbytes = args.calib_copy_mib << 20
+        src = torch.ones(nbytes, dtype=torch.uint8, device=device)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        print(f"bench: calibration copy of {nbytes} bytes", file=sys.stderr, flush=True)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
     hip = HipEvents()
     ev_b = hip.create(args.steps)
     ev_e = hip.create(args.steps)
@@ -211,6 +250,8 @@ def main(argv=None) -> int:
         cpu = cpu_baseline(cfg, N, (host[0], kq, vq), args.cpu_seconds)
 
     ref_us = REFERENCE_US.get(N) if args.config == "c3" else None
+    workload = f"{args.config}: decode B={B} H_q={Hq} H_kv={Hkv} D={D} {bits}-bit gs={gs} {dt} N={N}"
+    traffic = measured_traffic(workload)
     line = {
         "metric": METRIC,
         "value": round(us_step, 3),
@@ -224,11 +265,10 @@ def main(argv=None) -> int:
         "vs_baseline": round(us_step / ref_us, 5) if ref_us else None,
         "vs_baseline_ref": (f"M2 Ultra fused decode {ref_us} us (mlx-qsdpa README.md:89)"
                             if ref_us else None),
-        "dtype": "f32",
+        "dtype": dt,
         "data": "synthetic",
         "config": {
-            "workload": (f"{args.config}: decode B={B} H_q={Hq} H_kv={Hkv} D={D} {bits}-bit "
-                         f"gs={gs} {dt} N={N}"),
+            "workload": workload,
             "B": B, "H_q": Hq, "H_kv": Hkv, "D": D, "N": N, "bits": bits, "group_size": gs,
             "kv_dtype": dt, "num_splits": splits, "kv_sets": n_sets,
         },
@@ -240,7 +280,7 @@ def main(argv=None) -> int:
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(kern_gbps / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": traffic,
             "kernel_us": round(kern_us, 3),
             "algorithmic_bytes": alg_bytes,
         },

@@ -108,9 +108,10 @@ typedef struct {
   size_t workspace_bytes;
 
   /* Optional profiling hook: two hipEvent_t handles (or NULL).  When set,
-   * the library records prof_begin on `stream` right before the main decode
-   * kernel and prof_end right after it (before any merge kernel), so a
-   * caller can time that kernel alone with hipEventElapsedTime.          */
+   * the main decode kernel is launched with hipExtLaunchKernel carrying
+   * them as its start / stop events, so hipEventElapsedTime(prof_begin,
+   * prof_end) is that kernel's own execution time (any merge kernel runs
+   * after prof_end).                                                     */
   void* prof_begin;
   void* prof_end;
 } qsdpa_decode_args;

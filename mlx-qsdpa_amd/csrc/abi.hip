@@ -183,17 +183,10 @@ int qsdpa_decode(const qsdpa_decode_args* args, void* stream) {
     part_ml = part_acc + static_cast<int64_t>(args->B) * args->H_q * splits * args->D;
   }
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  if (args->prof_begin) {
-    const hipError_t e = hipEventRecord(static_cast<hipEvent_t>(args->prof_begin), s);
-    if (e != hipSuccess) return fail(QSDPA_ERR_LAUNCH, "hipEventRecord: %s", hipGetErrorString(e));
-  }
+  // (prof_begin / prof_end ride on the main kernel's own dispatch)
   if (mfma_supports(args)) rc = launch_decode_mfma(args, splits, part_acc, part_ml, s);
   else rc = launch_decode_valu(args, splits, part_acc, part_ml, s);
   if (rc) return rc;
-  if (args->prof_end) {
-    const hipError_t e = hipEventRecord(static_cast<hipEvent_t>(args->prof_end), s);
-    if (e != hipSuccess) return fail(QSDPA_ERR_LAUNCH, "hipEventRecord: %s", hipGetErrorString(e));
-  }
   if (splits > 1) rc = launch_merge(args, splits, part_acc, part_ml, s);
   return rc;
 }

@@ -1,6 +1,7 @@
 // Host-side helpers shared by the C-ABI entry points.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -24,6 +25,20 @@ struct View {
   int64_t sb, sh, sn;
 };
 inline View view_of(const qsdpa_view& v) { return View{v.ptr, v.stride_b, v.stride_h, v.stride_n}; }
+
+// Launch a one-argument kernel.  With profiling events (either non-null) the
+// launch goes through hipExtLaunchKernel, which attaches the events to the
+// kernel's own dispatch: their elapsed time is the kernel's execution time,
+// with no marker packets queued before or after it.
+template <typename P>
+void launch_profiled(void (*kernel)(P), dim3 grid, dim3 block, hipStream_t stream, void* ev_begin,
+                     void* ev_end, const P& p) {
+  if (ev_begin || ev_end)
+    hipExtLaunchKernelGGL(kernel, grid, block, 0, stream, static_cast<hipEvent_t>(ev_begin),
+                          static_cast<hipEvent_t>(ev_end), 0, p);
+  else
+    hipLaunchKernelGGL(kernel, grid, block, 0, stream, p);
+}
 
 // Launch hooks implemented in the kernel translation units.
 int launch_quantize(const qsdpa_quantize_args* a, hipStream_t stream);

@@ -732,19 +732,18 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(MfmaParams p) {
 }
 
 template <typename Tag, int D, int BITS>
-void launch_gs(const MfmaParams& p, int gs, hipStream_t stream) {
+void launch_gs(const MfmaParams& p, int gs, hipStream_t stream, const qsdpa_decode_args* a) {
   const dim3 grid(p.num_splits, p.Hkv * p.hb_count, p.B);
-  switch (gs) {
-    case 32: decode_mfma_kernel<Tag, D, BITS, 32><<<grid, dim3(kThreads), 0, stream>>>(p); break;
-    case 64: decode_mfma_kernel<Tag, D, BITS, 64><<<grid, dim3(kThreads), 0, stream>>>(p); break;
-    default: decode_mfma_kernel<Tag, D, BITS, 128><<<grid, dim3(kThreads), 0, stream>>>(p); break;
-  }
+  void (*k)(MfmaParams) = gs == 32   ? decode_mfma_kernel<Tag, D, BITS, 32>
+                          : gs == 64 ? decode_mfma_kernel<Tag, D, BITS, 64>
+                                     : decode_mfma_kernel<Tag, D, BITS, 128>;
+  launch_profiled(k, grid, dim3(kThreads), stream, a->prof_begin, a->prof_end, p);
 }
 
 template <typename Tag, int D>
-void launch_bits(const MfmaParams& p, int bits, int gs, hipStream_t stream) {
-  if (bits == 4) launch_gs<Tag, D, 4>(p, gs, stream);
-  else launch_gs<Tag, D, 8>(p, gs, stream);
+void launch_bits(const MfmaParams& p, int bits, int gs, hipStream_t stream, const qsdpa_decode_args* a) {
+  if (bits == 4) launch_gs<Tag, D, 4>(p, gs, stream, a);
+  else launch_gs<Tag, D, 8>(p, gs, stream, a);
 }
 
 bool aligned_view(const qsdpa_view& v, int bytes, int64_t elem_bytes) {
@@ -834,11 +833,11 @@ int launch_decode_mfma(const qsdpa_decode_args* a, int num_splits, float* part_a
   p.part_ml = part_ml;
   const bool f16 = a->dtype == QSDPA_F16;
   if (a->D == 128) {
-    if (f16) launch_bits<F16, 128>(p, a->bits, a->group_size, stream);
-    else launch_bits<BF16, 128>(p, a->bits, a->group_size, stream);
+    if (f16) launch_bits<F16, 128>(p, a->bits, a->group_size, stream, a);
+    else launch_bits<BF16, 128>(p, a->bits, a->group_size, stream, a);
   } else {
-    if (f16) launch_bits<F16, 256>(p, a->bits, a->group_size, stream);
-    else launch_bits<BF16, 256>(p, a->bits, a->group_size, stream);
+    if (f16) launch_bits<F16, 256>(p, a->bits, a->group_size, stream, a);
+    else launch_bits<BF16, 256>(p, a->bits, a->group_size, stream, a);
   }
   return check_launch("decode_mfma");
 }

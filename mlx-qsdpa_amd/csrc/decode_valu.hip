@@ -57,6 +57,8 @@ struct DecodeParams {
   const int32_t* kv_start;
   float* part_acc;  // [B][Hq][splits][D]
   float* part_ml;   // [B][Hq][splits][2]
+  void* ev_begin;   // profiling events (host side only)
+  void* ev_end;
 };
 
 template <int WORDS>
@@ -307,7 +309,7 @@ template <typename Tag, int D, int BITS, int HB>
 void launch_valu(const DecodeParams& p, hipStream_t stream) {
   constexpr int E = (HB == 1) ? 32 : (HB <= 4 ? 16 : 8);
   const dim3 grid(p.num_splits, p.Hkv * p.hb_count, p.B);
-  decode_valu_kernel<Tag, D, BITS, HB, E><<<grid, dim3(256), 0, stream>>>(p);
+  launch_profiled(decode_valu_kernel<Tag, D, BITS, HB, E>, grid, dim3(256), stream, p.ev_begin, p.ev_end, p);
 }
 
 template <typename Tag, int D, int BITS>
@@ -373,6 +375,8 @@ int launch_decode_valu(const qsdpa_decode_args* a, int num_splits, float* part_a
   p.kv_start = a->kv_start;
   p.part_acc = part_acc;
   p.part_ml = part_ml;
+  p.ev_begin = a->prof_begin;
+  p.ev_end = a->prof_end;
   if (a->dtype == QSDPA_F16) dispatch_shape<F16>(p, a->bits, hb, stream);
   else dispatch_shape<BF16>(p, a->bits, hb, stream);
   return check_launch("decode_valu");
