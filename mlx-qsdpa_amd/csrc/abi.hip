@@ -42,6 +42,7 @@ int mfma_num_splits(const qsdpa_decode_args* a, int cus);
 int launch_decode_mfma(const qsdpa_decode_args* a, int num_splits, float* part_acc, float* part_ml,
                        hipStream_t stream);
 
+
 namespace {
 
 constexpr int kMaxSplits = 1024;

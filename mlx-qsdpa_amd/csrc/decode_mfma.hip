@@ -44,10 +44,7 @@
 // zero and their scores are set to -inf.  Q^T is staged once per workgroup in
 // LDS.  The 8 waves merge through LDS; one split writes the normalised
 // output, otherwise float32 partials for the merge kernel (merge.hip).
-#include <algorithm>
-
-#include "abi_internal.h"
-#include "common.h"
+#include "mfma_common.h"
 
 namespace qsdpa {
 
@@ -55,132 +52,6 @@ int launch_merge(const qsdpa_decode_args* a, int num_splits, const float* part_a
                  const float* part_ml, hipStream_t stream);
 
 namespace {
-
-constexpr int kWaves = 8;
-constexpr int kThreads = kWaves * 64;
-constexpr int kTile = 32;
-constexpr float kLog2e = 1.4426950408889634f;
-constexpr float kNegBig = -1.0e30f;
-constexpr float kRescale = 8.0f;
-
-typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-typedef __bf16 b8 __attribute__((ext_vector_type(8)));
-typedef float f4 __attribute__((ext_vector_type(4)));
-
-struct MfmaParams {
-  int B, Hq, Hkv, N, G, hb_count, num_splits, chunk;
-  float qscale;  // softmax scale * log2(e)
-  int has_bias;
-  const uint16_t* q;
-  int64_t q_sb, q_sh;
-  const uint32_t* kp;
-  int64_t kp_sb, kp_sh, kp_sn;
-  const uint32_t* vp;
-  int64_t vp_sb, vp_sh, vp_sn;
-  const uint16_t* ks;
-  int64_t ks_sb, ks_sh, ks_sn;
-  const uint16_t* vs;
-  int64_t vs_sb, vs_sh, vs_sn;
-  const uint16_t* kb;
-  int64_t kb_sb, kb_sh, kb_sn;
-  const uint16_t* vb;
-  int64_t vb_sb, vb_sh, vb_sn;
-  uint16_t* out;
-  int64_t o_sb, o_sh;
-  const void* mask;
-  int mask_kind;
-  int64_t m_sb, m_sh, m_sn;
-  const int32_t* kv_start;
-  float* part_acc;
-  float* part_ml;
-};
-
-__device__ __forceinline__ uint32_t bitop_and_or(uint32_t a, uint32_t mask, uint32_t c) {
-  return __builtin_amdgcn_bitop3_b32(a, mask, c, 0xEA);  // (a & mask) | c
-}
-__device__ __forceinline__ uint32_t perm(uint32_t hi_src, uint32_t lo_src, uint32_t sel) {
-  return __builtin_amdgcn_perm(hi_src, lo_src, sel);
-}
-
-constexpr uint32_t kNib = 0x000F000Fu;     // nibble of each 16-bit half
-constexpr uint32_t kMagic = 0x64006400u;   // fp16 1024.0 in both halves
-constexpr uint32_t kMagic8 = 0x64646464u;  // byte source for v_perm_b32
-constexpr uint32_t kSelB01 = 0x04010400u;  // [src.b0, 0x64, src.b1, 0x64]
-constexpr uint32_t kSelB23 = 0x04030402u;  // [src.b2, 0x64, src.b3, 0x64]
-
-__device__ __forceinline__ uint32_t f16x2_sub1024(uint32_t t) {
-  const f16x2 k1024 = {static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};
-  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, t) - k1024);
-}
-__device__ __forceinline__ uint32_t f16x2_fma(uint32_t c, uint32_t s, uint32_t b) {
-  return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(f16x2, c),
-                                                                __builtin_bit_cast(f16x2, s),
-                                                                __builtin_bit_cast(f16x2, b)));
-}
-// Both halves = the low (sel 0x01000100) or high (0x03020302) half of x.
-__device__ __forceinline__ uint32_t splat_lo(uint32_t x) { return perm(x, x, 0x01000100u); }
-__device__ __forceinline__ uint32_t splat_hi(uint32_t x) { return perm(x, x, 0x03020302u); }
-
-// Order of the 8 dims of one QK k-slice as the K dequantizer produces them:
-// slot j holds dim perm8(j) of the slice.
-template <typename Tag, int BITS>
-__device__ __forceinline__ constexpr int perm8(int j) {
-  if constexpr (Tag::kId == QSDPA_F16 && BITS == 4) return (j >> 1) + 4 * (j & 1);
-  else return j;
-}
-
-// K slice (8 dims of one token, BITS/4 packed words) -> A operand (4 pairs).
-// f16: s2 / b2 hold the group's scale / bias in both halves.  bf16: sf / bf
-// are the float scale / bias.
-template <typename Tag, int BITS>
-__device__ __forceinline__ void dequant_k(const uint32_t* w, uint32_t s2, uint32_t b2, float sf,
-                                          float bf, uint32_t out[4]) {
-  if constexpr (Tag::kId == QSDPA_F16) {
-    uint32_t t[4];
-    if constexpr (BITS == 4) {
-      const uint32_t x = w[0];
-      t[0] = bitop_and_or(x, kNib, kMagic);        // codes 0, 4
-      t[1] = bitop_and_or(x >> 4, kNib, kMagic);   // codes 1, 5
-      t[2] = bitop_and_or(x >> 8, kNib, kMagic);   // codes 2, 6
-      t[3] = bitop_and_or(x >> 12, kNib, kMagic);  // codes 3, 7
-    } else {
-      t[0] = perm(kMagic8, w[0], kSelB01);
-      t[1] = perm(kMagic8, w[0], kSelB23);
-      t[2] = perm(kMagic8, w[1], kSelB01);
-      t[3] = perm(kMagic8, w[1], kSelB23);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) out[i] = f16x2_fma(f16x2_sub1024(t[i]), s2, b2);
-  } else {
-    float c[8];
-    if constexpr (BITS == 4) {
-      const uint32_t lo = w[0] & 0x0F0F0F0Fu;
-      const uint32_t hi = (w[0] >> 4) & 0x0F0F0F0Fu;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        c[2 * i] = static_cast<float>((lo >> (8 * i)) & 0xFFu);
-        c[2 * i + 1] = static_cast<float>((hi >> (8 * i)) & 0xFFu);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) c[i] = static_cast<float>((w[i >> 2] >> (8 * (i & 3))) & 0xFFu);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) out[i] = pack_T2<Tag>(fmaf(sf, c[2 * i], bf), fmaf(sf, c[2 * i + 1], bf));
-  }
-}
-
-template <typename Tag>
-__device__ __forceinline__ f4 mfma(const uint32_t a[4], const uint32_t b[4], f4 c) {
-  const uint4 av = {a[0], a[1], a[2], a[3]};
-  const uint4 bv = {b[0], b[1], b[2], b[3]};
-  if constexpr (Tag::kId == QSDPA_F16)
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, av), __builtin_bit_cast(h8, bv), c,
-                                                  0, 0, 0);
-  else
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(b8, av), __builtin_bit_cast(b8, bv), c,
-                                                   0, 0, 0);
-}
 
 template <int WORDS>
 __device__ __forceinline__ void load_words(const uint32_t* p, uint32_t* w) {
@@ -201,19 +72,6 @@ __device__ __forceinline__ void load_words(const uint32_t* p, uint32_t* w) {
 template <typename T>
 __device__ __forceinline__ const T* add_bytes(const T* p, int64_t bytes) {
   return reinterpret_cast<const T*>(reinterpret_cast<const uint8_t*>(p) + bytes);
-}
-
-__device__ __forceinline__ float mask_value(const MfmaParams& p, int64_t o) {
-  switch (p.mask_kind) {
-    case QSDPA_BOOL:
-      return static_cast<const uint8_t*>(p.mask)[o] ? 0.0f : -__builtin_huge_valf();
-    case QSDPA_F16:
-      return f16_bits_to_f32(static_cast<const uint16_t*>(p.mask)[o]) * kLog2e;
-    case QSDPA_BF16:
-      return bf16_bits_to_f32(static_cast<const uint16_t*>(p.mask)[o]) * kLog2e;
-    default:
-      return static_cast<const float*>(p.mask)[o] * kLog2e;
-  }
 }
 
 // Geometry of one (D, BITS, GS) instantiation.
@@ -250,18 +108,11 @@ struct LaneOffsets {
   uint32_t k_r, ks_r, kb_r, v_r, vs_r, vb_r;
 };
 
-typedef __amdgpu_buffer_rsrc_t rsrc_t;
-
 // Buffer descriptors of one workgroup's rows and the token strides in bytes.
 struct Rsrcs {
   rsrc_t k, ks, kb, v, vs, vb;
   uint32_t k_sn, ks_sn, kb_sn, v_sn, vs_sn, vb_sn;
 };
-
-// Raw buffer descriptor (gfx9 dword3: 32-bit data format, no swizzle).
-__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), 0x00020000);
-}
 
 template <int WORDS>
 __device__ __forceinline__ void buffer_words(rsrc_t rs, uint32_t off, uint32_t* w) {
@@ -746,13 +597,6 @@ void launch_bits(const MfmaParams& p, int bits, int gs, hipStream_t stream, cons
   else launch_gs<Tag, D, 8>(p, gs, stream, a);
 }
 
-bool aligned_view(const qsdpa_view& v, int bytes, int64_t elem_bytes) {
-  if (v.ptr == nullptr) return true;
-  if (reinterpret_cast<uintptr_t>(v.ptr) % bytes) return false;
-  const int64_t m = bytes / elem_bytes;
-  return m <= 1 || (v.stride_b % m == 0 && v.stride_h % m == 0 && v.stride_n % m == 0);
-}
-
 }  // namespace
 
 // The MFMA path covers D in {128, 256} for any GQA factor (heads padded to
@@ -797,40 +641,7 @@ int mfma_num_splits(const qsdpa_decode_args* a, int cus) {
 
 int launch_decode_mfma(const qsdpa_decode_args* a, int num_splits, float* part_acc, float* part_ml,
                        hipStream_t stream) {
-  MfmaParams p;
-  p.B = a->B; p.Hq = a->H_q; p.Hkv = a->H_kv; p.N = a->N;
-  p.G = a->H_q / a->H_kv;
-  p.hb_count = (p.G + 15) / 16;
-  p.num_splits = num_splits;
-  // Whole tiles per split; the last split absorbs the remainder.
-  const int64_t per = (static_cast<int64_t>(a->N) + num_splits - 1) / num_splits;
-  p.chunk = static_cast<int>(((per + kTile - 1) / kTile) * kTile);
-  p.qscale = a->scale * kLog2e;
-  p.has_bias = a->k_biases.ptr != nullptr;
-  p.q = static_cast<const uint16_t*>(a->q.ptr); p.q_sb = a->q.stride_b; p.q_sh = a->q.stride_h;
-  p.kp = static_cast<const uint32_t*>(a->k_packed.ptr);
-  p.kp_sb = a->k_packed.stride_b; p.kp_sh = a->k_packed.stride_h; p.kp_sn = a->k_packed.stride_n;
-  p.vp = static_cast<const uint32_t*>(a->v_packed.ptr);
-  p.vp_sb = a->v_packed.stride_b; p.vp_sh = a->v_packed.stride_h; p.vp_sn = a->v_packed.stride_n;
-  p.ks = static_cast<const uint16_t*>(a->k_scales.ptr);
-  p.ks_sb = a->k_scales.stride_b; p.ks_sh = a->k_scales.stride_h; p.ks_sn = a->k_scales.stride_n;
-  p.vs = static_cast<const uint16_t*>(a->v_scales.ptr);
-  p.vs_sb = a->v_scales.stride_b; p.vs_sh = a->v_scales.stride_h; p.vs_sn = a->v_scales.stride_n;
-  p.kb = static_cast<const uint16_t*>(a->k_biases.ptr);
-  p.kb_sb = a->k_biases.stride_b; p.kb_sh = a->k_biases.stride_h; p.kb_sn = a->k_biases.stride_n;
-  p.vb = static_cast<const uint16_t*>(a->v_biases.ptr);
-  p.vb_sb = a->v_biases.stride_b; p.vb_sh = a->v_biases.stride_h; p.vb_sn = a->v_biases.stride_n;
-  if (!p.has_bias) {
-    p.kb_sb = p.ks_sb; p.kb_sh = p.ks_sh; p.kb_sn = p.ks_sn;
-    p.vb_sb = p.vs_sb; p.vb_sh = p.vs_sh; p.vb_sn = p.vs_sn;
-  }
-  p.out = static_cast<uint16_t*>(const_cast<void*>(a->out.ptr));
-  p.o_sb = a->out.stride_b; p.o_sh = a->out.stride_h;
-  p.mask = a->mask.ptr; p.mask_kind = a->mask_dtype;
-  p.m_sb = a->mask.stride_b; p.m_sh = a->mask.stride_h; p.m_sn = a->mask.stride_n;
-  p.kv_start = a->kv_start;
-  p.part_acc = part_acc;
-  p.part_ml = part_ml;
+  MfmaParams p = mfma_params(a, num_splits, part_acc, part_ml);
   const bool f16 = a->dtype == QSDPA_F16;
   if (a->D == 128) {
     if (f16) launch_bits<F16, 128>(p, a->bits, a->group_size, stream, a);
