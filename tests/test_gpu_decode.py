@@ -283,3 +283,22 @@ def test_headline_full_size_properties(device, N):
     outp = mq.quantized_sdpa(q, pq[0][0], pq[1][0], pq[0][1], pq[1][1], pq[0][2], pq[1][2],
                              bits=bits, group_size=gs)
     assert (outp.float() - out.float()).abs().max().item() < 2e-3
+
+
+@pytest.mark.parametrize("case", [(1, 32, 2, 4096, 256, 4, 32, "f16"), (2, 16, 4, 3000, 128, 8, 64, "bf16")],
+                         ids=["C3_small", "B2_G4_bf16"])
+def test_repeated_calls_reuse_workspace(device, case):
+    """Split-K calls through one DecodePlan (one workspace, reused): every call
+    gives the same output, within tolerance of the oracle."""
+    B, Hq, Hkv, N, D, bits, gs, dt = case
+    rng = np.random.default_rng(77)
+    inp = make_inputs(rng, B, Hq, Hkv, N, D, bits, gs, dt)
+    g = to_dev(inp, device)
+    plan = kernels.DecodePlan(g["q"], g["kp"], g["vp"], g["ks"], g["vs"], g["kb"], g["vb"],
+                              scale=D ** -0.5, bits=bits, group_size=gs, num_splits=0)
+    assert plan.num_splits > 1
+    outs = [plan().clone() for _ in range(4)]
+    torch.cuda.synchronize()
+    for o in outs[1:]:
+        assert torch.equal(o, outs[0])
+    assert_close(to_np(outs[0]), oracle_out(inp), f"{case}")
