@@ -7,14 +7,16 @@
 // narrower) form the N side of 16x16x32 MFMA tiles, so each K/V element is
 // read from HBM and dequantized exactly once per workgroup.
 //
-// Workgroup = 8 waves = one (batch, kv head, block of 16 query heads, token
-// chunk).  Wave w streams the 32-token tiles w, w + 8, w + 16, ... of the
-// chunk with one register set: the next tile's K loads are issued as soon as
-// the current K has been consumed, its V loads once the current V has been
+// Workgroup = 8 waves = one split of a (batch, kv head, block of 16 query
+// heads).  The sequence is cut into 32-token tiles; split s of S owns tiles
+// s, s + S, s + 2S, ..., so the whole grid streams one compact window of the
+// cache at a time.  Each wave streams its share of the split's tiles with
+// one register set: the next tile's K loads are issued as soon as the
+// current K has been consumed, its V loads once the current V has been
 // re-arranged for the PV operands.  All K / V / scale / bias reads are raw
-// buffer loads through per-workgroup descriptors that end at the chunk's
-// last row (hardware range checking; out-of-range rows read as zero, and a
-// missing bias is a zero-size descriptor).  Per 32-token tile:
+// buffer loads through descriptors that end at the sequence's last row
+// (hardware range checking; out-of-range rows read as zero, and a missing
+// bias is a zero-size descriptor).  Per 32-token tile:
 //
 //   S^T[t, h] = K[t, :] . Q[h, :]       v_mfma_f32_16x16x32_{f16,bf16}, two
 //       16-token halves.  A = K rows: lane (quad, r) holds token r of the half
@@ -39,10 +41,9 @@
 // v_cvt_pk_bf16_f32; P is split into two bf16 terms (hi + lo) so the P.V
 // product keeps 16 significant bits.
 //
-// Split boundaries are multiples of 32 tokens from the sequence start, so
-// only the sequence's last tile is partial; its rows past the end read as
-// zero and their scores are set to -inf.  Q^T is staged once per workgroup in
-// LDS.  The 8 waves merge through LDS; one split writes the normalised
+// Tiles start at multiples of 32 tokens from the sequence start, so only the
+// sequence's last tile is partial; its rows past the end read as zero and
+// their scores are set to -inf.  Q^T is staged once per workgroup in LDS.  The 8 waves merge through LDS; one split writes the normalised
 // output, otherwise float32 partials for the merge kernel (merge.hip).
 #include "mfma_common.h"
 
@@ -151,9 +152,9 @@ struct Kernel {
   static __device__ __forceinline__ int tau(int q, int j) { return 16 * (j >> 2) + 4 * q + (j & 3); }
 
   // Issue the K (load_k) or V (load_v) loads of the tile whose first token is
-  // `rel0` rows past the workgroup's first token.  Rows past the chunk end
-  // fall outside the buffer descriptors and read as zero (only the
-  // sequence's last tile has such rows; their scores are set to -inf).
+  // `rel0` rows past the sequence's first key.  Rows past the end fall
+  // outside the buffer descriptors and read as zero (only the sequence's
+  // last tile has such rows; their scores are set to -inf).
   static __device__ __forceinline__ void load_k(Regs& R, const Rsrcs& rs, const LaneOffsets& L, int rel0) {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
@@ -404,54 +405,42 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(MfmaParams p) {
   const int nh = min(16, p.G - hblk * 16);     // real heads in the block
   const int hq_lane = h0 + min(r, nh - 1);     // this lane's head (clamped)
 
+  // Keys [s0, N) of this sequence, in 32-token tiles from s0.  Split s owns
+  // tiles s, s + S, s + 2S, ... (positions j = 0, 1, ..., J - 1), so at any
+  // moment the grid streams one compact window of the cache.
   const int s0 = p.kv_start ? min(max(p.kv_start[b], 0), p.N) : 0;
-  const int n0 = min(s0 + split * p.chunk, p.N);
-  const int n1 = min(n0 + p.chunk, p.N);
+  const int len = p.N - s0;
+  const int T = (len + kTile - 1) / kTile;
+  const int S = p.num_splits;
+  const int J = T > split ? (T - split + S - 1) / S : 0;
+  // Positions below J - E go round-robin to the 8 waves; the last E go to
+  // waves 0-3 only.  Waves 4-7 share their SIMDs with waves 0-3, and the
+  // older waves' loads are served first, so equal shares would leave 0-3
+  // idle at the end; E = J / 4 (in whole rounds of 8) gives 0-3 five tiles
+  // for every three of 4-7.
+  const int E = 8 * (J / 32);
+  const int J8 = J - E;
+  auto next_pos = [&](int j) -> int {
+    if (j + kWaves < J8) return j + kWaves;
+    if (wave >= 4) return J;
+    return j < J8 ? J8 + wave : j + 4;
+  };
+  // Rows of a position relative to s0; past the end, rows outside every
+  // descriptor (the loads read zero without touching memory).  Every tile
+  // issues the same loads, so the compiler's vmcnt waits stay exact.
+  const int oob = len + kTile;
+  auto row_of = [&](int j) -> int { return j < J ? (j * S + split) * kTile : oob; };
 
-  // Q^T B operands in LDS, [m][lane] x 16 B: head r, dims quad*QD + 8m +
-  // perm8(j), zero for padding heads.  Written by wave 0, read by all.  The
-  // area is reused by the wave merge after the main loop.
-  uint8_t* lds_q = reinterpret_cast<uint8_t*>(s_acc);
-  if (wave == 0) {
-    const uint16_t* qp = p.q + static_cast<int64_t>(b) * p.q_sb + static_cast<int64_t>(hq_lane) * p.q_sh +
-                         quad * G::QD;
-#pragma unroll
-    for (int m = 0; m < G::NM; ++m) {
-      const uint32_t* q32 = reinterpret_cast<const uint32_t*>(qp + 8 * m);
-      const uint32_t d0 = q32[0], d1 = q32[1], d2 = q32[2], d3 = q32[3];
-      uint4 v;
-      if constexpr (Tag::kId == QSDPA_F16 && BITS == 4) {
-        v = uint4{perm(d2, d0, 0x05040100u),   // dims 0, 4
-                  perm(d2, d0, 0x07060302u),   // dims 1, 5
-                  perm(d3, d1, 0x05040100u),   // dims 2, 6
-                  perm(d3, d1, 0x07060302u)};  // dims 3, 7
-      } else {
-        v = uint4{d0, d1, d2, d3};
-      }
-      if (r >= nh) v = uint4{0u, 0u, 0u, 0u};
-      *reinterpret_cast<uint4*>(lds_q + m * 1024 + lane * 16) = v;
-    }
-  }
-  __syncthreads();
-  const uint8_t* lds_q_lane = lds_q + lane * 16;
-
-  f4 acc[G::NB];
-#pragma unroll
-  for (int i = 0; i < G::NB; ++i) acc[i] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-  float mrun = kNegBig;
-  float lrun = 0.0f;
-
-  // Buffer descriptors over rows [n0, n1) of this (batch, kv head).
+  // Buffer descriptors over rows [s0, N) of this (batch, kv head).
   Rsrcs rs;
   {
-    const int rows = n1 - n0;
-    const int64_t tok0 = n0;
+    const int64_t tok0 = s0;
     auto rsrc = [&](const void* base, int64_t sb, int64_t sh, int64_t sn, int esz, int row_bytes,
                     bool present) {
       const uint8_t* p0 = static_cast<const uint8_t*>(base) +
                           (static_cast<int64_t>(b) * sb + static_cast<int64_t>(kvh) * sh + tok0 * sn) * esz;
       const uint32_t bytes =
-          (present && rows > 0) ? static_cast<uint32_t>((rows - 1) * sn * esz + row_bytes) : 0u;
+          (present && len > 0) ? static_cast<uint32_t>((len - 1) * sn * esz + row_bytes) : 0u;
       return make_rsrc(p0, bytes);
     };
     constexpr int kRow = D * BITS / 8;
@@ -493,19 +482,66 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(MfmaParams p) {
     vm.shift = half ? 0u : 16u;
   }
 
-  constexpr int kStride = kWaves * kTile;
-  typename K::Regs R;
-  int tb = n0 + wave * kTile;
-  if (tb < n1) {
-    K::load_k(R, rs, L, tb - n0);
-    K::load_v(R, rs, L, tb - n0);
+  // Q^T B operands in LDS, [m][lane] x 16 B: head r, dims quad*QD + 8m +
+  // perm8(j), zero for padding heads.  Wave 0 loads Q, then every wave
+  // issues its first tile before Q is written to LDS, so the tile loads are
+  // in flight during the Q round trip.  The area is reused by the wave merge
+  // after the main loop.
+  uint8_t* lds_q = reinterpret_cast<uint8_t*>(s_acc);
+  uint32_t qd[G::NM][4];
+  if (wave == 0) {
+    const uint16_t* qp = p.q + static_cast<int64_t>(b) * p.q_sb + static_cast<int64_t>(hq_lane) * p.q_sh +
+                         quad * G::QD;
+#pragma unroll
+    for (int m = 0; m < G::NM; ++m) {
+      const uint32_t* q32 = reinterpret_cast<const uint32_t*>(qp + 8 * m);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) qd[m][i] = q32[i];
+    }
   }
-  for (; tb < n1; tb += kStride) {
-    const int nt = tb + kStride;
-    const bool more = nt < n1;
-    auto ik = [&](typename K::Regs& X) { if (more) K::load_k(X, rs, L, nt - n0); };
-    auto iv = [&](typename K::Regs& X) { if (more) K::load_v(X, rs, L, nt - n0); };
-    K::compute_tile(R, p, lds_q_lane, acc, mrun, lrun, tb, n1, quad, b, hq_lane, vm, ik, iv);
+  __builtin_amdgcn_sched_barrier(0);
+  typename K::Regs R;
+  int j = wave;
+  K::load_k(R, rs, L, row_of(j));
+  __builtin_amdgcn_sched_barrier(0);
+  K::load_v(R, rs, L, row_of(j));
+  __builtin_amdgcn_sched_barrier(0);
+  if (wave == 0) {
+#pragma unroll
+    for (int m = 0; m < G::NM; ++m) {
+      const uint32_t d0 = qd[m][0], d1 = qd[m][1], d2 = qd[m][2], d3 = qd[m][3];
+      uint4 v;
+      if constexpr (Tag::kId == QSDPA_F16 && BITS == 4) {
+        v = uint4{perm(d2, d0, 0x05040100u),   // dims 0, 4
+                  perm(d2, d0, 0x07060302u),   // dims 1, 5
+                  perm(d3, d1, 0x05040100u),   // dims 2, 6
+                  perm(d3, d1, 0x07060302u)};  // dims 3, 7
+      } else {
+        v = uint4{d0, d1, d2, d3};
+      }
+      if (r >= nh) v = uint4{0u, 0u, 0u, 0u};
+      *reinterpret_cast<uint4*>(lds_q + m * 1024 + lane * 16) = v;
+    }
+  }
+  // LDS-only barrier: the tile loads stay in flight across it.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+  const uint8_t* lds_q_lane = lds_q + lane * 16;
+
+  f4 acc[G::NB];
+#pragma unroll
+  for (int i = 0; i < G::NB; ++i) acc[i] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  float mrun = kNegBig;
+  float lrun = 0.0f;
+
+  while (j < J) {
+    const int nj = next_pos(j);
+    const int nrow = row_of(nj);
+    auto ik = [&](typename K::Regs& X) { K::load_k(X, rs, L, nrow); };
+    auto iv = [&](typename K::Regs& X) { K::load_v(X, rs, L, nrow); };
+    K::compute_tile(R, p, lds_q_lane, acc, mrun, lrun, s0 + row_of(j), p.N, quad, b, hq_lane, vm, ik, iv);
+    j = nj;
   }
 
   // ---- per-head totals over the four quads ----
@@ -619,17 +655,18 @@ bool mfma_supports(const qsdpa_decode_args* a) {
   if (a->D / a->group_size >= 2) {
     if (!aligned_view(a->v_scales, 4, 2) || !aligned_view(a->v_biases, 4, 2)) return false;
   }
-  // Lane offsets inside a tile are 32-bit.
+  // Byte offsets of rows within the sequence (up to two tiles past its end)
+  // are 32-bit.
   const int64_t max_sn = std::max({a->k_packed.stride_n * 4, a->v_packed.stride_n * 4,
                                    a->k_scales.stride_n * 2, a->v_scales.stride_n * 2,
                                    a->k_biases.stride_n * 2, a->v_biases.stride_n * 2});
-  if (max_sn < 0 || max_sn * kTile >= (int64_t(1) << 30)) return false;
+  if (max_sn < 0 || max_sn * (static_cast<int64_t>(a->N) + 3 * kTile) >= (int64_t(1) << 31)) return false;
   return true;
 }
 
 // Splits per (batch, kv head, head block): one workgroup per CU in total
 // (LDS and registers allow one 8-wave group per CU), each split at least one
-// tile per wave.  Chunks are whole tiles.
+// tile per wave.
 int mfma_num_splits(const qsdpa_decode_args* a, int cus) {
   const int hb = (a->H_q / a->H_kv + 15) / 16;
   const int64_t units = static_cast<int64_t>(a->B) * a->H_kv * hb;

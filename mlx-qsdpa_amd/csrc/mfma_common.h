@@ -23,7 +23,7 @@ typedef __bf16 b8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
 struct MfmaParams {
-  int B, Hq, Hkv, N, G, hb_count, num_splits, chunk;
+  int B, Hq, Hkv, N, G, hb_count, num_splits;
   float qscale;  // softmax scale * log2(e)
   int has_bias;
   const uint16_t* q;
@@ -173,9 +173,6 @@ inline MfmaParams mfma_params(const qsdpa_decode_args* a, int num_splits, float*
   p.G = a->H_q / a->H_kv;
   p.hb_count = (p.G + 15) / 16;
   p.num_splits = num_splits;
-  // Whole tiles per split; the last split absorbs the remainder.
-  const int64_t per = (static_cast<int64_t>(a->N) + num_splits - 1) / num_splits;
-  p.chunk = static_cast<int>(((per + kTile - 1) / kTile) * kTile);
   p.qscale = a->scale * kLog2e;
   p.has_bias = a->k_biases.ptr != nullptr;
   p.q = static_cast<const uint16_t*>(a->q.ptr); p.q_sb = a->q.stride_b; p.q_sh = a->q.stride_h;
