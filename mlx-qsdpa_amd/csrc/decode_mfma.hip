@@ -36,15 +36,17 @@
 //       with the per-token scale / bias pairs.
 //
 // Float16: codes become exact fp16 values through the "1024 + code" exponent
-// trick (v_bitop3_b32 / v_perm_b32), then v_pk_fma_f16 applies scale and
-// bias.  Bfloat16: dequantization runs in fp32 and is rounded with
+// trick (v_bitop3_b32 / v_perm_b32; a nibble at bits 4-7 of a half uses
+// 64 + code instead, so it needs no shift), then v_pk_fma_f16 applies scale
+// and bias.  Bfloat16: dequantization runs in fp32 and is rounded with
 // v_cvt_pk_bf16_f32; P is split into two bf16 terms (hi + lo) so the P.V
 // product keeps 16 significant bits.
 //
 // Tiles start at multiples of 32 tokens from the sequence start, so only the
 // sequence's last tile is partial; its rows past the end read as zero and
-// their scores are set to -inf.  Q^T is staged once per workgroup in LDS.  The 8 waves merge through LDS; one split writes the normalised
-// output, otherwise float32 partials for the merge kernel (merge.hip).
+// their scores are set to -inf.  Each wave keeps Q^T in registers.  The 8
+// waves merge through LDS; one split writes the normalised output, otherwise
+// float32 partials for the merge kernel (merge.hip).
 #include "mfma_common.h"
 
 namespace qsdpa {
@@ -194,11 +196,11 @@ struct Kernel {
   // has been consumed, and its V loads (issue_v) once V is in the PV
   // operands' pre-permuted form, so one register set suffices.
   template <typename IK, typename IV>
-  static __device__ __forceinline__ void compute_tile(Regs& R, const MfmaParams& p, const uint8_t* lds_q,
+  static __device__ __forceinline__ void compute_tile(Regs& R, const MfmaParams& p, const uint32_t (&qt)[G::NM][4],
                                                       f4 (&acc)[G::NB], float& mrun, float& lrun, int tb,
                                                       int n1, int quad, int b, int hq_lane, const VMetaLane& vm,
                                                       IK&& issue_k, IV&& issue_v) {
-    // ---- S^T = K Q^T (Q^T operand m read from LDS: 16 B per lane) ----
+    // ---- S^T = K Q^T (Q^T operand m: 16 B per lane, in registers) ----
     f4 S[2] = {f4{0.0f, 0.0f, 0.0f, 0.0f}, f4{0.0f, 0.0f, 0.0f, 0.0f}};
     uint32_t s2[2][2], b2[2][2];
     float sf[2][2], bf[2][2];
@@ -220,14 +222,12 @@ struct Kernel {
     }
 #pragma unroll
     for (int m = 0; m < G::NM; ++m) {
-      const uint4 qv = *reinterpret_cast<const uint4*>(lds_q + m * 1024);
-      const uint32_t qb[4] = {qv.x, qv.y, qv.z, qv.w};
       const int gsel = (G::KG == 2 && m >= G::NM / 2) ? 1 : 0;
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         uint32_t a[4];
         dequant_k<Tag, BITS>(R.kw[u] + m * G::WPS, s2[u][gsel], b2[u][gsel], sf[u][gsel], bf[u][gsel], a);
-        S[u] = mfma<Tag>(a, qb, S[u]);
+        S[u] = mfma<Tag>(a, qt[m], S[u]);
       }
     }
     issue_k(R);
@@ -244,7 +244,7 @@ struct Kernel {
         sc[j] += mask_value(p, mrow + static_cast<int64_t>(t) * p.m_sn);
       }
     }
-    if (tb + kTile > n1) {  // the sequence's last, partial tile
+    if (__builtin_expect(tb + kTile > n1, 0)) {  // the sequence's last, partial tile
 #pragma unroll
       for (int j = 0; j < 8; ++j)
         if (tb + tau(quad, j) >= n1) sc[j] = -__builtin_huge_valf();
@@ -311,8 +311,8 @@ struct Kernel {
           uint32_t a[4];
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const uint32_t src = (k < 4 ? X[i][w] : Y[i][w]) >> (4 * (k & 3));
-            a[i] = f16x2_fma(f16x2_sub1024(bitop_and_or(src, kNib, kMagic)), sv2[i], bv2[i]);
+            const uint32_t src = k < 4 ? X[i][w] : Y[i][w];
+            a[i] = f16x2_fma(nib_codes(src, src >> 8, k & 3), sv2[i], bv2[i]);
           }
           acc[nb] = mfma<Tag>(a, pb, acc[nb]);
         }
@@ -482,21 +482,19 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(MfmaParams p) {
     vm.shift = half ? 0u : 16u;
   }
 
-  // Q^T B operands in LDS, [m][lane] x 16 B: head r, dims quad*QD + 8m +
-  // perm8(j), zero for padding heads.  Wave 0 loads Q, then every wave
-  // issues its first tile before Q is written to LDS, so the tile loads are
-  // in flight during the Q round trip.  The area is reused by the wave merge
-  // after the main loop.
-  uint8_t* lds_q = reinterpret_cast<uint8_t*>(s_acc);
-  uint32_t qd[G::NM][4];
-  if (wave == 0) {
+  // Q^T B operands, one 16-byte piece per lane and QK step m: head r, dims
+  // quad*QD + 8m + perm8(j), zero for padding heads.  Every wave loads its
+  // own copy (Q is a few KB and stays in L2), ahead of its first tile, so no
+  // wave waits for another before streaming.
+  uint32_t qt[G::NM][4];
+  {
     const uint16_t* qp = p.q + static_cast<int64_t>(b) * p.q_sb + static_cast<int64_t>(hq_lane) * p.q_sh +
                          quad * G::QD;
 #pragma unroll
     for (int m = 0; m < G::NM; ++m) {
       const uint32_t* q32 = reinterpret_cast<const uint32_t*>(qp + 8 * m);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) qd[m][i] = q32[i];
+      for (int i = 0; i < 4; ++i) qt[m][i] = q32[i];
     }
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -506,28 +504,17 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(MfmaParams p) {
   __builtin_amdgcn_sched_barrier(0);
   K::load_v(R, rs, L, row_of(j));
   __builtin_amdgcn_sched_barrier(0);
-  if (wave == 0) {
 #pragma unroll
-    for (int m = 0; m < G::NM; ++m) {
-      const uint32_t d0 = qd[m][0], d1 = qd[m][1], d2 = qd[m][2], d3 = qd[m][3];
-      uint4 v;
-      if constexpr (Tag::kId == QSDPA_F16 && BITS == 4) {
-        v = uint4{perm(d2, d0, 0x05040100u),   // dims 0, 4
-                  perm(d2, d0, 0x07060302u),   // dims 1, 5
-                  perm(d3, d1, 0x05040100u),   // dims 2, 6
-                  perm(d3, d1, 0x07060302u)};  // dims 3, 7
-      } else {
-        v = uint4{d0, d1, d2, d3};
-      }
-      if (r >= nh) v = uint4{0u, 0u, 0u, 0u};
-      *reinterpret_cast<uint4*>(lds_q + m * 1024 + lane * 16) = v;
+  for (int m = 0; m < G::NM; ++m) {
+    const uint32_t d0 = qt[m][0], d1 = qt[m][1], d2 = qt[m][2], d3 = qt[m][3];
+    if constexpr (Tag::kId == QSDPA_F16 && BITS == 4) {
+      qt[m][0] = perm(d2, d0, 0x05040100u);  // dims 0, 4
+      qt[m][1] = perm(d2, d0, 0x07060302u);  // dims 1, 5
+      qt[m][2] = perm(d3, d1, 0x05040100u);  // dims 2, 6
+      qt[m][3] = perm(d3, d1, 0x07060302u);  // dims 3, 7
     }
+    if (r >= nh) qt[m][0] = qt[m][1] = qt[m][2] = qt[m][3] = 0u;
   }
-  // LDS-only barrier: the tile loads stay in flight across it.
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-  const uint8_t* lds_q_lane = lds_q + lane * 16;
 
   f4 acc[G::NB];
 #pragma unroll
@@ -540,7 +527,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(MfmaParams p) {
     const int nrow = row_of(nj);
     auto ik = [&](typename K::Regs& X) { K::load_k(X, rs, L, nrow); };
     auto iv = [&](typename K::Regs& X) { K::load_v(X, rs, L, nrow); };
-    K::compute_tile(R, p, lds_q_lane, acc, mrun, lrun, s0 + row_of(j), p.N, quad, b, hq_lane, vm, ik, iv);
+    K::compute_tile(R, p, qt, acc, mrun, lrun, s0 + row_of(j), p.N, quad, b, hq_lane, vm, ik, iv);
     j = nj;
   }
 
@@ -548,16 +535,11 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(MfmaParams p) {
   lrun += shfl_xor_f32(lrun, 16);
   lrun += shfl_xor_f32(lrun, 32);
 
-  // ---- merge the waves through LDS ----
+  // ---- merge the waves through LDS: raw rows plus each wave's (m, l) ----
   if (quad == 0) {
     s_ml[wave][r][0] = mrun;
     s_ml[wave][r][1] = lrun;
   }
-  __syncthreads();
-  float M = s_ml[0][r][0];
-#pragma unroll
-  for (int w = 1; w < kWaves; ++w) M = fmaxf(M, s_ml[w][r][0]);
-  const float f = fast_exp2(mrun - M);
   // acc[nb][i] is out^T[dim (4*quad + i)*NB + nb][head r]: 4 runs of NB dims.
   float* row = s_acc + (wave * 16 + r) * kRowF;
 #pragma unroll
@@ -565,8 +547,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(MfmaParams p) {
     float* dst = row + (4 * quad + i) * G::NB;
 #pragma unroll
     for (int nb = 0; nb < G::NB; nb += 4)
-      *reinterpret_cast<f4*>(dst + nb) =
-          f4{acc[nb][i] * f, acc[nb + 1][i] * f, acc[nb + 2][i] * f, acc[nb + 3][i] * f};
+      *reinterpret_cast<f4*>(dst + nb) = f4{acc[nb][i], acc[nb + 1][i], acc[nb + 2][i], acc[nb + 3][i]};
   }
   __syncthreads();
 
@@ -585,12 +566,15 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(MfmaParams p) {
     for (int e = 0; e < kPer; ++e) v[e] = 0.0f;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) {
-      L = fmaf(s_ml[w][h][1], fast_exp2(s_ml[w][h][0] - Mh), L);
+      const float f = fast_exp2(s_ml[w][h][0] - Mh);
+      L = fmaf(s_ml[w][h][1], f, L);
       const float* src = s_acc + (w * 16 + h) * kRowF + d;
       const f4 a0 = *reinterpret_cast<const f4*>(src);
       const f4 a1 = *reinterpret_cast<const f4*>(src + 4);
-      v[0] += a0[0]; v[1] += a0[1]; v[2] += a0[2]; v[3] += a0[3];
-      v[4] += a1[0]; v[5] += a1[1]; v[6] += a1[2]; v[7] += a1[3];
+      v[0] = fmaf(a0[0], f, v[0]); v[1] = fmaf(a0[1], f, v[1]);
+      v[2] = fmaf(a0[2], f, v[2]); v[3] = fmaf(a0[3], f, v[3]);
+      v[4] = fmaf(a1[0], f, v[4]); v[5] = fmaf(a1[1], f, v[5]);
+      v[6] = fmaf(a1[2], f, v[6]); v[7] = fmaf(a1[3], f, v[7]);
     }
     const int hh = h0 + h;
     if (p.num_splits == 1) {

@@ -9,9 +9,12 @@
 // out[b, h, :] = sum_s acc_s * exp2(m_s - M) / sum_s l_s * exp2(m_s - M),
 // M = max_s m_s, and 0 when every split is empty (l = 0).
 //
-// Launch: grid (B*H_q, D/16), 256 threads = 16 split lanes x 16 dims.  A
-// thread's first kPrefetch partial loads are issued before the block
-// reductions of (m, l), so one memory round trip covers up to 128 splits.
+// Launch: grid (B*H_q, D/32), 256 threads = 32 split groups x 8 dim
+// quads.  Thread (g, q) owns dims 4q..4q+3 of the block's 32 (one 16-byte
+// load per split) and splits g, g + 32, ...; it issues all its loads of a
+// round of 32 * kPer splits at once and keeps a running (m, l, acc) with
+// rescaling, so 128 splits cost one memory round trip.  The 32 groups then
+// merge with shuffles (8 per wave) and LDS (4 waves).
 #include "abi_internal.h"
 #include "common.h"
 
@@ -19,19 +22,9 @@ namespace qsdpa {
 namespace {
 
 constexpr int kMaxSplits = 1024;
-constexpr int kPrefetch = 8;
+constexpr int kGroups = 32;  // split groups per block
+constexpr int kPer = 4;      // splits per thread per round
 constexpr float kNegBig = -1.0e30f;
-
-__device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) x = fmaxf(x, shfl_xor_f32(x, m));
-  return x;
-}
-__device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) x += shfl_xor_f32(x, m);
-  return x;
-}
 
 template <typename Tag>
 __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ part_acc,
@@ -40,59 +33,73 @@ __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ pa
                                                     int64_t o_sb, int64_t o_sh) {
   const int bh = blockIdx.x;
   const int tid = threadIdx.x;
-  const int dd = tid & 15;
-  const int sg = tid >> 4;
+  const int q = tid & 7;
+  const int g = tid >> 3;
   const int wave = tid >> 6;
-  const int d = blockIdx.y * 16 + dd;
-  const float* ml = part_ml + static_cast<int64_t>(bh) * splits * 2;
+  const int d = blockIdx.y * 32 + 4 * q;
+  const float2* ml = reinterpret_cast<const float2*>(part_ml) + static_cast<int64_t>(bh) * splits;
   const float* pa = part_acc + static_cast<int64_t>(bh) * splits * D + d;
 
-  float x[kPrefetch];
+  float m = kNegBig, l = 0.0f;
+  float4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int s0 = 0; s0 < splits; s0 += kGroups * kPer) {
+    float4 x[kPer];
+    float2 w[kPer];
 #pragma unroll
-  for (int k = 0; k < kPrefetch; ++k) {
-    const int s = sg + 16 * k;
-    x[k] = s < splits ? pa[static_cast<int64_t>(s) * D] : 0.0f;
+    for (int k = 0; k < kPer; ++k) {
+      const int s = s0 + g + kGroups * k;
+      const bool ok = s < splits;
+      x[k] = ok ? *reinterpret_cast<const float4*>(pa + static_cast<int64_t>(s) * D) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+      w[k] = ok ? ml[s] : float2{kNegBig, 0.0f};
+    }
+    float mr = m;
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) mr = fmaxf(mr, w[k].x);
+    const float f = fast_exp2(m - mr);
+    l *= f;
+    acc.x *= f; acc.y *= f; acc.z *= f; acc.w *= f;
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const float e = fast_exp2(w[k].x - mr);
+      l = fmaf(w[k].y, e, l);
+      acc.x = fmaf(x[k].x, e, acc.x); acc.y = fmaf(x[k].y, e, acc.y);
+      acc.z = fmaf(x[k].z, e, acc.z); acc.w = fmaf(x[k].w, e, acc.w);
+    }
+    m = mr;
   }
 
-  __shared__ float s_w[kMaxSplits];
-  __shared__ float s_red[2][4];
-  __shared__ float s_acc[16][17];
-
-  float mloc = kNegBig;
-  for (int s = tid; s < splits; s += 256) mloc = fmaxf(mloc, ml[2 * s]);
-  mloc = wave_max(mloc);
-  if ((tid & 63) == 0) s_red[0][wave] = mloc;
-  __syncthreads();
-  const float M = fmaxf(fmaxf(s_red[0][0], s_red[0][1]), fmaxf(s_red[0][2], s_red[0][3]));
-  float lloc = 0.0f;
-  for (int s = tid; s < splits; s += 256) {
-    const float w = fast_exp2(ml[2 * s] - M);
-    s_w[s] = w;
-    lloc = fmaf(ml[2 * s + 1], w, lloc);
-  }
-  lloc = wave_sum(lloc);
-  if ((tid & 63) == 0) s_red[1][wave] = lloc;
-  __syncthreads();
-  const float L = (s_red[1][0] + s_red[1][1]) + (s_red[1][2] + s_red[1][3]);
-
-  float acc = 0.0f;
+  // Block max of m (the same for every dim quad of a group).
+  __shared__ float s_m[4];
+  __shared__ float s_l[4];
+  __shared__ float4 s_acc[4][8];
+  float mw = m;
 #pragma unroll
-  for (int k = 0; k < kPrefetch; ++k) {
-    const int s = sg + 16 * k;
-    if (s < splits) acc = fmaf(x[k], s_w[s], acc);
-  }
-  for (int s = sg + 16 * kPrefetch; s < splits; s += 16)
-    acc = fmaf(pa[static_cast<int64_t>(s) * D], s_w[s], acc);
-  s_acc[sg][dd] = acc;
+  for (int o = 8; o < 64; o <<= 1) mw = fmaxf(mw, shfl_xor_f32(mw, o));
+  if ((tid & 63) == 0) s_m[wave] = mw;
   __syncthreads();
-  if (tid < 16) {
-    float t = 0.0f;
+  const float M = fmaxf(fmaxf(s_m[0], s_m[1]), fmaxf(s_m[2], s_m[3]));
+  const float f = fast_exp2(m - M);
+  l *= f;
+  acc.x *= f; acc.y *= f; acc.z *= f; acc.w *= f;
 #pragma unroll
-    for (int g = 0; g < 16; ++g) t += s_acc[g][tid];
+  for (int o = 8; o < 64; o <<= 1) {
+    l += shfl_xor_f32(l, o);
+    acc.x += shfl_xor_f32(acc.x, o); acc.y += shfl_xor_f32(acc.y, o);
+    acc.z += shfl_xor_f32(acc.z, o); acc.w += shfl_xor_f32(acc.w, o);
+  }
+  if ((tid & 63) < 8) s_acc[wave][q] = acc;
+  if ((tid & 63) == 0) s_l[wave] = l;
+  __syncthreads();
+  if (tid < 8) {
+    const float L = (s_l[0] + s_l[1]) + (s_l[2] + s_l[3]);
+    const float4 a0 = s_acc[0][tid], a1 = s_acc[1][tid], a2 = s_acc[2][tid], a3 = s_acc[3][tid];
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    const float o[4] = {((a0.x + a1.x) + (a2.x + a3.x)) * inv, ((a0.y + a1.y) + (a2.y + a3.y)) * inv,
+                        ((a0.z + a1.z) + (a2.z + a3.z)) * inv, ((a0.w + a1.w) + (a2.w + a3.w)) * inv};
     const int b = bh / Hq, h = bh % Hq;
-    const float o = L > 0.0f ? t / L : 0.0f;
-    out[static_cast<int64_t>(b) * o_sb + static_cast<int64_t>(h) * o_sh + blockIdx.y * 16 + tid] =
-        from_f32<Tag>(o);
+    uint16_t* dst = out + static_cast<int64_t>(b) * o_sb + static_cast<int64_t>(h) * o_sh + blockIdx.y * 32 + 4 * tid;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) dst[e] = from_f32<Tag>(o[e]);
   }
 }
 
@@ -103,7 +110,7 @@ int launch_merge(const qsdpa_decode_args* a, int num_splits, const float* part_a
   if (num_splits > kMaxSplits)
     return fail(QSDPA_ERR_INVALID, "merge: %d splits exceed %d", num_splits, kMaxSplits);
   uint16_t* out = static_cast<uint16_t*>(const_cast<void*>(a->out.ptr));
-  const dim3 grid(a->B * a->H_q, a->D / 16);
+  const dim3 grid(a->B * a->H_q, a->D / 32);
   if (a->dtype == QSDPA_F16)
     merge_kernel<F16><<<grid, dim3(256), 0, stream>>>(part_acc, part_ml, a->D, num_splits, a->H_q,
                                                       out, a->out.stride_b, a->out.stride_h);

@@ -59,6 +59,10 @@ __device__ __forceinline__ uint32_t perm(uint32_t hi_src, uint32_t lo_src, uint3
 
 constexpr uint32_t kNib = 0x000F000Fu;     // nibble of each 16-bit half
 constexpr uint32_t kMagic = 0x64006400u;   // fp16 1024.0 in both halves
+// A nibble at bits 4-7 of a half, or-ed into fp16 64.0 (ulp 1/16), reads as
+// 64 + code: the second nibble of a half needs no shift.
+constexpr uint32_t kNib1 = 0x00F000F0u;
+constexpr uint32_t kMagic64 = 0x54005400u;
 constexpr uint32_t kMagic8 = 0x64646464u;  // byte source for v_perm_b32
 constexpr uint32_t kSelB01 = 0x04010400u;  // [src.b0, 0x64, src.b1, 0x64]
 constexpr uint32_t kSelB23 = 0x04030402u;  // [src.b2, 0x64, src.b3, 0x64]
@@ -66,6 +70,17 @@ constexpr uint32_t kSelB23 = 0x04030402u;  // [src.b2, 0x64, src.b3, 0x64]
 __device__ __forceinline__ uint32_t f16x2_sub1024(uint32_t t) {
   const f16x2 k1024 = {static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};
   return __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, t) - k1024);
+}
+__device__ __forceinline__ uint32_t f16x2_sub64(uint32_t t) {
+  const f16x2 k64 = {static_cast<_Float16>(64.0f), static_cast<_Float16>(64.0f)};
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, t) - k64);
+}
+// Codes (as exact fp16 pairs) of nibble k (0-3) of both halves of x, given
+// x8 = x >> 8.  Nibbles 0 and 1 of a half come from x, 2 and 3 from x8.
+__device__ __forceinline__ uint32_t nib_codes(uint32_t x, uint32_t x8, int k) {
+  const uint32_t src = k < 2 ? x : x8;
+  return (k & 1) ? f16x2_sub64(bitop_and_or(src, kNib1, kMagic64))
+                 : f16x2_sub1024(bitop_and_or(src, kNib, kMagic));
 }
 __device__ __forceinline__ uint32_t f16x2_fma(uint32_t c, uint32_t s, uint32_t b) {
   return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(f16x2, c),
@@ -93,19 +108,17 @@ __device__ __forceinline__ void dequant_k(const uint32_t* w, uint32_t s2, uint32
   if constexpr (Tag::kId == QSDPA_F16) {
     uint32_t t[4];
     if constexpr (BITS == 4) {
-      const uint32_t x = w[0];
-      t[0] = bitop_and_or(x, kNib, kMagic);        // codes 0, 4
-      t[1] = bitop_and_or(x >> 4, kNib, kMagic);   // codes 1, 5
-      t[2] = bitop_and_or(x >> 8, kNib, kMagic);   // codes 2, 6
-      t[3] = bitop_and_or(x >> 12, kNib, kMagic);  // codes 3, 7
+      const uint32_t x = w[0], x8 = w[0] >> 8;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) t[i] = nib_codes(x, x8, i);  // codes (i, i + 4)
     } else {
-      t[0] = perm(kMagic8, w[0], kSelB01);
-      t[1] = perm(kMagic8, w[0], kSelB23);
-      t[2] = perm(kMagic8, w[1], kSelB01);
-      t[3] = perm(kMagic8, w[1], kSelB23);
+      t[0] = f16x2_sub1024(perm(kMagic8, w[0], kSelB01));
+      t[1] = f16x2_sub1024(perm(kMagic8, w[0], kSelB23));
+      t[2] = f16x2_sub1024(perm(kMagic8, w[1], kSelB01));
+      t[3] = f16x2_sub1024(perm(kMagic8, w[1], kSelB23));
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) out[i] = f16x2_fma(f16x2_sub1024(t[i]), s2, b2);
+    for (int i = 0; i < 4; ++i) out[i] = f16x2_fma(t[i], s2, b2);
   } else {
     float c[8];
     if constexpr (BITS == 4) {
