@@ -592,8 +592,9 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(MfmaParams p) {
     } else {
       const int64_t slot = (static_cast<int64_t>(b) * p.Hq + hh) * p.num_splits + split;
       float* dst = p.part_acc + slot * D + d;
-      *reinterpret_cast<f4*>(dst) = f4{v[0], v[1], v[2], v[3]};
-      *reinterpret_cast<f4*>(dst + 4) = f4{v[4], v[5], v[6], v[7]};
+      // Streaming stores: the partials are read once, by the merge kernel.
+      __builtin_nontemporal_store(f4{v[0], v[1], v[2], v[3]}, reinterpret_cast<f4*>(dst));
+      __builtin_nontemporal_store(f4{v[4], v[5], v[6], v[7]}, reinterpret_cast<f4*>(dst + 4));
       if (d == 0) {
         p.part_ml[slot * 2] = Mh;
         p.part_ml[slot * 2 + 1] = L;
