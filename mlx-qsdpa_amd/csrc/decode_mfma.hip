@@ -100,7 +100,10 @@ template <int D, int BITS, int GS>
 struct TileRegs {
   using G = Geo<D, BITS, GS>;
   uint32_t kw[2][G::KW];
-  uint32_t ks[2], kb[2];     // KG == 2: both groups (16-bit each); else low half
+  uint32_t ks[2];            // KG == 2: both groups (16-bit each); else low half
+  // float16: A operand of the K-bias MFMA (4 biases of the token's row);
+  // bfloat16: kb[u][0] = the lane's own group bias word, as ks.
+  uint32_t kb[2][2];
   uint32_t vw[8][G::VW];
   uint32_t vs[2], vb[2];     // V scale / bias row words (A layout, per half)
 };
@@ -145,10 +148,20 @@ struct VMetaLane {
   uint32_t shift;
 };
 
+typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+
 template <typename Tag, int D, int BITS, int GS>
 struct Kernel {
   using G = Geo<D, BITS, GS>;
   using Regs = TileRegs<D, BITS, GS>;
+  // Float16 folds the dequantization biases into MFMAs: a K / V element
+  // becomes fma(M + code, scale, -M * scale) = round(scale * code) (one
+  // rounding; M * scale is exact), and the bias terms are added as
+  //   S^T[t, h]   += sum_g kbias_g[t] * sum_{d in g} Q[h, d]   (16x16x16 MFMA)
+  //   out^T[d, h] += sum_t vbias_g(d)[t] * P^T[t, h]         (16x16x32 MFMA)
+  // -1024 * scale overflows float16 for |scale| >= 64: a tile holding such
+  // a scale runs with its scales times 2^-11 and its products scaled back.
+  static constexpr bool kFold = Tag::kId == QSDPA_F16;
 
   // Token of slot j (0..7) of quad q within a 32-token tile (the S^T C layout).
   static __device__ __forceinline__ int tau(int q, int j) { return 16 * (j >> 2) + 4 * q + (j & 3); }
@@ -162,12 +175,25 @@ struct Kernel {
     for (int u = 0; u < 2; ++u) {
       const uint32_t row = static_cast<uint32_t>(rel0 + 16 * u);
       buffer_words<G::KW>(rs.k, row * rs.k_sn + L.k_r, R.kw[u]);
-      if constexpr (G::KG == 2) {
+      if constexpr (G::KG == 2)
         R.ks[u] = __builtin_amdgcn_raw_buffer_load_b32(rs.ks, row * rs.ks_sn + L.ks_r, 0, 0);
-        R.kb[u] = __builtin_amdgcn_raw_buffer_load_b32(rs.kb, row * rs.kb_sn + L.kb_r, 0, 0);
-      } else {
+      else
         R.ks[u] = __builtin_amdgcn_raw_buffer_load_b16(rs.ks, row * rs.ks_sn + L.ks_r, 0, 0);
-        R.kb[u] = __builtin_amdgcn_raw_buffer_load_b16(rs.kb, row * rs.kb_sn + L.kb_r, 0, 0);
+      if constexpr (kFold) {
+        // Biases of groups 4 * (quad & 1) .. + 3 of the row (zero past NG).
+        const uint32_t off = row * rs.kb_sn + L.kb_r;
+        if constexpr (G::NG >= 4) {
+          const u2 v = __builtin_amdgcn_raw_buffer_load_b64(rs.kb, off, 0, 0);
+          R.kb[u][0] = v[0]; R.kb[u][1] = v[1];
+        } else if constexpr (G::NG == 2) {
+          R.kb[u][0] = __builtin_amdgcn_raw_buffer_load_b32(rs.kb, off, 0, 0); R.kb[u][1] = 0u;
+        } else {
+          R.kb[u][0] = __builtin_amdgcn_raw_buffer_load_b16(rs.kb, off, 0, 0); R.kb[u][1] = 0u;
+        }
+      } else if constexpr (G::KG == 2) {
+        R.kb[u][0] = __builtin_amdgcn_raw_buffer_load_b32(rs.kb, row * rs.kb_sn + L.kb_r, 0, 0);
+      } else {
+        R.kb[u][0] = __builtin_amdgcn_raw_buffer_load_b16(rs.kb, row * rs.kb_sn + L.kb_r, 0, 0);
       }
     }
   }
@@ -191,44 +217,155 @@ struct Kernel {
     }
   }
 
+  // S^T for one 16-token half u: K dequantized into the A operand, Q^T as
+  // B.  FOLD: round(scale * code) only (the bias enters through the K-bias
+  // MFMA); otherwise scale * code + bias with the lane's group biases kbl.
+  // FOLD: ssc = 1.0 or 2^-11 in both halves, a factor applied to the
+  // scales (the caller multiplies the result back).
+  template <bool FOLD>
+  static __device__ __forceinline__ f4 qk_half(const Regs& R, int u, const uint32_t (&qt)[G::NM][4],
+                                               const uint32_t (&kbl)[2], uint32_t ssc) {
+    uint32_t s2[2], b2[2], n1k[2], n64[2];
+    float sf[2], bf[2];
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      const uint32_t sw = (G::KG == 2 && g == 1) ? (R.ks[u] >> 16) : R.ks[u];
+      const uint32_t bw = (G::KG == 2 && g == 1) ? (kbl[u] >> 16) : kbl[u];
+      s2[g] = splat_lo(sw);
+      sf[g] = to_f32<Tag>(static_cast<uint16_t>(sw));
+      if constexpr (FOLD) {
+        s2[g] = f16x2_mul(s2[g], ssc);
+        n1k[g] = f16x2_mul(s2[g], kNeg1024);
+        n64[g] = f16x2_mul(s2[g], kNeg64);
+      } else {
+        b2[g] = splat_lo(bw);
+        bf[g] = to_f32<Tag>(static_cast<uint16_t>(bw));
+      }
+    }
+    f4 S = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int m = 0; m < G::NM; ++m) {
+      const int g = (G::KG == 2 && m >= G::NM / 2) ? 1 : 0;
+      uint32_t a[4];
+      if constexpr (FOLD) {
+        const uint32_t* w = R.kw[u] + m * G::WPS;
+        if constexpr (BITS == 4) {
+          const uint32_t x = w[0], x8 = w[0] >> 8;
+          a[0] = f16x2_fma(bitop_and_or(x, kNib, kMagic), s2[g], n1k[g]);
+          a[1] = f16x2_fma(bitop_and_or(x, kNib1, kMagic64), s2[g], n64[g]);
+          a[2] = f16x2_fma(bitop_and_or(x8, kNib, kMagic), s2[g], n1k[g]);
+          a[3] = f16x2_fma(bitop_and_or(x8, kNib1, kMagic64), s2[g], n64[g]);
+        } else {
+          a[0] = f16x2_fma(perm(kMagic8, w[0], kSelB01), s2[g], n1k[g]);
+          a[1] = f16x2_fma(perm(kMagic8, w[0], kSelB23), s2[g], n1k[g]);
+          a[2] = f16x2_fma(perm(kMagic8, w[1], kSelB01), s2[g], n1k[g]);
+          a[3] = f16x2_fma(perm(kMagic8, w[1], kSelB23), s2[g], n1k[g]);
+        }
+      } else {
+        dequant_k<Tag, BITS>(R.kw[u] + m * G::WPS, s2[g], b2[g], sf[g], bf[g], a);
+      }
+      S = mfma<Tag>(a, qt[m], S);
+    }
+    return S;
+  }
+
+  // out^T += V^T P^T: MFMA nb takes dim r*NB + nb of the lane's 8 tokens.
+  // sv2 / bv2: V scale / bias pairs of tokens (2i, 2i+1) of the lane's group.
+  // FOLD: the A operand is round(scale * code); the caller adds the bias.
+  template <bool FOLD, typename IV>
+  static __device__ __forceinline__ void pv_f16(Regs& R, const uint32_t (&sv2)[4], const uint32_t (&bv2)[4],
+                                                const uint32_t (&pb)[4], f4 (&acc)[G::NB], IV&& issue_v) {
+    uint32_t c1k[4], c64[4];  // FOLD: -1024 * scale, -64 * scale; else the bias
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (FOLD) {
+        c1k[i] = f16x2_mul(sv2[i], kNeg1024);
+        c64[i] = f16x2_mul(sv2[i], kNeg64);
+      } else {
+        c1k[i] = c64[i] = bv2[i];
+      }
+    }
+    if constexpr (BITS == 4) {
+      // X: nibbles 0-3 of tokens (2i, 2i+1), Y: nibbles 4-7.
+      uint32_t X[4][G::VW], Y[4][G::VW];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int w = 0; w < G::VW; ++w) {
+          X[i][w] = perm(R.vw[2 * i + 1][w], R.vw[2 * i][w], 0x05040100u);
+          Y[i][w] = perm(R.vw[2 * i + 1][w], R.vw[2 * i][w], 0x07060302u);
+        }
+      issue_v(R);
+#pragma unroll
+      for (int nb = 0; nb < G::NB; ++nb) {
+        const int w = nb >> 3, k = nb & 7;
+        uint32_t a[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t src = k < 4 ? X[i][w] : Y[i][w];
+          const uint32_t sh = (k & 3) < 2 ? src : src >> 8;
+          if constexpr (FOLD)
+            a[i] = (k & 1) ? f16x2_fma(bitop_and_or(sh, kNib1, kMagic64), sv2[i], c64[i])
+                           : f16x2_fma(bitop_and_or(sh, kNib, kMagic), sv2[i], c1k[i]);
+          else
+            a[i] = f16x2_fma(nib_codes(src, src >> 8, k & 3), sv2[i], c1k[i]);
+        }
+        acc[nb] = mfma<Tag>(a, pb, acc[nb]);
+      }
+    } else {
+      // Z0: bytes 0-1 of tokens (2i, 2i+1) interleaved, Z1: bytes 2-3.
+      uint32_t Z[4][G::VW][2];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int w = 0; w < G::VW; ++w) {
+          Z[i][w][0] = perm(R.vw[2 * i + 1][w], R.vw[2 * i][w], 0x05010400u);
+          Z[i][w][1] = perm(R.vw[2 * i + 1][w], R.vw[2 * i][w], 0x07030602u);
+        }
+      issue_v(R);
+#pragma unroll
+      for (int nb = 0; nb < G::NB; ++nb) {
+        const int w = nb >> 2, k = nb & 3;
+        uint32_t a[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t t = perm(kMagic8, Z[i][w][k >> 1], (k & 1) ? kSelB23 : kSelB01);
+          a[i] = FOLD ? f16x2_fma(t, sv2[i], c1k[i]) : f16x2_fma(f16x2_sub1024(t), sv2[i], c1k[i]);
+        }
+        acc[nb] = mfma<Tag>(a, pb, acc[nb]);
+      }
+    }
+  }
+
   // One tile: QK, online softmax, PV.
   // The next tile's K loads are issued (issue_k) as soon as this tile's K
   // has been consumed, and its V loads (issue_v) once V is in the PV
   // operands' pre-permuted form, so one register set suffices.
+  // qsB: the K-bias MFMA's B operand (float16).
   template <typename IK, typename IV>
   static __device__ __forceinline__ void compute_tile(Regs& R, const MfmaParams& p, const uint32_t (&qt)[G::NM][4],
-                                                      f4 (&acc)[G::NB], float& mrun, float& lrun, int tb,
-                                                      int n1, int quad, int b, int hq_lane, const VMetaLane& vm,
-                                                      IK&& issue_k, IV&& issue_v) {
+                                                      const uint32_t (&qsB)[2], f4 (&acc)[G::NB], f4& accB,
+                                                      float& mrun, float& lrun, int tb, int n1, int quad, int b,
+                                                      int hq_lane, const VMetaLane& vm, IK&& issue_k,
+                                                      IV&& issue_v) {
     // ---- S^T = K Q^T (Q^T operand m: 16 B per lane, in registers) ----
-    f4 S[2] = {f4{0.0f, 0.0f, 0.0f, 0.0f}, f4{0.0f, 0.0f, 0.0f, 0.0f}};
-    uint32_t s2[2][2], b2[2][2];
-    float sf[2][2], bf[2][2];
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      if constexpr (G::KG == 2) {
-        s2[u][0] = splat_lo(R.ks[u]); s2[u][1] = splat_hi(R.ks[u]);
-        b2[u][0] = splat_lo(R.kb[u]); b2[u][1] = splat_hi(R.kb[u]);
-        sf[u][0] = to_f32<Tag>(static_cast<uint16_t>(R.ks[u]));
-        sf[u][1] = to_f32<Tag>(static_cast<uint16_t>(R.ks[u] >> 16));
-        bf[u][0] = to_f32<Tag>(static_cast<uint16_t>(R.kb[u]));
-        bf[u][1] = to_f32<Tag>(static_cast<uint16_t>(R.kb[u] >> 16));
-      } else {
-        s2[u][0] = s2[u][1] = splat_lo(R.ks[u]);
-        b2[u][0] = b2[u][1] = splat_lo(R.kb[u]);
-        sf[u][0] = sf[u][1] = to_f32<Tag>(static_cast<uint16_t>(R.ks[u]));
-        bf[u][0] = bf[u][1] = to_f32<Tag>(static_cast<uint16_t>(R.kb[u]));
-      }
-    }
-#pragma unroll
-    for (int m = 0; m < G::NM; ++m) {
-      const int gsel = (G::KG == 2 && m >= G::NM / 2) ? 1 : 0;
+    f4 S[2];
+    if constexpr (kFold) {
+      // A tile holding a K scale >= 64 runs with the scales times 2^-11
+      // (exact), and its QK product is multiplied back by 2^11.
+      const bool big = __builtin_amdgcn_ballot_w64((f16x2_ge64(R.ks[0]) | f16x2_ge64(R.ks[1])) != 0u);
+      const uint32_t ssc = big ? kF16x2TwoM11 : kF16x2One;
+      const float back = big ? 2048.0f : 1.0f;
+      const uint32_t none[2] = {0u, 0u};
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
-        uint32_t a[4];
-        dequant_k<Tag, BITS>(R.kw[u] + m * G::WPS, s2[u][gsel], b2[u][gsel], sf[u][gsel], bf[u][gsel], a);
-        S[u] = mfma<Tag>(a, qt[m], S[u]);
+        S[u] = qk_half<true>(R, u, qt, none, ssc);
+        S[u] = mfma16_f16(R.kb[u], qsB, S[u] * back);
       }
+    } else {
+      const uint32_t kbl[2] = {R.kb[0][0], R.kb[1][0]};
+#pragma unroll
+      for (int u = 0; u < 2; ++u) S[u] = qk_half<false>(R, u, qt, kbl, 0u);
     }
     issue_k(R);
 
@@ -261,6 +398,7 @@ struct Kernel {
       lrun *= f;
 #pragma unroll
       for (int i = 0; i < G::NB; ++i) acc[i] *= f;
+      accB *= f;
     }
     float pr[8];
 #pragma unroll
@@ -294,50 +432,22 @@ struct Kernel {
         sv2[i] = perm(dS[2 * i + 1], dS[2 * i], vm.sel);
         bv2[i] = perm(dB[2 * i + 1], dB[2 * i], vm.sel);
       }
-      if constexpr (BITS == 4) {
-        // X: nibbles 0-3 of tokens (2i, 2i+1), Y: nibbles 4-7.
-        uint32_t X[4][G::VW], Y[4][G::VW];
+      // Bias rows of the A operand: row r holds the lane's group (that of
+      // dims r*NB ..), the same for every nb, so one MFMA per tile.
+      accB = mfma<Tag>(bv2, pb, accB);
+      // A tile holding a V scale >= 64 runs with the scales times 2^-11 and
+      // the accumulators scaled down around its products (all exact).
+      const bool big = __builtin_amdgcn_ballot_w64((f16x2_ge64(R.vs[0]) | f16x2_ge64(R.vs[1])) != 0u);
+      if (big) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 4; ++i) sv2[i] = f16x2_mul(sv2[i], kF16x2TwoM11);
 #pragma unroll
-          for (int w = 0; w < G::VW; ++w) {
-            X[i][w] = perm(R.vw[2 * i + 1][w], R.vw[2 * i][w], 0x05040100u);
-            Y[i][w] = perm(R.vw[2 * i + 1][w], R.vw[2 * i][w], 0x07060302u);
-          }
-        issue_v(R);
+        for (int nb = 0; nb < G::NB; ++nb) acc[nb] *= 1.0f / 2048.0f;
+      }
+      pv_f16<true>(R, sv2, bv2, pb, acc, issue_v);
+      if (big) {
 #pragma unroll
-        for (int nb = 0; nb < G::NB; ++nb) {
-          const int w = nb >> 3, k = nb & 7;
-          uint32_t a[4];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const uint32_t src = k < 4 ? X[i][w] : Y[i][w];
-            a[i] = f16x2_fma(nib_codes(src, src >> 8, k & 3), sv2[i], bv2[i]);
-          }
-          acc[nb] = mfma<Tag>(a, pb, acc[nb]);
-        }
-      } else {
-        // Z0: bytes 0-1 of tokens (2i, 2i+1) interleaved, Z1: bytes 2-3.
-        uint32_t Z[4][G::VW][2];
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int w = 0; w < G::VW; ++w) {
-            Z[i][w][0] = perm(R.vw[2 * i + 1][w], R.vw[2 * i][w], 0x05010400u);
-            Z[i][w][1] = perm(R.vw[2 * i + 1][w], R.vw[2 * i][w], 0x07030602u);
-          }
-        issue_v(R);
-#pragma unroll
-        for (int nb = 0; nb < G::NB; ++nb) {
-          const int w = nb >> 2, k = nb & 3;
-          uint32_t a[4];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const uint32_t t = perm(kMagic8, Z[i][w][k >> 1], (k & 1) ? kSelB23 : kSelB01);
-            a[i] = f16x2_fma(f16x2_sub1024(t), sv2[i], bv2[i]);
-          }
-          acc[nb] = mfma<Tag>(a, pb, acc[nb]);
-        }
+        for (int nb = 0; nb < G::NB; ++nb) acc[nb] *= 2048.0f;
       }
     } else {
       float svf[8], bvf[8];
@@ -386,12 +496,14 @@ struct Kernel {
 };
 
 template <typename Tag, int D, int BITS, int GS>
-__global__ __launch_bounds__(kThreads) void decode_mfma_kernel(MfmaParams p) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_mfma_kernel(MfmaParams p) {
   using G = Geo<D, BITS, GS>;
   using K = Kernel<Tag, D, BITS, GS>;
   constexpr int kRowF = D + 4;  // LDS floats per (wave, head) row
   __shared__ __attribute__((aligned(16))) float s_acc[kWaves * 16 * kRowF];
   __shared__ float s_ml[kWaves][16][2];
+  constexpr int kQRow = D * 2 + 16;  // bytes per staged Q row
+  __shared__ __attribute__((aligned(16))) uint8_t s_q[16 * kQRow];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -466,7 +578,9 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(MfmaParams p) {
   LaneOffsets L;
   L.k_r = quad * G::KW * 4 + r * rs.k_sn;
   L.ks_r = kg0 * 2 + r * rs.ks_sn;
-  L.kb_r = kg0 * 2 + r * rs.kb_sn;
+  // float16: the row piece of groups 4 * (quad & 1) .. (K-bias MFMA A
+  // operand); bfloat16: the lane's own groups, as the scales.
+  L.kb_r = (K::kFold ? (G::NG == 8 ? 8 * (quad & 1) : 0) : kg0 * 2) + r * rs.kb_sn;
   L.v_r = r * G::VW * 4 + 4 * quad * rs.v_sn;
   L.vs_r = vword * 4 + r * rs.vs_sn;
   L.vb_r = vword * 4 + r * rs.vb_sn;
@@ -482,28 +596,39 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(MfmaParams p) {
     vm.shift = half ? 0u : 16u;
   }
 
-  // Q^T B operands, one 16-byte piece per lane and QK step m: head r, dims
-  // quad*QD + 8m + perm8(j), zero for padding heads.  Every wave loads its
-  // own copy (Q is a few KB and stays in L2), ahead of its first tile, so no
-  // wave waits for another before streaming.
-  uint32_t qt[G::NM][4];
-  {
-    const uint16_t* qp = p.q + static_cast<int64_t>(b) * p.q_sb + static_cast<int64_t>(hq_lane) * p.q_sh +
-                         quad * G::QD;
-#pragma unroll
-    for (int m = 0; m < G::NM; ++m) {
-      const uint32_t* q32 = reinterpret_cast<const uint32_t*>(qp + 8 * m);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) qt[m][i] = q32[i];
-    }
+  // The block's Q rows (16 heads x D, zero rows for padding heads) are read
+  // once per workgroup, one 16-byte piece per thread, and staged in LDS
+  // (rows padded by 16 bytes so the per-lane row reads below are
+  // conflict-free).
+  constexpr int kQChunks = D / 8;  // 16-byte pieces per row
+  const int qh = threadIdx.x / kQChunks, qc = threadIdx.x % kQChunks;
+  u4 qv = u4{0u, 0u, 0u, 0u};
+  if (qh < 16) {
+    const uint8_t* q0 = reinterpret_cast<const uint8_t*>(p.q) +
+                        (static_cast<int64_t>(b) * p.q_sb + static_cast<int64_t>(h0) * p.q_sh) * 2;
+    const rsrc_t rq = make_rsrc(q0, static_cast<uint32_t>((nh - 1) * p.q_sh * 2 + D * 2));
+    qv = __builtin_amdgcn_raw_buffer_load_b128(rq, static_cast<uint32_t>(min(qh, nh - 1) * p.q_sh * 2 + qc * 16), 0,
+                                               0);
   }
-  __builtin_amdgcn_sched_barrier(0);
+  // Q is staged before any K / V load is issued: issued together, the
+  // grid's first tiles (20 MB at C3) would queue in front of it.
+  if (qh < 16) *reinterpret_cast<u4*>(s_q + qh * kQRow + qc * 16) = qh < nh ? qv : u4{0u, 0u, 0u, 0u};
+  __syncthreads();
   typename K::Regs R;
   int j = wave;
   K::load_k(R, rs, L, row_of(j));
   __builtin_amdgcn_sched_barrier(0);
   K::load_v(R, rs, L, row_of(j));
   __builtin_amdgcn_sched_barrier(0);
+
+  // Q^T B operands, one 16-byte piece per lane and QK step m: head r, dims
+  // quad*QD + 8m + perm8(j).
+  uint32_t qt[G::NM][4];
+#pragma unroll
+  for (int m = 0; m < G::NM; ++m) {
+    const u4 v = *reinterpret_cast<const u4*>(s_q + r * kQRow + (quad * G::QD + 8 * m) * 2);
+    qt[m][0] = v[0]; qt[m][1] = v[1]; qt[m][2] = v[2]; qt[m][3] = v[3];
+  }
 #pragma unroll
   for (int m = 0; m < G::NM; ++m) {
     const uint32_t d0 = qt[m][0], d1 = qt[m][1], d2 = qt[m][2], d3 = qt[m][3];
@@ -513,12 +638,48 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(MfmaParams p) {
       qt[m][2] = perm(d3, d1, 0x05040100u);  // dims 2, 6
       qt[m][3] = perm(d3, d1, 0x07060302u);  // dims 3, 7
     }
-    if (r >= nh) qt[m][0] = qt[m][1] = qt[m][2] = qt[m][3] = 0u;
+  }
+
+  // float16: B operand of the K-bias MFMA.  k slots 4*quad + i hold, for
+  // head r, the sum of Q over group 4 * (quad & 1) + i (zero past NG), as
+  // its float16 value (quads 0, 1) or the float16 residual (quads 2, 3).
+  uint32_t qsB[2] = {0u, 0u};
+  if constexpr (K::kFold) {
+    float part[G::NG];
+#pragma unroll
+    for (int g = 0; g < G::NG; ++g) part[g] = 0.0f;
+#pragma unroll
+    for (int m = 0; m < G::NM; ++m) {
+      float t = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) t += unpack_T2_lo<Tag>(qt[m][i]) + unpack_T2_hi<Tag>(qt[m][i]);
+      const int g = (quad * G::QD + 8 * m) / GS;  // dims of slice m lie in one group
+#pragma unroll
+      for (int gg = 0; gg < G::NG; ++gg) part[gg] += gg == g ? t : 0.0f;
+    }
+    float sel[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sel[i] = 0.0f;
+#pragma unroll
+    for (int g = 0; g < G::NG; ++g) {
+      float tot = part[g] + shfl_xor_f32(part[g], 16);
+      tot += shfl_xor_f32(tot, 32);
+      if ((g >> 2) == (quad & 1)) sel[g & 3] = tot;
+    }
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float hi = static_cast<float>(static_cast<_Float16>(sel[i]));
+      v[i] = quad < 2 ? hi : sel[i] - hi;
+    }
+    qsB[0] = pack_T2<Tag>(v[0], v[1]);
+    qsB[1] = pack_T2<Tag>(v[2], v[3]);
   }
 
   f4 acc[G::NB];
 #pragma unroll
   for (int i = 0; i < G::NB; ++i) acc[i] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  f4 accB = f4{0.0f, 0.0f, 0.0f, 0.0f};  // float16: the V bias rows
   float mrun = kNegBig;
   float lrun = 0.0f;
 
@@ -527,8 +688,12 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(MfmaParams p) {
     const int nrow = row_of(nj);
     auto ik = [&](typename K::Regs& X) { K::load_k(X, rs, L, nrow); };
     auto iv = [&](typename K::Regs& X) { K::load_v(X, rs, L, nrow); };
-    K::compute_tile(R, p, qt, acc, mrun, lrun, s0 + row_of(j), p.N, quad, b, hq_lane, vm, ik, iv);
+    K::compute_tile(R, p, qt, qsB, acc, accB, mrun, lrun, s0 + row_of(j), p.N, quad, b, hq_lane, vm, ik, iv);
     j = nj;
+  }
+  if constexpr (K::kFold) {
+#pragma unroll
+    for (int i = 0; i < G::NB; ++i) acc[i] += accB;
   }
 
   // ---- per-head totals over the four quads ----

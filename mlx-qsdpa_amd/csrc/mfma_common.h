@@ -21,6 +21,8 @@ constexpr float kRescale = 8.0f;
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef __bf16 b8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 
 struct MfmaParams {
   int B, Hq, Hkv, N, G, hb_count, num_splits;
@@ -149,6 +151,26 @@ __device__ __forceinline__ f4 mfma(const uint32_t a[4], const uint32_t b[4], f4 
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(b8, av), __builtin_bit_cast(b8, bv), c,
                                                    0, 0, 0);
 }
+
+// 16x16x16 f16 MFMA (k = 4 values per lane): the bias products.
+__device__ __forceinline__ f4 mfma16_f16(const uint32_t a[2], const uint32_t b[2], f4 c) {
+  const uint2 av = {a[0], a[1]};
+  const uint2 bv = {b[0], b[1]};
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(h4, av), __builtin_bit_cast(h4, bv), c, 0, 0, 0);
+}
+
+// Nonzero when some 16-bit half of the float16 pair x has |value| >= 64 (or
+// is inf / NaN): adding 0x2C00 to a magnitude >= 0x5400 sets bit 15.
+__device__ __forceinline__ uint32_t f16x2_ge64(uint32_t x) {
+  return ((x & 0x7FFF7FFFu) + 0x2C002C00u) & 0x80008000u;
+}
+__device__ __forceinline__ uint32_t f16x2_mul(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, a) * __builtin_bit_cast(f16x2, b));
+}
+constexpr uint32_t kNeg1024 = 0xE400E400u;  // -1024.0 in both halves
+constexpr uint32_t kNeg64 = 0xD400D400u;    // -64.0 in both halves
+constexpr uint32_t kF16x2One = 0x3C003C00u;     // 1.0 in both halves
+constexpr uint32_t kF16x2TwoM11 = 0x10001000u;  // 2^-11 in both halves
 
 __device__ __forceinline__ float mask_value(const MfmaParams& p, int64_t o) {
   switch (p.mask_kind) {
