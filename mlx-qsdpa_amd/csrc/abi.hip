@@ -36,7 +36,7 @@ int valu_heads_per_block(int G);
 int launch_decode_valu(const qsdpa_decode_args* a, int num_splits, float* part_acc, float* part_ml,
                        hipStream_t stream);
 int launch_merge(const qsdpa_decode_args* a, int num_splits, const float* part_acc,
-                 const float* part_ml, hipStream_t stream);
+                 const float* part_ml, bool half_parts, hipStream_t stream);
 bool mfma_supports(const qsdpa_decode_args* a);
 int mfma_num_splits(const qsdpa_decode_args* a, int cus);
 int launch_decode_mfma(const qsdpa_decode_args* a, int num_splits, float* part_acc, float* part_ml,
@@ -185,10 +185,13 @@ int qsdpa_decode(const qsdpa_decode_args* args, void* stream) {
   }
   const hipStream_t s = static_cast<hipStream_t>(stream);
   // (prof_begin / prof_end ride on the main kernel's own dispatch)
-  if (mfma_supports(args)) rc = launch_decode_mfma(args, splits, part_acc, part_ml, s);
+  const bool mfma = mfma_supports(args);
+  if (mfma) rc = launch_decode_mfma(args, splits, part_acc, part_ml, s);
   else rc = launch_decode_valu(args, splits, part_acc, part_ml, s);
   if (rc) return rc;
-  if (splits > 1) rc = launch_merge(args, splits, part_acc, part_ml, s);
+  // The MFMA kernel stores float16 inputs' partials as normalised float16
+  // rows (in the first half of the float32 area).
+  if (splits > 1) rc = launch_merge(args, splits, part_acc, part_ml, mfma && args->dtype == QSDPA_F16, s);
   return rc;
 }
 

@@ -51,9 +51,6 @@
 
 namespace qsdpa {
 
-int launch_merge(const qsdpa_decode_args* a, int num_splits, const float* part_acc,
-                 const float* part_ml, hipStream_t stream);
-
 namespace {
 
 template <int WORDS>
@@ -756,10 +753,20 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       }
     } else {
       const int64_t slot = (static_cast<int64_t>(b) * p.Hq + hh) * p.num_splits + split;
-      float* dst = p.part_acc + slot * D + d;
       // Streaming stores: the partials are read once, by the merge kernel.
-      __builtin_nontemporal_store(f4{v[0], v[1], v[2], v[3]}, reinterpret_cast<f4*>(dst));
-      __builtin_nontemporal_store(f4{v[4], v[5], v[6], v[7]}, reinterpret_cast<f4*>(dst + 4));
+      if constexpr (Tag::kId == QSDPA_F16) {
+        // float16 rows of the split's normalised output (acc / L, within
+        // the range of V), so the partials are half the bytes.
+        const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+        uint16_t* dst = reinterpret_cast<uint16_t*>(p.part_acc) + slot * D + d;
+        __builtin_nontemporal_store(u4{pack_T2<Tag>(v[0] * inv, v[1] * inv), pack_T2<Tag>(v[2] * inv, v[3] * inv),
+                                       pack_T2<Tag>(v[4] * inv, v[5] * inv), pack_T2<Tag>(v[6] * inv, v[7] * inv)},
+                                    reinterpret_cast<u4*>(dst));
+      } else {
+        float* dst = p.part_acc + slot * D + d;
+        __builtin_nontemporal_store(f4{v[0], v[1], v[2], v[3]}, reinterpret_cast<f4*>(dst));
+        __builtin_nontemporal_store(f4{v[4], v[5], v[6], v[7]}, reinterpret_cast<f4*>(dst + 4));
+      }
       if (d == 0) {
         p.part_ml[slot * 2] = Mh;
         p.part_ml[slot * 2 + 1] = L;

@@ -26,7 +26,10 @@ constexpr int kGroups = 32;  // split groups per block
 constexpr int kPer = 4;      // splits per thread per round
 constexpr float kNegBig = -1.0e30f;
 
-template <typename Tag>
+// HALF: the partial rows are float16 and normalised (acc / l), as the MFMA
+// decode stores them for float16 inputs; the weight of split s is then
+// l_s * exp2(m_s - M) for its row as well as for the sum.
+template <typename Tag, bool HALF>
 __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ part_acc,
                                                     const float* __restrict__ part_ml, int D,
                                                     int splits, int Hq, uint16_t* __restrict__ out,
@@ -39,6 +42,7 @@ __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ pa
   const int d = blockIdx.y * 32 + 4 * q;
   const float2* ml = reinterpret_cast<const float2*>(part_ml) + static_cast<int64_t>(bh) * splits;
   const float* pa = part_acc + static_cast<int64_t>(bh) * splits * D + d;
+  const uint16_t* ph = reinterpret_cast<const uint16_t*>(part_acc) + static_cast<int64_t>(bh) * splits * D + d;
 
   float m = kNegBig, l = 0.0f;
   float4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -49,7 +53,13 @@ __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ pa
     for (int k = 0; k < kPer; ++k) {
       const int s = s0 + g + kGroups * k;
       const bool ok = s < splits;
-      x[k] = ok ? *reinterpret_cast<const float4*>(pa + static_cast<int64_t>(s) * D) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+      if constexpr (HALF) {
+        const uint2 hv = ok ? *reinterpret_cast<const uint2*>(ph + static_cast<int64_t>(s) * D) : uint2{0u, 0u};
+        x[k] = float4{f16_bits_to_f32(static_cast<uint16_t>(hv.x)), f16_bits_to_f32(static_cast<uint16_t>(hv.x >> 16)),
+                      f16_bits_to_f32(static_cast<uint16_t>(hv.y)), f16_bits_to_f32(static_cast<uint16_t>(hv.y >> 16))};
+      } else {
+        x[k] = ok ? *reinterpret_cast<const float4*>(pa + static_cast<int64_t>(s) * D) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+      }
       w[k] = ok ? ml[s] : float2{kNegBig, 0.0f};
     }
     float mr = m;
@@ -62,8 +72,9 @@ __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ pa
     for (int k = 0; k < kPer; ++k) {
       const float e = fast_exp2(w[k].x - mr);
       l = fmaf(w[k].y, e, l);
-      acc.x = fmaf(x[k].x, e, acc.x); acc.y = fmaf(x[k].y, e, acc.y);
-      acc.z = fmaf(x[k].z, e, acc.z); acc.w = fmaf(x[k].w, e, acc.w);
+      const float ex = HALF ? w[k].y * e : e;  // weight of the row
+      acc.x = fmaf(x[k].x, ex, acc.x); acc.y = fmaf(x[k].y, ex, acc.y);
+      acc.z = fmaf(x[k].z, ex, acc.z); acc.w = fmaf(x[k].w, ex, acc.w);
     }
     m = mr;
   }
@@ -106,17 +117,20 @@ __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ pa
 }  // namespace
 
 int launch_merge(const qsdpa_decode_args* a, int num_splits, const float* part_acc,
-                 const float* part_ml, hipStream_t stream) {
+                 const float* part_ml, bool half_parts, hipStream_t stream) {
   if (num_splits > kMaxSplits)
     return fail(QSDPA_ERR_INVALID, "merge: %d splits exceed %d", num_splits, kMaxSplits);
   uint16_t* out = static_cast<uint16_t*>(const_cast<void*>(a->out.ptr));
   const dim3 grid(a->B * a->H_q, a->D / 32);
-  if (a->dtype == QSDPA_F16)
-    merge_kernel<F16><<<grid, dim3(256), 0, stream>>>(part_acc, part_ml, a->D, num_splits, a->H_q,
-                                                      out, a->out.stride_b, a->out.stride_h);
+  if (a->dtype == QSDPA_F16 && half_parts)
+    merge_kernel<F16, true><<<grid, dim3(256), 0, stream>>>(part_acc, part_ml, a->D, num_splits, a->H_q,
+                                                            out, a->out.stride_b, a->out.stride_h);
+  else if (a->dtype == QSDPA_F16)
+    merge_kernel<F16, false><<<grid, dim3(256), 0, stream>>>(part_acc, part_ml, a->D, num_splits, a->H_q,
+                                                             out, a->out.stride_b, a->out.stride_h);
   else
-    merge_kernel<BF16><<<grid, dim3(256), 0, stream>>>(part_acc, part_ml, a->D, num_splits, a->H_q,
-                                                       out, a->out.stride_b, a->out.stride_h);
+    merge_kernel<BF16, false><<<grid, dim3(256), 0, stream>>>(part_acc, part_ml, a->D, num_splits, a->H_q,
+                                                              out, a->out.stride_b, a->out.stride_h);
   return check_launch("merge");
 }
 
