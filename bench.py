@@ -63,7 +63,7 @@ def parse_args(argv=None):
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=300)
     ap.add_argument("--warmup", type=int, default=30)
-    ap.add_argument("--config", default="c3", choices=sorted(CONFIGS))
+    ap.add_argument("--config", default="c3", choices=sorted(CONFIGS) + ["c4"])
     ap.add_argument("--n", type=int, default=None, help="override the key count N")
     ap.add_argument("--kv-bytes", type=float, default=1.2e9,
                     help="distinct KV bytes cycled through (defeats the MALL)")
@@ -183,12 +183,130 @@ def cpu_baseline(cfg, N, host_set, budget_s):
                        f"(oracle.attention.decode_fp32), median")}
 
 
+# continuous-batching decode through the batch cache's
+# layout -- B sequences left-padded to the longest, each step appends one
+# token per sequence (quantize-on-append into the shared column) and then
+# decodes with kv_start = the left padding, so padded slots are never read.
+C4 = {"B": 16, "H_q": 32, "H_kv": 8, "D": 128, "bits": 4, "group_size": 64, "dtype": "f16",
+      "len_lo": 1024, "len_hi": 32768}
+
+
+def run_c4(args) -> int:
+    import numpy as np
+    import torch
+
+    from mlx_qsdpa_amd import _lib, kernels, metric
+
+    c = C4
+    B, Hq, Hkv, D, bits, gs = c["B"], c["H_q"], c["H_kv"], c["D"], c["bits"], c["group_size"]
+    device = torch.device("cuda:0")
+    T = torch.float16
+    gen = torch.Generator(device="cpu")
+    gen.manual_seed(args.seed)
+    lengths = torch.randint(c["len_lo"], c["len_hi"] + 1, (B,), generator=gen)
+    lmax = int(lengths.max())
+    total = args.warmup + 2 * args.steps
+    cap = lmax + total
+    W, G = D * bits // 32, D // gs
+    bufs = []
+    for _ in range(2):  # K, V
+        bufs.append((torch.empty((B, Hkv, cap, W), dtype=torch.uint32, device=device),
+                     torch.empty((B, Hkv, cap, G), dtype=T, device=device),
+                     torch.empty((B, Hkv, cap, G), dtype=T, device=device)))
+    g = torch.Generator(device=device)
+    g.manual_seed(args.seed)
+    chunk = 4096
+    for t0 in range(0, lmax, chunk):  # synthetic prompt (the padded slots' content is never read)
+        n = min(chunk, lmax - t0)
+        for kv in bufs:
+            w = torch.randn((B, Hkv, n, D), generator=g, device=device, dtype=torch.float32).to(T)
+            kernels.quantize_into(w, kv, t0, bits, gs)
+    q = torch.randn((B, Hq, 1, D), generator=g, device=device, dtype=torch.float32).to(T)
+    new = [torch.randn((B, Hkv, 1, D), generator=g, device=device, dtype=torch.float32).to(T) for _ in range(2)]
+    kv_start = (lmax - lengths).to(device=device, dtype=torch.int32)
+    torch.cuda.synchronize()
+
+    # Launch arguments built once: each step only moves the append column
+    # and the decode's key count (the caches grow in place).
+    lib = _lib.load()
+    qargs = [_lib.QuantizeArgs(B, Hkv, 1, D, bits, gs, kernels.dtype_code(T), 0, kernels._view(x),
+                               kernels._view(kv[0]), kernels._view(kv[1]), kernels._view(kv[2]))
+             for kv, x in zip(bufs, new)]
+    qrefs = [ctypes.byref(a) for a in qargs]
+    v0 = [t[:, :, :lmax + 1] for kv in bufs for t in kv]  # the split count is chosen for the first step
+    plan = kernels.DecodePlan(q, v0[0], v0[3], v0[1], v0[4], v0[2], v0[5], scale=D ** -0.5, bits=bits,
+                              group_size=gs, kv_start=kv_start, num_splits=args.splits, capacity=cap)
+    splits = plan.num_splits
+    stream = torch.cuda.current_stream(device).cuda_stream
+
+    def step(n, ev=None):
+        for a, ref in zip(qargs, qrefs):
+            a.t0 = n
+            _lib.check(lib.qsdpa_quantize(ref, stream))
+        plan.set_keys(n + 1)
+        plan(ev)
+
+    n = lmax
+    for _ in range(args.warmup):
+        step(n)
+        n += 1
+    torch.cuda.synchronize()
+    n_first = n
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step(n)
+        n += 1
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    hip = HipEvents()
+    ev_b, ev_e = hip.create(args.steps), hip.create(args.steps)
+    n2 = n
+    for i in range(args.steps):
+        step(n, (ev_b[i], ev_e[i]))
+        n += 1
+    torch.cuda.synchronize()
+    kern_us = float(np.mean([hip.elapsed_ms(ev_b[i], ev_e[i]) for i in range(args.steps)])) * 1e3
+    hip.destroy(ev_b + ev_e)
+
+    us_step = wall / args.steps * 1e6
+    valid = lambda n_: int((lengths + (n_ + 1 - lmax)).sum())  # noqa: E731 (keys per sequence after the append)
+    bytes_wall = np.mean([metric.decode_bytes(B, Hq, Hkv, D, bits, gs, valid(k))
+                          for k in range(n_first, n_first + args.steps)])
+    bytes_kern = np.mean([metric.decode_bytes(B, Hq, Hkv, D, bits, gs, valid(k))
+                          for k in range(n2, n2 + args.steps)])
+    step_gbps = bytes_wall / (us_step * 1e-6) / 1e9
+    kern_gbps = bytes_kern / (kern_us * 1e-6) / 1e9
+    print(f"bench: c4 {us_step:.2f} us/step wall (append + decode), decode kernel {kern_us:.2f} us "
+          f"({kern_gbps:.0f} GB/s), splits={splits}", file=sys.stderr, flush=True)
+    workload = (f"c4: batched decode B={B} H_q={Hq} H_kv={Hkv} D={D} {bits}-bit gs={gs} f16, lengths "
+                f"U[{c['len_lo']},{c['len_hi']}] left-padded, append + decode per step")
+    line = {
+        "metric": "µs/decode step (append + decode) + effective HBM GB/s (% peak), C4 batched",
+        "value": round(us_step, 3), "unit": "us/step", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(us_step / 1e3, 6), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f16", "data": "synthetic",
+        "config": {"workload": workload, "B": B, "H_q": Hq, "H_kv": Hkv, "D": D, "bits": bits,
+                   "group_size": gs, "mean_valid_keys": round(bytes_wall / metric.kv_bytes_per_token(Hkv, D, bits, gs) / B, 1),
+                   "num_splits": splits},
+        "effective_gbps": round(step_gbps, 1),
+        "pct_hbm_peak": round(100.0 * step_gbps / HBM_PEAK_GBPS, 2),
+        "roofline": {"bound": "hbm", "achieved": round(kern_gbps, 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(kern_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "kernel_us": round(kern_us, 3), "algorithmic_bytes": int(bytes_kern)},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main(argv=None) -> int:
     args = parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the decode path is "
               "single-GPU in this build, see DESIGN.md for how it would shard.", file=sys.stderr)
         return 2
+    if args.config == "c4":
+        return run_c4(args)
     import numpy as np
     import torch
 

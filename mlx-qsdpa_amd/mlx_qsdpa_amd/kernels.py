@@ -219,7 +219,7 @@ class DecodePlan:
     """
 
     def __init__(self, q, pk, pv, ks, vs, kb, vb, *, scale, bits, group_size, mask=None,
-                 kv_start=None, num_splits=0):
+                 kv_start=None, num_splits=0, capacity=None):
         _require_device(q, pk, pv, ks, vs, kb, vb, mask, kv_start)
         self.q = _inner_contig(q)
         self.out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
@@ -240,6 +240,17 @@ class DecodePlan:
             self.args.workspace_bytes = ws
         self._args_ref = ctypes.byref(self.args)
         self.device = q.device
+        # Rows set_keys may reach: the views' own length unless the caller
+        # states how many rows the underlying buffers hold.
+        self.capacity = int(capacity) if capacity is not None else int(pk.shape[2])
+        self.args.num_splits = self.num_splits  # fixed from here on (set_keys)
+
+    def set_keys(self, n: int) -> None:
+        """Re-target the plan to the first n keys of the same buffers (a cache
+        that grew in place); the split count chosen at construction is kept."""
+        if not 1 <= n <= self.capacity:
+            raise ValueError(f"n={n} outside [1, {self.capacity}]")
+        self.args.N = int(n)
 
     def __call__(self, prof_events=None):
         if prof_events is not None:
