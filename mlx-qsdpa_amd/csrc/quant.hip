@@ -27,11 +27,14 @@ struct QuantParams {
   int64_t z_sb, z_sh, z_sn;
 };
 
-template <typename Tag, int BITS>
+// The group's GS values are read once, all loads issued together (16-byte
+// pieces when VEC, i.e. the rows are 16-byte aligned), and kept in
+// registers for both passes.
+template <typename Tag, int BITS, int GS, bool VEC>
 __global__ __launch_bounds__(256) void quantize_kernel(QuantParams p) {
   constexpr int PER = 32 / BITS;
   constexpr float kBins = static_cast<float>((1 << BITS) - 1);
-  const int ng = p.D / p.gs;
+  const int ng = p.D / GS;
   const int64_t total = static_cast<int64_t>(p.B) * p.H * p.S * ng;
   const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (gid >= total) return;
@@ -42,11 +45,28 @@ __global__ __launch_bounds__(256) void quantize_kernel(QuantParams p) {
   const int h = static_cast<int>(row % p.H);
   const int b = static_cast<int>(row / p.H);
 
-  const uint16_t* src = p.src + off3(b, h, s, p.s_sb, p.s_sh, p.s_sn) + g * p.gs;
+  const uint16_t* src = p.src + off3(b, h, s, p.s_sb, p.s_sh, p.s_sn) + g * GS;
+  uint16_t raw[GS];
+  if constexpr (VEC) {
+#pragma unroll
+    for (int i = 0; i < GS / 8; ++i) {
+      const uint4 v = reinterpret_cast<const uint4*>(src)[i];
+      const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        raw[8 * i + 2 * k] = static_cast<uint16_t>(wv[k]);
+        raw[8 * i + 2 * k + 1] = static_cast<uint16_t>(wv[k] >> 16);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < GS; ++i) raw[i] = src[i];
+  }
 
   float w_min = __builtin_huge_valf(), w_max = -__builtin_huge_valf();
-  for (int i = 0; i < p.gs; ++i) {
-    const float v = to_f32<Tag>(src[i]);
+#pragma unroll
+  for (int i = 0; i < GS; ++i) {
+    const float v = to_f32<Tag>(raw[i]);
     w_min = fminf(w_min, v);
     w_max = fmaxf(w_max, v);
   }
@@ -60,12 +80,13 @@ __global__ __launch_bounds__(256) void quantize_kernel(QuantParams p) {
   const float bias = nz ? edge : 0.0f;
 
   const int t = p.t0 + s;
-  uint32_t* dst = p.dp + off3(b, h, t, p.p_sb, p.p_sh, p.p_sn) + (g * p.gs) / PER;
-  for (int w = 0; w < p.gs / PER; ++w) {
+  uint32_t* dst = p.dp + off3(b, h, t, p.p_sb, p.p_sh, p.p_sn) + (g * GS) / PER;
+#pragma unroll
+  for (int w = 0; w < GS / PER; ++w) {
     uint32_t word = 0;
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
-      const float v = to_f32<Tag>(src[w * PER + j]);
+      const float v = to_f32<Tag>(raw[w * PER + j]);
       float q = rintf(__fdiv_rn(__fsub_rn(v, bias), scale));
       q = fminf(fmaxf(q, 0.0f), kBins);
       word |= static_cast<uint32_t>(q) << (j * BITS);
@@ -74,6 +95,19 @@ __global__ __launch_bounds__(256) void quantize_kernel(QuantParams p) {
   }
   p.ds[off3(b, h, t, p.c_sb, p.c_sh, p.c_sn) + g] = from_f32<Tag>(scale);
   p.db[off3(b, h, t, p.z_sb, p.z_sh, p.z_sn) + g] = from_f32<Tag>(bias);
+}
+
+template <typename Tag, int BITS, int GS>
+void launch_quantize_gs(const QuantParams& p, bool vec, dim3 grid, hipStream_t stream) {
+  if (vec) quantize_kernel<Tag, BITS, GS, true><<<grid, dim3(256), 0, stream>>>(p);
+  else quantize_kernel<Tag, BITS, GS, false><<<grid, dim3(256), 0, stream>>>(p);
+}
+
+template <typename Tag, int BITS>
+void launch_quantize_bits(const QuantParams& p, bool vec, dim3 grid, hipStream_t stream) {
+  if (p.gs == 32) launch_quantize_gs<Tag, BITS, 32>(p, vec, grid, stream);
+  else if (p.gs == 64) launch_quantize_gs<Tag, BITS, 64>(p, vec, grid, stream);
+  else launch_quantize_gs<Tag, BITS, 128>(p, vec, grid, stream);
 }
 
 struct DequantParams {
@@ -131,14 +165,17 @@ int launch_quantize(const qsdpa_quantize_args* a, hipStream_t stream) {
   p.z_sb = a->dst_biases.stride_b; p.z_sh = a->dst_biases.stride_h; p.z_sn = a->dst_biases.stride_n;
   const int64_t total = static_cast<int64_t>(a->B) * a->H * a->S * (a->D / a->group_size);
   if (total == 0) return QSDPA_OK;
-  const dim3 block(256);
   const dim3 grid(static_cast<unsigned>((total + 255) / 256));
+  // 16-byte group loads need 16-byte aligned rows (group offsets are
+  // multiples of 32 elements).
+  const bool vec = aligned(a->src.ptr, 16) && a->src.stride_b % 8 == 0 && a->src.stride_h % 8 == 0 &&
+                   a->src.stride_n % 8 == 0;
   if (a->dtype == QSDPA_F16) {
-    if (a->bits == 4) quantize_kernel<F16, 4><<<grid, block, 0, stream>>>(p);
-    else quantize_kernel<F16, 8><<<grid, block, 0, stream>>>(p);
+    if (a->bits == 4) launch_quantize_bits<F16, 4>(p, vec, grid, stream);
+    else launch_quantize_bits<F16, 8>(p, vec, grid, stream);
   } else {
-    if (a->bits == 4) quantize_kernel<BF16, 4><<<grid, block, 0, stream>>>(p);
-    else quantize_kernel<BF16, 8><<<grid, block, 0, stream>>>(p);
+    if (a->bits == 4) launch_quantize_bits<BF16, 4>(p, vec, grid, stream);
+    else launch_quantize_bits<BF16, 8>(p, vec, grid, stream);
   }
   return check_launch("quantize");
 }
