@@ -10,6 +10,7 @@
 #include <mutex>
 
 #include "abi_internal.h"
+#include "common.h"
 
 namespace qsdpa {
 
@@ -36,11 +37,11 @@ int valu_heads_per_block(int G);
 int launch_decode_valu(const qsdpa_decode_args* a, int num_splits, float* part_acc, float* part_ml,
                        hipStream_t stream);
 int launch_merge(const qsdpa_decode_args* a, int num_splits, const float* part_acc,
-                 const float* part_ml, bool half_parts, hipStream_t stream);
+                 const float* part_ml, bool half_parts, const int* sched, int units, hipStream_t stream);
 bool mfma_supports(const qsdpa_decode_args* a);
 int mfma_num_splits(const qsdpa_decode_args* a, int cus);
 int launch_decode_mfma(const qsdpa_decode_args* a, int num_splits, float* part_acc, float* part_ml,
-                       hipStream_t stream);
+                       int units, int* sched, hipStream_t stream);
 
 
 namespace {
@@ -138,9 +139,22 @@ int decode_plan(const qsdpa_decode_args* a, int* num_splits, int64_t* workspace_
   }
   splits = std::min(splits, std::max(1, a->N));
   *num_splits = splits;
+  // Partials (B * H_q * splits rows of D + 2 floats), then the balanced
+  // schedule's (first unit, units) pair per sequence.
   *workspace_bytes =
-      splits > 1 ? static_cast<int64_t>(a->B) * a->H_q * splits * (a->D + 2) * 4 + 256 : 0;
+      splits > 1 ? static_cast<int64_t>(a->B) * a->H_q * splits * (a->D + 2) * 4 + 8LL * a->B + 256 : 0;
   return QSDPA_OK;
+}
+
+// A left-padded batch on the MFMA path shares splits * B units out over its
+// sequences in proportion to their lengths (the balanced schedule of
+// common.h) instead of giving every sequence `splits`; 0 = uniform splits.
+int ragged_units(const qsdpa_decode_args* a, int splits) {
+  if (!a->kv_start || a->B < 2 || splits < 2 || !mfma_supports(a)) return 0;
+  const int64_t units = static_cast<int64_t>(splits) * a->B;
+  if (units >= (int64_t(1) << 31) / 2) return 0;
+  if (static_cast<int64_t>(a->B) * (a->N / kSchedTile + 1) >= (int64_t(1) << 31)) return 0;
+  return static_cast<int>(units);
 }
 
 }  // namespace qsdpa
@@ -183,15 +197,20 @@ int qsdpa_decode(const qsdpa_decode_args* args, void* stream) {
     part_acc = static_cast<float*>(args->workspace);
     part_ml = part_acc + static_cast<int64_t>(args->B) * args->H_q * splits * args->D;
   }
+  int* sched = part_ml ? reinterpret_cast<int*>(part_ml + static_cast<int64_t>(args->B) * args->H_q * splits * 2)
+                       : nullptr;
   const hipStream_t s = static_cast<hipStream_t>(stream);
   // (prof_begin / prof_end ride on the main kernel's own dispatch)
   const bool mfma = mfma_supports(args);
-  if (mfma) rc = launch_decode_mfma(args, splits, part_acc, part_ml, s);
+  const int units = ragged_units(args, splits);
+  if (mfma) rc = launch_decode_mfma(args, splits, part_acc, part_ml, units, sched, s);
   else rc = launch_decode_valu(args, splits, part_acc, part_ml, s);
   if (rc) return rc;
   // The MFMA kernel stores float16 inputs' partials as normalised float16
   // rows (in the first half of the float32 area).
-  if (splits > 1) rc = launch_merge(args, splits, part_acc, part_ml, mfma && args->dtype == QSDPA_F16, s);
+  if (splits > 1)
+    rc = launch_merge(args, splits, part_acc, part_ml, mfma && args->dtype == QSDPA_F16, units ? sched : nullptr,
+                      units, s);
   return rc;
 }
 

@@ -506,10 +506,25 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int quad = lane >> 4;
   const int r = lane & 15;
-  const int split = blockIdx.x;
   const int hblk = blockIdx.y % p.hb_count;
   const int kvh = blockIdx.y / p.hb_count;
-  const int b = blockIdx.z;
+  // Uniform splits: grid (S, H_kv * head blocks, B).  Left-padded batch
+  // (units > 0): grid (U, H_kv * head blocks, 1), unit x of the balanced
+  // schedule (common.h) is split `split` of `S` of sequence b.
+  int b, split, S;
+  if (p.units) {
+    const int C = ragged_budget(p.kv_start, p.B, p.N, p.units);
+    if (blockIdx.x == 0 && blockIdx.y == 0 && wave == 0) ragged_write_sched(p.kv_start, p.B, p.N, C, p.sched);
+    const RaggedUnit ru = ragged_unit(p.kv_start, p.B, p.N, C, blockIdx.x);
+    if (ru.b < 0) return;  // the whole workgroup: no work, nothing to store
+    b = ru.b;
+    split = ru.split;
+    S = ru.count;
+  } else {
+    b = blockIdx.z;
+    split = blockIdx.x;
+    S = p.num_splits;
+  }
   const int h0 = kvh * p.G + hblk * 16;        // first query head of the block
   const int nh = min(16, p.G - hblk * 16);     // real heads in the block
   const int hq_lane = h0 + min(r, nh - 1);     // this lane's head (clamped)
@@ -520,7 +535,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int s0 = p.kv_start ? min(max(p.kv_start[b], 0), p.N) : 0;
   const int len = p.N - s0;
   const int T = (len + kTile - 1) / kTile;
-  const int S = p.num_splits;
   const int J = T > split ? (T - split + S - 1) / S : 0;
   // Positions below J - E go round-robin to the 8 waves; the last E go to
   // waves 0-3 only.  Waves 4-7 share their SIMDs with waves 0-3, and the
@@ -752,7 +766,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         dst[2 * e + 1] = static_cast<uint16_t>(pk[e] >> 16);
       }
     } else {
-      const int64_t slot = (static_cast<int64_t>(b) * p.Hq + hh) * p.num_splits + split;
+      const int64_t slot = p.units ? static_cast<int64_t>(hh) * p.units + blockIdx.x
+                                   : (static_cast<int64_t>(b) * p.Hq + hh) * p.num_splits + split;
       // Streaming stores: the partials are read once, by the merge kernel.
       if constexpr (Tag::kId == QSDPA_F16) {
         // float16 rows of the split's normalised output (acc / L, within
@@ -777,7 +792,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 
 template <typename Tag, int D, int BITS>
 void launch_gs(const MfmaParams& p, int gs, hipStream_t stream, const qsdpa_decode_args* a) {
-  const dim3 grid(p.num_splits, p.Hkv * p.hb_count, p.B);
+  const dim3 grid(p.units ? p.units : p.num_splits, p.Hkv * p.hb_count, p.units ? 1 : p.B);
   void (*k)(MfmaParams) = gs == 32   ? decode_mfma_kernel<Tag, D, BITS, 32>
                           : gs == 64 ? decode_mfma_kernel<Tag, D, BITS, 64>
                                      : decode_mfma_kernel<Tag, D, BITS, 128>;
@@ -823,24 +838,25 @@ bool mfma_supports(const qsdpa_decode_args* a) {
 
 // Splits per (batch, kv head, head block): one workgroup per CU in total
 // (LDS and registers allow one 8-wave group per CU), each split at least one
-// tile per wave.
+// tile per wave.  A left-padded batch (kv_start, B > 1) runs the balanced
+// schedule over splits * B units, which also sizes for one round: measured
+// at C4 (B=16, H_kv=8, lengths U[1K, 32K]) the decode takes 59.1 us with 2
+// splits (32 units per kv head, one round), 62.1 us with 4 (two rounds) and
+// 80.5 us with 3 (one and a half); uniform splits took 66.1 us at best.
 int mfma_num_splits(const qsdpa_decode_args* a, int cus) {
   const int hb = (a->H_q / a->H_kv + 15) / 16;
   const int64_t units = static_cast<int64_t>(a->B) * a->H_kv * hb;
-  // Sequences of one batch that start at different kv_start (left padding)
-  // have unequal work per unit: two rounds of workgroups let the dispatcher
-  // fill the CUs that finish short sequences early.  (Measured at C4: B=16,
-  // H_kv=8, lengths U[1K, 32K]: 63.7 us with 4 splits, 74.4 us with 2.)
-  const int64_t target = a->kv_start ? 2LL * cus : cus;
-  int64_t s = (target + units - 1) / units;
+  int64_t s = (cus + units - 1) / units;
   s = std::min<int64_t>(s, std::max<int64_t>(1, a->N / (kWaves * kTile)));
   s = std::min<int64_t>(s, 1024);
   return static_cast<int>(std::max<int64_t>(s, 1));
 }
 
 int launch_decode_mfma(const qsdpa_decode_args* a, int num_splits, float* part_acc, float* part_ml,
-                       hipStream_t stream) {
+                       int units, int* sched, hipStream_t stream) {
   MfmaParams p = mfma_params(a, num_splits, part_acc, part_ml);
+  p.units = units;
+  p.sched = sched;
   const bool f16 = a->dtype == QSDPA_F16;
   if (a->D == 128) {
     if (f16) launch_bits<F16, 128>(p, a->bits, a->group_size, stream, a);

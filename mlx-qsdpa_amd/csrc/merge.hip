@@ -29,20 +29,31 @@ constexpr float kNegBig = -1.0e30f;
 // HALF: the partial rows are float16 and normalised (acc / l), as the MFMA
 // decode stores them for float16 inputs; the weight of split s is then
 // l_s * exp2(m_s - M) for its row as well as for the sum.
+//
+// sched != null (balanced schedule of a left-padded batch): the partials of
+// head h are rows h * units + u, and sequence b owns units
+// sched[2b] .. sched[2b] + sched[2b + 1] - 1.
 template <typename Tag, bool HALF>
 __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ part_acc,
                                                     const float* __restrict__ part_ml, int D,
                                                     int splits, int Hq, uint16_t* __restrict__ out,
-                                                    int64_t o_sb, int64_t o_sh) {
+                                                    int64_t o_sb, int64_t o_sh, const int* __restrict__ sched,
+                                                    int units) {
   const int bh = blockIdx.x;
   const int tid = threadIdx.x;
   const int q = tid & 7;
   const int g = tid >> 3;
   const int wave = tid >> 6;
   const int d = blockIdx.y * 32 + 4 * q;
-  const float2* ml = reinterpret_cast<const float2*>(part_ml) + static_cast<int64_t>(bh) * splits;
-  const float* pa = part_acc + static_cast<int64_t>(bh) * splits * D + d;
-  const uint16_t* ph = reinterpret_cast<const uint16_t*>(part_acc) + static_cast<int64_t>(bh) * splits * D + d;
+  int64_t first = static_cast<int64_t>(bh) * splits;
+  if (sched) {
+    const int2 e = *reinterpret_cast<const int2*>(sched + 2 * (bh / Hq));
+    first = static_cast<int64_t>(bh % Hq) * units + e.x;
+    splits = e.y;
+  }
+  const float2* ml = reinterpret_cast<const float2*>(part_ml) + first;
+  const float* pa = part_acc + first * D + d;
+  const uint16_t* ph = reinterpret_cast<const uint16_t*>(part_acc) + first * D + d;
 
   float m = kNegBig, l = 0.0f;
   float4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -117,20 +128,20 @@ __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ pa
 }  // namespace
 
 int launch_merge(const qsdpa_decode_args* a, int num_splits, const float* part_acc,
-                 const float* part_ml, bool half_parts, hipStream_t stream) {
+                 const float* part_ml, bool half_parts, const int* sched, int units, hipStream_t stream) {
   if (num_splits > kMaxSplits)
     return fail(QSDPA_ERR_INVALID, "merge: %d splits exceed %d", num_splits, kMaxSplits);
   uint16_t* out = static_cast<uint16_t*>(const_cast<void*>(a->out.ptr));
   const dim3 grid(a->B * a->H_q, a->D / 32);
   if (a->dtype == QSDPA_F16 && half_parts)
     merge_kernel<F16, true><<<grid, dim3(256), 0, stream>>>(part_acc, part_ml, a->D, num_splits, a->H_q,
-                                                            out, a->out.stride_b, a->out.stride_h);
+                                                            out, a->out.stride_b, a->out.stride_h, sched, units);
   else if (a->dtype == QSDPA_F16)
     merge_kernel<F16, false><<<grid, dim3(256), 0, stream>>>(part_acc, part_ml, a->D, num_splits, a->H_q,
-                                                             out, a->out.stride_b, a->out.stride_h);
+                                                             out, a->out.stride_b, a->out.stride_h, sched, units);
   else
     merge_kernel<BF16, false><<<grid, dim3(256), 0, stream>>>(part_acc, part_ml, a->D, num_splits, a->H_q,
-                                                              out, a->out.stride_b, a->out.stride_h);
+                                                              out, a->out.stride_b, a->out.stride_h, sched, units);
   return check_launch("merge");
 }
 

@@ -50,7 +50,11 @@ struct MfmaParams {
   const int32_t* kv_start;
   float* part_acc;
   float* part_ml;
+  int units;   // > 0: balanced schedule of a left-padded batch over this many units
+  int* sched;  // (P_b, n_b) per sequence, written for the merge when units > 0
 };
+
+static_assert(kTile == kSchedTile, "the balanced schedule counts the decode's key tiles");
 
 __device__ __forceinline__ uint32_t bitop_and_or(uint32_t a, uint32_t mask, uint32_t c) {
   return __builtin_amdgcn_bitop3_b32(a, mask, c, 0xEA);  // (a & mask) | c
@@ -234,6 +238,8 @@ inline MfmaParams mfma_params(const qsdpa_decode_args* a, int num_splits, float*
   p.kv_start = a->kv_start;
   p.part_acc = part_acc;
   p.part_ml = part_ml;
+  p.units = 0;
+  p.sched = nullptr;
   return p;
 }
 

@@ -1,6 +1,6 @@
 // Quantize-on-append and dequantize kernels (MLX affine format).
 //
-// quantize: one thread per (row, group).  The per-group rule is the float32
+// quantize: GS / 8 lanes per (row, group), 8 values per lane.  The per-group rule is the float32
 // edge-snapped affine quantizer (see oracle/affine.py for the written
 // contract); every operation is spelled with an explicitly rounded intrinsic
 // so the compiler can neither contract nor reassociate it, which keeps the
@@ -27,49 +27,72 @@ struct QuantParams {
   int64_t z_sb, z_sh, z_sn;
 };
 
-// The group's GS values are read once, all loads issued together (16-byte
-// pieces when VEC, i.e. the rows are 16-byte aligned), and kept in
-// registers for both passes.
+// Min / max over aligned groups of L consecutive lanes (L in {4, 8, 16});
+// every lane of a group gets the result.  Exact in any order.
+template <int L>
+__device__ __forceinline__ void group_minmax(float& lo, float& hi) {
+  lo = fminf(lo, dpp_f32<0xB1>(lo));
+  hi = fmaxf(hi, dpp_f32<0xB1>(hi));
+  lo = fminf(lo, dpp_f32<0x4E>(lo));
+  hi = fmaxf(hi, dpp_f32<0x4E>(hi));
+  if constexpr (L >= 8) {
+    lo = fminf(lo, dpp_f32<0x141>(lo));
+    hi = fmaxf(hi, dpp_f32<0x141>(hi));
+  }
+  if constexpr (L >= 16) {
+    lo = fminf(lo, dpp_f32<0x140>(lo));
+    hi = fmaxf(hi, dpp_f32<0x140>(hi));
+  }
+}
+
+// One group of GS values is spread over L = GS / 8 consecutive lanes, 8
+// values (one 16-byte piece when VEC, i.e. the rows are 16-byte aligned) per
+// lane; the group's min / max are reduced across the L lanes and every lane
+// quantizes and packs its own 8 values.  The latency of a one-row append is
+// then that of 8 values, not GS.  A group's lanes are all in range or all
+// out of it, so the cross-lane steps never read an exited lane.
 template <typename Tag, int BITS, int GS, bool VEC>
 __global__ __launch_bounds__(256) void quantize_kernel(QuantParams p) {
+  constexpr int L = GS / 8;
   constexpr int PER = 32 / BITS;
+  constexpr int WORDS = 8 / PER;  // packed words per lane: 1 (4-bit) or 2 (8-bit)
   constexpr float kBins = static_cast<float>((1 << BITS) - 1);
   const int ng = p.D / GS;
   const int64_t total = static_cast<int64_t>(p.B) * p.H * p.S * ng;
   const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (gid >= total) return;
-  const int g = static_cast<int>(gid % ng);
-  int64_t row = gid / ng;
+  const int64_t grp = gid / L;
+  const int part = static_cast<int>(gid % L);
+  if (grp >= total) return;
+  const int g = static_cast<int>(grp % ng);
+  int64_t row = grp / ng;
   const int s = static_cast<int>(row % p.S);
   row /= p.S;
   const int h = static_cast<int>(row % p.H);
   const int b = static_cast<int>(row / p.H);
 
-  const uint16_t* src = p.src + off3(b, h, s, p.s_sb, p.s_sh, p.s_sn) + g * GS;
-  uint16_t raw[GS];
+  const uint16_t* src = p.src + off3(b, h, s, p.s_sb, p.s_sh, p.s_sn) + g * GS + part * 8;
+  uint16_t raw[8];
   if constexpr (VEC) {
+    const uint4 v = *reinterpret_cast<const uint4*>(src);
+    const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-    for (int i = 0; i < GS / 8; ++i) {
-      const uint4 v = reinterpret_cast<const uint4*>(src)[i];
-      const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        raw[8 * i + 2 * k] = static_cast<uint16_t>(wv[k]);
-        raw[8 * i + 2 * k + 1] = static_cast<uint16_t>(wv[k] >> 16);
-      }
+    for (int k = 0; k < 4; ++k) {
+      raw[2 * k] = static_cast<uint16_t>(wv[k]);
+      raw[2 * k + 1] = static_cast<uint16_t>(wv[k] >> 16);
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < GS; ++i) raw[i] = src[i];
+    for (int i = 0; i < 8; ++i) raw[i] = src[i];
   }
 
   float w_min = __builtin_huge_valf(), w_max = -__builtin_huge_valf();
 #pragma unroll
-  for (int i = 0; i < GS; ++i) {
+  for (int i = 0; i < 8; ++i) {
     const float v = to_f32<Tag>(raw[i]);
     w_min = fminf(w_min, v);
     w_max = fmaxf(w_max, v);
   }
+  group_minmax<L>(w_min, w_max);
   float scale = fmaxf(__fdiv_rn(__fsub_rn(w_max, w_min), kBins), 1e-7f);
   const bool side = fabsf(w_min) > fabsf(w_max);
   scale = side ? scale : -scale;
@@ -80,9 +103,9 @@ __global__ __launch_bounds__(256) void quantize_kernel(QuantParams p) {
   const float bias = nz ? edge : 0.0f;
 
   const int t = p.t0 + s;
-  uint32_t* dst = p.dp + off3(b, h, t, p.p_sb, p.p_sh, p.p_sn) + (g * GS) / PER;
+  uint32_t* dst = p.dp + off3(b, h, t, p.p_sb, p.p_sh, p.p_sn) + (g * GS + part * 8) / PER;
 #pragma unroll
-  for (int w = 0; w < GS / PER; ++w) {
+  for (int w = 0; w < WORDS; ++w) {
     uint32_t word = 0;
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
@@ -93,8 +116,10 @@ __global__ __launch_bounds__(256) void quantize_kernel(QuantParams p) {
     }
     dst[w] = word;
   }
-  p.ds[off3(b, h, t, p.c_sb, p.c_sh, p.c_sn) + g] = from_f32<Tag>(scale);
-  p.db[off3(b, h, t, p.z_sb, p.z_sh, p.z_sn) + g] = from_f32<Tag>(bias);
+  if (part == 0) {
+    p.ds[off3(b, h, t, p.c_sb, p.c_sh, p.c_sn) + g] = from_f32<Tag>(scale);
+    p.db[off3(b, h, t, p.z_sb, p.z_sh, p.z_sn) + g] = from_f32<Tag>(bias);
+  }
 }
 
 template <typename Tag, int BITS, int GS>
@@ -163,7 +188,8 @@ int launch_quantize(const qsdpa_quantize_args* a, hipStream_t stream) {
   p.c_sb = a->dst_scales.stride_b; p.c_sh = a->dst_scales.stride_h; p.c_sn = a->dst_scales.stride_n;
   p.db = static_cast<uint16_t*>(const_cast<void*>(a->dst_biases.ptr));
   p.z_sb = a->dst_biases.stride_b; p.z_sh = a->dst_biases.stride_h; p.z_sn = a->dst_biases.stride_n;
-  const int64_t total = static_cast<int64_t>(a->B) * a->H * a->S * (a->D / a->group_size);
+  // Threads: 8 values each, GS / 8 per group.
+  const int64_t total = static_cast<int64_t>(a->B) * a->H * a->S * (a->D / 8);
   if (total == 0) return QSDPA_OK;
   const dim3 grid(static_cast<unsigned>((total + 255) / 256));
   // 16-byte group loads need 16-byte aligned rows (group offsets are

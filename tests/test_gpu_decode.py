@@ -198,6 +198,41 @@ def test_kv_start_left_padding(device, heads):
     assert_close(run(inp, device, mask=m), want, "additive left padding")
 
 
+@pytest.mark.parametrize("case", [
+    # (B, Hq, Hkv, N, D, gs, dtype, splits)
+    (70, 8, 2, 300, 128, 64, "f16", (None, 2, 3)),    # more sequences than a wave's 64 lanes
+    (5, 32, 8, 1100, 128, 32, "f16", (2, 7, 64)),
+    (6, 16, 1, 700, 256, 32, "bf16", (None, 4, 16)),
+], ids=["B70", "B5-G4", "B6-D256-bf16"])
+def test_kv_start_balanced_schedule(device, case):
+    """A left-padded batch shares splits * B units out over its sequences by
+    length: ragged lengths, empty sequences (kv_start >= N, also past N),
+    negative kv_start (clamped to 0) and split counts from 2 to 64 all match
+    the oracle with an additive -inf mask on the skipped keys; repeated calls
+    are bitwise identical."""
+    B, Hq, Hkv, N, D, gs, dtype, splits_list = case
+    rng = np.random.default_rng(31 + B)
+    inp = make_inputs(rng, B, Hq, Hkv, N, D, 4, gs, dtype=dtype)
+    starts = rng.integers(0, N, size=B)
+    starts[0] = N          # empty
+    starts[1] = N + 50     # past the end: empty
+    starts[2] = -7         # clamped to 0: the whole sequence
+    starts[3] = N - 1      # one key
+    if B > 5:
+        starts[5] = N - 33  # one key past a tile
+    keep_from = np.clip(starts, 0, N)
+    add = np.where(np.arange(N)[None, :] >= keep_from[:, None], 0.0, -np.inf)[:, None, None, :]
+    want = oracle_out(inp, mask=add)
+    want[keep_from >= N] = 0.0  # no keys: zero output
+    ks = torch.tensor(starts, dtype=torch.int32, device=device)
+    for splits in splits_list:
+        got = run(inp, device, kv_start=ks, num_splits=splits)
+        assert_close(got, want, f"balanced kv_start splits={splits}")
+        assert np.all(got[keep_from >= N] == 0)
+        again = run(inp, device, kv_start=ks, num_splits=splits)
+        assert np.array_equal(got, again), f"splits={splits}: repeated call differs"
+
+
 def test_fully_masked_row_is_zero(device):
     rng = np.random.default_rng(14)
     inp = make_inputs(rng, 2, 4, 2, 64, 128, 4, 32)
