@@ -229,10 +229,10 @@ def run_c4(args) -> int:
     # Launch arguments built once: each step only moves the append column
     # and the decode's key count (the caches grow in place).
     lib = _lib.load()
-    qargs = [_lib.QuantizeArgs(B, Hkv, 1, D, bits, gs, kernels.dtype_code(T), 0, kernels._view(x),
-                               kernels._view(kv[0]), kernels._view(kv[1]), kernels._view(kv[2]))
-             for kv, x in zip(bufs, new)]
-    qrefs = [ctypes.byref(a) for a in qargs]
+    qjobs = (_lib.QuantizeArgs * 2)(*[
+        _lib.QuantizeArgs(B, Hkv, 1, D, bits, gs, kernels.dtype_code(T), 0, kernels._view(x),
+                          kernels._view(kv[0]), kernels._view(kv[1]), kernels._view(kv[2]))
+        for kv, x in zip(bufs, new)])
     v0 = [t[:, :, :lmax + 1] for kv in bufs for t in kv]  # the split count is chosen for the first step
     plan = kernels.DecodePlan(q, v0[0], v0[3], v0[1], v0[4], v0[2], v0[5], scale=D ** -0.5, bits=bits,
                               group_size=gs, kv_start=kv_start, num_splits=args.splits, capacity=cap)
@@ -240,9 +240,8 @@ def run_c4(args) -> int:
     stream = torch.cuda.current_stream(device).cuda_stream
 
     def step(n, ev=None):
-        for a, ref in zip(qargs, qrefs):
-            a.t0 = n
-            _lib.check(lib.qsdpa_quantize(ref, stream))
+        qjobs[0].t0 = qjobs[1].t0 = n  # the appended column, K and V in one launch
+        _lib.check(lib.qsdpa_quantize_batch(qjobs, 2, stream))
         plan.set_keys(n + 1)
         plan(ev)
 

@@ -25,6 +25,8 @@
  *                       slice assignment into the cache buffers
  *                       (mlx_qsdpa/cache.py:186-192, 314-318, 576-581,
  *                       610-614, 798-804, 830-834).
+ *   qsdpa_quantize_batch <- the key and value mx.quantize pair of one
+ *                       update_and_fetch (same call sites), in one launch.
  *   qsdpa_dequantize <- mx.dequantize(...) (mlx_qsdpa/dispatch.py:69-78,
  *                       mlx_qsdpa/__init__.py:50-57) and the dequantize +
  *                       temporal reorder of cache.py:622-634, 842-857.
@@ -145,6 +147,15 @@ typedef struct {
 } qsdpa_quantize_args;
 
 int qsdpa_quantize(const qsdpa_quantize_args* args, void* stream);
+
+/*
+ * `count` (1..4) quantize jobs in one launch, e.g. the keys and the values
+ * of one cache update (the mx.quantize pair of update_and_fetch,
+ * mlx_qsdpa/cache.py:186-192, 314-318, 576-581, 610-614).  The jobs share
+ * bits, group_size and dtype; shapes and destinations are their own.
+ * qsdpa_quantize(args, s) is qsdpa_quantize_batch(args, 1, s).
+ */
+int qsdpa_quantize_batch(const qsdpa_quantize_args* jobs, int32_t count, void* stream);
 
 /*
  * Dequantize N tokens to T:  dst[b, h, t, :] = dequant(src[b, h, u(t), :])

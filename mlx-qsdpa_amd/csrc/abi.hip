@@ -215,22 +215,35 @@ int qsdpa_decode(const qsdpa_decode_args* args, void* stream) {
 }
 
 int qsdpa_quantize(const qsdpa_quantize_args* a, void* stream) {
+  return qsdpa_quantize_batch(a, 1, stream);
+}
+
+int qsdpa_quantize_batch(const qsdpa_quantize_args* jobs, int32_t count, void* stream) {
   clear_error();
-  if (!a) return fail(QSDPA_ERR_INVALID, "null args");
-  if (a->bits != 4 && a->bits != 8) return fail(QSDPA_ERR_INVALID, "bits must be 4 or 8, got %d", a->bits);
-  if (a->group_size != 32 && a->group_size != 64 && a->group_size != 128)
-    return fail(QSDPA_ERR_UNSUPPORTED, "group_size=%d not supported (32, 64, 128)", a->group_size);
-  if (a->B < 0 || a->H < 0 || a->S < 0 || a->D <= 0 || a->D % a->group_size != 0)
-    return fail(QSDPA_ERR_INVALID, "bad shape B=%d H=%d S=%d D=%d gs=%d", a->B, a->H, a->S, a->D,
-                a->group_size);
-  if (a->t0 < 0) return fail(QSDPA_ERR_INVALID, "t0 must be >= 0");
-  if (!valid_dtype(a->dtype)) return fail(QSDPA_ERR_INVALID, "dtype must be F16 or BF16");
-  int rc;
-  if ((rc = check_view(a->src, "src", 2, 1, true))) return rc;
-  if ((rc = check_view(a->dst_packed, "dst_packed", 4, 1, true))) return rc;
-  if ((rc = check_view(a->dst_scales, "dst_scales", 2, 1, true))) return rc;
-  if ((rc = check_view(a->dst_biases, "dst_biases", 2, 1, true))) return rc;
-  return launch_quantize(a, static_cast<hipStream_t>(stream));
+  if (!jobs) return fail(QSDPA_ERR_INVALID, "null args");
+  if (count < 1 || count > 4) return fail(QSDPA_ERR_INVALID, "count must be in [1, 4], got %d", count);
+  for (int i = 1; i < count; ++i)
+    if (jobs[i].bits != jobs[0].bits || jobs[i].group_size != jobs[0].group_size || jobs[i].dtype != jobs[0].dtype)
+      return fail(QSDPA_ERR_INVALID, "quantize jobs of one call must share bits, group_size and dtype");
+  const qsdpa_quantize_args* ptrs[4];
+  for (int i = 0; i < count; ++i) {
+    const qsdpa_quantize_args* a = jobs + i;
+    if (a->bits != 4 && a->bits != 8) return fail(QSDPA_ERR_INVALID, "bits must be 4 or 8, got %d", a->bits);
+    if (a->group_size != 32 && a->group_size != 64 && a->group_size != 128)
+      return fail(QSDPA_ERR_UNSUPPORTED, "group_size=%d not supported (32, 64, 128)", a->group_size);
+    if (a->B < 0 || a->H < 0 || a->S < 0 || a->D <= 0 || a->D % a->group_size != 0)
+      return fail(QSDPA_ERR_INVALID, "bad shape B=%d H=%d S=%d D=%d gs=%d", a->B, a->H, a->S, a->D,
+                  a->group_size);
+    if (a->t0 < 0) return fail(QSDPA_ERR_INVALID, "t0 must be >= 0");
+    if (!valid_dtype(a->dtype)) return fail(QSDPA_ERR_INVALID, "dtype must be F16 or BF16");
+    int rc;
+    if ((rc = check_view(a->src, "src", 2, 1, true))) return rc;
+    if ((rc = check_view(a->dst_packed, "dst_packed", 4, 1, true))) return rc;
+    if ((rc = check_view(a->dst_scales, "dst_scales", 2, 1, true))) return rc;
+    if ((rc = check_view(a->dst_biases, "dst_biases", 2, 1, true))) return rc;
+    ptrs[i] = a;
+  }
+  return launch_quantize(ptrs, count, static_cast<hipStream_t>(stream));
 }
 
 int qsdpa_dequantize(const qsdpa_dequantize_args* a, void* stream) {

@@ -9,6 +9,8 @@
 // dequantize: one thread per packed word; value = round_T(fmaf(s, q, b)).
 // Replaces mx.quantize + slice assignment (mlx_qsdpa/cache.py:186-192) and
 // mx.dequantize (mlx_qsdpa/dispatch.py:69-78, cache.py:628-633).
+#include <algorithm>
+
 #include "abi_internal.h"
 #include "common.h"
 
@@ -45,26 +47,36 @@ __device__ __forceinline__ void group_minmax(float& lo, float& hi) {
   }
 }
 
+// Up to kMaxJobs quantize jobs (the keys and values of one cache update)
+// run in one launch, job = blockIdx.y; they share dtype, bits and
+// group_size.
+constexpr int kMaxJobs = 4;
+struct QuantJobs {
+  QuantParams p[kMaxJobs];
+};
+
 // One group of GS values is spread over L = GS / 8 consecutive lanes, 8
 // values (one 16-byte piece when VEC, i.e. the rows are 16-byte aligned) per
 // lane; the group's min / max are reduced across the L lanes and every lane
 // quantizes and packs its own 8 values.  The latency of a one-row append is
 // then that of 8 values, not GS.  A group's lanes are all in range or all
-// out of it, so the cross-lane steps never read an exited lane.
-template <typename Tag, int BITS, int GS, bool VEC>
-__global__ __launch_bounds__(256) void quantize_kernel(QuantParams p) {
+// out of it, so the cross-lane steps never read an exited lane.  I is the
+// index type: 32-bit whenever the launch's thread count fits.
+template <typename Tag, int BITS, int GS, bool VEC, typename I>
+__global__ __launch_bounds__(256) void quantize_kernel(QuantJobs jobs) {
   constexpr int L = GS / 8;
   constexpr int PER = 32 / BITS;
   constexpr int WORDS = 8 / PER;  // packed words per lane: 1 (4-bit) or 2 (8-bit)
   constexpr float kBins = static_cast<float>((1 << BITS) - 1);
+  const QuantParams& p = jobs.p[blockIdx.y];
   const int ng = p.D / GS;
-  const int64_t total = static_cast<int64_t>(p.B) * p.H * p.S * ng;
-  const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const int64_t grp = gid / L;
+  const I total = static_cast<I>(p.B) * p.H * p.S * ng;
+  const I gid = static_cast<I>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const I grp = gid / L;
   const int part = static_cast<int>(gid % L);
   if (grp >= total) return;
   const int g = static_cast<int>(grp % ng);
-  int64_t row = grp / ng;
+  I row = grp / ng;
   const int s = static_cast<int>(row % p.S);
   row /= p.S;
   const int h = static_cast<int>(row % p.H);
@@ -123,16 +135,21 @@ __global__ __launch_bounds__(256) void quantize_kernel(QuantParams p) {
 }
 
 template <typename Tag, int BITS, int GS>
-void launch_quantize_gs(const QuantParams& p, bool vec, dim3 grid, hipStream_t stream) {
-  if (vec) quantize_kernel<Tag, BITS, GS, true><<<grid, dim3(256), 0, stream>>>(p);
-  else quantize_kernel<Tag, BITS, GS, false><<<grid, dim3(256), 0, stream>>>(p);
+void launch_quantize_gs(const QuantJobs& j, bool vec, bool wide, dim3 grid, hipStream_t stream) {
+  if (wide) {
+    if (vec) quantize_kernel<Tag, BITS, GS, true, int64_t><<<grid, dim3(256), 0, stream>>>(j);
+    else quantize_kernel<Tag, BITS, GS, false, int64_t><<<grid, dim3(256), 0, stream>>>(j);
+  } else {
+    if (vec) quantize_kernel<Tag, BITS, GS, true, uint32_t><<<grid, dim3(256), 0, stream>>>(j);
+    else quantize_kernel<Tag, BITS, GS, false, uint32_t><<<grid, dim3(256), 0, stream>>>(j);
+  }
 }
 
 template <typename Tag, int BITS>
-void launch_quantize_bits(const QuantParams& p, bool vec, dim3 grid, hipStream_t stream) {
-  if (p.gs == 32) launch_quantize_gs<Tag, BITS, 32>(p, vec, grid, stream);
-  else if (p.gs == 64) launch_quantize_gs<Tag, BITS, 64>(p, vec, grid, stream);
-  else launch_quantize_gs<Tag, BITS, 128>(p, vec, grid, stream);
+void launch_quantize_bits(const QuantJobs& j, int gs, bool vec, bool wide, dim3 grid, hipStream_t stream) {
+  if (gs == 32) launch_quantize_gs<Tag, BITS, 32>(j, vec, wide, grid, stream);
+  else if (gs == 64) launch_quantize_gs<Tag, BITS, 64>(j, vec, wide, grid, stream);
+  else launch_quantize_gs<Tag, BITS, 128>(j, vec, wide, grid, stream);
 }
 
 struct DequantParams {
@@ -177,31 +194,42 @@ __global__ __launch_bounds__(256) void dequantize_kernel(DequantParams p) {
 
 }  // namespace
 
-int launch_quantize(const qsdpa_quantize_args* a, hipStream_t stream) {
-  QuantParams p;
-  p.B = a->B; p.H = a->H; p.S = a->S; p.D = a->D; p.gs = a->group_size; p.t0 = a->t0;
-  p.src = static_cast<const uint16_t*>(a->src.ptr);
-  p.s_sb = a->src.stride_b; p.s_sh = a->src.stride_h; p.s_sn = a->src.stride_n;
-  p.dp = static_cast<uint32_t*>(const_cast<void*>(a->dst_packed.ptr));
-  p.p_sb = a->dst_packed.stride_b; p.p_sh = a->dst_packed.stride_h; p.p_sn = a->dst_packed.stride_n;
-  p.ds = static_cast<uint16_t*>(const_cast<void*>(a->dst_scales.ptr));
-  p.c_sb = a->dst_scales.stride_b; p.c_sh = a->dst_scales.stride_h; p.c_sn = a->dst_scales.stride_n;
-  p.db = static_cast<uint16_t*>(const_cast<void*>(a->dst_biases.ptr));
-  p.z_sb = a->dst_biases.stride_b; p.z_sh = a->dst_biases.stride_h; p.z_sn = a->dst_biases.stride_n;
-  // Threads: 8 values each, GS / 8 per group.
-  const int64_t total = static_cast<int64_t>(a->B) * a->H * a->S * (a->D / 8);
-  if (total == 0) return QSDPA_OK;
-  const dim3 grid(static_cast<unsigned>((total + 255) / 256));
-  // 16-byte group loads need 16-byte aligned rows (group offsets are
-  // multiples of 32 elements).
-  const bool vec = aligned(a->src.ptr, 16) && a->src.stride_b % 8 == 0 && a->src.stride_h % 8 == 0 &&
-                   a->src.stride_n % 8 == 0;
+int launch_quantize(const qsdpa_quantize_args* const* jobs, int count, hipStream_t stream) {
+  if (count < 1 || count > kMaxJobs) return fail(QSDPA_ERR_INVALID, "quantize: %d jobs (1..%d)", count, kMaxJobs);
+  QuantJobs j{};
+  int64_t most = 0;  // threads of the largest job: 8 values each, GS / 8 per group
+  bool vec = true;
+  for (int i = 0; i < count; ++i) {
+    const qsdpa_quantize_args* a = jobs[i];
+    QuantParams& p = j.p[i];
+    p.B = a->B; p.H = a->H; p.S = a->S; p.D = a->D; p.gs = a->group_size; p.t0 = a->t0;
+    p.src = static_cast<const uint16_t*>(a->src.ptr);
+    p.s_sb = a->src.stride_b; p.s_sh = a->src.stride_h; p.s_sn = a->src.stride_n;
+    p.dp = static_cast<uint32_t*>(const_cast<void*>(a->dst_packed.ptr));
+    p.p_sb = a->dst_packed.stride_b; p.p_sh = a->dst_packed.stride_h; p.p_sn = a->dst_packed.stride_n;
+    p.ds = static_cast<uint16_t*>(const_cast<void*>(a->dst_scales.ptr));
+    p.c_sb = a->dst_scales.stride_b; p.c_sh = a->dst_scales.stride_h; p.c_sn = a->dst_scales.stride_n;
+    p.db = static_cast<uint16_t*>(const_cast<void*>(a->dst_biases.ptr));
+    p.z_sb = a->dst_biases.stride_b; p.z_sh = a->dst_biases.stride_h; p.z_sn = a->dst_biases.stride_n;
+    most = std::max<int64_t>(most, static_cast<int64_t>(a->B) * a->H * a->S * (a->D / 8));
+    // 16-byte loads need 16-byte aligned rows (a lane's offset in the row
+    // is a multiple of 8 elements).
+    vec = vec && aligned(a->src.ptr, 16) && a->src.stride_b % 8 == 0 && a->src.stride_h % 8 == 0 &&
+          a->src.stride_n % 8 == 0;
+  }
+  if (most == 0) return QSDPA_OK;
+  const int64_t blocks = (most + 255) / 256;
+  if (blocks >= (int64_t(1) << 31)) return fail(QSDPA_ERR_UNSUPPORTED, "quantize: %lld rows too many",
+                                                static_cast<long long>(most));
+  const bool wide = blocks * 256 >= (int64_t(1) << 32);
+  const dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>(count));
+  const qsdpa_quantize_args* a = jobs[0];
   if (a->dtype == QSDPA_F16) {
-    if (a->bits == 4) launch_quantize_bits<F16, 4>(p, vec, grid, stream);
-    else launch_quantize_bits<F16, 8>(p, vec, grid, stream);
+    if (a->bits == 4) launch_quantize_bits<F16, 4>(j, a->group_size, vec, wide, grid, stream);
+    else launch_quantize_bits<F16, 8>(j, a->group_size, vec, wide, grid, stream);
   } else {
-    if (a->bits == 4) launch_quantize_bits<BF16, 4>(p, vec, grid, stream);
-    else launch_quantize_bits<BF16, 8>(p, vec, grid, stream);
+    if (a->bits == 4) launch_quantize_bits<BF16, 4>(j, a->group_size, vec, wide, grid, stream);
+    else launch_quantize_bits<BF16, 8>(j, a->group_size, vec, wide, grid, stream);
   }
   return check_launch("quantize");
 }

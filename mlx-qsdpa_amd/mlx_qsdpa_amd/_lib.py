@@ -30,6 +30,7 @@ EXPORTED_SYMBOLS = (
     "qsdpa_decode_workspace_size",
     "qsdpa_decode",
     "qsdpa_quantize",
+    "qsdpa_quantize_batch",
     "qsdpa_dequantize",
     "qsdpa_last_error",
     "qsdpa_abi_version",
@@ -109,6 +110,8 @@ def load(path: os.PathLike | str | None = None) -> ctypes.CDLL:
     lib.qsdpa_decode.restype = ctypes.c_int
     lib.qsdpa_quantize.argtypes = [ctypes.POINTER(QuantizeArgs), ctypes.c_void_p]
     lib.qsdpa_quantize.restype = ctypes.c_int
+    lib.qsdpa_quantize_batch.argtypes = [ctypes.POINTER(QuantizeArgs), ctypes.c_int32, ctypes.c_void_p]
+    lib.qsdpa_quantize_batch.restype = ctypes.c_int
     lib.qsdpa_dequantize.argtypes = [ctypes.POINTER(DequantizeArgs), ctypes.c_void_p]
     lib.qsdpa_dequantize.restype = ctypes.c_int
     lib.qsdpa_last_error.argtypes = []

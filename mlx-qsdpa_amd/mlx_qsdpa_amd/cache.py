@@ -180,8 +180,8 @@ class QuantizedSDPACache:
         if self._keys is None or prev + S > self._keys[0].shape[2]:
             self._grow(B, H, S, Dk, Dv, keys.dtype, keys.device, prev)
         self.offset += S
-        kernels.quantize_into(keys, self._keys, prev, self.bits, self.group_size)
-        kernels.quantize_into(values, self._values, prev, self.bits, self.group_size)
+        kernels.quantize_kv_into(keys, values, self._keys, self._values, prev, self.bits,
+                                 self.group_size)
         return _sl(self._keys, 0, self.offset), _sl(self._values, 0, self.offset)
 
     def _grow(self, B, H, S, Dk, Dv, dtype, device, prev):
@@ -262,8 +262,8 @@ class BatchQuantizedSDPACache:
                 self._keys, self._values = nk, nv
         self.offset = self.offset + S
         self._idx += S
-        kernels.quantize_into(keys, self._keys, prev, self.bits, self.group_size)
-        kernels.quantize_into(values, self._values, prev, self.bits, self.group_size)
+        kernels.quantize_kv_into(keys, values, self._keys, self._values, prev, self.bits,
+                                 self.group_size)
         return _sl(self._keys, 0, self._idx), _sl(self._values, 0, self._idx)
 
     def prepare(self, *, left_padding=None, lengths=None, right_padding=None):
@@ -460,8 +460,8 @@ class QuantizedRotatingSDPACache:
     def _update_decode(self, keys, values):
         """cache.py:574-591."""
         wp = self._write_pos()
-        kernels.quantize_into(keys, self._keys, wp, self.bits, self.group_size)
-        kernels.quantize_into(values, self._values, wp, self.bits, self.group_size)
+        kernels.quantize_kv_into(keys, values, self._keys, self._values, wp, self.bits,
+                                 self.group_size)
         self._idx = wp + 1
         self.offset += 1
         n_visible = min(self.offset, self.max_size)
@@ -494,8 +494,8 @@ class QuantizedRotatingSDPACache:
             all_k = torch.cat([all_k[:, :, :self.keep], all_k[:, :, total - tail:]], dim=2)
             all_v = torch.cat([all_v[:, :, :self.keep], all_v[:, :, total - tail:]], dim=2)
             total = self.max_size
-        kernels.quantize_into(all_k, self._keys, 0, self.bits, self.group_size)
-        kernels.quantize_into(all_v, self._values, 0, self.bits, self.group_size)
+        kernels.quantize_kv_into(all_k, all_v, self._keys, self._values, 0, self.bits,
+                                 self.group_size)
         self.offset += S
         self._idx = total if total < self.max_size else self.keep
         n_visible = min(self.offset, self.max_size)
@@ -617,8 +617,8 @@ class BatchQuantizedRotatingSDPACache:
     def _update_decode(self, keys, values):
         """cache.py:796-811."""
         wp = self._write_pos()
-        kernels.quantize_into(keys, self._keys, wp, self.bits, self.group_size)
-        kernels.quantize_into(values, self._values, wp, self.bits, self.group_size)
+        kernels.quantize_kv_into(keys, values, self._keys, self._values, wp, self.bits,
+                                 self.group_size)
         self.offset = self.offset + 1
         self._idx += 1
         n = min(self._idx, self.max_size)
@@ -651,8 +651,8 @@ class BatchQuantizedRotatingSDPACache:
             all_k = torch.cat([all_k[:, :, :self.keep], all_k[:, :, total - tail:]], dim=2)
             all_v = torch.cat([all_v[:, :, :self.keep], all_v[:, :, total - tail:]], dim=2)
             total = self.max_size
-        kernels.quantize_into(all_k, self._keys, 0, self.bits, self.group_size)
-        kernels.quantize_into(all_v, self._values, 0, self.bits, self.group_size)
+        kernels.quantize_kv_into(all_k, all_v, self._keys, self._values, 0, self.bits,
+                                 self.group_size)
         self.offset = self.offset + S
         self._idx = total
         return _sl(self._keys, 0, total), _sl(self._values, 0, total)

@@ -61,8 +61,7 @@ def _expect_shape(name, t, shape):
         raise ValueError(f"{name}: expected shape {tuple(shape)}, got {tuple(t.shape)}")
 
 
-def quantize_into(src: torch.Tensor, dst: tuple, t0: int, bits: int, group_size: int) -> None:
-    """dst[b, h, t0 + s, :] = quantize(src[b, h, s, :]) for the 3 dst tensors."""
+def _quantize_args(src: torch.Tensor, dst: tuple, t0: int, bits: int, group_size: int):
     _require_device(src, *dst)
     src = _inner_contig(src)
     B, H, S, D = src.shape
@@ -76,10 +75,26 @@ def quantize_into(src: torch.Tensor, dst: tuple, t0: int, bits: int, group_size:
     _expect_shape("dst_biases", dst[2], (B, H, cap, D // group_size))
     if dst[0].dtype != torch.uint32 or dst[1].dtype != src.dtype or dst[2].dtype != src.dtype:
         raise ValueError("destination dtypes must be (uint32, src.dtype, src.dtype)")
-    a = _lib.QuantizeArgs(B, H, S, D, bits, group_size, dtype_code(src.dtype), int(t0),
-                          _view(src), _view(dst[0]), _view(dst[1]), _view(dst[2]))
-    lib = _lib.load()
-    _lib.check(lib.qsdpa_quantize(ctypes.byref(a), _stream(src)))
+    # (the caller keeps `src` alive until the launch is queued)
+    return src, _lib.QuantizeArgs(B, H, S, D, bits, group_size, dtype_code(src.dtype), int(t0),
+                                  _view(src), _view(dst[0]), _view(dst[1]), _view(dst[2]))
+
+
+def quantize_into(src: torch.Tensor, dst: tuple, t0: int, bits: int, group_size: int) -> None:
+    """dst[b, h, t0 + s, :] = quantize(src[b, h, s, :]) for the 3 dst tensors."""
+    src, a = _quantize_args(src, dst, t0, bits, group_size)
+    _lib.check(_lib.load().qsdpa_quantize(ctypes.byref(a), _stream(src)))
+
+
+def quantize_kv_into(keys: torch.Tensor, values: torch.Tensor, kdst: tuple, vdst: tuple, t0: int,
+                     bits: int, group_size: int) -> None:
+    """quantize_into for the keys and the values of one cache update, in one launch."""
+    if keys.dtype != values.dtype:
+        raise ValueError("keys and values must share a dtype")
+    keys, ka = _quantize_args(keys, kdst, t0, bits, group_size)
+    values, va = _quantize_args(values, vdst, t0, bits, group_size)
+    jobs = (_lib.QuantizeArgs * 2)(ka, va)
+    _lib.check(_lib.load().qsdpa_quantize_batch(jobs, 2, _stream(keys)))
 
 
 def quantize(w: torch.Tensor, group_size: int = 64, bits: int = 4):

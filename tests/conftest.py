@@ -94,10 +94,16 @@ def _cpu_dequantize(packed, scales, biases=None, group_size=64, bits=4, keep=0, 
     return from_np(out, scales.dtype)
 
 
+def _cpu_quantize_kv_into(keys, values, kdst, vdst, t0, bits, group_size):
+    _cpu_quantize_into(keys, kdst, t0, bits, group_size)
+    _cpu_quantize_into(values, vdst, t0, bits, group_size)
+
+
 @pytest.fixture
 def cpu_kernels(monkeypatch):
     from mlx_qsdpa_amd import kernels
     monkeypatch.setattr(kernels, "quantize_into", _cpu_quantize_into)
+    monkeypatch.setattr(kernels, "quantize_kv_into", _cpu_quantize_kv_into)
     monkeypatch.setattr(kernels, "dequantize", _cpu_dequantize)
     return kernels
 

@@ -75,6 +75,14 @@ def test_invalid_arguments_return_codes():
     q.group_size = 32
     assert lib.qsdpa_quantize(ctypes.byref(q), None) == _lib.QSDPA_ERR_INVALID
     assert b"bits" in lib.qsdpa_last_error()
+    jobs = (_lib.QuantizeArgs * 2)()
+    for j in jobs:
+        j.bits, j.group_size, j.D, j.B, j.H, j.S = 4, 32, 64, 1, 1, 1
+    jobs[1].group_size = 64
+    assert lib.qsdpa_quantize_batch(jobs, 2, None) == _lib.QSDPA_ERR_INVALID
+    assert b"share" in lib.qsdpa_last_error()
+    assert lib.qsdpa_quantize_batch(jobs, 5, None) == _lib.QSDPA_ERR_INVALID
+    assert lib.qsdpa_quantize_batch(jobs, 0, None) == _lib.QSDPA_ERR_INVALID
     d = _lib.DequantizeArgs()
     d.bits, d.group_size, d.D = 4, 48, 96
     assert lib.qsdpa_dequantize(ctypes.byref(d), None) == _lib.QSDPA_ERR_UNSUPPORTED

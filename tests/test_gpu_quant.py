@@ -72,6 +72,46 @@ def test_quantize_into_strided_destination(device, dtype):
     assert np.all(to_np(dst[2])[:, :, :t0] == 7.0)
 
 
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("aligned", [True, False], ids=["vec", "unaligned"])
+def test_quantize_batch_matches_oracle(device, dtype, aligned):
+    """qsdpa_quantize_batch: a key job and a value job of different shapes
+    (D 128 and 64, 5 and 3 rows) in one launch land bit-exactly at [t0,
+    t0 + S) of their own capacity-padded buffers; nothing else is written.
+    A value source with rows 2-byte aligned only takes the element-wise
+    load path for both jobs."""
+    rng = np.random.default_rng(11)
+    T = torch_dtype(dtype)
+    bits, gs, t0, cap = 4, 32, 9, 24
+    shapes = [(2, 3, 5, 128), (2, 3, 3, 64)]
+    srcs, dsts, views = [], [], []
+    for i, (B, H, S, D) in enumerate(shapes):
+        w = affine.random_T(rng, (B, H, S, D), dtype, outlier_frac=0.02)
+        w[0, 0, 0] = 0.0
+        if aligned or i == 0:
+            v = from_np(w, T, device)
+        else:  # rows start one element into a D + 1 wide buffer
+            base = torch.zeros((B, H, S, D + 1), dtype=T, device=device)
+            base[..., 1:] = from_np(w, T, device)
+            v = base[..., 1:]
+        srcs.append(w)
+        views.append(v)
+        dsts.append((torch.full((B, H, cap, D * bits // 32), 0x5A5A, dtype=torch.int32, device=device)
+                     .view(torch.uint32),
+                     torch.full((B, H, cap, D // gs), 7.0, dtype=T, device=device),
+                     torch.full((B, H, cap, D // gs), 7.0, dtype=T, device=device)))
+    kernels.quantize_kv_into(views[0], views[1], dsts[0], dsts[1], t0, bits, gs)
+    for w, dst in zip(srcs, dsts):
+        S = w.shape[2]
+        want = affine.quantize(w, gs, bits, dtype)
+        p = to_np(dst[0])
+        assert np.array_equal(p[:, :, t0:t0 + S], want[0])
+        assert np.all(p[:, :, :t0] == 0x5A5A) and np.all(p[:, :, t0 + S:] == 0x5A5A)
+        assert _bits_equal(to_np(dst[1])[:, :, t0:t0 + S], want[1], dtype)
+        assert _bits_equal(to_np(dst[2])[:, :, t0:t0 + S], want[2], dtype)
+        assert np.all(to_np(dst[1])[:, :, t0 + S:] == 7.0) and np.all(to_np(dst[2])[:, :, :t0] == 7.0)
+
+
 def _scalar_T(bits_hex, dt, device):
     v = int(bits_hex, 16)
     v = v - (1 << 16) if v >= 1 << 15 else v
