@@ -22,7 +22,8 @@ Printed JSON line (rank 0, N=1):
                    (hipExtLaunchKernel start / stop events);
                    traffic = HBM bytes per launch from the committed
                    rocprofv3 FETCH_SIZE / WRITE_SIZE summary
-                   (profiles/traffic.txt) when it covers this workload
+                   (profiles/traffic.txt) when it covers this workload;
+                   kernel_us_p5_p50_p95 = percentiles of the per-step durations
   cpu_baseline     the oracle's float32 dequantize + attention (the
                    reference's CPU-capable path) on a bounded sample
 """
@@ -191,6 +192,12 @@ C4 = {"B": 16, "H_q": 32, "H_kv": 8, "D": 128, "bits": 4, "group_size": 64, "dty
       "len_lo": 1024, "len_hi": 32768}
 
 
+def _pcts(ms):
+    """p5 / median / p95 of per-step kernel times (ms in, us out)."""
+    import numpy as np
+    return [round(float(x) * 1e3, 3) for x in np.percentile(np.asarray(ms), [5, 50, 95])]
+
+
 def run_c4(args) -> int:
     import numpy as np
     import torch
@@ -264,7 +271,8 @@ def run_c4(args) -> int:
         step(n, (ev_b[i], ev_e[i]))
         n += 1
     torch.cuda.synchronize()
-    kern_us = float(np.mean([hip.elapsed_ms(ev_b[i], ev_e[i]) for i in range(args.steps)])) * 1e3
+    kern_ms = [hip.elapsed_ms(ev_b[i], ev_e[i]) for i in range(args.steps)]
+    kern_us = float(np.mean(kern_ms)) * 1e3
     hip.destroy(ev_b + ev_e)
 
     us_step = wall / args.steps * 1e6
@@ -291,7 +299,8 @@ def run_c4(args) -> int:
         "pct_hbm_peak": round(100.0 * step_gbps / HBM_PEAK_GBPS, 2),
         "roofline": {"bound": "hbm", "achieved": round(kern_gbps, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(kern_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
-                     "kernel_us": round(kern_us, 3), "algorithmic_bytes": int(bytes_kern)},
+                     "kernel_us": round(kern_us, 3), "kernel_us_p5_p50_p95": _pcts(kern_ms),
+                     "algorithmic_bytes": int(bytes_kern)},
         "cpu_baseline": None,
     }
     print(json.dumps(line), flush=True)
@@ -408,6 +417,7 @@ def main(argv=None) -> int:
             "frac": round(kern_gbps / HBM_PEAK_GBPS, 4),
             "traffic": traffic,
             "kernel_us": round(kern_us, 3),
+            "kernel_us_p5_p50_p95": _pcts(kern_ms),
             "algorithmic_bytes": alg_bytes,
         },
         "cpu_baseline": cpu,

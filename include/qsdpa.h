@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define QSDPA_ABI_VERSION 1
+#define QSDPA_ABI_VERSION 2
 
 enum {
   QSDPA_OK = 0,
@@ -72,8 +72,10 @@ typedef struct {
 } qsdpa_view;
 
 /*
- * Decode attention: out[b, h, 0, :] = softmax(scale * q[b,h] . K[b, h/G]^T
- * + mask) V[b, h/G] with G = H_q / H_kv, K/V dequantized on the fly.
+ * Decode attention: out[b, h, i, :] = softmax(scale * q[b,h,i] . K[b, h/G]^T
+ * + mask) V[b, h/G] with G = H_q / H_kv, K/V dequantized on the fly, for
+ * the q_len query positions i (1 for a decode step; more for speculative
+ * or chunked decoding and prefill).
  */
 typedef struct {
   int32_t B, H_q, H_kv, N, D;
@@ -82,18 +84,20 @@ typedef struct {
   int32_t dtype;      /* QSDPA_F16 or QSDPA_BF16: q, scales, biases, out */
   float scale;        /* softmax scale applied to q.k */
 
-  qsdpa_view q;        /* [B, H_q, 1, D]          (stride_n unused)     */
+  qsdpa_view q;        /* [B, H_q, q_len, D]  (stride_n: query position) */
   qsdpa_view k_packed; /* [B, H_kv, N, D*bits/32] uint32                 */
   qsdpa_view v_packed;
   qsdpa_view k_scales; /* [B, H_kv, N, D/group_size] dtype               */
   qsdpa_view v_scales;
   qsdpa_view k_biases; /* ptr NULL => zero biases (symmetric format)     */
   qsdpa_view v_biases;
-  qsdpa_view out;      /* [B, H_q, 1, D] dtype     (stride_n unused)     */
+  qsdpa_view out;      /* [B, H_q, q_len, D] dtype (stride_n: position)  */
 
-  /* Optional mask over keys, broadcastable [B|1, H_q|1, 1, N]: a stride of
-   * 0 broadcasts.  QSDPA_BOOL: nonzero keeps the key; QSDPA_F16/BF16/F32:
-   * additive (added to the scaled score).  ptr NULL = no mask.            */
+  /* Optional mask over keys, broadcastable [B|1, H_q|1, q_len|1, N]: a
+   * stride of 0 broadcasts; stride_n is the KEY stride and mask_stride_q
+   * (below) the query-position stride.  QSDPA_BOOL: nonzero keeps the key;
+   * QSDPA_F16/BF16/F32: additive (added to the scaled score).  ptr NULL =
+   * no mask.                                                              */
   qsdpa_view mask;
   int32_t mask_dtype;
 
@@ -119,6 +123,17 @@ typedef struct {
    * after prof_end).                                                     */
   void* prof_begin;
   void* prof_end;
+
+  /* Query positions per (batch, head); 0 or 1 = one (a decode step).
+   * q_len > 1 needs D in {128, 256} and the alignment of the matrix-core
+   * path (else QSDPA_ERR_UNSUPPORTED); mlx_qsdpa's dispatch.py:68-83 sends
+   * such calls through dequantize + attention instead.                    */
+  int32_t q_len;
+  /* Nonzero: causal, aligned to the last key (mask="causal" of the
+   * reference): query i sees keys t <= N - q_len + i.  Combines with mask
+   * and kv_start.                                                         */
+  int32_t causal;
+  int64_t mask_stride_q; /* mask stride over query positions (0 = broadcast) */
 } qsdpa_decode_args;
 
 /* Bytes of workspace qsdpa_decode needs for these args (0 for a single

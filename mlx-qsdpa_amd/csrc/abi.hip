@@ -107,6 +107,11 @@ int validate_decode(const qsdpa_decode_args* a) {
   if ((rc = check_view(a->v_biases, "v_biases", 2, 1, false))) return rc;
   if ((a->k_biases.ptr == nullptr) != (a->v_biases.ptr == nullptr))
     return fail(QSDPA_ERR_INVALID, "k_biases and v_biases must both be given or both be NULL");
+  if (a->q_len < 0) return fail(QSDPA_ERR_INVALID, "q_len must be >= 0, got %d", a->q_len);
+  if (a->q_len > 1 && !mfma_supports(a))
+    return fail(QSDPA_ERR_UNSUPPORTED,
+                "q_len=%d needs the matrix-core path (D 128 or 256, aligned views); use dequantize + attention",
+                a->q_len);
   if (a->mask.ptr) {
     const int md = a->mask_dtype;
     if (md != QSDPA_F16 && md != QSDPA_BF16 && md != QSDPA_F32 && md != QSDPA_BOOL)
@@ -141,8 +146,8 @@ int decode_plan(const qsdpa_decode_args* a, int* num_splits, int64_t* workspace_
   *num_splits = splits;
   // Partials (B * H_q * splits rows of D + 2 floats), then the balanced
   // schedule's (first unit, units) pair per sequence.
-  *workspace_bytes =
-      splits > 1 ? static_cast<int64_t>(a->B) * a->H_q * splits * (a->D + 2) * 4 + 8LL * a->B + 256 : 0;
+  const int64_t rows = static_cast<int64_t>(a->B) * a->H_q * std::max(a->q_len, 1);
+  *workspace_bytes = splits > 1 ? rows * splits * (a->D + 2) * 4 + 8LL * a->B + 256 : 0;
   return QSDPA_OK;
 }
 
@@ -195,9 +200,10 @@ int qsdpa_decode(const qsdpa_decode_args* args, void* stream) {
                   static_cast<long long>(ws), static_cast<long long>(args->workspace_bytes));
     if (!aligned(args->workspace, 16)) return fail(QSDPA_ERR_INVALID, "workspace not 16-byte aligned");
     part_acc = static_cast<float*>(args->workspace);
-    part_ml = part_acc + static_cast<int64_t>(args->B) * args->H_q * splits * args->D;
+    part_ml = part_acc + static_cast<int64_t>(args->B) * args->H_q * std::max(args->q_len, 1) * splits * args->D;
   }
-  int* sched = part_ml ? reinterpret_cast<int*>(part_ml + static_cast<int64_t>(args->B) * args->H_q * splits * 2)
+  int* sched = part_ml ? reinterpret_cast<int*>(part_ml + static_cast<int64_t>(args->B) * args->H_q *
+                                                              std::max(args->q_len, 1) * splits * 2)
                        : nullptr;
   const hipStream_t s = static_cast<hipStream_t>(stream);
   // (prof_begin / prof_end ride on the main kernel's own dispatch)

@@ -7,8 +7,14 @@
 // narrower) form the N side of 16x16x32 MFMA tiles, so each K/V element is
 // read from HBM and dequantized exactly once per workgroup.
 //
+// Several query positions (qL > 1: speculative or chunked decoding,
+// prefill; the reference dequantizes and runs SDPA for those,
+// dispatch.py:68-83) extend the N side to the kv head's G * qL rows
+// (position v / G, head v % G); a causal mask aligned to the last key ends
+// each block's keys at its last row's limit and each lane's at its own.
+//
 // Workgroup = 8 waves = one split of a (batch, kv head, block of 16 query
-// heads).  The sequence is cut into 32-token tiles; split s of S owns tiles
+// rows).  The sequence is cut into 32-token tiles; split s of S owns tiles
 // s, s + S, s + 2S, ..., so the whole grid streams one compact window of the
 // cache at a time.  Each wave streams its share of the split's tiles with
 // one register set: the next tile's K loads are issued as soon as the
@@ -46,7 +52,8 @@
 // sequence's last tile is partial; its rows past the end read as zero and
 // their scores are set to -inf.  Each wave keeps Q^T in registers.  The 8
 // waves merge through LDS; one split writes the normalised output, otherwise
-// float32 partials for the merge kernel (merge.hip).
+// partials for the merge kernel (merge.hip): float16 inputs store the
+// normalised row acc / l as float16 (half the bytes), bfloat16 float32 rows.
 #include "mfma_common.h"
 
 namespace qsdpa {
@@ -98,9 +105,7 @@ struct TileRegs {
   using G = Geo<D, BITS, GS>;
   uint32_t kw[2][G::KW];
   uint32_t ks[2];            // KG == 2: both groups (16-bit each); else low half
-  // float16: A operand of the K-bias MFMA (4 biases of the token's row);
-  // bfloat16: kb[u][0] = the lane's own group bias word, as ks.
-  uint32_t kb[2][2];
+  uint32_t kb[2];            // the K bias word(s) of the lane's group(s), as ks
   uint32_t vw[8][G::VW];
   uint32_t vs[2], vb[2];     // V scale / bias row words (A layout, per half)
 };
@@ -145,20 +150,16 @@ struct VMetaLane {
   uint32_t shift;
 };
 
-typedef uint32_t u2 __attribute__((ext_vector_type(2)));
-
 template <typename Tag, int D, int BITS, int GS>
 struct Kernel {
   using G = Geo<D, BITS, GS>;
   using Regs = TileRegs<D, BITS, GS>;
-  // Float16 folds the dequantization biases into MFMAs: a K / V element
-  // becomes fma(M + code, scale, -M * scale) = round(scale * code) (one
-  // rounding; M * scale is exact), and the bias terms are added as
-  //   S^T[t, h]   += sum_g kbias_g[t] * sum_{d in g} Q[h, d]   (16x16x16 MFMA)
-  //   out^T[d, h] += sum_t vbias_g(d)[t] * P^T[t, h]         (16x16x32 MFMA)
-  // -1024 * scale overflows float16 for |scale| >= 64: a tile holding such
-  // a scale runs with its scales times 2^-11 and its products scaled back.
-  static constexpr bool kFold = Tag::kId == QSDPA_F16;
+  // Every K / V element is dequantized as mx.dequantize rounds it, T(fma(
+  // scale, code, bias)): float16 builds the code as an exact half (the
+  // 1024 + code bit trick, minus 1024) and uses one v_pk_fma_f16 per pair.
+  // (Rounding scale * code first and adding the bias afterwards saves an
+  // op per pair but is off by up to half an ulp of |scale * code|, which
+  // outruns the parity tolerance where a few keys carry a row.)
 
   // Token of slot j (0..7) of quad q within a 32-token tile (the S^T C layout).
   static __device__ __forceinline__ int tau(int q, int j) { return 16 * (j >> 2) + 4 * q + (j & 3); }
@@ -176,21 +177,10 @@ struct Kernel {
         R.ks[u] = __builtin_amdgcn_raw_buffer_load_b32(rs.ks, row * rs.ks_sn + L.ks_r, 0, 0);
       else
         R.ks[u] = __builtin_amdgcn_raw_buffer_load_b16(rs.ks, row * rs.ks_sn + L.ks_r, 0, 0);
-      if constexpr (kFold) {
-        // Biases of groups 4 * (quad & 1) .. + 3 of the row (zero past NG).
-        const uint32_t off = row * rs.kb_sn + L.kb_r;
-        if constexpr (G::NG >= 4) {
-          const u2 v = __builtin_amdgcn_raw_buffer_load_b64(rs.kb, off, 0, 0);
-          R.kb[u][0] = v[0]; R.kb[u][1] = v[1];
-        } else if constexpr (G::NG == 2) {
-          R.kb[u][0] = __builtin_amdgcn_raw_buffer_load_b32(rs.kb, off, 0, 0); R.kb[u][1] = 0u;
-        } else {
-          R.kb[u][0] = __builtin_amdgcn_raw_buffer_load_b16(rs.kb, off, 0, 0); R.kb[u][1] = 0u;
-        }
-      } else if constexpr (G::KG == 2) {
-        R.kb[u][0] = __builtin_amdgcn_raw_buffer_load_b32(rs.kb, row * rs.kb_sn + L.kb_r, 0, 0);
+      if constexpr (G::KG == 2) {
+        R.kb[u] = __builtin_amdgcn_raw_buffer_load_b32(rs.kb, row * rs.kb_sn + L.kb_r, 0, 0);
       } else {
-        R.kb[u][0] = __builtin_amdgcn_raw_buffer_load_b16(rs.kb, row * rs.kb_sn + L.kb_r, 0, 0);
+        R.kb[u] = __builtin_amdgcn_raw_buffer_load_b16(rs.kb, row * rs.kb_sn + L.kb_r, 0, 0);
       }
     }
   }
@@ -214,53 +204,26 @@ struct Kernel {
     }
   }
 
-  // S^T for one 16-token half u: K dequantized into the A operand, Q^T as
-  // B.  FOLD: round(scale * code) only (the bias enters through the K-bias
-  // MFMA); otherwise scale * code + bias with the lane's group biases kbl.
-  // FOLD: ssc = 1.0 or 2^-11 in both halves, a factor applied to the
-  // scales (the caller multiplies the result back).
-  template <bool FOLD>
-  static __device__ __forceinline__ f4 qk_half(const Regs& R, int u, const uint32_t (&qt)[G::NM][4],
-                                               const uint32_t (&kbl)[2], uint32_t ssc) {
-    uint32_t s2[2], b2[2], n1k[2], n64[2];
+  // S^T for one 16-token half u: K dequantized into the A operand (scale *
+  // code + bias with the lane's group scales / biases), Q^T as B.
+  static __device__ __forceinline__ f4 qk_half(const Regs& R, int u, const uint32_t (&qt)[G::NM][4]) {
+    uint32_t s2[2], b2[2];
     float sf[2], bf[2];
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
       const uint32_t sw = (G::KG == 2 && g == 1) ? (R.ks[u] >> 16) : R.ks[u];
-      const uint32_t bw = (G::KG == 2 && g == 1) ? (kbl[u] >> 16) : kbl[u];
+      const uint32_t bw = (G::KG == 2 && g == 1) ? (R.kb[u] >> 16) : R.kb[u];
       s2[g] = splat_lo(sw);
       sf[g] = to_f32<Tag>(static_cast<uint16_t>(sw));
-      if constexpr (FOLD) {
-        s2[g] = f16x2_mul(s2[g], ssc);
-        n1k[g] = f16x2_mul(s2[g], kNeg1024);
-        n64[g] = f16x2_mul(s2[g], kNeg64);
-      } else {
-        b2[g] = splat_lo(bw);
-        bf[g] = to_f32<Tag>(static_cast<uint16_t>(bw));
-      }
+      b2[g] = splat_lo(bw);
+      bf[g] = to_f32<Tag>(static_cast<uint16_t>(bw));
     }
     f4 S = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int m = 0; m < G::NM; ++m) {
       const int g = (G::KG == 2 && m >= G::NM / 2) ? 1 : 0;
       uint32_t a[4];
-      if constexpr (FOLD) {
-        const uint32_t* w = R.kw[u] + m * G::WPS;
-        if constexpr (BITS == 4) {
-          const uint32_t x = w[0], x8 = w[0] >> 8;
-          a[0] = f16x2_fma(bitop_and_or(x, kNib, kMagic), s2[g], n1k[g]);
-          a[1] = f16x2_fma(bitop_and_or(x, kNib1, kMagic64), s2[g], n64[g]);
-          a[2] = f16x2_fma(bitop_and_or(x8, kNib, kMagic), s2[g], n1k[g]);
-          a[3] = f16x2_fma(bitop_and_or(x8, kNib1, kMagic64), s2[g], n64[g]);
-        } else {
-          a[0] = f16x2_fma(perm(kMagic8, w[0], kSelB01), s2[g], n1k[g]);
-          a[1] = f16x2_fma(perm(kMagic8, w[0], kSelB23), s2[g], n1k[g]);
-          a[2] = f16x2_fma(perm(kMagic8, w[1], kSelB01), s2[g], n1k[g]);
-          a[3] = f16x2_fma(perm(kMagic8, w[1], kSelB23), s2[g], n1k[g]);
-        }
-      } else {
-        dequant_k<Tag, BITS>(R.kw[u] + m * G::WPS, s2[g], b2[g], sf[g], bf[g], a);
-      }
+      dequant_k<Tag, BITS>(R.kw[u] + m * G::WPS, s2[g], b2[g], sf[g], bf[g], a);
       S = mfma<Tag>(a, qt[m], S);
     }
     return S;
@@ -268,20 +231,9 @@ struct Kernel {
 
   // out^T += V^T P^T: MFMA nb takes dim r*NB + nb of the lane's 8 tokens.
   // sv2 / bv2: V scale / bias pairs of tokens (2i, 2i+1) of the lane's group.
-  // FOLD: the A operand is round(scale * code); the caller adds the bias.
-  template <bool FOLD, typename IV>
+  template <typename IV>
   static __device__ __forceinline__ void pv_f16(Regs& R, const uint32_t (&sv2)[4], const uint32_t (&bv2)[4],
                                                 const uint32_t (&pb)[4], f4 (&acc)[G::NB], IV&& issue_v) {
-    uint32_t c1k[4], c64[4];  // FOLD: -1024 * scale, -64 * scale; else the bias
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if constexpr (FOLD) {
-        c1k[i] = f16x2_mul(sv2[i], kNeg1024);
-        c64[i] = f16x2_mul(sv2[i], kNeg64);
-      } else {
-        c1k[i] = c64[i] = bv2[i];
-      }
-    }
     if constexpr (BITS == 4) {
       // X: nibbles 0-3 of tokens (2i, 2i+1), Y: nibbles 4-7.
       uint32_t X[4][G::VW], Y[4][G::VW];
@@ -300,12 +252,7 @@ struct Kernel {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const uint32_t src = k < 4 ? X[i][w] : Y[i][w];
-          const uint32_t sh = (k & 3) < 2 ? src : src >> 8;
-          if constexpr (FOLD)
-            a[i] = (k & 1) ? f16x2_fma(bitop_and_or(sh, kNib1, kMagic64), sv2[i], c64[i])
-                           : f16x2_fma(bitop_and_or(sh, kNib, kMagic), sv2[i], c1k[i]);
-          else
-            a[i] = f16x2_fma(nib_codes(src, src >> 8, k & 3), sv2[i], c1k[i]);
+          a[i] = f16x2_fma(nib_codes(src, src >> 8, k & 3), sv2[i], bv2[i]);
         }
         acc[nb] = mfma<Tag>(a, pb, acc[nb]);
       }
@@ -327,7 +274,7 @@ struct Kernel {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const uint32_t t = perm(kMagic8, Z[i][w][k >> 1], (k & 1) ? kSelB23 : kSelB01);
-          a[i] = FOLD ? f16x2_fma(t, sv2[i], c1k[i]) : f16x2_fma(f16x2_sub1024(t), sv2[i], c1k[i]);
+          a[i] = f16x2_fma(f16x2_sub1024(t), sv2[i], bv2[i]);
         }
         acc[nb] = mfma<Tag>(a, pb, acc[nb]);
       }
@@ -338,43 +285,26 @@ struct Kernel {
   // The next tile's K loads are issued (issue_k) as soon as this tile's K
   // has been consumed, and its V loads (issue_v) once V is in the PV
   // operands' pre-permuted form, so one register set suffices.
-  // qsB: the K-bias MFMA's B operand (float16).
   template <typename IK, typename IV>
   static __device__ __forceinline__ void compute_tile(Regs& R, const MfmaParams& p, const uint32_t (&qt)[G::NM][4],
-                                                      const uint32_t (&qsB)[2], f4 (&acc)[G::NB], f4& accB,
-                                                      float& mrun, float& lrun, int tb, int n1, int quad, int b,
-                                                      int hq_lane, const VMetaLane& vm, IK&& issue_k,
+                                                      f4 (&acc)[G::NB], float& mrun, float& lrun, int tb, int n1, int quad,
+                                                      int64_t mrow, const VMetaLane& vm, IK&& issue_k,
                                                       IV&& issue_v) {
     // ---- S^T = K Q^T (Q^T operand m: 16 B per lane, in registers) ----
     f4 S[2];
-    if constexpr (kFold) {
-      // A tile holding a K scale >= 64 runs with the scales times 2^-11
-      // (exact), and its QK product is multiplied back by 2^11.
-      const bool big = __builtin_amdgcn_ballot_w64((f16x2_ge64(R.ks[0]) | f16x2_ge64(R.ks[1])) != 0u);
-      const uint32_t ssc = big ? kF16x2TwoM11 : kF16x2One;
-      const float back = big ? 2048.0f : 1.0f;
-      const uint32_t none[2] = {0u, 0u};
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        S[u] = qk_half<true>(R, u, qt, none, ssc);
-        S[u] = mfma16_f16(R.kb[u], qsB, S[u] * back);
-      }
-    } else {
-      const uint32_t kbl[2] = {R.kb[0][0], R.kb[1][0]};
-#pragma unroll
-      for (int u = 0; u < 2; ++u) S[u] = qk_half<false>(R, u, qt, kbl, 0u);
-    }
+    for (int u = 0; u < 2; ++u) S[u] = qk_half(R, u, qt);
     issue_k(R);
 
-    // ---- scores of (head hq_lane, tokens tau(quad, j)), online softmax ----
+    // ---- scores of (the lane's row, tokens tau(quad, j)), online softmax ----
+    // n1: this lane's end of keys (the sequence's, or its causal limit).
     float sc[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) sc[j] = S[j >> 2][j & 3] * p.qscale;
     if (p.mask) {
-      const int64_t mrow = static_cast<int64_t>(b) * p.m_sb + static_cast<int64_t>(hq_lane) * p.m_sh;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const int t = min(tb + tau(quad, j), n1 - 1);
+        const int t = min(tb + tau(quad, j), p.N - 1);
         sc[j] += mask_value(p, mrow + static_cast<int64_t>(t) * p.m_sn);
       }
     }
@@ -395,7 +325,6 @@ struct Kernel {
       lrun *= f;
 #pragma unroll
       for (int i = 0; i < G::NB; ++i) acc[i] *= f;
-      accB *= f;
     }
     float pr[8];
 #pragma unroll
@@ -429,23 +358,7 @@ struct Kernel {
         sv2[i] = perm(dS[2 * i + 1], dS[2 * i], vm.sel);
         bv2[i] = perm(dB[2 * i + 1], dB[2 * i], vm.sel);
       }
-      // Bias rows of the A operand: row r holds the lane's group (that of
-      // dims r*NB ..), the same for every nb, so one MFMA per tile.
-      accB = mfma<Tag>(bv2, pb, accB);
-      // A tile holding a V scale >= 64 runs with the scales times 2^-11 and
-      // the accumulators scaled down around its products (all exact).
-      const bool big = __builtin_amdgcn_ballot_w64((f16x2_ge64(R.vs[0]) | f16x2_ge64(R.vs[1])) != 0u);
-      if (big) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) sv2[i] = f16x2_mul(sv2[i], kF16x2TwoM11);
-#pragma unroll
-        for (int nb = 0; nb < G::NB; ++nb) acc[nb] *= 1.0f / 2048.0f;
-      }
-      pv_f16<true>(R, sv2, bv2, pb, acc, issue_v);
-      if (big) {
-#pragma unroll
-        for (int nb = 0; nb < G::NB; ++nb) acc[nb] *= 2048.0f;
-      }
+      pv_f16(R, sv2, bv2, pb, acc, issue_v);
     } else {
       float svf[8], bvf[8];
 #pragma unroll
@@ -525,15 +438,25 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     split = blockIdx.x;
     S = p.num_splits;
   }
-  const int h0 = kvh * p.G + hblk * 16;        // first query head of the block
-  const int nh = min(16, p.G - hblk * 16);     // real heads in the block
-  const int hq_lane = h0 + min(r, nh - 1);     // this lane's head (clamped)
+  // The block's rows: v0 .. v0 + nh - 1 of the kv head's G * qL rows; row v
+  // is query position v / G of head kvh * G + v % G (with one position, the
+  // 16 heads of a GQA group).
+  const int v0 = hblk * 16;
+  const int nh = min(16, p.G * p.qL - v0);       // real rows in the block
+  const int v_lane = v0 + min(r, nh - 1);        // this lane's row (clamped)
+  const int hq_lane = kvh * p.G + v_lane % p.G;  // its head
+  const int iq_lane = v_lane / p.G;              // its query position
 
-  // Keys [s0, N) of this sequence, in 32-token tiles from s0.  Split s owns
-  // tiles s, s + S, s + 2S, ... (positions j = 0, 1, ..., J - 1), so at any
-  // moment the grid streams one compact window of the cache.
+  // Causal (aligned to the last key): position i sees keys t <= N - qL + i,
+  // so the block needs keys below n_end and each lane below n_lane.
+  const int n_end = p.causal ? min(p.N, max(0, p.N - p.qL + (v0 + nh - 1) / p.G + 1)) : p.N;
+  const int n_lane = p.causal ? min(n_end, max(0, p.N - p.qL + iq_lane + 1)) : n_end;
+
+  // Keys [s0, n_end) of this sequence, in 32-token tiles from s0.  Split s
+  // owns tiles s, s + S, s + 2S, ... (positions j = 0, 1, ..., J - 1), so at
+  // any moment the grid streams one compact window of the cache.
   const int s0 = p.kv_start ? min(max(p.kv_start[b], 0), p.N) : 0;
-  const int len = p.N - s0;
+  const int len = max(n_end - s0, 0);
   const int T = (len + kTile - 1) / kTile;
   const int J = T > split ? (T - split + S - 1) / S : 0;
   // Positions below J - E go round-robin to the 8 waves; the last E go to
@@ -589,9 +512,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   LaneOffsets L;
   L.k_r = quad * G::KW * 4 + r * rs.k_sn;
   L.ks_r = kg0 * 2 + r * rs.ks_sn;
-  // float16: the row piece of groups 4 * (quad & 1) .. (K-bias MFMA A
-  // operand); bfloat16: the lane's own groups, as the scales.
-  L.kb_r = (K::kFold ? (G::NG == 8 ? 8 * (quad & 1) : 0) : kg0 * 2) + r * rs.kb_sn;
+  L.kb_r = kg0 * 2 + r * rs.kb_sn;
   L.v_r = r * G::VW * 4 + 4 * quad * rs.v_sn;
   L.vs_r = vword * 4 + r * rs.vs_sn;
   L.vb_r = vword * 4 + r * rs.vb_sn;
@@ -607,19 +528,21 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     vm.shift = half ? 0u : 16u;
   }
 
-  // The block's Q rows (16 heads x D, zero rows for padding heads) are read
-  // once per workgroup, one 16-byte piece per thread, and staged in LDS
-  // (rows padded by 16 bytes so the per-lane row reads below are
-  // conflict-free).
+  // The block's Q rows (16 rows x D, zero rows for padding) are read once
+  // per workgroup, one 16-byte piece per thread, and staged in LDS (rows
+  // padded by 16 bytes so the per-lane row reads below are conflict-free).
   constexpr int kQChunks = D / 8;  // 16-byte pieces per row
   const int qh = threadIdx.x / kQChunks, qc = threadIdx.x % kQChunks;
   u4 qv = u4{0u, 0u, 0u, 0u};
   if (qh < 16) {
+    // Descriptor over the kv head's G heads x qL positions of this batch.
     const uint8_t* q0 = reinterpret_cast<const uint8_t*>(p.q) +
-                        (static_cast<int64_t>(b) * p.q_sb + static_cast<int64_t>(h0) * p.q_sh) * 2;
-    const rsrc_t rq = make_rsrc(q0, static_cast<uint32_t>((nh - 1) * p.q_sh * 2 + D * 2));
-    qv = __builtin_amdgcn_raw_buffer_load_b128(rq, static_cast<uint32_t>(min(qh, nh - 1) * p.q_sh * 2 + qc * 16), 0,
-                                               0);
+                        (static_cast<int64_t>(b) * p.q_sb + static_cast<int64_t>(kvh) * p.G * p.q_sh) * 2;
+    const rsrc_t rq = make_rsrc(
+        q0, static_cast<uint32_t>(((p.G - 1) * p.q_sh + static_cast<int64_t>(p.qL - 1) * p.q_sq) * 2 + D * 2));
+    const int v = v0 + min(qh, nh - 1);
+    const int64_t off = (static_cast<int64_t>(v % p.G) * p.q_sh + static_cast<int64_t>(v / p.G) * p.q_sq) * 2;
+    qv = __builtin_amdgcn_raw_buffer_load_b128(rq, static_cast<uint32_t>(off + qc * 16), 0, 0);
   }
   // Q is staged before any K / V load is issued: issued together, the
   // grid's first tiles (20 MB at C3) would queue in front of it.
@@ -651,46 +574,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     }
   }
 
-  // float16: B operand of the K-bias MFMA.  k slots 4*quad + i hold, for
-  // head r, the sum of Q over group 4 * (quad & 1) + i (zero past NG), as
-  // its float16 value (quads 0, 1) or the float16 residual (quads 2, 3).
-  uint32_t qsB[2] = {0u, 0u};
-  if constexpr (K::kFold) {
-    float part[G::NG];
-#pragma unroll
-    for (int g = 0; g < G::NG; ++g) part[g] = 0.0f;
-#pragma unroll
-    for (int m = 0; m < G::NM; ++m) {
-      float t = 0.0f;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) t += unpack_T2_lo<Tag>(qt[m][i]) + unpack_T2_hi<Tag>(qt[m][i]);
-      const int g = (quad * G::QD + 8 * m) / GS;  // dims of slice m lie in one group
-#pragma unroll
-      for (int gg = 0; gg < G::NG; ++gg) part[gg] += gg == g ? t : 0.0f;
-    }
-    float sel[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) sel[i] = 0.0f;
-#pragma unroll
-    for (int g = 0; g < G::NG; ++g) {
-      float tot = part[g] + shfl_xor_f32(part[g], 16);
-      tot += shfl_xor_f32(tot, 32);
-      if ((g >> 2) == (quad & 1)) sel[g & 3] = tot;
-    }
-    float v[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float hi = static_cast<float>(static_cast<_Float16>(sel[i]));
-      v[i] = quad < 2 ? hi : sel[i] - hi;
-    }
-    qsB[0] = pack_T2<Tag>(v[0], v[1]);
-    qsB[1] = pack_T2<Tag>(v[2], v[3]);
-  }
-
+  const int64_t mrow = static_cast<int64_t>(b) * p.m_sb + static_cast<int64_t>(hq_lane) * p.m_sh +
+                       static_cast<int64_t>(iq_lane) * p.m_sq;  // the lane's mask row
   f4 acc[G::NB];
 #pragma unroll
   for (int i = 0; i < G::NB; ++i) acc[i] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-  f4 accB = f4{0.0f, 0.0f, 0.0f, 0.0f};  // float16: the V bias rows
   float mrun = kNegBig;
   float lrun = 0.0f;
 
@@ -699,12 +587,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     const int nrow = row_of(nj);
     auto ik = [&](typename K::Regs& X) { K::load_k(X, rs, L, nrow); };
     auto iv = [&](typename K::Regs& X) { K::load_v(X, rs, L, nrow); };
-    K::compute_tile(R, p, qt, qsB, acc, accB, mrun, lrun, s0 + row_of(j), p.N, quad, b, hq_lane, vm, ik, iv);
+    K::compute_tile(R, p, qt, acc, mrun, lrun, s0 + row_of(j), n_lane, quad, mrow, vm, ik, iv);
     j = nj;
-  }
-  if constexpr (K::kFold) {
-#pragma unroll
-    for (int i = 0; i < G::NB; ++i) acc[i] += accB;
   }
 
   // ---- per-head totals over the four quads ----
@@ -752,13 +636,16 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       v[4] = fmaf(a1[0], f, v[4]); v[5] = fmaf(a1[1], f, v[5]);
       v[6] = fmaf(a1[2], f, v[6]); v[7] = fmaf(a1[3], f, v[7]);
     }
-    const int hh = h0 + h;
+    const int vh = v0 + h;
+    const int hh = kvh * p.G + vh % p.G;  // head and query position of the row
+    const int iq = vh / p.G;
     if (p.num_splits == 1) {
       const float inv = L > 0.0f ? 1.0f / L : 0.0f;
       uint32_t pk[kPer / 2];
 #pragma unroll
       for (int e = 0; e < kPer / 2; ++e) pk[e] = pack_T2<Tag>(v[2 * e] * inv, v[2 * e + 1] * inv);
-      uint16_t* dst = p.out + static_cast<int64_t>(b) * p.o_sb + static_cast<int64_t>(hh) * p.o_sh + d;
+      uint16_t* dst = p.out + static_cast<int64_t>(b) * p.o_sb + static_cast<int64_t>(hh) * p.o_sh +
+                      static_cast<int64_t>(iq) * p.o_sq + d;
       // out rows are only 2-byte aligned in general: store pairs.
 #pragma unroll
       for (int e = 0; e < kPer / 2; ++e) {
@@ -766,8 +653,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         dst[2 * e + 1] = static_cast<uint16_t>(pk[e] >> 16);
       }
     } else {
-      const int64_t slot = p.units ? static_cast<int64_t>(hh) * p.units + blockIdx.x
-                                   : (static_cast<int64_t>(b) * p.Hq + hh) * p.num_splits + split;
+      // Partial rows: (b, head, position) rows, each with its splits.
+      const int64_t prow = static_cast<int64_t>(hh) * p.qL + iq;
+      const int64_t slot = p.units ? prow * p.units + blockIdx.x
+                                   : (static_cast<int64_t>(b) * p.Hq * p.qL + prow) * p.num_splits + split;
       // Streaming stores: the partials are read once, by the merge kernel.
       if constexpr (Tag::kId == QSDPA_F16) {
         // float16 rows of the split's normalised output (acc / L, within
@@ -833,6 +722,13 @@ bool mfma_supports(const qsdpa_decode_args* a) {
                                    a->k_scales.stride_n * 2, a->v_scales.stride_n * 2,
                                    a->k_biases.stride_n * 2, a->v_biases.stride_n * 2});
   if (max_sn < 0 || max_sn * (static_cast<int64_t>(a->N) + 3 * kTile) >= (int64_t(1) << 31)) return false;
+  // Q of a kv head (G heads x q_len positions) is read through one
+  // descriptor with 32-bit byte offsets.
+  const int64_t qL = std::max(a->q_len, 1);
+  const int64_t q_sn = qL > 1 ? a->q.stride_n : 0;
+  if (a->q.stride_h < 0 || q_sn < 0 ||
+      ((a->H_q / a->H_kv - 1) * a->q.stride_h + (qL - 1) * q_sn) * 2 + a->D * 2 >= (int64_t(1) << 31))
+    return false;
   return true;
 }
 
@@ -844,7 +740,7 @@ bool mfma_supports(const qsdpa_decode_args* a) {
 // splits (32 units per kv head, one round), 62.1 us with 4 (two rounds) and
 // 80.5 us with 3 (one and a half); uniform splits took 66.1 us at best.
 int mfma_num_splits(const qsdpa_decode_args* a, int cus) {
-  const int hb = (a->H_q / a->H_kv + 15) / 16;
+  const int hb = (a->H_q / a->H_kv * std::max(a->q_len, 1) + 15) / 16;
   const int64_t units = static_cast<int64_t>(a->B) * a->H_kv * hb;
   int64_t s = (cus + units - 1) / units;
   s = std::min<int64_t>(s, std::max<int64_t>(1, a->N / (kWaves * kTile)));

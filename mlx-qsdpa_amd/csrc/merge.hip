@@ -30,15 +30,17 @@ constexpr float kNegBig = -1.0e30f;
 // decode stores them for float16 inputs; the weight of split s is then
 // l_s * exp2(m_s - M) for its row as well as for the sum.
 //
-// sched != null (balanced schedule of a left-padded batch): the partials of
-// head h are rows h * units + u, and sequence b owns units
+// Rows are (b, h, i) for the qL query positions i, numbered
+// (b * H_q + h) * qL + i; each holds `splits` partials.  sched != null
+// (balanced schedule of a left-padded batch): the partials of (h, i) are
+// rows (h * qL + i) * units + u, and sequence b owns units
 // sched[2b] .. sched[2b] + sched[2b + 1] - 1.
 template <typename Tag, bool HALF>
 __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ part_acc,
                                                     const float* __restrict__ part_ml, int D,
-                                                    int splits, int Hq, uint16_t* __restrict__ out,
-                                                    int64_t o_sb, int64_t o_sh, const int* __restrict__ sched,
-                                                    int units) {
+                                                    int splits, int Hq, int qL, uint16_t* __restrict__ out,
+                                                    int64_t o_sb, int64_t o_sh, int64_t o_sq,
+                                                    const int* __restrict__ sched, int units) {
   const int bh = blockIdx.x;
   const int tid = threadIdx.x;
   const int q = tid & 7;
@@ -46,9 +48,10 @@ __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ pa
   const int wave = tid >> 6;
   const int d = blockIdx.y * 32 + 4 * q;
   int64_t first = static_cast<int64_t>(bh) * splits;
+  const int rows_b = Hq * qL;  // rows per sequence
   if (sched) {
-    const int2 e = *reinterpret_cast<const int2*>(sched + 2 * (bh / Hq));
-    first = static_cast<int64_t>(bh % Hq) * units + e.x;
+    const int2 e = *reinterpret_cast<const int2*>(sched + 2 * (bh / rows_b));
+    first = static_cast<int64_t>(bh % rows_b) * units + e.x;
     splits = e.y;
   }
   const float2* ml = reinterpret_cast<const float2*>(part_ml) + first;
@@ -118,8 +121,9 @@ __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ pa
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
     const float o[4] = {((a0.x + a1.x) + (a2.x + a3.x)) * inv, ((a0.y + a1.y) + (a2.y + a3.y)) * inv,
                         ((a0.z + a1.z) + (a2.z + a3.z)) * inv, ((a0.w + a1.w) + (a2.w + a3.w)) * inv};
-    const int b = bh / Hq, h = bh % Hq;
-    uint16_t* dst = out + static_cast<int64_t>(b) * o_sb + static_cast<int64_t>(h) * o_sh + blockIdx.y * 32 + 4 * tid;
+    const int b = bh / rows_b, h = (bh % rows_b) / qL, i = bh % qL;
+    uint16_t* dst = out + static_cast<int64_t>(b) * o_sb + static_cast<int64_t>(h) * o_sh +
+                    static_cast<int64_t>(i) * o_sq + blockIdx.y * 32 + 4 * tid;
 #pragma unroll
     for (int e = 0; e < 4; ++e) dst[e] = from_f32<Tag>(o[e]);
   }
@@ -132,16 +136,18 @@ int launch_merge(const qsdpa_decode_args* a, int num_splits, const float* part_a
   if (num_splits > kMaxSplits)
     return fail(QSDPA_ERR_INVALID, "merge: %d splits exceed %d", num_splits, kMaxSplits);
   uint16_t* out = static_cast<uint16_t*>(const_cast<void*>(a->out.ptr));
-  const dim3 grid(a->B * a->H_q, a->D / 32);
+  const int qL = a->q_len > 1 ? a->q_len : 1;
+  const int64_t o_sq = qL > 1 ? a->out.stride_n : 0;
+  const dim3 grid(a->B * a->H_q * qL, a->D / 32);
   if (a->dtype == QSDPA_F16 && half_parts)
-    merge_kernel<F16, true><<<grid, dim3(256), 0, stream>>>(part_acc, part_ml, a->D, num_splits, a->H_q,
-                                                            out, a->out.stride_b, a->out.stride_h, sched, units);
+    merge_kernel<F16, true><<<grid, dim3(256), 0, stream>>>(part_acc, part_ml, a->D, num_splits, a->H_q, qL,
+                                                            out, a->out.stride_b, a->out.stride_h, o_sq, sched, units);
   else if (a->dtype == QSDPA_F16)
-    merge_kernel<F16, false><<<grid, dim3(256), 0, stream>>>(part_acc, part_ml, a->D, num_splits, a->H_q,
-                                                             out, a->out.stride_b, a->out.stride_h, sched, units);
+    merge_kernel<F16, false><<<grid, dim3(256), 0, stream>>>(part_acc, part_ml, a->D, num_splits, a->H_q, qL,
+                                                             out, a->out.stride_b, a->out.stride_h, o_sq, sched, units);
   else
-    merge_kernel<BF16, false><<<grid, dim3(256), 0, stream>>>(part_acc, part_ml, a->D, num_splits, a->H_q,
-                                                              out, a->out.stride_b, a->out.stride_h, sched, units);
+    merge_kernel<BF16, false><<<grid, dim3(256), 0, stream>>>(part_acc, part_ml, a->D, num_splits, a->H_q, qL,
+                                                              out, a->out.stride_b, a->out.stride_h, o_sq, sched, units);
   return check_launch("merge");
 }
 

@@ -1,6 +1,5 @@
-// Device helpers, launch parameters and host-side set-up shared by the two
-// MFMA decode kernels (decode_mfma.hip: K / V tiles in registers;
-// decode_lds.hip: K / V / scale / bias tiles copied straight into LDS).
+// Device helpers, launch parameters and host-side set-up of the MFMA decode
+// kernel (decode_mfma.hip).
 #pragma once
 
 #include <algorithm>
@@ -22,7 +21,6 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef __bf16 b8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
-typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 
 struct MfmaParams {
   int B, Hq, Hkv, N, G, hb_count, num_splits;
@@ -52,6 +50,10 @@ struct MfmaParams {
   float* part_ml;
   int units;   // > 0: balanced schedule of a left-padded batch over this many units
   int* sched;  // (P_b, n_b) per sequence, written for the merge when units > 0
+  // Query positions: the G * qL rows of a kv head are (position v / G, head
+  // v % G); a block takes 16 consecutive rows.
+  int qL, causal;
+  int64_t q_sq, o_sq, m_sq;  // position strides of q, out and the mask
 };
 
 static_assert(kTile == kSchedTile, "the balanced schedule counts the decode's key tiles");
@@ -156,26 +158,6 @@ __device__ __forceinline__ f4 mfma(const uint32_t a[4], const uint32_t b[4], f4 
                                                    0, 0, 0);
 }
 
-// 16x16x16 f16 MFMA (k = 4 values per lane): the bias products.
-__device__ __forceinline__ f4 mfma16_f16(const uint32_t a[2], const uint32_t b[2], f4 c) {
-  const uint2 av = {a[0], a[1]};
-  const uint2 bv = {b[0], b[1]};
-  return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(h4, av), __builtin_bit_cast(h4, bv), c, 0, 0, 0);
-}
-
-// Nonzero when some 16-bit half of the float16 pair x has |value| >= 64 (or
-// is inf / NaN): adding 0x2C00 to a magnitude >= 0x5400 sets bit 15.
-__device__ __forceinline__ uint32_t f16x2_ge64(uint32_t x) {
-  return ((x & 0x7FFF7FFFu) + 0x2C002C00u) & 0x80008000u;
-}
-__device__ __forceinline__ uint32_t f16x2_mul(uint32_t a, uint32_t b) {
-  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, a) * __builtin_bit_cast(f16x2, b));
-}
-constexpr uint32_t kNeg1024 = 0xE400E400u;  // -1024.0 in both halves
-constexpr uint32_t kNeg64 = 0xD400D400u;    // -64.0 in both halves
-constexpr uint32_t kF16x2One = 0x3C003C00u;     // 1.0 in both halves
-constexpr uint32_t kF16x2TwoM11 = 0x10001000u;  // 2^-11 in both halves
-
 __device__ __forceinline__ float mask_value(const MfmaParams& p, int64_t o) {
   switch (p.mask_kind) {
     case QSDPA_BOOL:
@@ -210,11 +192,16 @@ inline MfmaParams mfma_params(const qsdpa_decode_args* a, int num_splits, float*
   MfmaParams p;
   p.B = a->B; p.Hq = a->H_q; p.Hkv = a->H_kv; p.N = a->N;
   p.G = a->H_q / a->H_kv;
-  p.hb_count = (p.G + 15) / 16;
+  p.qL = a->q_len > 1 ? a->q_len : 1;
+  p.causal = a->causal != 0;
+  p.hb_count = (p.G * p.qL + 15) / 16;
   p.num_splits = num_splits;
   p.qscale = a->scale * kLog2e;
   p.has_bias = a->k_biases.ptr != nullptr;
   p.q = static_cast<const uint16_t*>(a->q.ptr); p.q_sb = a->q.stride_b; p.q_sh = a->q.stride_h;
+  p.q_sq = p.qL > 1 ? a->q.stride_n : 0;
+  p.o_sq = p.qL > 1 ? a->out.stride_n : 0;
+  p.m_sq = p.qL > 1 ? a->mask_stride_q : 0;
   p.kp = static_cast<const uint32_t*>(a->k_packed.ptr);
   p.kp_sb = a->k_packed.stride_b; p.kp_sh = a->k_packed.stride_h; p.kp_sn = a->k_packed.stride_n;
   p.vp = static_cast<const uint32_t*>(a->v_packed.ptr);

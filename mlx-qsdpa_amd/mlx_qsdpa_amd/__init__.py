@@ -27,8 +27,10 @@ def cache_sdpa(q, k_quant, v_quant, cache, scale=None, mask=None, crossover=None
                kv_start=None):
     """Attention over a quantized cache with length-based dispatch.
 
-    mlx_qsdpa/__init__.py:12-68: prefill (qL > 1) or N < crossover goes
-    through dequantize + attention; otherwise the fused quantized decode.
+    mlx_qsdpa/__init__.py:12-68: N < crossover goes through dequantize +
+    attention; otherwise the fused quantized kernel.  Prefill (qL > 1),
+    which the reference always dequantizes, runs fused where the
+    matrix-core kernel takes the shape.
     ``crossover=None`` uses DEFAULT_CROSSOVER.  ``kv_start`` (extension) is
     forwarded to quantized_sdpa (or folded into the mask on the fallback).
     """
@@ -39,9 +41,11 @@ def cache_sdpa(q, k_quant, v_quant, cache, scale=None, mask=None, crossover=None
         scale = D ** -0.5
     if crossover is None:
         crossover = DEFAULT_CROSSOVER
-    if qL > 1 or N < crossover:
+    if qL == 1 and N < crossover:
         return fallback_sdpa(q, k_quant, v_quant, bits=cache.bits, group_size=cache.group_size,
                              scale=scale, mask=mask, kv_start=kv_start)
+    # qL > 1: the fused kernel where it takes the shape, else the reference's
+    # dequantize + attention (quantized_sdpa decides).
     return quantized_sdpa(q, k_quant[0], v_quant[0], k_quant[1], v_quant[1], k_quant[2],
                           v_quant[2], scale=scale, mask=mask, bits=cache.bits,
                           group_size=cache.group_size, kv_start=kv_start)

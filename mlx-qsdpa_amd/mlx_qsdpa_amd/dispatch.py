@@ -1,7 +1,7 @@
 """quantized_sdpa: validation and routing onto the HIP decode kernels.
 
 Mirrors mlx_qsdpa/dispatch.py:8-111 (same signature, same ValueError set,
-same defaults for ``scale`` and for missing biases), with three MI355X
+same defaults for ``scale`` and for missing biases), with four MI355X
 choices:
 
 * Masked decode runs in-kernel (bool keep-mask or additive mask), where the
@@ -12,15 +12,19 @@ choices:
 * ``kv_start`` (extension) skips keys before a per-sequence start index, the
   left padding of a batched cache, without reading them.
 
-Prefill (qL > 1) dequantizes with the HIP kernel and runs float32 attention
-with torch on the GPU (the reference's fallback, dispatch.py:68-83).
+* Several query positions (qL > 1: speculative or chunked decoding,
+  prefill) run on the fused matrix-core kernel, including mask="causal"
+  (aligned to the last key), where the reference dequantizes and runs SDPA.
+  Shapes that kernel does not take (D = 64, unaligned views) keep the
+  reference's path: HIP dequantize, then float32 attention with torch on
+  the GPU (dispatch.py:68-83).
 """
 
 from __future__ import annotations
 
 import torch
 
-from . import kernels
+from . import _lib, kernels
 
 
 def _validate(q, packed_k, packed_v, bits, group_size):
@@ -149,18 +153,21 @@ def quantized_sdpa(
     if scale is None:
         scale = D ** -0.5                                          # dispatch.py:86-87
 
-    if qL > 1:                                                     # dispatch.py:68-83
-        return fallback_sdpa(q, (packed_k, k_scales, k_biases), (packed_v, v_scales, v_biases),
-                             bits=bits, group_size=group_size, scale=scale, mask=mask,
-                             kv_start=kv_start)
+    if qL > 1 and not _fused_takes(q, packed_k, packed_v, k_scales, v_scales, k_biases,
+                                   v_biases, scale, bits, group_size):
+        return fallback_sdpa(q, (packed_k, k_scales, k_biases),    # dispatch.py:68-83
+                             (packed_v, v_scales, v_biases), bits=bits, group_size=group_size,
+                             scale=scale, mask=mask, kv_start=kv_start)
 
     has_biases = k_biases is not None and v_biases is not None     # dispatch.py:89-94
     if not has_biases:
         k_biases = v_biases = None
+    causal = False
     if isinstance(mask, str):
         if mask != "causal":
             raise ValueError(f"unknown mask {mask!r}")
-        mask = None                                                # qL == 1: sees every key
+        causal = qL > 1                                            # qL == 1: sees every key
+        mask = None
 
     if num_splits is None:
         if threshold is None:
@@ -174,4 +181,21 @@ def quantized_sdpa(
             num_splits = max(2, auto)
     return kernels.decode(q, packed_k, packed_v, k_scales, v_scales, k_biases, v_biases,
                           scale=scale, bits=bits, group_size=group_size, mask=mask,
-                          kv_start=kv_start, num_splits=num_splits)
+                          kv_start=kv_start, num_splits=num_splits, causal=causal)
+
+
+def _fused_takes(q, packed_k, packed_v, k_scales, v_scales, k_biases, v_biases, scale, bits,
+                 group_size):
+    """Whether the fused kernel takes several query positions for these
+    inputs (the matrix-core path: D 128 or 256, aligned views).  Extension:
+    the reference sends every qL > 1 call to dequantize + attention."""
+    if k_biases is None or v_biases is None:
+        k_biases = v_biases = None
+    try:
+        kernels.decode_plan(q, packed_k, packed_v, k_scales, v_scales, k_biases, v_biases,
+                            scale=scale, bits=bits, group_size=group_size)
+    except _lib.QsdpaError as e:
+        if e.code == _lib.QSDPA_ERR_UNSUPPORTED:
+            return False
+        raise
+    return True

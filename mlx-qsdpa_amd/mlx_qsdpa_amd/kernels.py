@@ -155,11 +155,11 @@ def dequantize(packed: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor 
 # decode
 # ---------------------------------------------------------------------------
 def _decode_args(q, pk, pv, ks, vs, kb, vb, out, scale, bits, group_size, mask, kv_start,
-                 num_splits):
+                 num_splits, causal=False):
     B, Hq, qL, D = q.shape
     _, Hkv, N, _ = pk.shape
-    if qL != 1:
-        raise ValueError("the fused decode takes one query position (qL == 1)")
+    if qL < 1:
+        raise ValueError("q must hold at least one query position")
     if bits not in (4, 8) or D % group_size:
         raise ValueError(f"bad bits={bits} / group_size={group_size} for D={D}")
     for name, t, inner, dt in (("packed_k", pk, D * bits // 32, torch.uint32),
@@ -171,11 +171,12 @@ def _decode_args(q, pk, pv, ks, vs, kb, vb, out, scale, bits, group_size, mask, 
         _expect_shape(name, t, (B, Hkv, N, inner))
         if t is not None and t.dtype != dt:
             raise ValueError(f"{name}: dtype {t.dtype}, expected {dt}")
-    _expect_shape("out", out, (B, Hq, 1, D))
+    _expect_shape("out", out, (B, Hq, qL, D))
     if kv_start is not None and tuple(kv_start.shape) != (B,):
         raise ValueError(f"kv_start must have shape ({B},)")
     mview = _lib.View(None, 0, 0, 0)
     mcode = 0
+    mask_sq = 0
     if mask is not None:
         if mask.dtype not in _MASK_CODE:
             raise ValueError(f"unsupported mask dtype {mask.dtype}")
@@ -184,15 +185,16 @@ def _decode_args(q, pk, pv, ks, vs, kb, vb, out, scale, bits, group_size, mask, 
             m = m.unsqueeze(0)
         if m.shape[-1] != N:
             raise ValueError(f"mask last dim {m.shape[-1]} != number of keys {N}")
-        if m.shape[-2] != 1:
-            raise ValueError("decode mask must have a query dim of 1")
-        m = m.expand(B, Hq, 1, N)
+        if m.shape[-2] not in (1, qL):
+            raise ValueError(f"mask query dim {m.shape[-2]} must be 1 or {qL}")
+        m = m.expand(B, Hq, m.shape[-2], N)
         if m.stride(-1) != 1:
             m = m.contiguous()
         if m.dtype == torch.bool:
             m = m.view(torch.uint8)
         s = m.stride()
         mview = _lib.View(m.data_ptr(), s[0], s[1], s[3])
+        mask_sq = s[2] if m.shape[-2] > 1 else 0
         mcode = _MASK_CODE[mask.dtype]
         mask = m
     ks_ptr = None
@@ -211,11 +213,16 @@ def _decode_args(q, pk, pv, ks, vs, kb, vb, out, scale, bits, group_size, mask, 
     a.mask, a.mask_dtype = mview, mcode
     a.kv_start = ks_ptr
     a.num_splits = int(num_splits)
+    a.q_len = qL
+    a.causal = int(bool(causal))
+    a.mask_stride_q = mask_sq
     return a, mask
 
 
 def decode_plan(q, pk, pv, ks, vs, kb, vb, *, scale, bits, group_size, num_splits=0):
-    """(num_splits, workspace_bytes) the library would use for these inputs."""
+    """(num_splits, workspace_bytes) the library would use for these inputs.
+
+    Raises QsdpaError (code QSDPA_ERR_UNSUPPORTED) for inputs no kernel takes."""
     out = torch.empty_like(q)
     a, _ = _decode_args(q, pk, pv, ks, vs, kb, vb, out, scale, bits, group_size, None, None,
                         num_splits)
@@ -277,8 +284,12 @@ class DecodePlan:
 
 
 def decode(q, pk, pv, ks, vs, kb, vb, *, scale, bits, group_size, mask=None, kv_start=None,
-           num_splits=0, out=None, workspace=None, prof_events=None):
-    """Fused quantized decode; returns out [B, H_q, 1, D] (dtype of q).
+           num_splits=0, out=None, workspace=None, prof_events=None, causal=False):
+    """Fused quantized attention; returns out [B, H_q, qL, D] (dtype of q).
+
+    qL > 1 query positions (speculative or chunked decoding, prefill) run on
+    the matrix-core kernel; ``causal`` aligns the causal mask to the last
+    key (query i sees keys t <= N - qL + i).
 
     ``prof_events``: optional (begin, end) raw hipEvent_t handles recorded
     around the main decode kernel (see qsdpa_decode_args.prof_begin).
@@ -290,7 +301,7 @@ def decode(q, pk, pv, ks, vs, kb, vb, *, scale, bits, group_size, mask=None, kv_
     if kv_start is not None:
         kv_start = kv_start.to(device=q.device, dtype=torch.int32).contiguous()
     a, keep_alive = _decode_args(q, pk, pv, ks, vs, kb, vb, out, scale, bits, group_size, mask,
-                                 kv_start, num_splits)
+                                 kv_start, num_splits, causal)
     lib = _lib.load()
     n = ctypes.c_int32(0)
     ws = _lib.check(lib.qsdpa_decode_workspace_size(ctypes.byref(a), ctypes.byref(n)))

@@ -233,6 +233,85 @@ def test_kv_start_balanced_schedule(device, case):
         assert np.array_equal(got, again), f"splits={splits}: repeated call differs"
 
 
+def _fused(inp, device, **kw):
+    """The fused kernel through the C ABI (no routing, no fallback)."""
+    g = to_dev(inp, device)
+    D = inp["q"].shape[-1]
+    out = kernels.decode(g["q"], g["kp"], g["vp"], g["ks"], g["vs"], g["kb"], g["vb"],
+                         scale=D ** -0.5, bits=inp["bits"], group_size=inp["gs"], **kw)
+    torch.cuda.synchronize()
+    return to_np(out)
+
+
+@pytest.mark.parametrize("case", [
+    # (B, Hq, Hkv, N, D, bits, gs, dtype, qL, mask)
+    (2, 32, 2, 300, 256, 4, 32, "f16", 4, "causal"),     # G=16: 4 row blocks of one position
+    (1, 8, 2, 1000, 128, 4, 64, "f16", 3, None),        # G=4: 12 rows, one partial block
+    (2, 4, 4, 513, 128, 8, 128, "bf16", 33, "causal"),  # G=1: 33 positions, 3 blocks
+    (1, 16, 4, 700, 128, 8, 64, "bf16", 5, "additive"),  # per (head, position) additive mask
+    (3, 8, 1, 400, 256, 4, 64, "f16", 2, "bool"),        # bool mask broadcast over heads
+    (1, 16, 2, 40, 128, 4, 32, "f16", 48, "causal"),     # qL > N: the first rows see no key
+], ids=["G16-q4-causal", "G4-q3", "G1-q33-causal-bf16", "G4-q5-additive", "G8-q2-bool",
+        "q48-over-N40-causal"])
+def test_multi_query_matches_oracle(device, case):
+    """qL > 1 query positions (speculative / chunked decoding, prefill) on the
+    fused kernel: rows are (position, head) pairs of a kv head; causal is
+    aligned to the last key; masks index (batch, head, position, key)."""
+    B, Hq, Hkv, N, D, bits, gs, dtype, qL, mk = case
+    rng = np.random.default_rng(41 + qL)
+    inp = make_inputs(rng, B, Hq, Hkv, N, D, bits, gs, dtype=dtype)
+    inp["q"] = affine.random_T(rng, (B, Hq, qL, D), dtype)
+    kw, m_np = {}, None
+    if mk == "causal":
+        kw["causal"], m_np = True, "causal"
+    elif mk == "additive":
+        add = rng.standard_normal((1, Hq, qL, N)).astype(np.float32)
+        add[rng.random(add.shape) < 0.2] = -np.inf
+        add = add.astype(np.float16).astype(np.float32)
+        m_np, kw["mask"] = add, torch.from_numpy(add).to(device, torch.float16)
+    elif mk == "bool":
+        keep = rng.random((B, 1, qL, N)) < 0.7
+        keep[..., 0] = True
+        m_np, kw["mask"] = keep, torch.from_numpy(keep).to(device)
+    want = oracle_out(inp, mask=m_np)
+    for splits in (0, 1, 3):
+        got = _fused(inp, device, num_splits=splits, **kw)
+        assert got.shape == (B, Hq, qL, D)
+        assert_close(got, want, f"qL={qL} splits={splits}")
+
+
+def test_multi_query_kv_start_causal(device):
+    """qL > 1 with left padding (balanced schedule) and causal together."""
+    rng = np.random.default_rng(47)
+    B, Hq, Hkv, N, D, qL = 4, 16, 4, 600, 128, 6
+    inp = make_inputs(rng, B, Hq, Hkv, N, D, 4, 64)
+    inp["q"] = affine.random_T(rng, (B, Hq, qL, D), "f16")
+    starts = np.array([0, 100, 597, 600])
+    qi = np.arange(qL)[:, None] + (N - qL)
+    keep = (np.arange(N)[None, None, :] >= starts[:, None, None]) & (qi >= np.arange(N)[None, :])[None]
+    want = oracle_out(inp, mask=keep[:, None])
+    ks = torch.tensor(starts, dtype=torch.int32, device=device)
+    for splits in (0, 1, 4):
+        assert_close(_fused(inp, device, kv_start=ks, num_splits=splits, causal=True), want,
+                     f"kv_start causal splits={splits}")
+
+
+def test_multi_query_routes_to_fused_kernel(device, monkeypatch):
+    """quantized_sdpa with qL > 1 and mask="causal" runs the fused kernel
+    (the dequantize + attention fallback is made to fail)."""
+    from mlx_qsdpa_amd import dispatch
+
+    def no_fallback(*a, **k):
+        raise AssertionError("fallback used")
+
+    monkeypatch.setattr(dispatch, "fallback_sdpa", no_fallback)
+    rng = np.random.default_rng(48)
+    inp = make_inputs(rng, 1, 8, 2, 256, 128, 4, 64)
+    inp["q"] = affine.random_T(rng, (1, 8, 7, 128), "f16")
+    got = run(inp, device, mask="causal")
+    assert_close(got, oracle_out(inp, mask="causal"), "routed causal")
+
+
 def test_fully_masked_row_is_zero(device):
     rng = np.random.default_rng(14)
     inp = make_inputs(rng, 2, 4, 2, 64, 128, 4, 32)
