@@ -69,6 +69,9 @@ def parse_args(argv=None):
     ap.add_argument("--kv-bytes", type=float, default=1.2e9,
                     help="distinct KV bytes cycled through (defeats the MALL)")
     ap.add_argument("--splits", type=int, default=0, help="0 = library heuristic")
+    ap.add_argument("--qlen", type=int, default=1,
+                    help="query positions per call; > 1 times causal multi-query attention "
+                         "(fused vs dequantize + attention) instead of the decode step")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="time budget of the CPU baseline sample (0 = skip)")
     ap.add_argument("--seed", type=int, default=0)
@@ -307,6 +310,97 @@ def run_c4(args) -> int:
     return 0
 
 
+def run_multi_query(args) -> int:
+    """--qlen L > 1: L causal query positions per (batch, head) over the
+    config's cache (speculative or chunked decoding, prefill) on the fused
+    kernel, with the reference's path for such calls -- HIP dequantize, then
+    float32 attention with torch (mlx_qsdpa dispatch.py:68-83) -- timed on
+    the same inputs in the same run."""
+    import numpy as np
+    import torch
+
+    from mlx_qsdpa_amd import dispatch, kernels, metric
+
+    cfg = CONFIGS[args.config]
+    B, Hq, Hkv, D, bits, gs, dt, N0, _ = cfg
+    N, L = args.n or N0, args.qlen
+    device = torch.device("cuda:0")
+    T = torch.float16 if dt == "f16" else torch.bfloat16
+    kv_set_bytes = B * N * metric.kv_bytes_per_token(Hkv, D, bits, gs)
+    n_sets = max(2, math.ceil(args.kv_bytes / kv_set_bytes))
+    sets = make_sets(cfg, N, n_sets, device, args.seed)
+    g = torch.Generator(device=device)
+    g.manual_seed(args.seed + 1)
+    qs = [torch.randn((B, Hq, L, D), generator=g, device=device, dtype=torch.float32).to(T)
+          for _ in range(n_sets)]
+    plans = [kernels.DecodePlan(qq, kq[0], vq[0], kq[1], vq[1], kq[2], vq[2], scale=D ** -0.5,
+                                bits=bits, group_size=gs, num_splits=args.splits, causal=True)
+             for qq, (_, kq, vq) in zip(qs, sets)]
+    splits = plans[0].num_splits
+
+    def fallback(i):
+        _, kq, vq = sets[i]
+        return dispatch.fallback_sdpa(qs[i], kq, vq, bits=bits, group_size=gs, scale=D ** -0.5,
+                                      mask="causal")
+
+    got = plans[0]().float()
+    want = fallback(0).float()
+    max_diff = float((got - want).abs().max())
+    for i in range(args.warmup):
+        plans[i % n_sets]()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        plans[i % n_sets]()
+    torch.cuda.synchronize()
+    us = (time.perf_counter() - t0) / args.steps * 1e6
+    hip = HipEvents()
+    ev_b, ev_e = hip.create(args.steps), hip.create(args.steps)
+    for i in range(args.steps):
+        plans[i % n_sets]((ev_b[i], ev_e[i]))
+    torch.cuda.synchronize()
+    kern_ms = [hip.elapsed_ms(ev_b[i], ev_e[i]) for i in range(args.steps)]
+    hip.destroy(ev_b + ev_e)
+    kern_us = float(np.mean(kern_ms)) * 1e3
+    fb_steps = max(5, min(args.steps, 50))
+    for i in range(3):
+        fallback(i % n_sets)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(fb_steps):
+        fallback(i % n_sets)
+    torch.cuda.synchronize()
+    fb_us = (time.perf_counter() - t0) / fb_steps * 1e6
+
+    # Causal keys per query row, summed: position i sees N - L + i + 1 keys.
+    pairs = sum(max(0, min(N, N - L + i + 1)) for i in range(L))
+    flops = 4.0 * B * Hq * pairs * D
+    tflops = flops / (kern_us * 1e-6) / 1e12
+    peak = 2500.0  # dense fp16 / bf16 MFMA
+    print(f"bench: {args.config} qL={L} causal: fused {us:.2f} us/call wall, kernel {kern_us:.2f} us "
+          f"({tflops:.1f} TFLOP/s); dequantize + attention {fb_us:.2f} us; max |diff| {max_diff:.2e}",
+          file=sys.stderr, flush=True)
+    workload = (f"{args.config}-q{L}: causal attention B={B} H_q={Hq} H_kv={Hkv} D={D} {bits}-bit "
+                f"gs={gs} {dt} N={N} qL={L}")
+    line = {
+        "metric": f"µs per attention call, {L} causal query positions (fused vs dequantize + attention)",
+        "value": round(us, 3), "unit": "us/call", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(us / 1e3, 6), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": dt, "data": "synthetic",
+        "config": {"workload": workload, "B": B, "H_q": Hq, "H_kv": Hkv, "D": D, "N": N, "qL": L,
+                   "bits": bits, "group_size": gs, "num_splits": splits, "kv_sets": n_sets},
+        "reference_path_us": round(fb_us, 3),
+        "speedup_vs_reference_path": round(fb_us / us, 2),
+        "max_abs_diff_vs_reference_path": max_diff,
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": peak, "unit": "TFLOP/s",
+                     "frac": round(tflops / peak, 4), "traffic": None, "kernel_us": round(kern_us, 3),
+                     "kernel_us_p5_p50_p95": _pcts(kern_ms), "flops": flops},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main(argv=None) -> int:
     args = parse_args(argv)
     if args.gpus != 1:
@@ -315,6 +409,8 @@ def main(argv=None) -> int:
         return 2
     if args.config == "c4":
         return run_c4(args)
+    if args.qlen > 1:
+        return run_multi_query(args)
     import numpy as np
     import torch
 

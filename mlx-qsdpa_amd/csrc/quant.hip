@@ -29,10 +29,11 @@ struct QuantParams {
   int64_t z_sb, z_sh, z_sn;
 };
 
-// Min / max over aligned groups of L consecutive lanes (L in {4, 8, 16});
-// every lane of a group gets the result.  Exact in any order.
+// Min / max over aligned groups of L consecutive lanes (L in {1, 4, 8,
+// 16}); every lane of a group gets the result.  Exact in any order.
 template <int L>
 __device__ __forceinline__ void group_minmax(float& lo, float& hi) {
+  if constexpr (L == 1) return;
   lo = fminf(lo, dpp_f32<0xB1>(lo));
   hi = fmaxf(hi, dpp_f32<0xB1>(hi));
   lo = fminf(lo, dpp_f32<0x4E>(lo));
@@ -55,18 +56,20 @@ struct QuantJobs {
   QuantParams p[kMaxJobs];
 };
 
-// One group of GS values is spread over L = GS / 8 consecutive lanes, 8
-// values (one 16-byte piece when VEC, i.e. the rows are 16-byte aligned) per
-// lane; the group's min / max are reduced across the L lanes and every lane
-// quantizes and packs its own 8 values.  The latency of a one-row append is
-// then that of 8 values, not GS.  A group's lanes are all in range or all
-// out of it, so the cross-lane steps never read an exited lane.  I is the
-// index type: 32-bit whenever the launch's thread count fits.
-template <typename Tag, int BITS, int GS, bool VEC, typename I>
+// One group of GS values is spread over L consecutive lanes, GS / L values
+// per lane (16-byte pieces when VEC, i.e. the rows are 16-byte aligned); the
+// group's min / max are reduced across the L lanes and every lane quantizes
+// and packs its own values.  L = GS / 8 for small jobs (a one-row append:
+// its latency is that of 8 values, not GS); L = 1 for large ones, which
+// fill the GPU anyway and then do not repeat the scale's divisions in every
+// lane.  A group's lanes are all in range or all out of it, so the
+// cross-lane steps never read an exited lane.  I is the index type: 32-bit
+// whenever the launch's thread count fits.
+template <typename Tag, int BITS, int GS, int L, bool VEC, typename I>
 __global__ __launch_bounds__(256) void quantize_kernel(QuantJobs jobs) {
-  constexpr int L = GS / 8;
+  constexpr int VALS = GS / L;  // values per lane, a multiple of 8
   constexpr int PER = 32 / BITS;
-  constexpr int WORDS = 8 / PER;  // packed words per lane: 1 (4-bit) or 2 (8-bit)
+  constexpr int WORDS = VALS / PER;  // packed words per lane
   constexpr float kBins = static_cast<float>((1 << BITS) - 1);
   const QuantParams& p = jobs.p[blockIdx.y];
   const int ng = p.D / GS;
@@ -82,24 +85,27 @@ __global__ __launch_bounds__(256) void quantize_kernel(QuantJobs jobs) {
   const int h = static_cast<int>(row % p.H);
   const int b = static_cast<int>(row / p.H);
 
-  const uint16_t* src = p.src + off3(b, h, s, p.s_sb, p.s_sh, p.s_sn) + g * GS + part * 8;
-  uint16_t raw[8];
+  const uint16_t* src = p.src + off3(b, h, s, p.s_sb, p.s_sh, p.s_sn) + g * GS + part * VALS;
+  uint16_t raw[VALS];
   if constexpr (VEC) {
-    const uint4 v = *reinterpret_cast<const uint4*>(src);
-    const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      raw[2 * k] = static_cast<uint16_t>(wv[k]);
-      raw[2 * k + 1] = static_cast<uint16_t>(wv[k] >> 16);
+    for (int i = 0; i < VALS / 8; ++i) {
+      const uint4 v = reinterpret_cast<const uint4*>(src)[i];
+      const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        raw[8 * i + 2 * k] = static_cast<uint16_t>(wv[k]);
+        raw[8 * i + 2 * k + 1] = static_cast<uint16_t>(wv[k] >> 16);
+      }
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) raw[i] = src[i];
+    for (int i = 0; i < VALS; ++i) raw[i] = src[i];
   }
 
   float w_min = __builtin_huge_valf(), w_max = -__builtin_huge_valf();
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < VALS; ++i) {
     const float v = to_f32<Tag>(raw[i]);
     w_min = fminf(w_min, v);
     w_max = fmaxf(w_max, v);
@@ -115,7 +121,7 @@ __global__ __launch_bounds__(256) void quantize_kernel(QuantJobs jobs) {
   const float bias = nz ? edge : 0.0f;
 
   const int t = p.t0 + s;
-  uint32_t* dst = p.dp + off3(b, h, t, p.p_sb, p.p_sh, p.p_sn) + (g * GS + part * 8) / PER;
+  uint32_t* dst = p.dp + off3(b, h, t, p.p_sb, p.p_sh, p.p_sn) + (g * GS + part * VALS) / PER;
 #pragma unroll
   for (int w = 0; w < WORDS; ++w) {
     uint32_t word = 0;
@@ -134,22 +140,33 @@ __global__ __launch_bounds__(256) void quantize_kernel(QuantJobs jobs) {
   }
 }
 
-template <typename Tag, int BITS, int GS>
-void launch_quantize_gs(const QuantJobs& j, bool vec, bool wide, dim3 grid, hipStream_t stream) {
-  if (wide) {
-    if (vec) quantize_kernel<Tag, BITS, GS, true, int64_t><<<grid, dim3(256), 0, stream>>>(j);
-    else quantize_kernel<Tag, BITS, GS, false, int64_t><<<grid, dim3(256), 0, stream>>>(j);
+// Jobs with at least this many groups take one lane per group.
+constexpr int64_t kWideJobGroups = 1 << 18;
+
+template <typename Tag, int BITS, int GS, int L>
+void launch_quantize_l(const QuantJobs& j, bool vec, int64_t groups, int count, hipStream_t stream) {
+  const int64_t blocks = (groups * L + 255) / 256;
+  const dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>(count));
+  if (blocks * 256 >= (int64_t(1) << 32)) {
+    if (vec) quantize_kernel<Tag, BITS, GS, L, true, int64_t><<<grid, dim3(256), 0, stream>>>(j);
+    else quantize_kernel<Tag, BITS, GS, L, false, int64_t><<<grid, dim3(256), 0, stream>>>(j);
   } else {
-    if (vec) quantize_kernel<Tag, BITS, GS, true, uint32_t><<<grid, dim3(256), 0, stream>>>(j);
-    else quantize_kernel<Tag, BITS, GS, false, uint32_t><<<grid, dim3(256), 0, stream>>>(j);
+    if (vec) quantize_kernel<Tag, BITS, GS, L, true, uint32_t><<<grid, dim3(256), 0, stream>>>(j);
+    else quantize_kernel<Tag, BITS, GS, L, false, uint32_t><<<grid, dim3(256), 0, stream>>>(j);
   }
 }
 
+template <typename Tag, int BITS, int GS>
+void launch_quantize_gs(const QuantJobs& j, bool vec, int64_t groups, int count, hipStream_t stream) {
+  if (groups >= kWideJobGroups) launch_quantize_l<Tag, BITS, GS, 1>(j, vec, groups, count, stream);
+  else launch_quantize_l<Tag, BITS, GS, GS / 8>(j, vec, groups, count, stream);
+}
+
 template <typename Tag, int BITS>
-void launch_quantize_bits(const QuantJobs& j, int gs, bool vec, bool wide, dim3 grid, hipStream_t stream) {
-  if (gs == 32) launch_quantize_gs<Tag, BITS, 32>(j, vec, wide, grid, stream);
-  else if (gs == 64) launch_quantize_gs<Tag, BITS, 64>(j, vec, wide, grid, stream);
-  else launch_quantize_gs<Tag, BITS, 128>(j, vec, wide, grid, stream);
+void launch_quantize_bits(const QuantJobs& j, int gs, bool vec, int64_t groups, int count, hipStream_t stream) {
+  if (gs == 32) launch_quantize_gs<Tag, BITS, 32>(j, vec, groups, count, stream);
+  else if (gs == 64) launch_quantize_gs<Tag, BITS, 64>(j, vec, groups, count, stream);
+  else launch_quantize_gs<Tag, BITS, 128>(j, vec, groups, count, stream);
 }
 
 struct DequantParams {
@@ -197,7 +214,7 @@ __global__ __launch_bounds__(256) void dequantize_kernel(DequantParams p) {
 int launch_quantize(const qsdpa_quantize_args* const* jobs, int count, hipStream_t stream) {
   if (count < 1 || count > kMaxJobs) return fail(QSDPA_ERR_INVALID, "quantize: %d jobs (1..%d)", count, kMaxJobs);
   QuantJobs j{};
-  int64_t most = 0;  // threads of the largest job: 8 values each, GS / 8 per group
+  int64_t most = 0;  // groups of the largest job
   bool vec = true;
   for (int i = 0; i < count; ++i) {
     const qsdpa_quantize_args* a = jobs[i];
@@ -211,25 +228,22 @@ int launch_quantize(const qsdpa_quantize_args* const* jobs, int count, hipStream
     p.c_sb = a->dst_scales.stride_b; p.c_sh = a->dst_scales.stride_h; p.c_sn = a->dst_scales.stride_n;
     p.db = static_cast<uint16_t*>(const_cast<void*>(a->dst_biases.ptr));
     p.z_sb = a->dst_biases.stride_b; p.z_sh = a->dst_biases.stride_h; p.z_sn = a->dst_biases.stride_n;
-    most = std::max<int64_t>(most, static_cast<int64_t>(a->B) * a->H * a->S * (a->D / 8));
+    most = std::max<int64_t>(most, static_cast<int64_t>(a->B) * a->H * a->S * (a->D / a->group_size));
     // 16-byte loads need 16-byte aligned rows (a lane's offset in the row
     // is a multiple of 8 elements).
     vec = vec && aligned(a->src.ptr, 16) && a->src.stride_b % 8 == 0 && a->src.stride_h % 8 == 0 &&
           a->src.stride_n % 8 == 0;
   }
   if (most == 0) return QSDPA_OK;
-  const int64_t blocks = (most + 255) / 256;
-  if (blocks >= (int64_t(1) << 31)) return fail(QSDPA_ERR_UNSUPPORTED, "quantize: %lld rows too many",
-                                                static_cast<long long>(most));
-  const bool wide = blocks * 256 >= (int64_t(1) << 32);
-  const dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>(count));
+  if (most * 16 / 256 >= (int64_t(1) << 31))
+    return fail(QSDPA_ERR_UNSUPPORTED, "quantize: %lld groups too many", static_cast<long long>(most));
   const qsdpa_quantize_args* a = jobs[0];
   if (a->dtype == QSDPA_F16) {
-    if (a->bits == 4) launch_quantize_bits<F16, 4>(j, a->group_size, vec, wide, grid, stream);
-    else launch_quantize_bits<F16, 8>(j, a->group_size, vec, wide, grid, stream);
+    if (a->bits == 4) launch_quantize_bits<F16, 4>(j, a->group_size, vec, most, count, stream);
+    else launch_quantize_bits<F16, 8>(j, a->group_size, vec, most, count, stream);
   } else {
-    if (a->bits == 4) launch_quantize_bits<BF16, 4>(j, a->group_size, vec, wide, grid, stream);
-    else launch_quantize_bits<BF16, 8>(j, a->group_size, vec, wide, grid, stream);
+    if (a->bits == 4) launch_quantize_bits<BF16, 4>(j, a->group_size, vec, most, count, stream);
+    else launch_quantize_bits<BF16, 8>(j, a->group_size, vec, most, count, stream);
   }
   return check_launch("quantize");
 }

@@ -241,7 +241,7 @@ class DecodePlan:
     """
 
     def __init__(self, q, pk, pv, ks, vs, kb, vb, *, scale, bits, group_size, mask=None,
-                 kv_start=None, num_splits=0, capacity=None):
+                 kv_start=None, num_splits=0, capacity=None, causal=False):
         _require_device(q, pk, pv, ks, vs, kb, vb, mask, kv_start)
         self.q = _inner_contig(q)
         self.out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
@@ -249,7 +249,7 @@ class DecodePlan:
             kv_start = kv_start.to(device=q.device, dtype=torch.int32).contiguous()
         self._refs = (pk, pv, ks, vs, kb, vb, kv_start)
         self.args, self._mask = _decode_args(self.q, pk, pv, ks, vs, kb, vb, self.out, scale, bits,
-                                             group_size, mask, kv_start, num_splits)
+                                             group_size, mask, kv_start, num_splits, causal)
         self.lib = _lib.load()
         n = ctypes.c_int32(0)
         ws = _lib.check(self.lib.qsdpa_decode_workspace_size(ctypes.byref(self.args),

@@ -50,6 +50,21 @@ def test_quantize_kernel_matches_oracle(device, dtype, bits, gs, D):
     assert _bits_equal(to_np(got[2]), want[2], dtype)
 
 
+@pytest.mark.parametrize("dtype,bits,gs", [("f16", 4, 32), ("bf16", 8, 64)])
+def test_quantize_bulk_matches_oracle(device, dtype, bits, gs):
+    """A prompt-sized job (>= 2^18 groups) takes the one-lane-per-group
+    kernel; bit-exact like the per-token appends."""
+    rng = np.random.default_rng(bits * 7 + gs)
+    D = 128
+    S = (1 << 18) * gs // D // 8  # 8 heads x S rows x D / gs groups = 2^18
+    w = affine.random_T(rng, (1, 8, S, D), dtype, outlier_frac=0.01)
+    want = affine.quantize(w, gs, bits, dtype)
+    got = kernels.quantize(from_np(w, torch_dtype(dtype), device), gs, bits)
+    assert np.array_equal(to_np(got[0]), want[0])
+    assert _bits_equal(to_np(got[1]), want[1], dtype)
+    assert _bits_equal(to_np(got[2]), want[2], dtype)
+
+
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
 def test_quantize_into_strided_destination(device, dtype):
     """Writes land at [t0, t0+S) of a capacity-padded buffer; nothing else changes."""
