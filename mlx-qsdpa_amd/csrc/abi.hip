@@ -146,14 +146,17 @@ int decode_plan(const qsdpa_decode_args* a, int* num_splits, int64_t* workspace_
   *num_splits = splits;
   // Partials (B * H_q * splits rows of D + 2 floats), then the balanced
   // schedule's (first unit, units) pair per sequence.
+  // Partial slots per query row: splits, or splits + 1 columns per sequence
+  // (U + B, U = splits * B) under the stream-K schedule of a left-padded
+  // batch; then that schedule's (first column, count) per sequence.
   const int64_t rows = static_cast<int64_t>(a->B) * a->H_q * std::max(a->q_len, 1);
-  *workspace_bytes = splits > 1 ? rows * splits * (a->D + 2) * 4 + 8LL * a->B + 256 : 0;
+  *workspace_bytes = splits > 1 ? rows * (splits + 1) * (a->D + 2) * 4 + 8LL * a->B + 256 : 0;
   return QSDPA_OK;
 }
 
-// A left-padded batch on the MFMA path shares splits * B units out over its
-// sequences in proportion to their lengths (the balanced schedule of
-// common.h) instead of giving every sequence `splits`; 0 = uniform splits.
+// A left-padded batch on the MFMA path runs splits * B equal units of the
+// stream-K schedule (common.h) over its sequences laid end to end, instead
+// of giving every sequence `splits`; 0 = uniform splits.
 int ragged_units(const qsdpa_decode_args* a, int splits) {
   if (!a->kv_start || a->B < 2 || splits < 2 || !mfma_supports(a)) return 0;
   const int64_t units = static_cast<int64_t>(splits) * a->B;
@@ -200,10 +203,10 @@ int qsdpa_decode(const qsdpa_decode_args* args, void* stream) {
                   static_cast<long long>(ws), static_cast<long long>(args->workspace_bytes));
     if (!aligned(args->workspace, 16)) return fail(QSDPA_ERR_INVALID, "workspace not 16-byte aligned");
     part_acc = static_cast<float*>(args->workspace);
-    part_ml = part_acc + static_cast<int64_t>(args->B) * args->H_q * std::max(args->q_len, 1) * splits * args->D;
+    part_ml = part_acc + static_cast<int64_t>(args->B) * args->H_q * std::max(args->q_len, 1) * (splits + 1) * args->D;
   }
   int* sched = part_ml ? reinterpret_cast<int*>(part_ml + static_cast<int64_t>(args->B) * args->H_q *
-                                                              std::max(args->q_len, 1) * splits * 2)
+                                                              std::max(args->q_len, 1) * (splits + 1) * 2)
                        : nullptr;
   const hipStream_t s = static_cast<hipStream_t>(stream);
   // (prof_begin / prof_end ride on the main kernel's own dispatch)
@@ -216,7 +219,7 @@ int qsdpa_decode(const qsdpa_decode_args* args, void* stream) {
   // rows (in the first half of the float32 area).
   if (splits > 1)
     rc = launch_merge(args, splits, part_acc, part_ml, mfma && args->dtype == QSDPA_F16, units ? sched : nullptr,
-                      units, s);
+                      units + args->B, s);
   return rc;
 }
 

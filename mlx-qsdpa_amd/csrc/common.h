@@ -89,17 +89,20 @@ __device__ __forceinline__ int shfl_xor_i32(int x, int mask) {
 }
 
 // ---------------------------------------------------------------------------
-// Balanced split schedule of a left-padded batch (kv_start given, B > 1).
+// Stream-K schedule of a left-padded batch (kv_start given, B > 1).
 // Sequence b holds T_b = ceil((N - kv_start[b]) / 32) key tiles (kv_start
-// clamped to [0, N]).  U units are shared out over the batch: every unit
-// gets at most C tiles, C the smallest budget with sum_b ceil(T_b / C) <= U,
-// and sequence b gets n_b = ceil(T_b / C) units, numbered from
-// P_b = n_0 + ... + n_{b-1}; unit P_b + i owns the sequence's tiles
-// i, i + n_b, i + 2 n_b, ...  The longest unit is then about total / U
-// tiles instead of the longest sequence's T / splits.  Each wave computes
-// the schedule on its own from the B values of kv_start (the results are
-// identical in every wave and workgroup).  Requires U >= B and
-// B * (N / 32 + 1) < 2^31.
+// clamped to [0, N]).  The sequences' tiles are laid end to end, sequence b
+// from P_b = T_0 + ... + T_{b-1}, and unit u of U owns global tiles
+// [u * C, (u + 1) * C), C = ceil(total / U): every unit gets the same work
+// whatever the lengths.  A unit's part in sequence b is a segment with its
+// own partial, at column u + b of the rows' U + B partial slots (distinct:
+// when a unit u' > u also meets a sequence b' < b, sequence b' would have to
+// end after unit u starts and sequence b start before unit u' ends, but b
+// starts after b' ends).  Sequence b's partials are then the consecutive
+// columns u_first + b .. u_last + b, u_first = P_b / C, u_last =
+// (P_b + T_b - 1) / C.  Each wave computes what it needs from the B values
+// of kv_start (identical results everywhere).  Requires B * (N / 32 + 1)
+// < 2^31.
 // ---------------------------------------------------------------------------
 constexpr int kSchedTile = 32;
 
@@ -107,52 +110,6 @@ __device__ __forceinline__ int seq_tiles(const int32_t* kv_start, int b, int N) 
   const int s0 = min(max(kv_start[b], 0), N);
   return (N - s0 + kSchedTile - 1) / kSchedTile;
 }
-
-// The tile budget C (wave-uniform).
-__device__ __forceinline__ int ragged_budget(const int32_t* kv_start, int B, int N, int U) {
-  const int lane = __lane_id();
-  int tot = 0, mx = 0;
-  for (int c0 = 0; c0 < B; c0 += 64) {
-    const int b = c0 + lane;
-    const int t = b < B ? seq_tiles(kv_start, b, N) : 0;
-    tot += t;
-    mx = max(mx, t);
-  }
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    tot += shfl_xor_i32(tot, o);
-    mx = max(mx, shfl_xor_i32(mx, o));
-  }
-  tot = __builtin_amdgcn_readfirstlane(tot);
-  mx = __builtin_amdgcn_readfirstlane(mx);
-  if (tot == 0) return 1;
-  // count(c) = sum_b ceil(T_b / c) falls as c grows; count(c) >= tot / c,
-  // so count fails below ceil(tot / U); it holds at c = max_b T_b (count =
-  // nonempty sequences <= B <= U) and at ceil(tot / (U - B)) (count <=
-  // tot / c + B).  Invariant: lo fails (or is 0), hi holds.
-  int lo = (tot + U - 1) / U - 1;
-  int hi = mx;
-  if (U > B) hi = min(hi, (tot + (U - B) - 1) / (U - B));
-  while (hi - lo > 1) {
-    // 64 candidates at once, lane i testing lo + (i + 1) * step.
-    const int step = (hi - lo + 63) / 64;
-    const int c = min(lo + (lane + 1) * step, hi);
-    int cnt = 0;
-    for (int b = 0; b < B; ++b) cnt += (seq_tiles(kv_start, b, N) + c - 1) / c;
-    const uint64_t ok = __builtin_amdgcn_ballot_w64(cnt <= U);  // lane 63 tests hi: never 0
-    const int first = __builtin_ctzll(ok);
-    const int new_hi = min(lo + (first + 1) * step, hi);
-    lo = first == 0 ? lo : lo + first * step;
-    hi = new_hi;
-  }
-  return hi;
-}
-
-// The (sequence, split within it, splits of the sequence) of unit u under
-// budget C; b = -1 when u is past the last unit with work.
-struct RaggedUnit {
-  int b, split, count;
-};
 
 __device__ __forceinline__ int wave_inclusive_scan(int x) {
   const int lane = __lane_id();
@@ -164,34 +121,57 @@ __device__ __forceinline__ int wave_inclusive_scan(int x) {
   return x;
 }
 
-__device__ __forceinline__ RaggedUnit ragged_unit(const int32_t* kv_start, int B, int N, int C, int u) {
+// Total tiles of the batch (wave-uniform).
+__device__ __forceinline__ int streamk_total(const int32_t* kv_start, int B, int N) {
   const int lane = __lane_id();
-  int base = 0;
+  int tot = 0;
   for (int c0 = 0; c0 < B; c0 += 64) {
     const int b = c0 + lane;
-    const int n = b < B ? (seq_tiles(kv_start, b, N) + C - 1) / C : 0;
-    const int incl = wave_inclusive_scan(n);
-    const int first = base + incl - n;
-    const uint64_t hit = __builtin_amdgcn_ballot_w64(u >= first && u < first + n);
+    tot += b < B ? seq_tiles(kv_start, b, N) : 0;
+  }
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) tot += shfl_xor_i32(tot, o);
+  return __builtin_amdgcn_readfirstlane(tot);
+}
+
+// The sequence holding global tile g (g < total) and its first tile P_b
+// (wave-uniform).
+__device__ __forceinline__ void streamk_find(const int32_t* kv_start, int B, int N, int g, int& b_out,
+                                             int& p_out) {
+  const int lane = __lane_id();
+  int base = 0;
+  b_out = B;
+  p_out = 0;
+  for (int c0 = 0; c0 < B; c0 += 64) {
+    const int b = c0 + lane;
+    const int t = b < B ? seq_tiles(kv_start, b, N) : 0;
+    const int incl = wave_inclusive_scan(t);
+    const int first = base + incl - t;
+    const uint64_t hit = __builtin_amdgcn_ballot_w64(t > 0 && first <= g && g < first + t);
     if (hit) {
       const int l = __builtin_ctzll(hit);
-      return RaggedUnit{c0 + l, u - __builtin_amdgcn_readlane(first, l), __builtin_amdgcn_readlane(n, l)};
+      b_out = c0 + l;
+      p_out = __builtin_amdgcn_readlane(first, l);
+      return;
     }
     base += __builtin_amdgcn_readlane(incl, 63);
   }
-  return RaggedUnit{-1, 0, 0};
 }
 
-// Writes (P_b, n_b) of every sequence to sched[2b], sched[2b + 1] (one wave).
-__device__ __forceinline__ void ragged_write_sched(const int32_t* kv_start, int B, int N, int C,
-                                                   int* sched) {
+// Writes sequence b's (first partial column, partial count) to sched[2b],
+// sched[2b + 1] for the merge; (0, 0) for a sequence with no keys.  One wave.
+__device__ __forceinline__ void streamk_write_sched(const int32_t* kv_start, int B, int N, int C, int* sched) {
   const int lane = __lane_id();
   int base = 0;
   for (int c0 = 0; c0 < B; c0 += 64) {
     const int b = c0 + lane;
-    const int n = b < B ? (seq_tiles(kv_start, b, N) + C - 1) / C : 0;
-    const int incl = wave_inclusive_scan(n);
-    if (b < B) *reinterpret_cast<int2*>(sched + 2 * b) = int2{base + incl - n, n};
+    const int t = b < B ? seq_tiles(kv_start, b, N) : 0;
+    const int incl = wave_inclusive_scan(t);
+    const int first = base + incl - t;
+    if (b < B) {
+      const int uf = first / C, ul = (first + t - 1) / C;
+      *reinterpret_cast<int2*>(sched + 2 * b) = t > 0 ? int2{uf + b, ul - uf + 1} : int2{0, 0};
+    }
     base += __builtin_amdgcn_readlane(incl, 63);
   }
 }

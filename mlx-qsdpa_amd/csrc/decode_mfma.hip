@@ -405,39 +405,18 @@ struct Kernel {
   }
 };
 
+// One segment of a workgroup's work: tiles t_lo, t_lo + stride, ... (at
+// most jmax of them) of sequence b for the block's 16 query rows.  Writes the
+// normalised output (one split) or the partials at column `col` of the rows'
+// partial slots.  Called by the whole workgroup.
 template <typename Tag, int D, int BITS, int GS>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_mfma_kernel(MfmaParams p) {
+__device__ __forceinline__ void decode_segment(const MfmaParams& p, float* s_acc, float (*s_ml)[16][2],
+                                               uint8_t* s_q, int lane, int wave, int quad, int r, int hblk,
+                                               int kvh, int b, int t_lo, int stride, int jmax, int col) {
   using G = Geo<D, BITS, GS>;
   using K = Kernel<Tag, D, BITS, GS>;
-  constexpr int kRowF = D + 4;  // LDS floats per (wave, head) row
-  __shared__ __attribute__((aligned(16))) float s_acc[kWaves * 16 * kRowF];
-  __shared__ float s_ml[kWaves][16][2];
+  constexpr int kRowF = D + 4;       // LDS floats per (wave, head) row
   constexpr int kQRow = D * 2 + 16;  // bytes per staged Q row
-  __shared__ __attribute__((aligned(16))) uint8_t s_q[16 * kQRow];
-
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int quad = lane >> 4;
-  const int r = lane & 15;
-  const int hblk = blockIdx.y % p.hb_count;
-  const int kvh = blockIdx.y / p.hb_count;
-  // Uniform splits: grid (S, H_kv * head blocks, B).  Left-padded batch
-  // (units > 0): grid (U, H_kv * head blocks, 1), unit x of the balanced
-  // schedule (common.h) is split `split` of `S` of sequence b.
-  int b, split, S;
-  if (p.units) {
-    const int C = ragged_budget(p.kv_start, p.B, p.N, p.units);
-    if (blockIdx.x == 0 && blockIdx.y == 0 && wave == 0) ragged_write_sched(p.kv_start, p.B, p.N, C, p.sched);
-    const RaggedUnit ru = ragged_unit(p.kv_start, p.B, p.N, C, blockIdx.x);
-    if (ru.b < 0) return;  // the whole workgroup: no work, nothing to store
-    b = ru.b;
-    split = ru.split;
-    S = ru.count;
-  } else {
-    b = blockIdx.z;
-    split = blockIdx.x;
-    S = p.num_splits;
-  }
   // The block's rows: v0 .. v0 + nh - 1 of the kv head's G * qL rows; row v
   // is query position v / G of head kvh * G + v % G (with one position, the
   // 16 heads of a GQA group).
@@ -452,13 +431,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int n_end = p.causal ? min(p.N, max(0, p.N - p.qL + (v0 + nh - 1) / p.G + 1)) : p.N;
   const int n_lane = p.causal ? min(n_end, max(0, p.N - p.qL + iq_lane + 1)) : n_end;
 
-  // Keys [s0, n_end) of this sequence, in 32-token tiles from s0.  Split s
-  // owns tiles s, s + S, s + 2S, ... (positions j = 0, 1, ..., J - 1), so at
-  // any moment the grid streams one compact window of the cache.
+  // Keys [s0, n_end) of this sequence, in 32-token tiles from s0.  The
+  // segment owns tiles t_lo, t_lo + stride, ... (positions j = 0, 1, ...,
+  // J - 1).  Uniform splits: split s of S owns tiles s, s + S, ..., so at any
+  // moment the grid streams one compact window of the cache.
   const int s0 = p.kv_start ? min(max(p.kv_start[b], 0), p.N) : 0;
   const int len = max(n_end - s0, 0);
   const int T = (len + kTile - 1) / kTile;
-  const int J = T > split ? (T - split + S - 1) / S : 0;
+  const int J = T > t_lo ? min(jmax, (T - t_lo + stride - 1) / stride) : 0;
   // Positions below J - E go round-robin to the 8 waves; the last E go to
   // waves 0-3 only.  Waves 4-7 share their SIMDs with waves 0-3, and the
   // older waves' loads are served first, so equal shares would leave 0-3
@@ -475,7 +455,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   // descriptor (the loads read zero without touching memory).  Every tile
   // issues the same loads, so the compiler's vmcnt waits stay exact.
   const int oob = len + kTile;
-  auto row_of = [&](int j) -> int { return j < J ? (j * S + split) * kTile : oob; };
+  auto row_of = [&](int j) -> int { return j < J ? (t_lo + j * stride) * kTile : oob; };
 
   // Buffer descriptors over rows [s0, N) of this (batch, kv head).
   Rsrcs rs;
@@ -655,8 +635,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     } else {
       // Partial rows: (b, head, position) rows, each with its splits.
       const int64_t prow = static_cast<int64_t>(hh) * p.qL + iq;
-      const int64_t slot = p.units ? prow * p.units + blockIdx.x
-                                   : (static_cast<int64_t>(b) * p.Hq * p.qL + prow) * p.num_splits + split;
+      const int64_t slot = p.units ? prow * (p.units + p.B) + col
+                                   : (static_cast<int64_t>(b) * p.Hq * p.qL + prow) * p.num_splits + col;
       // Streaming stores: the partials are read once, by the merge kernel.
       if constexpr (Tag::kId == QSDPA_F16) {
         // float16 rows of the split's normalised output (acc / L, within
@@ -679,12 +659,66 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   }
 }
 
+// SK: the stream-K schedule of a left-padded batch (a loop over segments);
+// otherwise one uniform split (a separate instantiation, so the loop's
+// register pressure stays out of the common case).
+template <typename Tag, int D, int BITS, int GS, bool SK>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_mfma_kernel(MfmaParams p) {
+  constexpr int kRowF = D + 4;  // LDS floats per (wave, head) row
+  __shared__ __attribute__((aligned(16))) float s_acc[kWaves * 16 * kRowF];
+  __shared__ float s_ml[kWaves][16][2];
+  constexpr int kQRow = D * 2 + 16;  // bytes per staged Q row
+  __shared__ __attribute__((aligned(16))) uint8_t s_q[16 * kQRow];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int quad = lane >> 4;
+  const int r = lane & 15;
+  const int hblk = blockIdx.y % p.hb_count;
+  const int kvh = blockIdx.y / p.hb_count;
+  if constexpr (!SK) {
+    // Uniform splits: grid (S, H_kv * row blocks, B); split x of sequence z.
+    decode_segment<Tag, D, BITS, GS>(p, s_acc, s_ml, s_q, lane, wave, quad, r, hblk, kvh, blockIdx.z, blockIdx.x,
+                                     p.num_splits, 0x7FFFFFFF, blockIdx.x);
+  } else {
+    // Left-padded batch: grid (U, H_kv * row blocks, 1), unit x of the
+    // stream-K schedule (common.h) owns global tiles [x * C, (x + 1) * C) of
+    // the sequences laid end to end, one segment per sequence it touches.
+    const int total = streamk_total(p.kv_start, p.B, p.N);
+    const int C = max(1, (total + p.units - 1) / p.units);
+    if (blockIdx.x == 0 && blockIdx.y == 0 && wave == 0) streamk_write_sched(p.kv_start, p.B, p.N, C, p.sched);
+    int g = static_cast<int>(blockIdx.x) * C;
+    const int g_end = min(g + C, total);
+    if (g >= g_end) return;  // the whole workgroup: no work, nothing to store
+    int b, P;
+    streamk_find(p.kv_start, p.B, p.N, g, b, P);
+    while (g < g_end && b < p.B) {
+      const int Tb = seq_tiles(p.kv_start, b, p.N);
+      const int hi = min(g_end, P + Tb);
+      if (hi > g) {
+        decode_segment<Tag, D, BITS, GS>(p, s_acc, s_ml, s_q, lane, wave, quad, r, hblk, kvh, b, g - P, 1, hi - g,
+                                         static_cast<int>(blockIdx.x) + b);
+        __syncthreads();  // the next segment reuses the LDS
+        g = hi;
+      }
+      P += Tb;
+      ++b;
+    }
+  }
+}
+
 template <typename Tag, int D, int BITS>
 void launch_gs(const MfmaParams& p, int gs, hipStream_t stream, const qsdpa_decode_args* a) {
   const dim3 grid(p.units ? p.units : p.num_splits, p.Hkv * p.hb_count, p.units ? 1 : p.B);
-  void (*k)(MfmaParams) = gs == 32   ? decode_mfma_kernel<Tag, D, BITS, 32>
-                          : gs == 64 ? decode_mfma_kernel<Tag, D, BITS, 64>
-                                     : decode_mfma_kernel<Tag, D, BITS, 128>;
+  void (*k)(MfmaParams);
+  if (p.units)
+    k = gs == 32 ? decode_mfma_kernel<Tag, D, BITS, 32, true>
+      : gs == 64 ? decode_mfma_kernel<Tag, D, BITS, 64, true>
+                 : decode_mfma_kernel<Tag, D, BITS, 128, true>;
+  else
+    k = gs == 32 ? decode_mfma_kernel<Tag, D, BITS, 32, false>
+      : gs == 64 ? decode_mfma_kernel<Tag, D, BITS, 64, false>
+                 : decode_mfma_kernel<Tag, D, BITS, 128, false>;
   launch_profiled(k, grid, dim3(kThreads), stream, a->prof_begin, a->prof_end, p);
 }
 

@@ -32,9 +32,9 @@ constexpr float kNegBig = -1.0e30f;
 //
 // Rows are (b, h, i) for the qL query positions i, numbered
 // (b * H_q + h) * qL + i; each holds `splits` partials.  sched != null
-// (balanced schedule of a left-padded batch): the partials of (h, i) are
-// rows (h * qL + i) * units + u, and sequence b owns units
-// sched[2b] .. sched[2b] + sched[2b + 1] - 1.
+// (stream-K schedule of a left-padded batch): the partials of (h, i) are
+// rows (h * qL + i) * units + c for `units` columns c, and sequence b owns
+// columns sched[2b] .. sched[2b] + sched[2b + 1] - 1.
 template <typename Tag, bool HALF>
 __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ part_acc,
                                                     const float* __restrict__ part_ml, int D,
