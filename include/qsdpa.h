@@ -107,9 +107,9 @@ typedef struct {
 
   /* 0 = choose automatically, 1 = single pass, >1 = split-K with this many
    * splits per (batch, kv head).  With kv_start and B > 1 (D in {128, 256})
-   * the count is an average: the batch's num_splits * B splits per kv head
-   * are shared out over its sequences in proportion to their key counts
-   * (a sequence with no keys gets none).                                  */
+   * the count is an average: the batch's keys per kv head are cut into
+   * num_splits * B equal runs of tiles over the sequences laid end to end
+   * (a run may cross sequences; a sequence with no keys gets none).       */
   int32_t num_splits;
 
   /* Scratch for split-K partials, from qsdpa_decode_workspace_size().    */

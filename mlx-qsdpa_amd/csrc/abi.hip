@@ -144,8 +144,6 @@ int decode_plan(const qsdpa_decode_args* a, int* num_splits, int64_t* workspace_
   }
   splits = std::min(splits, std::max(1, a->N));
   *num_splits = splits;
-  // Partials (B * H_q * splits rows of D + 2 floats), then the balanced
-  // schedule's (first unit, units) pair per sequence.
   // Partial slots per query row: splits, or splits + 1 columns per sequence
   // (U + B, U = splits * B) under the stream-K schedule of a left-padded
   // batch; then that schedule's (first column, count) per sequence.

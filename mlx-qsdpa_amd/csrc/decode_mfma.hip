@@ -768,11 +768,11 @@ bool mfma_supports(const qsdpa_decode_args* a) {
 
 // Splits per (batch, kv head, head block): one workgroup per CU in total
 // (LDS and registers allow one 8-wave group per CU), each split at least one
-// tile per wave.  A left-padded batch (kv_start, B > 1) runs the balanced
+// tile per wave.  A left-padded batch (kv_start, B > 1) runs the stream-K
 // schedule over splits * B units, which also sizes for one round: measured
-// at C4 (B=16, H_kv=8, lengths U[1K, 32K]) the decode takes 59.1 us with 2
-// splits (32 units per kv head, one round), 62.1 us with 4 (two rounds) and
-// 80.5 us with 3 (one and a half); uniform splits took 66.1 us at best.
+// at C4 (B=16, H_kv=8, lengths U[1K, 32K]) the decode takes 60.0 us with 2
+// splits (32 units per kv head, one round), 69.6 us with 4 (two rounds) and
+// 79.1 us with 3 (one and a half); uniform splits took 66.1 us at best.
 int mfma_num_splits(const qsdpa_decode_args* a, int cus) {
   const int hb = (a->H_q / a->H_kv * std::max(a->q_len, 1) + 15) / 16;
   const int64_t units = static_cast<int64_t>(a->B) * a->H_kv * hb;

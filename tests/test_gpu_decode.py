@@ -204,9 +204,9 @@ def test_kv_start_left_padding(device, heads):
     (5, 32, 8, 1100, 128, 32, "f16", (2, 7, 64)),
     (6, 16, 1, 700, 256, 32, "bf16", (None, 4, 16)),
 ], ids=["B70", "B5-G4", "B6-D256-bf16"])
-def test_kv_start_balanced_schedule(device, case):
-    """A left-padded batch shares splits * B units out over its sequences by
-    length: ragged lengths, empty sequences (kv_start >= N, also past N),
+def test_kv_start_streamk_schedule(device, case):
+    """A left-padded batch runs splits * B equal units over its sequences laid
+    end to end (units cross sequences): ragged lengths, empty sequences (kv_start >= N, also past N),
     negative kv_start (clamped to 0) and split counts from 2 to 64 all match
     the oracle with an additive -inf mask on the skipped keys; repeated calls
     are bitwise identical."""
@@ -227,7 +227,7 @@ def test_kv_start_balanced_schedule(device, case):
     ks = torch.tensor(starts, dtype=torch.int32, device=device)
     for splits in splits_list:
         got = run(inp, device, kv_start=ks, num_splits=splits)
-        assert_close(got, want, f"balanced kv_start splits={splits}")
+        assert_close(got, want, f"stream-K kv_start splits={splits}")
         assert np.all(got[keep_from >= N] == 0)
         again = run(inp, device, kv_start=ks, num_splits=splits)
         assert np.array_equal(got, again), f"splits={splits}: repeated call differs"
@@ -281,7 +281,7 @@ def test_multi_query_matches_oracle(device, case):
 
 
 def test_multi_query_kv_start_causal(device):
-    """qL > 1 with left padding (balanced schedule) and causal together."""
+    """qL > 1 with left padding (stream-K schedule) and causal together."""
     rng = np.random.default_rng(47)
     B, Hq, Hkv, N, D, qL = 4, 16, 4, 600, 128, 6
     inp = make_inputs(rng, B, Hq, Hkv, N, D, 4, 64)
