@@ -323,3 +323,47 @@ def test_metric_known_answers():
     r, w = metric.compute_bytes(1, 32, 2, 131072, 256, 1, "quantized", 4, 32)
     assert r + w == 83_918_848
     assert metric.decode_bytes(1, 32, 2, 256, 4, 32, 131072) == 83_918_848
+
+
+# ---- stream-K schedule of a left-padded batch (device code in csrc/common.h) ----
+def _streamk_segments(T, U):
+    """Integer rules of the schedule (streamk_total / streamk_find /
+    streamk_write_sched and the kernel's segment loop): unit u owns global
+    tiles [u*C, (u+1)*C) of the sequences laid end to end; its part in
+    sequence b is a segment at partial column u + b."""
+    total = sum(T)
+    C = max(1, -(-total // U))
+    P = np.concatenate([[0], np.cumsum(T)[:-1]]).astype(int)
+    segs = []
+    for u in range(U):
+        g, g_end = u * C, min((u + 1) * C, total)
+        for b, (p, t) in enumerate(zip(P, T)):
+            lo, hi = max(g, p), min(g_end, p + t)
+            if hi > lo:
+                segs.append((u, b, lo - p, hi - p, u + b))
+    sched = [((p // C) + b, (p + t - 1) // C - p // C + 1) if t > 0 else (0, 0)
+             for b, (p, t) in enumerate(zip(P, T))]
+    return C, segs, sched
+
+
+@pytest.mark.parametrize("seed", range(20))
+def test_streamk_schedule_invariants(seed):
+    r = np.random.default_rng(seed)
+    B = int(r.integers(2, 80))
+    T = [int(x) for x in r.integers(0, 300, size=B)]
+    T[int(r.integers(B))] = 0                       # an empty sequence
+    U = B * int(r.integers(1, 5))
+    C, segs, sched = _streamk_segments(T, U)
+    cols = [s[4] for s in segs]
+    assert len(cols) == len(set(cols))              # one partial slot per segment
+    assert max(cols, default=0) < U + B             # within the U + B columns of a row
+    per_unit = {}
+    for u, b, lo, hi, _ in segs:
+        per_unit[u] = per_unit.get(u, 0) + hi - lo
+    assert max(per_unit.values(), default=0) <= C   # equal work: at most C tiles a unit
+    for b, t in enumerate(T):                       # every tile exactly once, columns consecutive
+        mine = sorted((lo, hi, col) for u, bb, lo, hi, col in segs if bb == b)
+        assert sum(hi - lo for lo, hi, _ in mine) == t
+        assert all(mine[i][1] == mine[i + 1][0] for i in range(len(mine) - 1))
+        first, count = sched[b]
+        assert [c for _, _, c in mine] == list(range(first, first + count))
