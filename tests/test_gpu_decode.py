@@ -399,6 +399,38 @@ def test_headline_full_size_properties(device, N):
     assert (outp.float() - out.float()).abs().max().item() < 2e-3
 
 
+def test_c4_full_size_batched(device):
+    """C4 at its full shape (B=16, H_q=32, H_kv=8, D=128, 4-bit gs64, lengths
+    U[1K, 32K] left-padded): the stream-K decode vs an independent torch
+    float32 reference with the padding masked, across split counts, and vs
+    the same left padding given as a bool mask (uniform splits)."""
+    torch.manual_seed(0)
+    gen = torch.Generator(device="cpu")
+    gen.manual_seed(0)
+    B, Hq, Hkv, D, bits, gs = 16, 32, 8, 128, 4, 64
+    lengths = torch.randint(1024, 32769, (B,), generator=gen)
+    N = int(lengths.max())
+    T = torch.float16
+    kq = kernels.quantize(torch.randn((B, Hkv, N, D), device=device).to(T), gs, bits)
+    vq = kernels.quantize(torch.randn((B, Hkv, N, D), device=device).to(T), gs, bits)
+    q = torch.randn((B, Hq, 1, D), device=device).to(T)
+    ks = (N - lengths).to(device=device, dtype=torch.int32)
+    keep = torch.arange(N, device=device)[None, :] >= ks[:, None].long()
+    from mlx_qsdpa_amd.dispatch import attention_fp32
+    ref = attention_fp32(q, _torch_dequant(*kq, bits, gs, T), _torch_dequant(*vq, bits, gs, T), D ** -0.5,
+                         keep[:, None, None, :]).float()
+    outs = {}
+    for splits in (None, 2, 4):
+        out = mq.quantized_sdpa(q, kq[0], vq[0], kq[1], vq[1], kq[2], vq[2], bits=bits, group_size=gs,
+                                kv_start=ks, num_splits=splits).float()
+        err = (out - ref).abs()
+        assert bool((err <= ATOL + RTOL * ref.abs()).all()), f"splits={splits}: max err {err.max().item():.3e}"
+        outs[splits] = out
+    masked = mq.quantized_sdpa(q, kq[0], vq[0], kq[1], vq[1], kq[2], vq[2], bits=bits, group_size=gs,
+                               mask=keep[:, None, None, :]).float()
+    assert (masked - outs[None]).abs().max().item() < 2e-3
+
+
 @pytest.mark.parametrize("case", [(1, 32, 2, 4096, 256, 4, 32, "f16"), (2, 16, 4, 3000, 128, 8, 64, "bf16")],
                          ids=["C3_small", "B2_G4_bf16"])
 def test_repeated_calls_reuse_workspace(device, case):
