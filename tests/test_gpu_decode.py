@@ -251,8 +251,14 @@ def _fused(inp, device, **kw):
     (1, 16, 4, 700, 128, 8, 64, "bf16", 5, "additive"),  # per (head, position) additive mask
     (3, 8, 1, 400, 256, 4, 64, "f16", 2, "bool"),        # bool mask broadcast over heads
     (1, 16, 2, 40, 128, 4, 32, "f16", 48, "causal"),     # qL > N: the first rows see no key
+    # many row blocks per kv head (>= 128 rows), partial last blocks
+    (1, 16, 4, 700, 128, 8, 64, "bf16", 64, "causal"),   # 256 rows, 2 workgroups
+    (2, 32, 2, 300, 256, 4, 32, "f16", 16, "causal"),    # D=256
+    (1, 8, 2, 500, 128, 4, 32, "f16", 37, "additive"),   # 148 rows: last workgroup part-filled
+    (2, 4, 4, 600, 256, 8, 128, "bf16", 130, "bool"),    # G=1, per-position bool mask
 ], ids=["G16-q4-causal", "G4-q3", "G1-q33-causal-bf16", "G4-q5-additive", "G8-q2-bool",
-        "q48-over-N40-causal"])
+        "q48-over-N40-causal", "rows-G4-q64-causal-bf16", "rows-D256-G16-q16-causal",
+        "rows-G4-q37-additive", "rows-G1-q130-bool-bf16"])
 def test_multi_query_matches_oracle(device, case):
     """qL > 1 query positions (speculative / chunked decoding, prefill) on the
     fused kernel: rows are (position, head) pairs of a kv head; causal is
@@ -280,10 +286,12 @@ def test_multi_query_matches_oracle(device, case):
         assert_close(got, want, f"qL={qL} splits={splits}")
 
 
-def test_multi_query_kv_start_causal(device):
-    """qL > 1 with left padding (stream-K schedule) and causal together."""
+@pytest.mark.parametrize("qL", [6, 40], ids=["q6", "q40-rows"])
+def test_multi_query_kv_start_causal(device, qL):
+    """qL > 1 with left padding and causal together (stream-K schedule when
+    split; 160 rows per kv head at qL=40)."""
     rng = np.random.default_rng(47)
-    B, Hq, Hkv, N, D, qL = 4, 16, 4, 600, 128, 6
+    B, Hq, Hkv, N, D = 4, 16, 4, 600, 128
     inp = make_inputs(rng, B, Hq, Hkv, N, D, 4, 64)
     inp["q"] = affine.random_T(rng, (B, Hq, qL, D), "f16")
     starts = np.array([0, 100, 597, 600])
