@@ -60,6 +60,17 @@ namespace qsdpa {
 
 namespace {
 
+// Cache policy of the K / V / scale / bias loads (the aux operand of the
+// buffer loads): non-temporal, as each row is read once per step; streaming
+// it past the caches keeps the split-K partials and Q resident (C3 25.7
+// against 26.4 us per step, C5 13.2 against 13.7).  Not where a lane reads
+// 64 contiguous bytes of a K row in four pieces (D = 256, 8-bit: C2 36.6
+// against 31.5 us with it).
+template <int D, int BITS>
+constexpr int load_policy() {
+  return D == 256 && BITS == 8 ? 0 : 2;
+}
+
 template <int WORDS>
 __device__ __forceinline__ void load_words(const uint32_t* p, uint32_t* w) {
   if constexpr (WORDS % 4 == 0) {
@@ -122,21 +133,21 @@ struct Rsrcs {
   uint32_t k_sn, ks_sn, kb_sn, v_sn, vs_sn, vb_sn;
 };
 
-template <int WORDS>
+template <int WORDS, int AUX>
 __device__ __forceinline__ void buffer_words(rsrc_t rs, uint32_t off, uint32_t* w) {
   typedef uint32_t u4 __attribute__((ext_vector_type(4)));
   typedef uint32_t u2 __attribute__((ext_vector_type(2)));
   if constexpr (WORDS % 4 == 0) {
 #pragma unroll
     for (int i = 0; i < WORDS / 4; ++i) {
-      const u4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16 * i, 0, 0);
+      const u4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16 * i, 0, AUX);
       w[4 * i] = v[0]; w[4 * i + 1] = v[1]; w[4 * i + 2] = v[2]; w[4 * i + 3] = v[3];
     }
   } else if constexpr (WORDS == 2) {
-    const u2 v = __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0);
+    const u2 v = __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, AUX);
     w[0] = v[0]; w[1] = v[1];
   } else {
-    w[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0);
+    w[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, AUX);
   }
 }
 
@@ -152,6 +163,7 @@ struct VMetaLane {
 
 template <typename Tag, int D, int BITS, int GS>
 struct Kernel {
+  static constexpr int kAux = load_policy<D, BITS>();
   using G = Geo<D, BITS, GS>;
   using Regs = TileRegs<D, BITS, GS>;
   // Every K / V element is dequantized as mx.dequantize rounds it, T(fma(
@@ -172,15 +184,15 @@ struct Kernel {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const uint32_t row = static_cast<uint32_t>(rel0 + 16 * u);
-      buffer_words<G::KW>(rs.k, row * rs.k_sn + L.k_r, R.kw[u]);
+      buffer_words<G::KW, kAux>(rs.k, row * rs.k_sn + L.k_r, R.kw[u]);
       if constexpr (G::KG == 2)
-        R.ks[u] = __builtin_amdgcn_raw_buffer_load_b32(rs.ks, row * rs.ks_sn + L.ks_r, 0, 0);
+        R.ks[u] = __builtin_amdgcn_raw_buffer_load_b32(rs.ks, row * rs.ks_sn + L.ks_r, 0, kAux);
       else
-        R.ks[u] = __builtin_amdgcn_raw_buffer_load_b16(rs.ks, row * rs.ks_sn + L.ks_r, 0, 0);
+        R.ks[u] = __builtin_amdgcn_raw_buffer_load_b16(rs.ks, row * rs.ks_sn + L.ks_r, 0, kAux);
       if constexpr (G::KG == 2) {
-        R.kb[u] = __builtin_amdgcn_raw_buffer_load_b32(rs.kb, row * rs.kb_sn + L.kb_r, 0, 0);
+        R.kb[u] = __builtin_amdgcn_raw_buffer_load_b32(rs.kb, row * rs.kb_sn + L.kb_r, 0, kAux);
       } else {
-        R.kb[u] = __builtin_amdgcn_raw_buffer_load_b16(rs.kb, row * rs.kb_sn + L.kb_r, 0, 0);
+        R.kb[u] = __builtin_amdgcn_raw_buffer_load_b16(rs.kb, row * rs.kb_sn + L.kb_r, 0, kAux);
       }
     }
   }
@@ -190,17 +202,17 @@ struct Kernel {
     for (int u = 0; u < 2; ++u) {
       const uint32_t row = static_cast<uint32_t>(rel0 + 16 * u);
       if constexpr (G::NG >= 2) {
-        R.vs[u] = __builtin_amdgcn_raw_buffer_load_b32(rs.vs, row * rs.vs_sn + L.vs_r, 0, 0);
-        R.vb[u] = __builtin_amdgcn_raw_buffer_load_b32(rs.vb, row * rs.vb_sn + L.vb_r, 0, 0);
+        R.vs[u] = __builtin_amdgcn_raw_buffer_load_b32(rs.vs, row * rs.vs_sn + L.vs_r, 0, kAux);
+        R.vb[u] = __builtin_amdgcn_raw_buffer_load_b32(rs.vb, row * rs.vb_sn + L.vb_r, 0, kAux);
       } else {
-        R.vs[u] = __builtin_amdgcn_raw_buffer_load_b16(rs.vs, row * rs.vs_sn + L.vs_r, 0, 0);
-        R.vb[u] = __builtin_amdgcn_raw_buffer_load_b16(rs.vb, row * rs.vb_sn + L.vb_r, 0, 0);
+        R.vs[u] = __builtin_amdgcn_raw_buffer_load_b16(rs.vs, row * rs.vs_sn + L.vs_r, 0, kAux);
+        R.vb[u] = __builtin_amdgcn_raw_buffer_load_b16(rs.vb, row * rs.vb_sn + L.vb_r, 0, kAux);
       }
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const uint32_t row = static_cast<uint32_t>(rel0 + 16 * (j >> 2) + (j & 3));
-      buffer_words<G::VW>(rs.v, row * rs.v_sn + L.v_r, R.vw[j]);
+      buffer_words<G::VW, kAux>(rs.v, row * rs.v_sn + L.v_r, R.vw[j]);
     }
   }
 
