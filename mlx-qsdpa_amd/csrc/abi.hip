@@ -155,7 +155,7 @@ int decode_plan(const qsdpa_decode_args* a, int* num_splits, int64_t* workspace_
 // A left-padded batch on the MFMA path runs splits * B equal units of the
 // stream-K schedule (common.h) over its sequences laid end to end, instead
 // of giving every sequence `splits`; 0 = uniform splits.
-int ragged_units(const qsdpa_decode_args* a, int splits) {
+int streamk_units(const qsdpa_decode_args* a, int splits) {
   if (!a->kv_start || a->B < 2 || splits < 2 || !mfma_supports(a)) return 0;
   const int64_t units = static_cast<int64_t>(splits) * a->B;
   if (units >= (int64_t(1) << 31) / 2) return 0;
@@ -209,7 +209,7 @@ int qsdpa_decode(const qsdpa_decode_args* args, void* stream) {
   const hipStream_t s = static_cast<hipStream_t>(stream);
   // (prof_begin / prof_end ride on the main kernel's own dispatch)
   const bool mfma = mfma_supports(args);
-  const int units = ragged_units(args, splits);
+  const int units = streamk_units(args, splits);
   if (mfma) rc = launch_decode_mfma(args, splits, part_acc, part_ml, units, sched, s);
   else rc = launch_decode_valu(args, splits, part_acc, part_ml, s);
   if (rc) return rc;

@@ -48,15 +48,15 @@ struct MfmaParams {
   const int32_t* kv_start;
   float* part_acc;
   float* part_ml;
-  int units;   // > 0: balanced schedule of a left-padded batch over this many units
-  int* sched;  // (P_b, n_b) per sequence, written for the merge when units > 0
+  int units;   // > 0: stream-K schedule of a left-padded batch over this many units per kv head
+  int* sched;  // (first partial column, count) per sequence, for the merge when units > 0
   // Query positions: the G * qL rows of a kv head are (position v / G, head
   // v % G); a block takes 16 consecutive rows.
   int qL, causal;
   int64_t q_sq, o_sq, m_sq;  // position strides of q, out and the mask
 };
 
-static_assert(kTile == kSchedTile, "the balanced schedule counts the decode's key tiles");
+static_assert(kTile == kSchedTile, "the stream-K schedule counts the decode's key tiles");
 
 __device__ __forceinline__ uint32_t bitop_and_or(uint32_t a, uint32_t mask, uint32_t c) {
   return __builtin_amdgcn_bitop3_b32(a, mask, c, 0xEA);  // (a & mask) | c
