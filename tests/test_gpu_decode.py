@@ -456,3 +456,42 @@ def test_repeated_calls_reuse_workspace(device, case):
     for o in outs[1:]:
         assert torch.equal(o, outs[0])
     assert_close(to_np(outs[0]), oracle_out(inp), f"{case}")
+
+
+def test_plan_grows_in_place_with_appends(device):
+    """A DecodePlan over a capacity-padded, left-padded batch cache: each step
+    appends one token per sequence (qsdpa_quantize_batch, K and V in one
+    launch), moves N with set_keys and decodes; every step matches the oracle
+    on the first N keys with the padding masked.  N past the capacity is
+    refused."""
+    rng = np.random.default_rng(91)
+    B, Hq, Hkv, D, bits, gs, n0, cap = 3, 8, 2, 128, 4, 64, 200, 260
+    T = torch.float16
+    starts = np.array([0, 150, 37])
+    kw = affine.random_T(rng, (B, Hkv, cap, D), "f16")
+    vw = affine.random_T(rng, (B, Hkv, cap, D), "f16")
+    bufs = []
+    for w in (kw, vw):
+        p, s, b = (torch.zeros((B, Hkv, cap, D * bits // 32), dtype=torch.uint32, device=device),
+                   torch.zeros((B, Hkv, cap, D // gs), dtype=T, device=device),
+                   torch.zeros((B, Hkv, cap, D // gs), dtype=T, device=device))
+        kernels.quantize_into(from_np(w[:, :, :n0], T, device), (p, s, b), 0, bits, gs)
+        bufs.append((p, s, b))
+    q = from_np(affine.random_T(rng, (B, Hq, 1, D), "f16"), T, device)
+    ks = torch.tensor(starts, dtype=torch.int32, device=device)
+    (kp, kss, kb), (vp, vs, vb) = bufs
+    plan = kernels.DecodePlan(q, kp[:, :, :n0], vp[:, :, :n0], kss[:, :, :n0], vs[:, :, :n0],
+                              kb[:, :, :n0], vb[:, :, :n0], scale=D ** -0.5, bits=bits, group_size=gs,
+                              kv_start=ks, num_splits=3, capacity=cap)
+    for n in range(n0, n0 + 3):
+        kernels.quantize_kv_into(from_np(kw[:, :, n:n + 1], T, device), from_np(vw[:, :, n:n + 1], T, device),
+                                 bufs[0], bufs[1], n, bits, gs)
+        plan.set_keys(n + 1)
+        got = to_np(plan())
+        inp = dict(q=to_np(q), kp=to_np(kp[:, :, :n + 1]), vp=to_np(vp[:, :, :n + 1]),
+                   ks=to_np(kss[:, :, :n + 1]), vs=to_np(vs[:, :, :n + 1]), kb=to_np(kb[:, :, :n + 1]),
+                   vb=to_np(vb[:, :, :n + 1]), bits=bits, gs=gs, dtype="f16")
+        add = np.where(np.arange(n + 1)[None, :] >= starts[:, None], 0.0, -np.inf)[:, None, None, :]
+        assert_close(got, oracle_out(inp, mask=add), f"n={n + 1}")
+    with pytest.raises(ValueError):
+        plan.set_keys(cap + 1)
