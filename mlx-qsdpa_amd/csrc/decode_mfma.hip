@@ -649,16 +649,18 @@ __device__ __forceinline__ void decode_segment(const MfmaParams& p, float* s_acc
       const int64_t prow = static_cast<int64_t>(hh) * p.qL + iq;
       const int64_t slot = p.units ? prow * (p.units + p.B) + col
                                    : (static_cast<int64_t>(b) * p.Hq * p.qL + prow) * p.num_splits + col;
-      // Streaming stores: the partials are read once, by the merge kernel.
       if constexpr (Tag::kId == QSDPA_F16) {
         // float16 rows of the split's normalised output (acc / L, within
-        // the range of V), so the partials are half the bytes.
+        // the range of V), so the partials are half the bytes.  Plain
+        // stores: with the K / V stream non-temporal the rows stay in the
+        // caches for the merge (C3 25.2 against 25.6 us per step with
+        // streaming stores).
         const float inv = L > 0.0f ? 1.0f / L : 0.0f;
         uint16_t* dst = reinterpret_cast<uint16_t*>(p.part_acc) + slot * D + d;
-        __builtin_nontemporal_store(u4{pack_T2<Tag>(v[0] * inv, v[1] * inv), pack_T2<Tag>(v[2] * inv, v[3] * inv),
-                                       pack_T2<Tag>(v[4] * inv, v[5] * inv), pack_T2<Tag>(v[6] * inv, v[7] * inv)},
-                                    reinterpret_cast<u4*>(dst));
+        *reinterpret_cast<u4*>(dst) = u4{pack_T2<Tag>(v[0] * inv, v[1] * inv), pack_T2<Tag>(v[2] * inv, v[3] * inv),
+                                         pack_T2<Tag>(v[4] * inv, v[5] * inv), pack_T2<Tag>(v[6] * inv, v[7] * inv)};
       } else {
+        // Streaming stores: the partials are read once, by the merge kernel.
         float* dst = p.part_acc + slot * D + d;
         __builtin_nontemporal_store(f4{v[0], v[1], v[2], v[3]}, reinterpret_cast<f4*>(dst));
         __builtin_nontemporal_store(f4{v[4], v[5], v[6], v[7]}, reinterpret_cast<f4*>(dst + 4));
