@@ -19,13 +19,6 @@ inline bool aligned(const void* p, int bytes) {
   return (reinterpret_cast<uintptr_t>(p) % static_cast<uintptr_t>(bytes)) == 0;
 }
 
-// Dispatch-time description of one strided operand.
-struct View {
-  const void* ptr;
-  int64_t sb, sh, sn;
-};
-inline View view_of(const qsdpa_view& v) { return View{v.ptr, v.stride_b, v.stride_h, v.stride_n}; }
-
 // Launch a one-argument kernel.  With profiling events (either non-null) the
 // launch goes through hipExtLaunchKernel, which attaches the events to the
 // kernel's own dispatch: their elapsed time is the kernel's execution time,

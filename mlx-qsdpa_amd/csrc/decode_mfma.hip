@@ -71,27 +71,6 @@ constexpr int load_policy() {
   return D == 256 && BITS == 8 ? 0 : 2;
 }
 
-template <int WORDS>
-__device__ __forceinline__ void load_words(const uint32_t* p, uint32_t* w) {
-  if constexpr (WORDS % 4 == 0) {
-#pragma unroll
-    for (int i = 0; i < WORDS / 4; ++i) {
-      const uint4 v = reinterpret_cast<const uint4*>(p)[i];
-      w[4 * i] = v.x; w[4 * i + 1] = v.y; w[4 * i + 2] = v.z; w[4 * i + 3] = v.w;
-    }
-  } else if constexpr (WORDS == 2) {
-    const uint2 v = *reinterpret_cast<const uint2*>(p);
-    w[0] = v.x; w[1] = v.y;
-  } else {
-    w[0] = p[0];
-  }
-}
-
-template <typename T>
-__device__ __forceinline__ const T* add_bytes(const T* p, int64_t bytes) {
-  return reinterpret_cast<const T*>(reinterpret_cast<const uint8_t*>(p) + bytes);
-}
-
 // Geometry of one (D, BITS, GS) instantiation.
 template <int D, int BITS, int GS>
 struct Geo {
@@ -548,7 +527,8 @@ __device__ __forceinline__ void decode_segment(const MfmaParams& p, float* s_acc
   __builtin_amdgcn_sched_barrier(0);
 
   // Q^T B operands, one 16-byte piece per lane and QK step m: head r, dims
-  // quad*QD + 8m + perm8(j).
+  // quad*QD + 8m + j, in the order the K dequantizer produces them (float16
+  // 4-bit: j = 0, 4, 1, 5, 2, 6, 3, 7; otherwise 0..7).
   uint32_t qt[G::NM][4];
 #pragma unroll
   for (int m = 0; m < G::NM; ++m) {

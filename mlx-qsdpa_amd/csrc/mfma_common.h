@@ -95,17 +95,8 @@ __device__ __forceinline__ uint32_t f16x2_fma(uint32_t c, uint32_t s, uint32_t b
                                                                 __builtin_bit_cast(f16x2, s),
                                                                 __builtin_bit_cast(f16x2, b)));
 }
-// Both halves = the low (sel 0x01000100) or high (0x03020302) half of x.
+// Both halves = the low half of x (v_perm_b32 selector 0x01000100).
 __device__ __forceinline__ uint32_t splat_lo(uint32_t x) { return perm(x, x, 0x01000100u); }
-__device__ __forceinline__ uint32_t splat_hi(uint32_t x) { return perm(x, x, 0x03020302u); }
-
-// Order of the 8 dims of one QK k-slice as the K dequantizer produces them:
-// slot j holds dim perm8(j) of the slice.
-template <typename Tag, int BITS>
-__device__ __forceinline__ constexpr int perm8(int j) {
-  if constexpr (Tag::kId == QSDPA_F16 && BITS == 4) return (j >> 1) + 4 * (j & 1);
-  else return j;
-}
 
 // K slice (8 dims of one token, BITS/4 packed words) -> A operand (4 pairs).
 // f16: s2 / b2 hold the group's scale / bias in both halves.  bf16: sf / bf
