@@ -433,9 +433,11 @@ __device__ __forceinline__ void decode_segment(const MfmaParams& p, float* s_acc
   // Positions below J - E go round-robin to the 8 waves; the last E go to
   // waves 0-3 only.  Waves 4-7 share their SIMDs with waves 0-3, and the
   // older waves' loads are served first, so equal shares would leave 0-3
-  // idle at the end; E = J / 4 (in whole rounds of 8) gives 0-3 five tiles
-  // for every three of 4-7.
-  const int E = 8 * (J / 32);
+  // idle at the end.  D = 256 (HBM-bound): E = J / 2 (in whole rounds of 8)
+  // gives 0-3 three tiles for every one of 4-7 (C3 24.6 against 25.9 us per
+  // step with five for three, C2 33.5 against 34.2); D = 128 (VALU-bound):
+  // E = J / 4, five for three (C4 62.5 against 65.5 us with three for one).
+  const int E = D == 256 ? 8 * (J / 16) : 8 * (J / 32);
   const int J8 = J - E;
   auto next_pos = [&](int j) -> int {
     if (j + kWaves < J8) return j + kWaves;
