@@ -437,7 +437,12 @@ __device__ __forceinline__ void decode_segment(const MfmaParams& p, float* s_acc
   // gives 0-3 three tiles for every one of 4-7 (C3 24.6 against 25.9 us per
   // step with five for three, C2 33.5 against 34.2); D = 128 (VALU-bound):
   // E = J / 4, five for three (C4 62.5 against 65.5 us with three for one).
-  const int E = D == 256 ? 8 * (J / 16) : 8 * (J / 32);
+  // Every wave's first position (its index) must lie in the round-robin part
+  // (J - E >= 8 whenever E > 0), or the waves' position sequences would
+  // overlap; both ratios keep E <= J / 2 with E = 0 below 16 positions, and
+  // the guard keeps it so.
+  const int E0 = D == 256 ? 8 * (J / 16) : 8 * (J / 32);
+  const int E = J - E0 >= kWaves ? E0 : 0;
   const int J8 = J - E;
   auto next_pos = [&](int j) -> int {
     if (j + kWaves < J8) return j + kWaves;
