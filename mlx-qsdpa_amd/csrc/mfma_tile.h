@@ -1,0 +1,433 @@
+// Per-tile building blocks of the matrix-core decode kernel
+// (decode_mfma.hip): tile geometry, the register layout of one 32-token K / V
+// tile, its QK / online softmax / PV step on v_mfma_f32_16x16x32_{f16,bf16}
+// tiles, and the cross-wave merge of a workgroup's rows.  The MFMA operand
+// layouts are described at the top of decode_mfma.hip.
+#pragma once
+
+#include "mfma_common.h"
+
+namespace qsdpa {
+namespace {
+// Cache policy of the K / V / scale / bias loads (the aux operand of the
+// buffer loads): non-temporal, as each row is read once per step; streaming
+// it past the caches keeps the split-K partials and Q resident (C3 25.7
+// against 26.4 us per step, C5 13.2 against 13.7).  Not where a lane reads
+// 64 contiguous bytes of a K row in four pieces (D = 256, 8-bit: C2 36.6
+// against 31.5 us with it).
+template <int D, int BITS>
+constexpr int load_policy() {
+  return D == 256 && BITS == 8 ? 0 : 2;
+}
+
+// Geometry of one (D, BITS, GS) instantiation.
+template <int D, int BITS, int GS>
+struct Geo {
+  static constexpr int NM = D / 32;             // QK MFMAs per 16-token half
+  static constexpr int NB = D / 16;             // PV MFMAs (dims per lane row)
+  static constexpr int QD = D / 4;              // K dims per lane (quarter row)
+  static constexpr int KW = QD * BITS / 32;     // K words per lane per half
+  static constexpr int WPS = BITS / 4;          // words per 8-dim slice
+  static constexpr int KG = QD >= GS ? QD / GS : 1;  // groups per K quarter (1 or 2)
+  static constexpr int VW = NB * BITS / 32;     // V words per lane per token
+  static constexpr int RW = D * BITS / 32;      // words per row
+  static constexpr int NG = D / GS;             // groups (scales) per row
+  static constexpr int ND = NG >= 2 ? NG / 2 : 1;  // 32-bit meta words per row
+  static_assert(KG == 1 || KG == 2, "groups per quarter");
+  static_assert(VW >= 1, "V piece");
+};
+
+// Registers of one tile: K (A layout, two halves), V (transposed pieces of the
+// lane's 8 tokens) and their scales / biases.
+template <int D, int BITS, int GS>
+struct TileRegs {
+  using G = Geo<D, BITS, GS>;
+  uint32_t kw[2][G::KW];
+  uint32_t ks[2];            // KG == 2: both groups (16-bit each); else low half
+  uint32_t kb[2];            // the K bias word(s) of the lane's group(s), as ks
+  uint32_t vw[8][G::VW];
+  uint32_t vs[2], vb[2];     // V scale / bias row words (A layout, per half)
+};
+
+// Per-lane constant byte offsets of a lane's loads relative to the tile's
+// first row: its row within the tile plus its piece of that row.
+struct LaneOffsets {
+  uint32_t k_r, ks_r, kb_r, v_r, vs_r, vb_r;
+};
+
+// Buffer descriptors of one workgroup's rows and the token strides in bytes.
+struct Rsrcs {
+  rsrc_t k, ks, kb, v, vs, vb;
+  uint32_t k_sn, ks_sn, kb_sn, v_sn, vs_sn, vb_sn;
+};
+
+template <int WORDS, int AUX>
+__device__ __forceinline__ void buffer_words(rsrc_t rs, uint32_t off, uint32_t* w) {
+  typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+  typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+  if constexpr (WORDS % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < WORDS / 4; ++i) {
+      const u4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16 * i, 0, AUX);
+      w[4 * i] = v[0]; w[4 * i + 1] = v[1]; w[4 * i + 2] = v[2]; w[4 * i + 3] = v[3];
+    }
+  } else if constexpr (WORDS == 2) {
+    const u2 v = __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, AUX);
+    w[0] = v[0]; w[1] = v[1];
+  } else {
+    w[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, AUX);
+  }
+}
+
+// Where a lane finds the V scale / bias of its group for its tokens:
+// ds_bpermute byte addresses of the source lanes for token slots j & 3, the
+// v_perm_b32 selector taking the right 16-bit half of two words, and the
+// shift that moves that half to the top (bf16 -> f32).
+struct VMetaLane {
+  int src[4];
+  uint32_t sel;
+  uint32_t shift;
+};
+
+template <typename Tag, int D, int BITS, int GS>
+struct Kernel {
+  static constexpr int kAux = load_policy<D, BITS>();
+  using G = Geo<D, BITS, GS>;
+  using Regs = TileRegs<D, BITS, GS>;
+  // Every K / V element is dequantized as mx.dequantize rounds it, T(fma(
+  // scale, code, bias)): float16 builds the code as an exact half (the
+  // 1024 + code bit trick, minus 1024) and uses one v_pk_fma_f16 per pair.
+  // (Rounding scale * code first and adding the bias afterwards saves an
+  // op per pair but is off by up to half an ulp of |scale * code|, which
+  // outruns the parity tolerance where a few keys carry a row.)
+
+  // Token of slot j (0..7) of quad q within a 32-token tile (the S^T C layout).
+  static __device__ __forceinline__ int tau(int q, int j) { return 16 * (j >> 2) + 4 * q + (j & 3); }
+
+  // Issue the K (load_k) or V (load_v) loads of the tile whose first token is
+  // `rel0` rows past the sequence's first key.  Rows past the end fall
+  // outside the buffer descriptors and read as zero (only the sequence's
+  // last tile has such rows; their scores are set to -inf).
+  static __device__ __forceinline__ void load_k(Regs& R, const Rsrcs& rs, const LaneOffsets& L, int rel0) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const uint32_t row = static_cast<uint32_t>(rel0 + 16 * u);
+      buffer_words<G::KW, kAux>(rs.k, row * rs.k_sn + L.k_r, R.kw[u]);
+      if constexpr (G::KG == 2)
+        R.ks[u] = __builtin_amdgcn_raw_buffer_load_b32(rs.ks, row * rs.ks_sn + L.ks_r, 0, kAux);
+      else
+        R.ks[u] = __builtin_amdgcn_raw_buffer_load_b16(rs.ks, row * rs.ks_sn + L.ks_r, 0, kAux);
+      if constexpr (G::KG == 2) {
+        R.kb[u] = __builtin_amdgcn_raw_buffer_load_b32(rs.kb, row * rs.kb_sn + L.kb_r, 0, kAux);
+      } else {
+        R.kb[u] = __builtin_amdgcn_raw_buffer_load_b16(rs.kb, row * rs.kb_sn + L.kb_r, 0, kAux);
+      }
+    }
+  }
+
+  static __device__ __forceinline__ void load_v(Regs& R, const Rsrcs& rs, const LaneOffsets& L, int rel0) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const uint32_t row = static_cast<uint32_t>(rel0 + 16 * u);
+      if constexpr (G::NG >= 2) {
+        R.vs[u] = __builtin_amdgcn_raw_buffer_load_b32(rs.vs, row * rs.vs_sn + L.vs_r, 0, kAux);
+        R.vb[u] = __builtin_amdgcn_raw_buffer_load_b32(rs.vb, row * rs.vb_sn + L.vb_r, 0, kAux);
+      } else {
+        R.vs[u] = __builtin_amdgcn_raw_buffer_load_b16(rs.vs, row * rs.vs_sn + L.vs_r, 0, kAux);
+        R.vb[u] = __builtin_amdgcn_raw_buffer_load_b16(rs.vb, row * rs.vb_sn + L.vb_r, 0, kAux);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t row = static_cast<uint32_t>(rel0 + 16 * (j >> 2) + (j & 3));
+      buffer_words<G::VW, kAux>(rs.v, row * rs.v_sn + L.v_r, R.vw[j]);
+    }
+  }
+
+  // S^T for one 16-token half u: K dequantized into the A operand (scale *
+  // code + bias with the lane's group scales / biases), Q^T as B.
+  static __device__ __forceinline__ f4 qk_half(const Regs& R, int u, const uint32_t (&qt)[G::NM][4]) {
+    uint32_t s2[2], b2[2];
+    float sf[2], bf[2];
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      const uint32_t sw = (G::KG == 2 && g == 1) ? (R.ks[u] >> 16) : R.ks[u];
+      const uint32_t bw = (G::KG == 2 && g == 1) ? (R.kb[u] >> 16) : R.kb[u];
+      s2[g] = splat_lo(sw);
+      sf[g] = to_f32<Tag>(static_cast<uint16_t>(sw));
+      b2[g] = splat_lo(bw);
+      bf[g] = to_f32<Tag>(static_cast<uint16_t>(bw));
+    }
+    f4 S = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int m = 0; m < G::NM; ++m) {
+      const int g = (G::KG == 2 && m >= G::NM / 2) ? 1 : 0;
+      uint32_t a[4];
+      dequant_k<Tag, BITS>(R.kw[u] + m * G::WPS, s2[g], b2[g], sf[g], bf[g], a);
+      S = mfma<Tag>(a, qt[m], S);
+    }
+    return S;
+  }
+
+  // out^T += V^T P^T: MFMA nb takes dim r*NB + nb of the lane's 8 tokens.
+  // sv2 / bv2: V scale / bias pairs of tokens (2i, 2i+1) of the lane's group.
+  template <typename IV>
+  static __device__ __forceinline__ void pv_f16(Regs& R, const uint32_t (&sv2)[4], const uint32_t (&bv2)[4],
+                                                const uint32_t (&pb)[4], f4 (&acc)[G::NB], IV&& issue_v) {
+    if constexpr (BITS == 4) {
+      // X: nibbles 0-3 of tokens (2i, 2i+1), Y: nibbles 4-7.
+      uint32_t X[4][G::VW], Y[4][G::VW];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int w = 0; w < G::VW; ++w) {
+          X[i][w] = perm(R.vw[2 * i + 1][w], R.vw[2 * i][w], 0x05040100u);
+          Y[i][w] = perm(R.vw[2 * i + 1][w], R.vw[2 * i][w], 0x07060302u);
+        }
+      issue_v(R);
+#pragma unroll
+      for (int nb = 0; nb < G::NB; ++nb) {
+        const int w = nb >> 3, k = nb & 7;
+        uint32_t a[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t src = k < 4 ? X[i][w] : Y[i][w];
+          a[i] = f16x2_fma(nib_codes(src, src >> 8, k & 3), sv2[i], bv2[i]);
+        }
+        acc[nb] = mfma<Tag>(a, pb, acc[nb]);
+      }
+    } else {
+      // Z0: bytes 0-1 of tokens (2i, 2i+1) interleaved, Z1: bytes 2-3.
+      uint32_t Z[4][G::VW][2];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int w = 0; w < G::VW; ++w) {
+          Z[i][w][0] = perm(R.vw[2 * i + 1][w], R.vw[2 * i][w], 0x05010400u);
+          Z[i][w][1] = perm(R.vw[2 * i + 1][w], R.vw[2 * i][w], 0x07030602u);
+        }
+      issue_v(R);
+#pragma unroll
+      for (int nb = 0; nb < G::NB; ++nb) {
+        const int w = nb >> 2, k = nb & 3;
+        uint32_t a[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t t = perm(kMagic8, Z[i][w][k >> 1], (k & 1) ? kSelB23 : kSelB01);
+          a[i] = f16x2_fma(f16x2_sub1024(t), sv2[i], bv2[i]);
+        }
+        acc[nb] = mfma<Tag>(a, pb, acc[nb]);
+      }
+    }
+  }
+
+  // One tile: QK, online softmax, PV.  Keys t of the tile (first key tb)
+  // outside [n0, n1) are masked (the sequence's first and last tiles may be
+  // partial).  The next tile's K loads are issued (issue_k) as soon as this
+  // tile's K has been consumed, and its V loads (issue_v) once V is in the PV
+  // operands' pre-permuted form, so one register set suffices.
+  template <typename IK, typename IV>
+  static __device__ __forceinline__ void compute_tile(Regs& R, const MfmaParams& p, const uint32_t (&qt)[G::NM][4],
+                                                      f4 (&acc)[G::NB], float& mrun, float& lrun, int tb, int n0,
+                                                      int n1, int quad, int64_t mrow, const VMetaLane& vm,
+                                                      IK&& issue_k, IV&& issue_v) {
+    // ---- S^T = K Q^T (Q^T operand m: 16 B per lane, in registers) ----
+    f4 S[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) S[u] = qk_half(R, u, qt);
+    issue_k(R);
+
+    // ---- scores of (the lane's row, tokens tau(quad, j)), online softmax ----
+    // n1: this lane's end of keys (the sequence's, or its causal limit).
+    float sc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sc[j] = S[j >> 2][j & 3] * p.qscale;
+    if (p.mask) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int t = min(tb + tau(quad, j), p.N - 1);
+        sc[j] += mask_value(p, mrow + static_cast<int64_t>(t) * p.m_sn);
+      }
+    }
+    if (__builtin_expect(tb + kTile > n1 || tb < n0, 0)) {  // a partial tile
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int t = tb + tau(quad, j);
+        if (t >= n1 || t < n0) sc[j] = -__builtin_huge_valf();
+      }
+    }
+    float tmax = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])),
+                       fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
+    tmax = fmaxf(tmax, shfl_xor_f32(tmax, 16));
+    tmax = fmaxf(tmax, shfl_xor_f32(tmax, 32));
+    const bool grow = tmax > mrun + kRescale;
+    if (__builtin_amdgcn_ballot_w64(grow)) {
+      const float mnew = grow ? tmax : mrun;
+      const float f = fast_exp2(mrun - mnew);
+      mrun = mnew;
+      lrun *= f;
+#pragma unroll
+      for (int i = 0; i < G::NB; ++i) acc[i] *= f;
+    }
+    float pr[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) pr[j] = fast_exp2(sc[j] - mrun);
+    lrun += ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
+
+    // ---- P^T operand: k slot 2i, 2i+1 = tokens tau(quad, 2i), tau(quad, 2i+1) ----
+    uint32_t pb[4], pb_lo[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pb[i] = pack_T2<Tag>(pr[2 * i], pr[2 * i + 1]);
+    if constexpr (Tag::kId == QSDPA_BF16) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        pb_lo[i] = pack_T2<Tag>(pr[2 * i] - unpack_T2_lo<Tag>(pb[i]),
+                                pr[2 * i + 1] - unpack_T2_hi<Tag>(pb[i]));
+    }
+
+    // ---- out^T += V^T P^T: MFMA nb takes dim r*NB + nb of the lane's tokens ----
+    // V scale / bias words of the lane's 8 tokens, gathered from the lanes
+    // that loaded those rows (A layout: token 16u + r, word quad % ND).
+    uint32_t dS[8], dB[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      dS[j] = __builtin_amdgcn_ds_bpermute(vm.src[j & 3], static_cast<int>(R.vs[j >> 2]));
+      dB[j] = __builtin_amdgcn_ds_bpermute(vm.src[j & 3], static_cast<int>(R.vb[j >> 2]));
+    }
+    if constexpr (Tag::kId == QSDPA_F16) {
+      uint32_t sv2[4], bv2[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sv2[i] = perm(dS[2 * i + 1], dS[2 * i], vm.sel);
+        bv2[i] = perm(dB[2 * i + 1], dB[2 * i], vm.sel);
+      }
+      pv_f16(R, sv2, bv2, pb, acc, issue_v);
+    } else {
+      float svf[8], bvf[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        svf[j] = __builtin_bit_cast(float, (dS[j] << vm.shift) & 0xFFFF0000u);
+        bvf[j] = __builtin_bit_cast(float, (dB[j] << vm.shift) & 0xFFFF0000u);
+      }
+      uint32_t lo[8][G::VW], hi[8][G::VW];
+      if constexpr (BITS == 4) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+          for (int w = 0; w < G::VW; ++w) {
+            lo[j][w] = R.vw[j][w] & 0x0F0F0F0Fu;         // nibbles 0, 2, 4, 6 as bytes
+            hi[j][w] = (R.vw[j][w] >> 4) & 0x0F0F0F0Fu;  // nibbles 1, 3, 5, 7
+          }
+      }
+#pragma unroll
+      for (int nb = 0; nb < G::NB; ++nb) {
+        uint32_t a[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float c[2];
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            const int j = 2 * i + e;
+            if constexpr (BITS == 4) {
+              const int w = nb >> 3, k = nb & 7;
+              const uint32_t src = (k & 1) ? hi[j][w] : lo[j][w];
+              c[e] = static_cast<float>((src >> (8 * (k >> 1))) & 0xFFu);
+            } else {
+              const int w = nb >> 2, k = nb & 3;
+              c[e] = static_cast<float>((R.vw[j][w] >> (8 * k)) & 0xFFu);
+            }
+            c[e] = fmaf(svf[j], c[e], bvf[j]);
+          }
+          a[i] = pack_T2<Tag>(c[0], c[1]);
+        }
+        acc[nb] = mfma<Tag>(a, pb, acc[nb]);
+        acc[nb] = mfma<Tag>(a, pb_lo, acc[nb]);
+      }
+      issue_v(R);
+    }
+  }
+};
+
+// Merge the NWV waves' running (m, l, acc) of a block's 16 query rows and
+// store the result: the normalised output (one split) or the split's partial
+// at column `col`.  row_of(w, h): wave w's accumulator row of query row h
+// (D floats, dims in order); ml_of(w, h): its (m, l).  Rows >= nh are
+// padding.  Called by all `nthreads` threads after a barrier.
+template <typename Tag, int D, int NWV, typename RowF, typename MlF>
+__device__ __forceinline__ void merge_store(const MfmaParams& p, RowF&& row_of, MlF&& ml_of, int nh, int v0,
+                                            int kvh, int b, int col, int nthreads) {
+  // 16 heads x D dims; thread -> (head, 8 consecutive dims).
+  constexpr int kPer = 8;
+  for (int idx = threadIdx.x; idx < 16 * (D / kPer); idx += nthreads) {
+    const int h = idx / (D / kPer);
+    const int d = (idx % (D / kPer)) * kPer;
+    if (h >= nh) continue;
+    f32x2 ml[NWV];
+#pragma unroll
+    for (int w = 0; w < NWV; ++w) ml[w] = ml_of(w, h);
+    float Mh = ml[0][0];
+#pragma unroll
+    for (int w = 1; w < NWV; ++w) Mh = fmaxf(Mh, ml[w][0]);
+    float L = 0.0f;
+    float v[kPer];
+#pragma unroll
+    for (int e = 0; e < kPer; ++e) v[e] = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NWV; ++w) {
+      const float f = fast_exp2(ml[w][0] - Mh);
+      L = fmaf(ml[w][1], f, L);
+      const float* src = row_of(w, h) + d;
+      const f4 a0 = *reinterpret_cast<const f4*>(src);
+      const f4 a1 = *reinterpret_cast<const f4*>(src + 4);
+      v[0] = fmaf(a0[0], f, v[0]); v[1] = fmaf(a0[1], f, v[1]);
+      v[2] = fmaf(a0[2], f, v[2]); v[3] = fmaf(a0[3], f, v[3]);
+      v[4] = fmaf(a1[0], f, v[4]); v[5] = fmaf(a1[1], f, v[5]);
+      v[6] = fmaf(a1[2], f, v[6]); v[7] = fmaf(a1[3], f, v[7]);
+    }
+    const int vh = v0 + h;
+    const int hh = kvh * p.G + vh % p.G;  // head and query position of the row
+    const int iq = vh / p.G;
+    if (p.num_splits == 1) {
+      const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+      uint32_t pk[kPer / 2];
+#pragma unroll
+      for (int e = 0; e < kPer / 2; ++e) pk[e] = pack_T2<Tag>(v[2 * e] * inv, v[2 * e + 1] * inv);
+      uint16_t* dst = p.out + static_cast<int64_t>(b) * p.o_sb + static_cast<int64_t>(hh) * p.o_sh +
+                      static_cast<int64_t>(iq) * p.o_sq + d;
+      // out rows are only 2-byte aligned in general: store pairs.
+#pragma unroll
+      for (int e = 0; e < kPer / 2; ++e) {
+        dst[2 * e] = static_cast<uint16_t>(pk[e]);
+        dst[2 * e + 1] = static_cast<uint16_t>(pk[e] >> 16);
+      }
+    } else {
+      // Partial rows: (b, head, position) rows, each with its splits.
+      const int64_t prow = static_cast<int64_t>(hh) * p.qL + iq;
+      const int64_t slot = p.units ? prow * (p.units + p.B) + col
+                                   : (static_cast<int64_t>(b) * p.Hq * p.qL + prow) * p.num_splits + col;
+      if constexpr (Tag::kId == QSDPA_F16) {
+        // float16 rows of the split's normalised output (acc / L, within
+        // the range of V), so the partials are half the bytes.  Plain
+        // stores: with the K / V stream non-temporal the rows stay in the
+        // caches for the merge (C3 25.2 against 25.6 us per step with
+        // streaming stores).
+        const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+        uint16_t* dst = reinterpret_cast<uint16_t*>(p.part_acc) + slot * D + d;
+        *reinterpret_cast<u4*>(dst) = u4{pack_T2<Tag>(v[0] * inv, v[1] * inv), pack_T2<Tag>(v[2] * inv, v[3] * inv),
+                                         pack_T2<Tag>(v[4] * inv, v[5] * inv), pack_T2<Tag>(v[6] * inv, v[7] * inv)};
+      } else {
+        // Streaming stores: the partials are read once, by the merge kernel.
+        float* dst = p.part_acc + slot * D + d;
+        __builtin_nontemporal_store(f4{v[0], v[1], v[2], v[3]}, reinterpret_cast<f4*>(dst));
+        __builtin_nontemporal_store(f4{v[4], v[5], v[6], v[7]}, reinterpret_cast<f4*>(dst + 4));
+      }
+      if (d == 0) {
+        p.part_ml[slot * 2] = Mh;
+        p.part_ml[slot * 2 + 1] = L;
+      }
+    }
+  }
+}
+
+}  // namespace
+}  // namespace qsdpa

@@ -1,0 +1,114 @@
+"""Per-phase timeline of the matrix-core decode kernel on one GPU.
+
+  python mlx-qsdpa_amd/timeline.py build            # here (hipcc): the probe library
+  python mlx-qsdpa_amd/timeline.py run [--config c3] # on the GPU
+
+``build`` compiles the library with -DQSDPA_TIMELINE into
+mlx_qsdpa_amd/libqsdpa_timeline.so: the same kernels, plus an s_memrealtime
+stamp (100 MHz clock) per wave at fixed points, copied out by
+qsdpa_debug_timeline().  ``run`` times the bench.py workload of a config
+(synthetic K/V cycled over enough sets to stream from HBM) and prints, for
+each point, the spread over the grid's waves in microseconds from the first
+wave's entry, plus the median per wave slot (0-7) of the workgroup.
+
+Points: entry; Q staged in LDS (after the workgroup barrier); k-th tile
+done; stream end (the wave's last tile); partials merged in LDS (after the
+barrier); stores issued; stores complete (after a full wait).  The last
+line compares the kernel's start / stop events (bench.py's measure) with
+the span of the stamps.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import sys
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+ROOT = HERE.parent
+LIB = HERE / "mlx_qsdpa_amd" / "libqsdpa_timeline.so"
+WGS, WAVES, SLOTS = 2048, 8, 18
+POINTS = [("entry", 0), ("Q staged", 1)] + [(f"tile {k} done", 2 + k) for k in range(12)] + [
+    ("stream end", 14), ("LDS merge done", 15), ("stores issued", 16), ("stores complete", 17)]
+
+
+def build() -> None:
+    sys.path.insert(0, str(HERE))
+    import build_lib
+
+    build_lib.build(jobs=8, extra_flags=["-DQSDPA_TIMELINE"], out=LIB)
+    print(f"built {LIB}")
+
+
+def run(config: str, n: int | None, calls: int, lib_path: Path = LIB) -> None:
+    for p in (ROOT, HERE):
+        sys.path.insert(0, str(p))
+    import numpy as np
+    import torch
+
+    import bench
+    from mlx_qsdpa_amd import _lib, kernels, metric
+
+    lib = _lib.load(lib_path)
+    _lib._lib = lib  # the kernels module launches through this library
+    lib.qsdpa_debug_timeline.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+    lib.qsdpa_debug_timeline.restype = ctypes.c_int
+    cfg = bench.CONFIGS[config]
+    B, Hq, Hkv, D, bits, gs, dt, N0, _ = cfg
+    N = n or N0
+    set_bytes = B * N * metric.kv_bytes_per_token(Hkv, D, bits, gs)
+    n_sets = max(2, int(1.2e9 // set_bytes) + 1)
+    sets = bench.make_sets(cfg, N, n_sets, torch.device("cuda:0"), 0)
+    plans = [kernels.DecodePlan(q, kq[0], vq[0], kq[1], vq[1], kq[2], vq[2], scale=D ** -0.5,
+                                bits=bits, group_size=gs) for q, kq, vq in sets]
+    nwg = plans[0].num_splits * Hkv * B * ((Hq // Hkv + 15) // 16)
+    if nwg > WGS:
+        raise SystemExit(f"{nwg} workgroups exceed the probe's {WGS}")
+    buf = np.zeros(WGS * WAVES * SLOTS, dtype=np.uint64)
+    hip = bench.HipEvents()
+    ev = hip.create(2 * calls)
+    for i in range(calls):
+        plans[i % n_sets]((ev[2 * i], ev[2 * i + 1]))
+    torch.cuda.synchronize()
+    ev_us = [hip.elapsed_ms(ev[2 * i], ev[2 * i + 1]) * 1e3 for i in range(calls)]
+    hip.destroy(ev)
+    if lib.qsdpa_debug_timeline(buf.ctypes.data, buf.nbytes) != 0:
+        raise SystemExit("qsdpa_debug_timeline failed")
+    t = buf[: nwg * WAVES * SLOTS].reshape(nwg, WAVES, SLOTS).astype(np.int64)
+    t0 = t[:, :, 0].min()
+    rel = np.where(t > 0, (t - t0) * 0.01, np.nan)  # 10 ns ticks -> us
+    print(f"# {config}: N={N}, {nwg} workgroups x {WAVES} waves, splits={plans[0].num_splits}, "
+          f"last of {calls} calls; us from the first wave's entry")
+    print("| point | p10 | p50 | p90 | max | median by wave 0-7 |")
+    print("|---|---|---|---|---|---|")
+    for name, k in POINTS:
+        x = rel[:, :, k]
+        if np.all(np.isnan(x)):
+            continue
+        by_wave = " ".join("-" if np.all(np.isnan(x[:, w])) else f"{np.nanmedian(x[:, w]):.2f}"
+                           for w in range(WAVES))
+        print(f"| {name} | {np.nanpercentile(x, 10):.2f} | {np.nanmedian(x):.2f} | "
+              f"{np.nanpercentile(x, 90):.2f} | {np.nanmax(x):.2f} | {by_wave} |")
+    span = (t[:, :, 17].max() - t0) * 0.01
+    print(f"\nkernel start / stop events: {ev_us[-1]:.2f} us for this call (median of the {calls}: "
+          f"{np.median(ev_us):.2f}); stamps span {span:.2f} us (first entry to last store complete)")
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("what", choices=["build", "run"])
+    ap.add_argument("--config", default="c3", choices=["c1", "c2", "c3", "c5"])
+    ap.add_argument("--n", type=int, default=None)
+    ap.add_argument("--calls", type=int, default=40)
+    ap.add_argument("--lib", default=str(LIB), help="probe library to run (default: the one `build` makes)")
+    a = ap.parse_args(argv)
+    if a.what == "build":
+        build()
+    else:
+        run(a.config, a.n, a.calls, Path(a.lib))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
