@@ -477,8 +477,11 @@ class QuantizedRotatingSDPACache:
         """cache.py:622-634, the reorder fused into the dequantize kernel."""
         n_visible = min(self.offset, self.max_size)
         src = _sl(tup, 0, n_visible)
+        rot = self._ring_rot(n_visible)
+        # Without a rotation the reorder is the identity (the window may hold
+        # fewer tokens than `keep` then).
         return kernels.dequantize(*src, group_size=self.group_size, bits=self.bits,
-                                  keep=self.keep, rot=self._ring_rot(n_visible))
+                                  keep=self.keep if rot else 0, rot=rot)
 
     def _update_prefill(self, keys, values):
         """cache.py:593-620: dequantize (temporal) + concat + keep window + requantize."""
@@ -634,8 +637,9 @@ class BatchQuantizedRotatingSDPACache:
     def _dequant_temporal(self, tup):
         """cache.py:842-857, reorder fused into the dequantize kernel."""
         n_visible = min(self._idx, self.max_size)
+        rot = self._ring_rot()
         return kernels.dequantize(*_sl(tup, 0, n_visible), group_size=self.group_size,
-                                  bits=self.bits, keep=self.keep, rot=self._ring_rot())
+                                  bits=self.bits, keep=self.keep if rot else 0, rot=rot)
 
     def _update_prefill(self, keys, values):
         """cache.py:813-840."""

@@ -152,6 +152,10 @@ def quantized_sdpa(
     B, H_q, qL, D, H_kv, N = _validate(q, packed_k, packed_v, bits, group_size)
     if scale is None:
         scale = D ** -0.5                                          # dispatch.py:86-87
+    # The kernels read packed rows in 16-byte pieces; a view whose rows are
+    # not 16-byte aligned is copied first, as the reference's kernel builder
+    # copies every input (ensure_row_contiguous, kernels.py:190).
+    packed_k, packed_v = _row_aligned(packed_k), _row_aligned(packed_v)
 
     if qL > 1 and not _fused_takes(q, packed_k, packed_v, k_scales, v_scales, k_biases,
                                    v_biases, scale, bits, group_size):
@@ -182,6 +186,13 @@ def quantized_sdpa(
     return kernels.decode(q, packed_k, packed_v, k_scales, v_scales, k_biases, v_biases,
                           scale=scale, bits=bits, group_size=group_size, mask=mask,
                           kv_start=kv_start, num_splits=num_splits, causal=causal)
+
+
+def _row_aligned(t):
+    """`t` itself if its rows start on 16-byte boundaries, else a contiguous copy."""
+    if t.data_ptr() % 16 == 0 and all(st % 4 == 0 for st in t.stride()[:3]) and t.stride(-1) == 1:
+        return t
+    return t.contiguous()
 
 
 def _fused_takes(q, packed_k, packed_v, k_scales, v_scales, k_biases, v_biases, scale, bits,

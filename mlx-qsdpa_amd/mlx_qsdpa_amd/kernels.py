@@ -45,6 +45,19 @@ def _view(t: torch.Tensor | None) -> _lib.View:
     return _lib.View(t.data_ptr(), s[0], s[1], s[2])
 
 
+def _rows_in_storage(t: torch.Tensor) -> int:
+    """Token rows (dim 2) a [B, H, N, inner] view could address within its
+    storage with its own strides: the largest n such that element
+    (B-1, H-1, n-1, inner-1) lies inside the storage."""
+    B, H, _, inner = t.shape
+    sb, sh, sn, _ = t.stride()
+    elems = t.untyped_storage().nbytes() // t.element_size()
+    last_other = t.storage_offset() + (B - 1) * sb + (H - 1) * sh + inner - 1
+    if sn <= 0:
+        return t.shape[2]
+    return max(0, (elems - 1 - last_other) // sn + 1)
+
+
 def _stream(t: torch.Tensor) -> int:
     return torch.cuda.current_stream(t.device).cuda_stream
 
@@ -242,6 +255,22 @@ class DecodePlan:
 
     def __init__(self, q, pk, pv, ks, vs, kb, vb, *, scale, bits, group_size, mask=None,
                  kv_start=None, num_splits=0, capacity=None, causal=False):
+        # Rows set_keys may reach: the views' own length unless the caller
+        # states how many rows the underlying buffers hold, never more than
+        # every buffer's storage holds, and never past a mask's last key.
+        n0 = int(pk.shape[2])
+        self.capacity = int(capacity) if capacity is not None else n0
+        if self.capacity < n0:
+            raise ValueError(f"capacity {self.capacity} is below the views' {n0} keys")
+        if self.capacity > n0:
+            if mask is not None:
+                raise ValueError("a mask covers the construction-time keys only: give capacity "
+                                 "without a mask, or build a new plan per mask")
+            for name, t in (("packed_k", pk), ("packed_v", pv), ("k_scales", ks), ("v_scales", vs),
+                            ("k_biases", kb), ("v_biases", vb)):
+                if t is not None and _rows_in_storage(t) < self.capacity:
+                    raise ValueError(f"{name}: its storage holds {_rows_in_storage(t)} rows, "
+                                     f"fewer than capacity {self.capacity}")
         _require_device(q, pk, pv, ks, vs, kb, vb, mask, kv_start)
         self.q = _inner_contig(q)
         self.out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
@@ -262,9 +291,6 @@ class DecodePlan:
             self.args.workspace_bytes = ws
         self._args_ref = ctypes.byref(self.args)
         self.device = q.device
-        # Rows set_keys may reach: the views' own length unless the caller
-        # states how many rows the underlying buffers hold.
-        self.capacity = int(capacity) if capacity is not None else int(pk.shape[2])
         self.args.num_splits = self.num_splits  # fixed from here on (set_keys)
 
     def set_keys(self, n: int) -> None:

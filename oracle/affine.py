@@ -63,13 +63,18 @@ DTYPES = ("f16", "bf16")
 # T rounding
 # ---------------------------------------------------------------------------
 def f32_to_bf16_bits(x) -> np.ndarray:
-    """Round float32 values to bfloat16 (nearest-even); returns uint16 bits."""
-    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
-    is_nan = (u & 0x7FFFFFFF) > 0x7F800000
-    lsb = (u >> 16) & 1
-    r = ((u + 0x7FFF + lsb) >> 16) & 0xFFFF
-    r = np.where(is_nan, ((u >> 16) | 0x40) & 0xFFFF, r)
-    return r.astype(np.uint16)
+    """Round float32 values to bfloat16 (nearest-even); returns uint16 bits.
+
+    uint32 arithmetic: u + 0x7FFF + lsb stays below 2^32 for every non-NaN
+    pattern (at most 0xFF800000 + 0x8000); NaN patterns, where it may wrap,
+    are replaced by the quiet-NaN branch.
+    """
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+    is_nan = (u & np.uint32(0x7FFFFFFF)) > np.uint32(0x7F800000)
+    lsb = (u >> np.uint32(16)) & np.uint32(1)
+    with np.errstate(over="ignore"):
+        r = ((u + np.uint32(0x7FFF) + lsb) >> np.uint32(16)).astype(np.uint16)
+    return np.where(is_nan, ((u >> np.uint32(16)) | np.uint32(0x40)).astype(np.uint16), r).astype(np.uint16)
 
 
 def bf16_bits_to_f32(b) -> np.ndarray:

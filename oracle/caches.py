@@ -4,20 +4,26 @@ TEST INFRASTRUCTURE.  Each buffer is a 3-tuple (packed uint32, scales,
 biases) with scales/biases T-valued float32 (see affine.py).  Index logic
 follows the reference line by line; the citations are on each method.
 
-Extension (parity unpinned: the reference asserts keep == 0 at
-cache.py:512, 732): ``keep > 0`` keeps the first ``keep`` slots as attention
-sinks.  Ring writes then cycle over [keep, max_size): the slot after the last
-one is ``keep`` instead of 0, temporal order is
+Extension (the reference asserts keep == 0 at cache.py:512, 732):
+``keep > 0`` keeps the first ``keep`` slots as attention sinks.  Ring
+writes then cycle over [keep, max_size): the slot after the last one is
+``keep`` instead of 0, temporal order is
 [0:keep] + [ring pointer:max_size] + [keep:ring pointer], and a prefill that
 overflows the window keeps the first ``keep`` and the newest
 ``max_size - keep`` tokens.  With keep == 0 every rule reduces to the
 reference's.
 
-Masks after the ring wraps (parity unpinned: the reference's mask width
+Masks after the ring wraps (the reference's mask width
 min(offset, max_size) + N disagrees with the returned key length there,
 cache.py:636-644 vs 588-591): ``make_mask`` below reproduces the reference
 exactly while offset + N <= max_size and otherwise returns the lower-right
 aligned causal mask over the returned window.
+
+Both extensions are pinned by tests/test_cache_invariants.py: a logical
+window model (tests/window_model.py, temporal order only, no ring
+arithmetic) must agree with these caches after every update of random
+decode / prefill sequences across several wraps, and a mask taken before an
+update must be lower-right causal over exactly the keys it returns.
 """
 
 from __future__ import annotations

@@ -83,6 +83,9 @@ def _cpu_quantize_into(src, dst, t0, bits, group_size):
 
 
 def _cpu_dequantize(packed, scales, biases=None, group_size=64, bits=4, keep=0, rot=0):
+    n = packed.shape[-2]
+    if not 0 <= keep <= n or rot < 0 or (rot > 0 and keep >= n):  # as kernels.dequantize_into
+        raise ValueError(f"bad keep={keep} / rot={rot} for N={n}")
     name = dtype_name(scales.dtype)
     out = affine.dequantize(to_np(packed), to_np(scales),
                             None if biases is None else to_np(biases), group_size, bits, name)

@@ -348,8 +348,11 @@ def test_strided_cache_views(device):
     assert_close(to_np(out), oracle_out(inp), "strided")
 
 
-def test_prefill_fallback(device):
-    """qL > 1 -> dequantize + attention (dispatch.py:68-83), causal and bool masks."""
+def test_multi_query_through_quantized_sdpa(device):
+    """qL > 1 through quantized_sdpa with aligned D = 128 inputs: the fused
+    kernel, without a mask and with mask="causal".  (The dequantize +
+    attention path for shapes the fused kernel does not take is covered by
+    test_gpu_parity_full.py::test_multi_query_fallback_path.)"""
     rng = np.random.default_rng(16)
     inp = make_inputs(rng, 1, 4, 2, 64, 128, 4, 32)
     q = affine.random_T(rng, (1, 4, 8, 128), "f16")

@@ -367,3 +367,33 @@ def test_streamk_schedule_invariants(seed):
         assert all(mine[i][1] == mine[i + 1][0] for i in range(len(mine) - 1))
         first, count = sched[b]
         assert [c for _, _, c in mine] == list(range(first, first + count))
+
+
+# ---- DecodePlan: how far set_keys may move N --------------------------------
+def test_plan_capacity_checks():
+    """A plan's capacity may not exceed any buffer's storage (set_keys would
+    send the kernel past it) nor go with a mask sized for fewer keys (the
+    kernel would read the mask past its end).  Checked before any device use."""
+    from mlx_qsdpa_amd import kernels
+
+    B, Hkv, cap, n0, D, bits, gs = 2, 2, 64, 40, 128, 4, 32
+    W, G = D * bits // 32, D // gs
+    full = [torch.zeros((B, Hkv, cap, w), dtype=dt) for w, dt in
+            ((W, torch.uint32), (W, torch.uint32), (G, torch.float16), (G, torch.float16),
+             (G, torch.float16), (G, torch.float16))]
+    views = [t[:, :, :n0] for t in full]
+    assert [kernels._rows_in_storage(v) for v in views] == [cap] * 6
+    # the last head's rows end where the storage ends
+    assert kernels._rows_in_storage(full[0][:, 1:, :n0]) == cap
+    q = torch.zeros((B, 8, 1, D), dtype=torch.float16)
+    args = dict(scale=1.0, bits=bits, group_size=gs)
+    with pytest.raises(ValueError, match="storage holds 64 rows"):
+        kernels.DecodePlan(q, *views[:2], views[2], views[3], views[4], views[5], capacity=cap + 1, **args)
+    with pytest.raises(ValueError, match="mask"):
+        kernels.DecodePlan(q, *views[:2], views[2], views[3], views[4], views[5], capacity=cap,
+                           mask=torch.ones((B, 1, 1, n0), dtype=torch.bool), **args)
+    with pytest.raises(ValueError, match="below"):
+        kernels.DecodePlan(q, *views[:2], views[2], views[3], views[4], views[5], capacity=n0 - 1, **args)
+    # within capacity the plan reaches the device check (these are CPU tensors)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        kernels.DecodePlan(q, *views[:2], views[2], views[3], views[4], views[5], capacity=cap, **args)
