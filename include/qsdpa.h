@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define QSDPA_ABI_VERSION 2
+#define QSDPA_ABI_VERSION 3
 
 enum {
   QSDPA_OK = 0,
@@ -144,6 +144,22 @@ int64_t qsdpa_decode_workspace_size(const qsdpa_decode_args* args,
 
 /* Launch the decode on `stream`. */
 int qsdpa_decode(const qsdpa_decode_args* args, void* stream);
+
+/*
+ * qsdpa_decode without a caller workspace: no counterpart in the reference.
+ * For callers that cannot allocate -- code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc.  Same arguments and
+ * results as qsdpa_decode, except that args->workspace / workspace_bytes are
+ * ignored: the split-K partials live in a static device array of
+ * QSDPA_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends.
+ * Arguments whose partials need more (qsdpa_decode_workspace_size) return
+ * QSDPA_ERR_WORKSPACE.  The call allocates and frees nothing (the first
+ * call on a device looks the array's address up).  Every call on one GPU
+ * shares that GPU's array: calls that overlap on one GPU (two streams, two
+ * host threads) race and must be serialised by the caller.
+ */
+#define QSDPA_NOALLOC_SCRATCH_BYTES (16u << 20)
+int qsdpa_decode_noalloc(const qsdpa_decode_args* args, void* stream);
 
 /*
  * Quantize rows of T values into the affine format and store them at token

@@ -163,6 +163,64 @@ int streamk_units(const qsdpa_decode_args* a, int splits) {
   return static_cast<int>(units);
 }
 
+// Launch the decode for validated arguments: the main kernel, then (split-K)
+// the merge, with the partials in `workspace` (decode_plan's layout).
+int run_decode(const qsdpa_decode_args* args, int splits, void* workspace, hipStream_t s) {
+  float* part_acc = nullptr;
+  float* part_ml = nullptr;
+  int* sched = nullptr;
+  if (splits > 1) {
+    const int64_t rows = static_cast<int64_t>(args->B) * args->H_q * std::max(args->q_len, 1);
+    part_acc = static_cast<float*>(workspace);
+    part_ml = part_acc + rows * (splits + 1) * args->D;
+    sched = reinterpret_cast<int*>(part_ml + rows * (splits + 1) * 2);
+  }
+  // (prof_begin / prof_end ride on the main kernel's own dispatch)
+  const bool mfma = mfma_supports(args);
+  const int units = streamk_units(args, splits);
+  int rc;
+  if (mfma) rc = launch_decode_mfma(args, splits, part_acc, part_ml, units, sched, s);
+  else rc = launch_decode_valu(args, splits, part_acc, part_ml, s);
+  if (rc) return rc;
+  // The MFMA kernel stores float16 inputs' partials as normalised float16
+  // rows (in the first half of the float32 area).
+  if (splits > 1)
+    rc = launch_merge(args, splits, part_acc, part_ml, mfma && args->dtype == QSDPA_F16, units ? sched : nullptr,
+                      units + args->B, s);
+  return rc;
+}
+
+// Split-K scratch of qsdpa_decode_noalloc: a static device array, one copy
+// per GPU, alive until the process ends.  Host code never passes the array's
+// name to a kernel (on the host it is only a stand-in): each device's address
+// comes from hipGetSymbolAddress on the first call on that device.  Every
+// call on one GPU shares that GPU's array, so calls that overlap on one GPU
+// (two streams, or two host threads) race on it.  Nothing in it needs to
+// start at zero: every partial the merge reads is written by the same call.
+constexpr size_t kScratchBytes = QSDPA_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+int scratch_address(void** out) {
+  constexpr int kMaxDevices = 64;
+  static void* addr[kMaxDevices] = {};
+  static std::mutex mu;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(QSDPA_ERR_LAUNCH, "hipGetDevice failed: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(QSDPA_ERR_UNSUPPORTED, "device %d beyond %d", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(mu);
+  if (!addr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(QSDPA_ERR_LAUNCH, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                  hipGetErrorString(e));
+    addr[dev] = p;
+  }
+  *out = addr[dev];
+  return QSDPA_OK;
+}
+
 }  // namespace qsdpa
 
 using namespace qsdpa;
@@ -193,32 +251,33 @@ int qsdpa_decode(const qsdpa_decode_args* args, void* stream) {
   int64_t ws = 0;
   rc = decode_plan(args, &splits, &ws);
   if (rc) return rc;
-  float* part_acc = nullptr;
-  float* part_ml = nullptr;
   if (splits > 1) {
     if (!args->workspace || static_cast<int64_t>(args->workspace_bytes) < ws)
       return fail(QSDPA_ERR_WORKSPACE, "workspace of %lld bytes required, got %lld",
                   static_cast<long long>(ws), static_cast<long long>(args->workspace_bytes));
     if (!aligned(args->workspace, 16)) return fail(QSDPA_ERR_INVALID, "workspace not 16-byte aligned");
-    part_acc = static_cast<float*>(args->workspace);
-    part_ml = part_acc + static_cast<int64_t>(args->B) * args->H_q * std::max(args->q_len, 1) * (splits + 1) * args->D;
   }
-  int* sched = part_ml ? reinterpret_cast<int*>(part_ml + static_cast<int64_t>(args->B) * args->H_q *
-                                                              std::max(args->q_len, 1) * (splits + 1) * 2)
-                       : nullptr;
-  const hipStream_t s = static_cast<hipStream_t>(stream);
-  // (prof_begin / prof_end ride on the main kernel's own dispatch)
-  const bool mfma = mfma_supports(args);
-  const int units = streamk_units(args, splits);
-  if (mfma) rc = launch_decode_mfma(args, splits, part_acc, part_ml, units, sched, s);
-  else rc = launch_decode_valu(args, splits, part_acc, part_ml, s);
+  return run_decode(args, splits, args->workspace, static_cast<hipStream_t>(stream));
+}
+
+int qsdpa_decode_noalloc(const qsdpa_decode_args* args, void* stream) {
+  clear_error();
+  int rc = validate_decode(args);
   if (rc) return rc;
-  // The MFMA kernel stores float16 inputs' partials as normalised float16
-  // rows (in the first half of the float32 area).
-  if (splits > 1)
-    rc = launch_merge(args, splits, part_acc, part_ml, mfma && args->dtype == QSDPA_F16, units ? sched : nullptr,
-                      units + args->B, s);
-  return rc;
+  int splits = 1;
+  int64_t ws = 0;
+  rc = decode_plan(args, &splits, &ws);
+  if (rc) return rc;
+  void* scratch_ptr = nullptr;
+  if (splits > 1) {
+    if (ws > static_cast<int64_t>(kScratchBytes))
+      return fail(QSDPA_ERR_WORKSPACE,
+                  "these arguments need %lld bytes of split-K scratch; the static scratch holds %lld "
+                  "(use qsdpa_decode with a workspace, or fewer splits / query rows)",
+                  static_cast<long long>(ws), static_cast<long long>(kScratchBytes));
+    if ((rc = scratch_address(&scratch_ptr))) return rc;
+  }
+  return run_decode(args, splits, scratch_ptr, static_cast<hipStream_t>(stream));
 }
 
 int qsdpa_quantize(const qsdpa_quantize_args* a, void* stream) {

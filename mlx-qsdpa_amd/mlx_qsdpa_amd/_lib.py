@@ -23,12 +23,14 @@ QSDPA_BF16 = 1
 QSDPA_F32 = 2
 QSDPA_BOOL = 3
 
-ABI_VERSION = 2
+ABI_VERSION = 3
+NOALLOC_SCRATCH_BYTES = 16 << 20
 
 # Every symbol include/qsdpa.h declares.
 EXPORTED_SYMBOLS = (
     "qsdpa_decode_workspace_size",
     "qsdpa_decode",
+    "qsdpa_decode_noalloc",
     "qsdpa_quantize",
     "qsdpa_quantize_batch",
     "qsdpa_dequantize",
@@ -109,6 +111,8 @@ def load(path: os.PathLike | str | None = None) -> ctypes.CDLL:
     lib.qsdpa_decode_workspace_size.restype = ctypes.c_int64
     lib.qsdpa_decode.argtypes = [ctypes.POINTER(DecodeArgs), ctypes.c_void_p]
     lib.qsdpa_decode.restype = ctypes.c_int
+    lib.qsdpa_decode_noalloc.argtypes = [ctypes.POINTER(DecodeArgs), ctypes.c_void_p]
+    lib.qsdpa_decode_noalloc.restype = ctypes.c_int
     lib.qsdpa_quantize.argtypes = [ctypes.POINTER(QuantizeArgs), ctypes.c_void_p]
     lib.qsdpa_quantize.restype = ctypes.c_int
     lib.qsdpa_quantize_batch.argtypes = [ctypes.POINTER(QuantizeArgs), ctypes.c_int32, ctypes.c_void_p]
