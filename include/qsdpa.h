@@ -207,6 +207,40 @@ typedef struct {
 
 int qsdpa_dequantize(const qsdpa_dequantize_args* args, void* stream);
 
+/*
+ * Rotating-window prefill in one launch per call (K and V: count = 2):
+ * the window's old tokens in temporal order, then the S new tokens; when
+ * there are more than max_size, the first `keep` and the newest
+ * max_size - keep are kept; all of them are quantized again into rows
+ * [0, total) of the destination, total = min(n_old + S, max_size).
+ *   old token c (temporal position c < n_old) is old row u(c) = c for
+ *   c < keep or rot == 0, else keep + (c - keep + rot) % (n_old - keep),
+ *   dequantized as qsdpa_dequantize does (T(fmaf(scale, q, bias)));
+ *   new token i is src row i;
+ *   each kept row is quantized as qsdpa_quantize does.
+ * The destination must not overlap the old window.
+ * Replaces the dequantize + concatenate + trim + quantize of
+ * mlx_qsdpa/cache.py:593-634 (QuantizedRotatingSDPACache._update_prefill,
+ * _dequant_temporal) and cache.py:813-857 (the batched cache's).
+ */
+typedef struct {
+  int32_t B, H, D;
+  int32_t bits, group_size, dtype;
+  int32_t n_old;            /* tokens in the old window (may be 0)        */
+  int32_t keep, rot;        /* the old window's ring order (see above)    */
+  int32_t S;                /* new tokens                                 */
+  int32_t max_size;         /* window size                                */
+  qsdpa_view old_packed;    /* [B, H, >= n_old, D*bits/32] uint32         */
+  qsdpa_view old_scales;    /* [B, H, >= n_old, D/group_size] dtype       */
+  qsdpa_view old_biases;    /* ptr NULL => zero biases                    */
+  qsdpa_view src;           /* [B, H, S, D] dtype                         */
+  qsdpa_view dst_packed;    /* [B, H, >= total, D*bits/32] (writable)     */
+  qsdpa_view dst_scales;
+  qsdpa_view dst_biases;
+} qsdpa_requant_args;
+
+int qsdpa_requant_window(const qsdpa_requant_args* jobs, int32_t count, void* stream);
+
 /* Thread-local message describing the last error ("" if none). */
 const char* qsdpa_last_error(void);
 

@@ -312,6 +312,42 @@ int qsdpa_quantize_batch(const qsdpa_quantize_args* jobs, int32_t count, void* s
   return launch_quantize(ptrs, count, static_cast<hipStream_t>(stream));
 }
 
+int qsdpa_requant_window(const qsdpa_requant_args* jobs, int32_t count, void* stream) {
+  clear_error();
+  if (!jobs) return fail(QSDPA_ERR_INVALID, "null args");
+  if (count < 1 || count > 2) return fail(QSDPA_ERR_INVALID, "count must be 1 or 2, got %d", count);
+  for (int i = 1; i < count; ++i)
+    if (jobs[i].bits != jobs[0].bits || jobs[i].group_size != jobs[0].group_size || jobs[i].dtype != jobs[0].dtype)
+      return fail(QSDPA_ERR_INVALID, "requant jobs of one call must share bits, group_size and dtype");
+  const qsdpa_requant_args* ptrs[2];
+  for (int i = 0; i < count; ++i) {
+    const qsdpa_requant_args* a = jobs + i;
+    if (a->bits != 4 && a->bits != 8) return fail(QSDPA_ERR_INVALID, "bits must be 4 or 8, got %d", a->bits);
+    if (a->group_size != 32 && a->group_size != 64 && a->group_size != 128)
+      return fail(QSDPA_ERR_UNSUPPORTED, "group_size=%d not supported (32, 64, 128)", a->group_size);
+    if (!valid_dtype(a->dtype)) return fail(QSDPA_ERR_INVALID, "dtype must be F16 or BF16");
+    if (a->B < 0 || a->H < 0 || a->D <= 0 || a->D % a->group_size != 0)
+      return fail(QSDPA_ERR_INVALID, "bad shape B=%d H=%d D=%d gs=%d", a->B, a->H, a->D, a->group_size);
+    if (a->max_size < 1 || a->keep < 0 || a->keep >= a->max_size || a->n_old < 0 || a->n_old > a->max_size ||
+        a->S < 0 || a->rot < 0 || (a->rot > 0 && a->n_old <= a->keep))
+      return fail(QSDPA_ERR_INVALID, "bad window (max_size=%d keep=%d n_old=%d S=%d rot=%d)", a->max_size,
+                  a->keep, a->n_old, a->S, a->rot);
+    int rc;
+    const bool old = a->n_old > 0, add = a->S > 0;
+    if ((rc = check_view(a->old_packed, "old_packed", 4, 1, old))) return rc;
+    if ((rc = check_view(a->old_scales, "old_scales", 2, 1, old))) return rc;
+    if ((rc = check_view(a->old_biases, "old_biases", 2, 1, false))) return rc;
+    if ((rc = check_view(a->src, "src", 2, 1, add))) return rc;
+    if ((rc = check_view(a->dst_packed, "dst_packed", 4, 1, true))) return rc;
+    if ((rc = check_view(a->dst_scales, "dst_scales", 2, 1, true))) return rc;
+    if ((rc = check_view(a->dst_biases, "dst_biases", 2, 1, true))) return rc;
+    if (a->old_packed.ptr && a->old_packed.ptr == a->dst_packed.ptr)
+      return fail(QSDPA_ERR_INVALID, "the destination must not be the old window");
+    ptrs[i] = a;
+  }
+  return launch_requant(ptrs, count, static_cast<hipStream_t>(stream));
+}
+
 int qsdpa_dequantize(const qsdpa_dequantize_args* a, void* stream) {
   clear_error();
   if (!a) return fail(QSDPA_ERR_INVALID, "null args");

@@ -48,6 +48,53 @@ __device__ __forceinline__ void group_minmax(float& lo, float& hi) {
   }
 }
 
+// Quantize one group of GS values spread over L consecutive lanes (VALS =
+// GS / L T values per lane, as raw 16-bit patterns): min / max across the
+// lanes, then the edge-snapped affine rule, every operation an explicitly
+// rounded intrinsic; each lane packs its own VALS codes to `dst` and lane 0
+// of the group stores the scale and bias.  Shared by quantize_kernel and
+// requant_kernel so the two stay bit-identical.
+template <typename Tag, int BITS, int GS, int L>
+__device__ __forceinline__ void quantize_group(const uint16_t (&raw)[GS / L], int part, uint32_t* dst,
+                                               uint16_t* scale_dst, uint16_t* bias_dst) {
+  constexpr int VALS = GS / L;
+  constexpr int PER = 32 / BITS;
+  constexpr int WORDS = VALS / PER;
+  constexpr float kBins = static_cast<float>((1 << BITS) - 1);
+  float w_min = __builtin_huge_valf(), w_max = -__builtin_huge_valf();
+#pragma unroll
+  for (int i = 0; i < VALS; ++i) {
+    const float v = to_f32<Tag>(raw[i]);
+    w_min = fminf(w_min, v);
+    w_max = fmaxf(w_max, v);
+  }
+  group_minmax<L>(w_min, w_max);
+  float scale = fmaxf(__fdiv_rn(__fsub_rn(w_max, w_min), kBins), 1e-7f);
+  const bool side = fabsf(w_min) > fabsf(w_max);
+  scale = side ? scale : -scale;
+  const float edge = side ? w_min : w_max;
+  const float q0 = rintf(__fdiv_rn(edge, scale));
+  const bool nz = q0 != 0.0f;
+  if (nz) scale = __fdiv_rn(edge, q0);
+  const float bias = nz ? edge : 0.0f;
+#pragma unroll
+  for (int w = 0; w < WORDS; ++w) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const float v = to_f32<Tag>(raw[w * PER + j]);
+      float q = rintf(__fdiv_rn(__fsub_rn(v, bias), scale));
+      q = fminf(fmaxf(q, 0.0f), kBins);
+      word |= static_cast<uint32_t>(q) << (j * BITS);
+    }
+    dst[w] = word;
+  }
+  if (part == 0) {
+    *scale_dst = from_f32<Tag>(scale);
+    *bias_dst = from_f32<Tag>(bias);
+  }
+}
+
 // Up to kMaxJobs quantize jobs (the keys and values of one cache update)
 // run in one launch, job = blockIdx.y; they share dtype, bits and
 // group_size.
@@ -69,8 +116,6 @@ template <typename Tag, int BITS, int GS, int L, bool VEC, typename I>
 __global__ __launch_bounds__(256) void quantize_kernel(QuantJobs jobs) {
   constexpr int VALS = GS / L;  // values per lane, a multiple of 8
   constexpr int PER = 32 / BITS;
-  constexpr int WORDS = VALS / PER;  // packed words per lane
-  constexpr float kBins = static_cast<float>((1 << BITS) - 1);
   const QuantParams& p = jobs.p[blockIdx.y];
   const int ng = p.D / GS;
   const I total = static_cast<I>(p.B) * p.H * p.S * ng;
@@ -103,41 +148,10 @@ __global__ __launch_bounds__(256) void quantize_kernel(QuantJobs jobs) {
     for (int i = 0; i < VALS; ++i) raw[i] = src[i];
   }
 
-  float w_min = __builtin_huge_valf(), w_max = -__builtin_huge_valf();
-#pragma unroll
-  for (int i = 0; i < VALS; ++i) {
-    const float v = to_f32<Tag>(raw[i]);
-    w_min = fminf(w_min, v);
-    w_max = fmaxf(w_max, v);
-  }
-  group_minmax<L>(w_min, w_max);
-  float scale = fmaxf(__fdiv_rn(__fsub_rn(w_max, w_min), kBins), 1e-7f);
-  const bool side = fabsf(w_min) > fabsf(w_max);
-  scale = side ? scale : -scale;
-  const float edge = side ? w_min : w_max;
-  const float q0 = rintf(__fdiv_rn(edge, scale));
-  const bool nz = q0 != 0.0f;
-  if (nz) scale = __fdiv_rn(edge, q0);
-  const float bias = nz ? edge : 0.0f;
-
   const int t = p.t0 + s;
-  uint32_t* dst = p.dp + off3(b, h, t, p.p_sb, p.p_sh, p.p_sn) + (g * GS + part * VALS) / PER;
-#pragma unroll
-  for (int w = 0; w < WORDS; ++w) {
-    uint32_t word = 0;
-#pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      const float v = to_f32<Tag>(raw[w * PER + j]);
-      float q = rintf(__fdiv_rn(__fsub_rn(v, bias), scale));
-      q = fminf(fmaxf(q, 0.0f), kBins);
-      word |= static_cast<uint32_t>(q) << (j * BITS);
-    }
-    dst[w] = word;
-  }
-  if (part == 0) {
-    p.ds[off3(b, h, t, p.c_sb, p.c_sh, p.c_sn) + g] = from_f32<Tag>(scale);
-    p.db[off3(b, h, t, p.z_sb, p.z_sh, p.z_sn) + g] = from_f32<Tag>(bias);
-  }
+  quantize_group<Tag, BITS, GS, L>(raw, part, p.dp + off3(b, h, t, p.p_sb, p.p_sh, p.p_sn) + (g * GS + part * VALS) / PER,
+                                   p.ds + off3(b, h, t, p.c_sb, p.c_sh, p.c_sn) + g,
+                                   p.db + off3(b, h, t, p.z_sb, p.z_sh, p.z_sn) + g);
 }
 
 // Jobs with at least this many groups take one lane per group.
@@ -209,6 +223,81 @@ __global__ __launch_bounds__(256) void dequantize_kernel(DequantParams p) {
   }
 }
 
+// Rotating-window prefill in one pass (reference: mlx_qsdpa/cache.py:593-634
+// and 813-857, dequantize the window in temporal order, append the chunk,
+// keep the newest max_size tokens, quantize again; plus keep > 0 sinks).
+// Output row t of the new window is combined token c = t (a sink, or no
+// token dropped) or t + drop (drop = n_old + S - total tokens leave after
+// the sinks).  Combined token c < n_old is old window row u(c) = c for
+// c < keep, else keep + (c - keep + rot) % (n_old - keep): dequantized
+// exactly as dequantize_kernel does, value = T(fmaf(s, q, b)); otherwise it
+// is chunk row c - n_old.  The row is then quantized as quantize_kernel
+// does (quantize_group), 8 values per lane, GS / 8 lanes per group, into
+// the destination buffers, which must not alias the old window.
+struct RequantParams {
+  int B, H, D, n_old, keep, rot, total, drop;
+  const uint32_t* op;
+  int64_t op_sb, op_sh, op_sn;
+  const uint16_t* os;
+  int64_t os_sb, os_sh, os_sn;
+  const uint16_t* ob;  // may be null (zero biases)
+  int64_t ob_sb, ob_sh, ob_sn;
+  const uint16_t* src;
+  int64_t s_sb, s_sh, s_sn;
+  uint32_t* dp;
+  int64_t p_sb, p_sh, p_sn;
+  uint16_t* ds;
+  int64_t c_sb, c_sh, c_sn;
+  uint16_t* db;
+  int64_t z_sb, z_sh, z_sn;
+};
+struct RequantJobs {
+  RequantParams p[2];
+};
+
+template <typename Tag, int BITS, int GS>
+__global__ __launch_bounds__(256) void requant_kernel(RequantJobs jobs) {
+  constexpr int L = GS / 8;  // lanes per group, 8 values each
+  constexpr int PER = 32 / BITS;
+  constexpr uint32_t kMask = (1u << BITS) - 1u;
+  const RequantParams& p = jobs.p[blockIdx.y];
+  const int ng = p.D / GS;
+  const int64_t groups = static_cast<int64_t>(p.B) * p.H * p.total * ng;
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t grp = gid / L;
+  const int part = static_cast<int>(gid % L);
+  if (grp >= groups) return;
+  const int g = static_cast<int>(grp % ng);
+  int64_t row = grp / ng;
+  const int t = static_cast<int>(row % p.total);
+  row /= p.total;
+  const int h = static_cast<int>(row % p.H);
+  const int b = static_cast<int>(row / p.H);
+  const int c = t < p.keep ? t : t + p.drop;
+  const int d0 = g * GS + part * 8;  // the lane's first dim
+  uint16_t raw[8];
+  if (c < p.n_old) {
+    const int u = (c < p.keep || p.rot == 0) ? c : p.keep + (c - p.keep + p.rot) % (p.n_old - p.keep);
+    const float sc = to_f32<Tag>(p.os[off3(b, h, u, p.os_sb, p.os_sh, p.os_sn) + g]);
+    const float bi = p.ob ? to_f32<Tag>(p.ob[off3(b, h, u, p.ob_sb, p.ob_sh, p.ob_sn) + g]) : 0.0f;
+    const uint32_t* words = p.op + off3(b, h, u, p.op_sb, p.op_sh, p.op_sn) + d0 / PER;
+#pragma unroll
+    for (int w = 0; w < 8 / PER; ++w) {
+      const uint32_t word = words[w];
+#pragma unroll
+      for (int j = 0; j < PER; ++j)
+        raw[w * PER + j] = from_f32<Tag>(__fmaf_rn(sc, static_cast<float>((word >> (j * BITS)) & kMask), bi));
+    }
+  } else {
+    const uint16_t* src = p.src + off3(b, h, c - p.n_old, p.s_sb, p.s_sh, p.s_sn) + d0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) raw[i] = src[i];
+  }
+  quantize_group<Tag, BITS, GS, L>(raw, part, p.dp + off3(b, h, t, p.p_sb, p.p_sh, p.p_sn) + d0 / PER,
+                                   p.ds + off3(b, h, t, p.c_sb, p.c_sh, p.c_sn) + g,
+                                   p.db + off3(b, h, t, p.z_sb, p.z_sh, p.z_sn) + g);
+}
+
 }  // namespace
 
 int launch_quantize(const qsdpa_quantize_args* const* jobs, int count, hipStream_t stream) {
@@ -273,6 +362,53 @@ int launch_dequantize(const qsdpa_dequantize_args* a, hipStream_t stream) {
     else dequantize_kernel<BF16, 8><<<grid, block, 0, stream>>>(p);
   }
   return check_launch("dequantize");
+}
+
+int launch_requant(const qsdpa_requant_args* const* jobs, int count, hipStream_t stream) {
+  RequantJobs j{};
+  int64_t most = 0;
+  const qsdpa_requant_args* a0 = jobs[0];
+  for (int i = 0; i < count; ++i) {
+    const qsdpa_requant_args* a = jobs[i];
+    RequantParams& p = j.p[i];
+    p.B = a->B; p.H = a->H; p.D = a->D; p.n_old = a->n_old; p.keep = a->keep; p.rot = a->rot;
+    p.total = std::min(a->n_old + a->S, a->max_size);
+    p.drop = a->n_old + a->S - p.total;
+    p.op = static_cast<const uint32_t*>(a->old_packed.ptr);
+    p.op_sb = a->old_packed.stride_b; p.op_sh = a->old_packed.stride_h; p.op_sn = a->old_packed.stride_n;
+    p.os = static_cast<const uint16_t*>(a->old_scales.ptr);
+    p.os_sb = a->old_scales.stride_b; p.os_sh = a->old_scales.stride_h; p.os_sn = a->old_scales.stride_n;
+    p.ob = static_cast<const uint16_t*>(a->old_biases.ptr);
+    p.ob_sb = a->old_biases.stride_b; p.ob_sh = a->old_biases.stride_h; p.ob_sn = a->old_biases.stride_n;
+    p.src = static_cast<const uint16_t*>(a->src.ptr);
+    p.s_sb = a->src.stride_b; p.s_sh = a->src.stride_h; p.s_sn = a->src.stride_n;
+    p.dp = static_cast<uint32_t*>(const_cast<void*>(a->dst_packed.ptr));
+    p.p_sb = a->dst_packed.stride_b; p.p_sh = a->dst_packed.stride_h; p.p_sn = a->dst_packed.stride_n;
+    p.ds = static_cast<uint16_t*>(const_cast<void*>(a->dst_scales.ptr));
+    p.c_sb = a->dst_scales.stride_b; p.c_sh = a->dst_scales.stride_h; p.c_sn = a->dst_scales.stride_n;
+    p.db = static_cast<uint16_t*>(const_cast<void*>(a->dst_biases.ptr));
+    p.z_sb = a->dst_biases.stride_b; p.z_sh = a->dst_biases.stride_h; p.z_sn = a->dst_biases.stride_n;
+    most = std::max<int64_t>(most, static_cast<int64_t>(a->B) * a->H * p.total * (a->D / a->group_size));
+  }
+  if (most == 0) return QSDPA_OK;
+  const int lanes = a0->group_size / 8;
+  const int64_t blocks = (most * lanes + 255) / 256;
+  if (blocks >= (int64_t(1) << 31)) return fail(QSDPA_ERR_UNSUPPORTED, "requant: window too large");
+  const dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>(count));
+  auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, dim3(256), 0, stream, j); };
+  const bool f16 = a0->dtype == QSDPA_F16;
+  const int gs = a0->group_size, bits = a0->bits;
+#define QSDPA_REQUANT_CASE(T, B_, G_) \
+  if (bits == B_ && gs == G_) go(requant_kernel<T, B_, G_>);
+  if (f16) {
+    QSDPA_REQUANT_CASE(F16, 4, 32) QSDPA_REQUANT_CASE(F16, 4, 64) QSDPA_REQUANT_CASE(F16, 4, 128)
+    QSDPA_REQUANT_CASE(F16, 8, 32) QSDPA_REQUANT_CASE(F16, 8, 64) QSDPA_REQUANT_CASE(F16, 8, 128)
+  } else {
+    QSDPA_REQUANT_CASE(BF16, 4, 32) QSDPA_REQUANT_CASE(BF16, 4, 64) QSDPA_REQUANT_CASE(BF16, 4, 128)
+    QSDPA_REQUANT_CASE(BF16, 8, 32) QSDPA_REQUANT_CASE(BF16, 8, 64) QSDPA_REQUANT_CASE(BF16, 8, 128)
+  }
+#undef QSDPA_REQUANT_CASE
+  return check_launch("requant");
 }
 
 }  // namespace qsdpa

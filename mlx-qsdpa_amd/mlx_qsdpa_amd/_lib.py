@@ -34,6 +34,7 @@ EXPORTED_SYMBOLS = (
     "qsdpa_quantize",
     "qsdpa_quantize_batch",
     "qsdpa_dequantize",
+    "qsdpa_requant_window",
     "qsdpa_last_error",
     "qsdpa_abi_version",
 )
@@ -84,6 +85,17 @@ class DequantizeArgs(ctypes.Structure):
     ]
 
 
+class RequantArgs(ctypes.Structure):
+    _fields_ = [
+        ("B", ctypes.c_int32), ("H", ctypes.c_int32), ("D", ctypes.c_int32),
+        ("bits", ctypes.c_int32), ("group_size", ctypes.c_int32), ("dtype", ctypes.c_int32),
+        ("n_old", ctypes.c_int32), ("keep", ctypes.c_int32), ("rot", ctypes.c_int32),
+        ("S", ctypes.c_int32), ("max_size", ctypes.c_int32),
+        ("old_packed", View), ("old_scales", View), ("old_biases", View), ("src", View),
+        ("dst_packed", View), ("dst_scales", View), ("dst_biases", View),
+    ]
+
+
 class QsdpaError(RuntimeError):
     """Raised when a C-ABI call returns a negative status."""
 
@@ -119,6 +131,8 @@ def load(path: os.PathLike | str | None = None) -> ctypes.CDLL:
     lib.qsdpa_quantize_batch.restype = ctypes.c_int
     lib.qsdpa_dequantize.argtypes = [ctypes.POINTER(DequantizeArgs), ctypes.c_void_p]
     lib.qsdpa_dequantize.restype = ctypes.c_int
+    lib.qsdpa_requant_window.argtypes = [ctypes.POINTER(RequantArgs), ctypes.c_int32, ctypes.c_void_p]
+    lib.qsdpa_requant_window.restype = ctypes.c_int
     lib.qsdpa_last_error.argtypes = []
     lib.qsdpa_last_error.restype = ctypes.c_char_p
     lib.qsdpa_abi_version.argtypes = []

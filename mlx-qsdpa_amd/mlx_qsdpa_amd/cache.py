@@ -82,6 +82,19 @@ def _ring_temporal(t, keep, ptr, n_visible):
     return torch.cat([t[:, :, :keep], t[:, :, ptr:n_visible], t[:, :, keep:ptr]], dim=2)
 
 
+def _spare_for(cache):
+    """The rotating cache's second buffer set (the target of a prefill's
+    requantization, which may not overwrite the window it reads), allocated
+    on first use and whenever the window's buffers changed shape.  It is
+    working memory, not cache state: nbytes does not count it."""
+    spare = getattr(cache, "_spare", None)
+    if spare is None or any(a.shape != b.shape or a.dtype != b.dtype or a.device != b.device
+                            for a, b in zip(spare[0] + spare[1], cache._keys + cache._values)):
+        spare = (tuple(torch.zeros_like(t) for t in cache._keys),
+                 tuple(torch.zeros_like(t) for t in cache._values))
+    return spare
+
+
 def _nbytes(tup):
     return sum(t.numel() * t.element_size() for t in tup)
 
@@ -473,32 +486,19 @@ class QuantizedRotatingSDPACache:
             return self._idx - self.keep
         return 0
 
-    def _dequant_temporal(self, tup):
-        """cache.py:622-634, the reorder fused into the dequantize kernel."""
-        n_visible = min(self.offset, self.max_size)
-        src = _sl(tup, 0, n_visible)
-        rot = self._ring_rot(n_visible)
-        # Without a rotation the reorder is the identity (the window may hold
-        # fewer tokens than `keep` then).
-        return kernels.dequantize(*src, group_size=self.group_size, bits=self.bits,
-                                  keep=self.keep if rot else 0, rot=rot)
-
     def _update_prefill(self, keys, values):
-        """cache.py:593-620: dequantize (temporal) + concat + keep window + requantize."""
+        """cache.py:593-634: the window dequantized in temporal order, the chunk
+        appended, the first `keep` and the newest max_size - keep kept,
+        quantized again -- one launch for K and V (qsdpa_requant_window) into
+        the spare buffer set, which then becomes the window."""
         S = keys.shape[2]
-        if self.offset > 0:
-            all_k = torch.cat([self._dequant_temporal(self._keys), keys], dim=2)
-            all_v = torch.cat([self._dequant_temporal(self._values), values], dim=2)
-        else:
-            all_k, all_v = keys, values
-        total = all_k.shape[2]
-        if total > self.max_size:
-            tail = self.max_size - self.keep
-            all_k = torch.cat([all_k[:, :, :self.keep], all_k[:, :, total - tail:]], dim=2)
-            all_v = torch.cat([all_v[:, :, :self.keep], all_v[:, :, total - tail:]], dim=2)
-            total = self.max_size
-        kernels.quantize_kv_into(all_k, all_v, self._keys, self._values, 0, self.bits,
-                                 self.group_size)
+        n_old = min(self.offset, self.max_size)
+        rot = self._ring_rot(n_old) if n_old else 0
+        spare = _spare_for(self)
+        total = kernels.requant_window((self._keys, self._values), (keys, values), spare, n_old, self.keep,
+                                       rot, self.max_size, self.bits, self.group_size)
+        self._spare = (self._keys, self._values)
+        self._keys, self._values = spare
         self.offset += S
         self._idx = total if total < self.max_size else self.keep
         n_visible = min(self.offset, self.max_size)
@@ -634,29 +634,17 @@ class BatchQuantizedRotatingSDPACache:
                 return ptr - self.keep
         return 0
 
-    def _dequant_temporal(self, tup):
-        """cache.py:842-857, reorder fused into the dequantize kernel."""
-        n_visible = min(self._idx, self.max_size)
-        rot = self._ring_rot()
-        return kernels.dequantize(*_sl(tup, 0, n_visible), group_size=self.group_size,
-                                  bits=self.bits, keep=self.keep if rot else 0, rot=rot)
-
     def _update_prefill(self, keys, values):
-        """cache.py:813-840."""
+        """cache.py:813-857: as QuantizedRotatingSDPACache._update_prefill, for
+        the batch (one launch for K and V into the spare buffer set)."""
         S = keys.shape[2]
-        if self._idx > 0:
-            all_k = torch.cat([self._dequant_temporal(self._keys), keys], dim=2)
-            all_v = torch.cat([self._dequant_temporal(self._values), values], dim=2)
-        else:
-            all_k, all_v = keys, values
-        total = all_k.shape[2]
-        if total > self.max_size:
-            tail = self.max_size - self.keep
-            all_k = torch.cat([all_k[:, :, :self.keep], all_k[:, :, total - tail:]], dim=2)
-            all_v = torch.cat([all_v[:, :, :self.keep], all_v[:, :, total - tail:]], dim=2)
-            total = self.max_size
-        kernels.quantize_kv_into(all_k, all_v, self._keys, self._values, 0, self.bits,
-                                 self.group_size)
+        n_old = min(self._idx, self.max_size)
+        rot = self._ring_rot() if n_old else 0
+        spare = _spare_for(self)
+        total = kernels.requant_window((self._keys, self._values), (keys, values), spare, n_old, self.keep,
+                                       rot, self.max_size, self.bits, self.group_size)
+        self._spare = (self._keys, self._values)
+        self._keys, self._values = spare
         self.offset = self.offset + S
         self._idx = total
         return _sl(self._keys, 0, total), _sl(self._values, 0, total)

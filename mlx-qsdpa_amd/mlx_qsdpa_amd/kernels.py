@@ -151,6 +151,37 @@ def dequantize_into(src: tuple, dst: torch.Tensor, bits: int, group_size: int,
     _lib.check(_lib.load().qsdpa_dequantize(ctypes.byref(a), _stream(dst)))
 
 
+def requant_window(old: tuple, new: tuple, dst: tuple, n_old: int, keep: int, rot: int,
+                   max_size: int, bits: int, group_size: int) -> int:
+    """A rotating window's prefill in one launch for K and V (qsdpa.h:
+    qsdpa_requant_window): the old window (ring order `keep` / `rot`, its
+    first n_old rows) in temporal order, then the new tokens, trimmed to the
+    first `keep` and the newest max_size - keep, quantized again into rows
+    [0, total) of `dst`.  old / dst: ((packed, scales, biases) of K, of V);
+    new: (keys, values) [B, H, S, D].  Returns total."""
+    keys, values = (_inner_contig(x) for x in new)
+    _require_device(keys, values, *dst[0], *dst[1], *(t for tup in old for t in tup))
+    if keys.dtype != values.dtype:
+        raise ValueError("keys and values must share a dtype")
+    B, H, S, D = keys.shape
+    if bits not in (4, 8) or D % group_size:
+        raise ValueError(f"bad bits={bits} / group_size={group_size} for D={D}")
+    if not (0 <= keep < max_size and 0 <= n_old <= max_size and rot >= 0 and (rot == 0 or n_old > keep)):
+        raise ValueError(f"bad window: max_size={max_size} keep={keep} n_old={n_old} rot={rot}")
+    total = min(n_old + S, max_size)
+    jobs = (_lib.RequantArgs * 2)()
+    for j, (o, x, d) in enumerate(zip(old, (keys, values), dst)):
+        if d[0].shape[2] < total or (n_old and o[0].shape[2] < n_old):
+            raise ValueError("window buffers too short")
+        if n_old and d[0].data_ptr() == o[0].data_ptr():
+            raise ValueError("the destination must not be the old window")
+        jobs[j] = _lib.RequantArgs(B, H, D, bits, group_size, dtype_code(keys.dtype), int(n_old), int(keep),
+                                   int(rot), S, int(max_size), _view(o[0]), _view(o[1]), _view(o[2]),
+                                   _view(x), _view(d[0]), _view(d[1]), _view(d[2]))
+    _lib.check(_lib.load().qsdpa_requant_window(jobs, 2, _stream(keys)))
+    return total
+
+
 def dequantize(packed: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor | None = None,
                group_size: int = 64, bits: int = 4, keep: int = 0, rot: int = 0):
     """mx.dequantize for [..., N, W] packed tensors (biases None = zero)."""

@@ -97,6 +97,29 @@ def _cpu_dequantize(packed, scales, biases=None, group_size=64, bits=4, keep=0, 
     return from_np(out, scales.dtype)
 
 
+def _cpu_requant_window(old, new, dst, n_old, keep, rot, max_size, bits, group_size):
+    """kernels.requant_window as its steps, with the oracle: dequantize the
+    old window in temporal order, append, keep the first `keep` and the
+    newest max_size - keep, quantize into rows [0, total) of dst."""
+    if not (0 <= keep < max_size and 0 <= n_old <= max_size and rot >= 0 and (rot == 0 or n_old > keep)):
+        raise ValueError(f"bad window: max_size={max_size} keep={keep} n_old={n_old} rot={rot}")
+    total = None
+    for o, x, d in zip(old, new, dst):
+        if n_old and d[0].data_ptr() == o[0].data_ptr():
+            raise ValueError("the destination must not be the old window")
+        allv = x
+        if n_old:
+            win = _cpu_dequantize(o[0][:, :, :n_old], o[1][:, :, :n_old], o[2][:, :, :n_old],
+                                  group_size=group_size, bits=bits, keep=keep if rot else 0, rot=rot)
+            allv = torch.cat([win, x], dim=2)
+        n = allv.shape[2]
+        if n > max_size:
+            allv = torch.cat([allv[:, :, :keep], allv[:, :, n - (max_size - keep):]], dim=2)
+        total = allv.shape[2]
+        _cpu_quantize_into(allv, d, 0, bits, group_size)
+    return total
+
+
 def _cpu_quantize_kv_into(keys, values, kdst, vdst, t0, bits, group_size):
     _cpu_quantize_into(keys, kdst, t0, bits, group_size)
     _cpu_quantize_into(values, vdst, t0, bits, group_size)
@@ -108,6 +131,7 @@ def cpu_kernels(monkeypatch):
     monkeypatch.setattr(kernels, "quantize_into", _cpu_quantize_into)
     monkeypatch.setattr(kernels, "quantize_kv_into", _cpu_quantize_kv_into)
     monkeypatch.setattr(kernels, "dequantize", _cpu_dequantize)
+    monkeypatch.setattr(kernels, "requant_window", _cpu_requant_window)
     return kernels
 
 

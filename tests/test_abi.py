@@ -42,6 +42,7 @@ _STRUCTS = {
     "qsdpa_decode_args": _lib.DecodeArgs,
     "qsdpa_quantize_args": _lib.QuantizeArgs,
     "qsdpa_dequantize_args": _lib.DequantizeArgs,
+    "qsdpa_requant_args": _lib.RequantArgs,
 }
 
 
@@ -86,6 +87,16 @@ def test_invalid_arguments_return_codes():
     d = _lib.DequantizeArgs()
     d.bits, d.group_size, d.D = 4, 48, 96
     assert lib.qsdpa_dequantize(ctypes.byref(d), None) == _lib.QSDPA_ERR_UNSUPPORTED
+    r = (_lib.RequantArgs * 2)()
+    for x in r:
+        x.B, x.H, x.D, x.bits, x.group_size, x.max_size, x.keep, x.n_old, x.S = 1, 1, 64, 4, 32, 8, 2, 2, 1
+    r[0].rot = 1  # a rotation needs more old tokens than sinks
+    assert lib.qsdpa_requant_window(r, 1, None) == _lib.QSDPA_ERR_INVALID
+    assert b"bad window" in lib.qsdpa_last_error()
+    r[0].rot, r[1].bits = 0, 8
+    assert lib.qsdpa_requant_window(r, 2, None) == _lib.QSDPA_ERR_INVALID
+    assert b"share" in lib.qsdpa_last_error()
+    assert lib.qsdpa_requant_window(r, 3, None) == _lib.QSDPA_ERR_INVALID
     a = _lib.DecodeArgs()
     a.B = a.H_q = a.H_kv = a.N = 1
     a.D, a.bits, a.group_size = 100, 4, 32

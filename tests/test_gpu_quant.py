@@ -172,3 +172,51 @@ def test_dequantize_ring_reorder(device, keep, rot):
     full = affine.dequantize(p, s, b, 32, 4, "f16")
     idx = [t if t < keep else keep + (t - keep + rot) % (N - keep) for t in range(N)]
     assert _bits_equal(to_np(got), full[:, :, idx], "f16")
+
+
+@pytest.mark.parametrize("case", [
+    # (max_size, keep, n_old, rot, S, bits, gs, dtype)
+    (64, 0, 0, 0, 40, 4, 32, "f16"),      # first prompt: no old window
+    (64, 0, 0, 0, 90, 8, 64, "bf16"),     # first prompt longer than the window
+    (64, 4, 3, 0, 5, 4, 32, "f16"),       # fewer old tokens than sinks
+    (64, 0, 64, 17, 9, 4, 64, "f16"),     # wrapped, keep = 0
+    (64, 4, 64, 29, 12, 8, 32, "bf16"),   # wrapped, keep = 4 sinks
+    (64, 4, 64, 59, 70, 4, 128, "f16"),   # chunk longer than the window
+    (4096, 4, 4096, 1234, 512, 8, 128, "bf16"),  # C5's chunk over its wrapped window
+])
+def test_requant_window_matches_oracle(device, case):
+    """qsdpa_requant_window (one launch, K and V) against the oracle's steps:
+    dequantize the old window in temporal order, append, keep the first
+    `keep` and the newest max_size - keep, quantize; bit-exact."""
+    W, keep, n_old, rot, S, bits, gs, dt = case
+    B, H, D = 2, 3, 128
+    rng = np.random.default_rng(W + keep + n_old + rot + S)
+    T = torch_dtype(dt)
+    old_np, new_np, dst = [], [], []
+    for _ in range(2):  # K, V
+        ring = affine.quantize(affine.random_T(rng, (B, H, W, D), dt, outlier_frac=0.02), gs, bits, dt)
+        old_np.append(ring)
+        new_np.append(affine.random_T(rng, (B, H, S, D), dt))
+        dst.append((torch.full((B, H, W, D * bits // 32), 0xDEADBEEF, dtype=torch.int64).to(torch.uint32).to(device),
+                    torch.zeros((B, H, W, D // gs), dtype=T, device=device),
+                    torch.zeros((B, H, W, D // gs), dtype=T, device=device)))
+    old = [tuple(from_np(x, T, device) for x in o) for o in old_np]
+    new = [from_np(x, T, device) for x in new_np]
+    total = kernels.requant_window(tuple(old), tuple(new), tuple(dst), n_old, keep, rot, W, bits, gs)
+    torch.cuda.synchronize()
+    assert total == min(n_old + S, W)
+    for o, x, d in zip(old_np, new_np, dst):
+        allv = x
+        if n_old:
+            win = affine.dequantize(*(t[:, :, :n_old] for t in o), gs, bits, dt)
+            idx = np.arange(n_old)
+            if rot:
+                idx = np.where(idx < keep, idx, keep + (idx - keep + rot) % (n_old - keep))
+            allv = np.concatenate([win[:, :, idx], x], axis=2)
+        n = allv.shape[2]
+        if n > W:
+            allv = np.concatenate([allv[:, :, :keep], allv[:, :, n - (W - keep):]], axis=2)
+        want = affine.quantize(allv, gs, bits, dt)
+        assert np.array_equal(to_np(d[0][:, :, :total]), want[0]), "packed words differ"
+        for i in (1, 2):
+            assert np.array_equal(affine.T_bits(to_np(d[i][:, :, :total]), dt), affine.T_bits(want[i], dt))
