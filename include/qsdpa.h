@@ -30,6 +30,10 @@
  *   qsdpa_dequantize <- mx.dequantize(...) (mlx_qsdpa/dispatch.py:69-78,
  *                       mlx_qsdpa/__init__.py:50-57) and the dequantize +
  *                       temporal reorder of cache.py:622-634, 842-857.
+ *   qsdpa_requant_window <- the rotating prefill's dequantize + concatenate
+ *                       + trim + quantize (cache.py:593-634, 813-857).
+ *   qsdpa_move_rows  <- the batch caches' slicing / padding / concatenation
+ *                       (cache.py:46-51, 337-348, 378-492, 868-1010).
  */
 #ifndef QSDPA_H_
 #define QSDPA_H_
@@ -41,7 +45,7 @@
 extern "C" {
 #endif
 
-#define QSDPA_ABI_VERSION 3
+#define QSDPA_ABI_VERSION 4
 
 enum {
   QSDPA_OK = 0,
@@ -240,6 +244,34 @@ typedef struct {
 } qsdpa_requant_args;
 
 int qsdpa_requant_window(const qsdpa_requant_args* jobs, int32_t count, void* stream);
+
+/*
+ * Token-row block moves, the device side of the batch caches'
+ * administration (filter, extend, extract, merge, the finalize roll).
+ * One move fills `tokens` token rows of row_bytes bytes for every head
+ * h < heads: row t (dst + h*dst_head_stride + t*dst_token_stride) receives
+ *     src + h*src_head_stride + (t - copy_begin)*src_token_stride
+ * for copy_begin <= t < copy_end, and zero bytes otherwise (all rows when
+ * src is NULL).  Strides are in bytes.  The moves of one call go to
+ * the device in kernel arguments (48 per launch): no device memory, no copy
+ * before the launch, no synchronization.  Moves of one call may run in any
+ * order and concurrently: no destination may overlap another destination
+ * or any source of the same call.
+ * Replaces the MLX gathers, slices, mx.pad / mx.concatenate and
+ * _dynamic_roll of mlx_qsdpa/cache.py:46-51, 337-348 (finalize), 378-492
+ * (filter, extend, extract, merge) and 868-1010 (the rotating batch's).
+ */
+typedef struct {
+  const void* src;          /* row of token copy_begin, head 0; NULL => zeros */
+  void* dst;                /* row of token 0, head 0                         */
+  int64_t src_head_stride, src_token_stride;   /* bytes, >= 0                 */
+  int64_t dst_head_stride, dst_token_stride;   /* bytes, >= 0                 */
+  int32_t heads, tokens;    /* >= 0                                           */
+  int32_t row_bytes;        /* >= 1                                           */
+  int32_t copy_begin, copy_end; /* 0 <= copy_begin <= copy_end <= tokens      */
+} qsdpa_row_move;
+
+int qsdpa_move_rows(const qsdpa_row_move* moves, int32_t count, void* stream);
 
 /* Thread-local message describing the last error ("" if none). */
 const char* qsdpa_last_error(void);

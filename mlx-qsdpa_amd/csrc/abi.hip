@@ -348,6 +348,25 @@ int qsdpa_requant_window(const qsdpa_requant_args* jobs, int32_t count, void* st
   return launch_requant(ptrs, count, static_cast<hipStream_t>(stream));
 }
 
+int qsdpa_move_rows(const qsdpa_row_move* moves, int32_t count, void* stream) {
+  clear_error();
+  if (count < 0) return fail(QSDPA_ERR_INVALID, "count must be >= 0, got %d", count);
+  if (count > 0 && !moves) return fail(QSDPA_ERR_INVALID, "null moves");
+  for (int i = 0; i < count; ++i) {
+    const qsdpa_row_move& m = moves[i];
+    if (m.heads < 0 || m.tokens < 0 || m.row_bytes < 1)
+      return fail(QSDPA_ERR_INVALID, "move %d: heads=%d tokens=%d row_bytes=%d", i, m.heads, m.tokens,
+                  m.row_bytes);
+    if (m.src_head_stride < 0 || m.src_token_stride < 0 || m.dst_head_stride < 0 || m.dst_token_stride < 0)
+      return fail(QSDPA_ERR_INVALID, "move %d: negative stride", i);
+    if (m.src && (m.copy_begin < 0 || m.copy_begin > m.copy_end || m.copy_end > m.tokens))
+      return fail(QSDPA_ERR_INVALID, "move %d: copy range [%d, %d) outside [0, %d)", i, m.copy_begin,
+                  m.copy_end, m.tokens);
+    if (m.heads > 0 && m.tokens > 0 && !m.dst) return fail(QSDPA_ERR_INVALID, "move %d: null dst", i);
+  }
+  return launch_move_rows(moves, count, static_cast<hipStream_t>(stream));
+}
+
 int qsdpa_dequantize(const qsdpa_dequantize_args* a, void* stream) {
   clear_error();
   if (!a) return fail(QSDPA_ERR_INVALID, "null args");

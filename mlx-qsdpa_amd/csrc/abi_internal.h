@@ -37,6 +37,7 @@ void launch_profiled(void (*kernel)(P), dim3 grid, dim3 block, hipStream_t strea
 int launch_quantize(const qsdpa_quantize_args* const* jobs, int count, hipStream_t stream);
 int launch_dequantize(const qsdpa_dequantize_args* a, hipStream_t stream);
 int launch_requant(const qsdpa_requant_args* const* jobs, int count, hipStream_t stream);
+int launch_move_rows(const qsdpa_row_move* moves, int count, hipStream_t stream);
 int launch_decode(const qsdpa_decode_args* a, int num_splits, hipStream_t stream);
 int decode_plan(const qsdpa_decode_args* a, int* num_splits, int64_t* workspace_bytes);
 

@@ -23,7 +23,7 @@ QSDPA_BF16 = 1
 QSDPA_F32 = 2
 QSDPA_BOOL = 3
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 NOALLOC_SCRATCH_BYTES = 16 << 20
 
 # Every symbol include/qsdpa.h declares.
@@ -35,6 +35,7 @@ EXPORTED_SYMBOLS = (
     "qsdpa_quantize_batch",
     "qsdpa_dequantize",
     "qsdpa_requant_window",
+    "qsdpa_move_rows",
     "qsdpa_last_error",
     "qsdpa_abi_version",
 )
@@ -96,6 +97,16 @@ class RequantArgs(ctypes.Structure):
     ]
 
 
+class RowMove(ctypes.Structure):
+    _fields_ = [
+        ("src", ctypes.c_void_p), ("dst", ctypes.c_void_p),
+        ("src_head_stride", ctypes.c_int64), ("src_token_stride", ctypes.c_int64),
+        ("dst_head_stride", ctypes.c_int64), ("dst_token_stride", ctypes.c_int64),
+        ("heads", ctypes.c_int32), ("tokens", ctypes.c_int32),
+        ("row_bytes", ctypes.c_int32), ("copy_begin", ctypes.c_int32), ("copy_end", ctypes.c_int32),
+    ]
+
+
 class QsdpaError(RuntimeError):
     """Raised when a C-ABI call returns a negative status."""
 
@@ -133,6 +144,8 @@ def load(path: os.PathLike | str | None = None) -> ctypes.CDLL:
     lib.qsdpa_dequantize.restype = ctypes.c_int
     lib.qsdpa_requant_window.argtypes = [ctypes.POINTER(RequantArgs), ctypes.c_int32, ctypes.c_void_p]
     lib.qsdpa_requant_window.restype = ctypes.c_int
+    lib.qsdpa_move_rows.argtypes = [ctypes.POINTER(RowMove), ctypes.c_int32, ctypes.c_void_p]
+    lib.qsdpa_move_rows.restype = ctypes.c_int
     lib.qsdpa_last_error.argtypes = []
     lib.qsdpa_last_error.restype = ctypes.c_char_p
     lib.qsdpa_abi_version.argtypes = []

@@ -54,16 +54,6 @@ def _create_causal_mask(N, offset, window_size=None, left_padding=None, device=N
     return mask if device is None else mask.to(device)
 
 
-def _dynamic_roll(x, shifts, axis):
-    """cache.py:46-51 for axis 2 of a (B, H, N, d) tensor, shifts (B,)."""
-    n = x.shape[axis]
-    idx = (torch.arange(n)[None, :] - shifts.to("cpu", torch.int64)[:, None]) % n
-    idx = idx.to(x.device)[:, None, :, None].expand(x.shape[0], x.shape[1], n, x.shape[3])
-    src = x.view(torch.int32) if x.dtype == torch.uint32 else x
-    out = torch.gather(src, axis, idx)
-    return out.view(torch.uint32) if x.dtype == torch.uint32 else out
-
-
 def _zeros_q(shape3, dim, bits, group_size, dtype, device):
     per = 32 // bits
     return (torch.zeros((*shape3, dim // per), dtype=torch.uint32, device=device),
@@ -75,11 +65,91 @@ def _sl(tup, start, stop):
     return tuple(t[:, :, start:stop, :] for t in tup)
 
 
+def _ring_runs(keep, ptr, n):
+    """Column runs (start, length) that read a ring's first n slots in
+    temporal order: the sinks [0, keep), the oldest other tokens [ptr, n),
+    then the newest [keep, ptr).  With ptr <= keep or ptr >= n the slots are
+    already in temporal order."""
+    if ptr <= keep or ptr >= n:
+        return [(0, n)] if n > 0 else []
+    return [r for r in ((0, keep), (ptr, n - ptr), (keep, ptr - keep)) if r[1] > 0]
+
+
+def _drop_front(runs, k):
+    """The runs without their first k columns."""
+    out = []
+    for c, n in runs:
+        if k >= n:
+            k -= n
+            continue
+        out.append((c + k, n - k))
+        k = 0
+    return out
+
+
 def _ring_temporal(t, keep, ptr, n_visible):
-    """Slots in temporal order: [0:keep] + [ptr:n] + [keep:ptr]."""
-    if ptr <= keep or ptr >= n_visible:
+    """A ring buffer's first n_visible slots in temporal order (a new tensor)."""
+    runs = _ring_runs(keep, ptr, n_visible)
+    if len(runs) <= 1:
         return t[:, :, :n_visible]
-    return torch.cat([t[:, :, :keep], t[:, :, ptr:n_visible], t[:, :, keep:ptr]], dim=2)
+    return torch.cat([t[:, :, c:c + n] for c, n in runs], dim=2)
+
+
+def _indices(batch_indices, B):
+    """Batch indices (list, range or tensor; negative counts from the end) as
+    a list of host ints.  A device tensor is read back, which waits for it."""
+    if isinstance(batch_indices, torch.Tensor):
+        batch_indices = batch_indices.reshape(-1).tolist()
+    out = []
+    for i in batch_indices:
+        i = int(i)
+        if not -B <= i < B:
+            raise IndexError(f"batch index {i} out of range for {B} sequences")
+        out.append(i % B)
+    return out
+
+
+class _Relayout:
+    """New (B, H, width, .) buffers shaped and typed like the six (packed,
+    scales, biases of keys and values) of a cache, filled row by row from
+    token runs of other buffers -- the batch administration's only device
+    work, one qsdpa_move_rows call (kernel-argument descriptors, no host
+    read, no synchronization).  Every slot of the new buffers is written:
+    the runs, and zeros around them."""
+
+    def __init__(self, like, B, width):
+        self.kv = tuple(tuple(torch.empty((B, t.shape[1], width, t.shape[3]), dtype=t.dtype, device=t.device)
+                              for t in tup) for tup in like)
+        self.width = width
+        self._moves = []
+
+    def row(self, row, start=0, src=None, src_row=0, runs=()):
+        """Batch row `row`: the columns `runs` ((start, length), in order) of
+        batch row `src_row` of `src` (a (keys, values) pair of buffer
+        triples) back to back from column `start`, cut at the width; zeros
+        before and after them (a row of zeros without runs)."""
+        dst = self.kv[0] + self.kv[1]
+        segs, col = [], start
+        for c, n in runs:
+            n = min(n, self.width - col)
+            if n > 0:
+                segs.append((col, n, c))
+                col += n
+        if not segs:
+            self._moves += [kernels.RowMove(d, row, 0, self.width) for d in dst]
+            return
+        srcs = src[0] + src[1]
+        for i, (col, n, c) in enumerate(segs):
+            # The first move also zeroes the columns before the runs, the
+            # last one those after them.
+            lo = 0 if i == 0 else col
+            hi = self.width if i == len(segs) - 1 else col + n
+            for d, sbuf in zip(dst, srcs):
+                self._moves.append(kernels.RowMove(d, row, lo, hi - lo, sbuf, src_row, c, col - lo, col + n - lo))
+
+    def run(self):
+        kernels.move_rows(self._moves)
+        return self.kv
 
 
 def _spare_for(cache):
@@ -292,14 +362,24 @@ class BatchQuantizedSDPACache:
             self._right_padding = torch.as_tensor(right_padding, dtype=torch.int64)
 
     def finalize(self):
-        """cache.py:337-348: roll right padding to the left."""
-        if self._right_padding is not None:
-            pad = self._right_padding
-            self._keys = tuple(_dynamic_roll(t, pad, 2) for t in self._keys)
-            self._values = tuple(_dynamic_roll(t, pad, 2) for t in self._values)
-            self.offset = self.offset - pad
-            self.left_padding = self.left_padding + pad
-            self._right_padding = None
+        """cache.py:337-348: sequences prefilled with right padding (prepare)
+        are rotated so that the padding sits on the left, where it joins
+        left_padding: column t of row b takes column (t - pad[b]) mod the
+        capacity."""
+        if self._right_padding is None:
+            return
+        pad = self._right_padding
+        if self._keys is not None:
+            kv = (self._keys, self._values)
+            B, cap = self._keys[0].shape[0], self._keys[0].shape[2]
+            rl = _Relayout(kv, B, cap)
+            for b, p in enumerate(pad.tolist()):
+                p = p % cap if cap else 0
+                rl.row(b, 0, kv, b, [(cap - p, p), (0, cap - p)])
+            self._keys, self._values = rl.run()
+        self.offset = self.offset - pad
+        self.left_padding = self.left_padding + pad
+        self._right_padding = None
 
     @property
     def state(self):
@@ -325,95 +405,86 @@ class BatchQuantizedSDPACache:
                                    window_size=kwargs.get("window_size"), device=dev)
 
     def filter(self, batch_indices):
-        """cache.py:378-391."""
-        bi = torch.as_tensor(batch_indices, dtype=torch.int64)
+        """cache.py:378-391: keep the listed sequences, in that order; the
+        leading columns that are left padding in every kept sequence are
+        dropped (capacity, _idx and left_padding shrink by their number)."""
+        keep = _indices(batch_indices, self.offset.shape[0])
+        lp = self.left_padding[keep]
+        drop = 0
         if self._keys is not None:
-            dev_bi = bi.to(self._keys[0].device)
-            self._keys = tuple(t.index_select(0, dev_bi) for t in self._keys)
-            self._values = tuple(t.index_select(0, dev_bi) for t in self._values)
-        self.offset = self.offset[bi]
-        self.left_padding = self.left_padding[bi]
-        min_pad = int(self.left_padding.min())
-        if min_pad > 0:
-            self._keys = tuple(t[:, :, min_pad:] for t in self._keys)
-            self._values = tuple(t[:, :, min_pad:] for t in self._values)
-            self._idx -= min_pad
-            self.left_padding = self.left_padding - min_pad
+            drop = int(lp.min()) if keep else 0
+            kv = (self._keys, self._values)
+            width = self._keys[0].shape[2] - drop
+            rl = _Relayout(kv, len(keep), width)
+            for j, b in enumerate(keep):
+                rl.row(j, 0, kv, b, [(drop, width)])
+            self._keys, self._values = rl.run()
+            self._idx -= drop
+        self.offset = self.offset[keep]
+        self.left_padding = lp - drop
 
     def extend(self, other):
-        """cache.py:393-427."""
-        max_idx = max(self._idx, other._idx)
-        max_size = max(self._keys[0].shape[2], other._keys[0].shape[2])
-
-        def pad_quant(c_idx, tuples):
-            left = max_idx - c_idx
-            right = max_size - tuples[0].shape[2] - left
-            res = []
-            for t in tuples:
-                tr = t
-                if right < 0:
-                    tr = tr[:, :, :right]
-                    right_actual = 0
-                else:
-                    right_actual = right
-                if left != 0 or right_actual != 0:
-                    tr = torch.nn.functional.pad(tr, (0, 0, left, right_actual))
-                res.append(tr)
-            return tuple(res), left
-
-        sk, s_left = pad_quant(self._idx, self._keys)
-        sv, _ = pad_quant(self._idx, self._values)
-        ok, o_left = pad_quant(other._idx, other._keys)
-        ov, _ = pad_quant(other._idx, other._values)
-        self._keys = tuple(torch.cat([s, o]) for s, o in zip(sk, ok))
-        self._values = tuple(torch.cat([s, o]) for s, o in zip(sv, ov))
+        """cache.py:393-427: other's sequences are appended after this
+        batch's.  Each side is shifted right so that both write at the larger
+        _idx (the shift joins its left padding), into buffers as wide as the
+        wider capacity; a side without buffers contributes zero rows."""
+        sides = (self, other)
+        end = max(c._idx for c in sides)
+        filled = [c for c in sides if c._keys is not None]
+        if filled:
+            width = max(c._keys[0].shape[2] for c in filled)
+            rl = _Relayout((filled[0]._keys, filled[0]._values), sum(c.offset.shape[0] for c in sides), width)
+            row = 0
+            for c in sides:
+                for b in range(c.offset.shape[0]):
+                    if c._keys is None:
+                        rl.row(row, end - c._idx)
+                    else:
+                        rl.row(row, end - c._idx, (c._keys, c._values), b, [(0, c._keys[0].shape[2])])
+                    row += 1
+            self._keys, self._values = rl.run()
         self.offset = torch.cat([self.offset, other.offset])
-        self.left_padding = torch.cat([self.left_padding + s_left, other.left_padding + o_left])
-        self._idx = max_idx
+        self.left_padding = torch.cat([self.left_padding + (end - self._idx),
+                                       other.left_padding + (end - other._idx)])
+        self._idx = end
 
     def extract(self, idx):
-        """cache.py:429-444."""
+        """cache.py:429-444: sequence idx as a QuantizedSDPACache holding the
+        columns after its left padding up to _idx (capacity = that count)."""
         cache = QuantizedSDPACache(bits=self.bits, group_size=self.group_size)
         if self._keys is None:
             return cache
-        padding = int(self.left_padding[idx])
-        cache._keys = tuple(t[idx:idx + 1, :, padding:self._idx].contiguous() for t in self._keys)
-        cache._values = tuple(t[idx:idx + 1, :, padding:self._idx].contiguous()
-                              for t in self._values)
-        cache.offset = self._idx - padding
+        (b,) = _indices([idx], self.offset.shape[0])
+        start = int(self.left_padding[b])
+        n = self._idx - start
+        kv = (self._keys, self._values)
+        rl = _Relayout(kv, 1, n)
+        rl.row(0, 0, kv, b, [(start, n)])
+        cache._keys, cache._values = rl.run()
+        cache.offset = n
         return cache
 
     @classmethod
     def merge(cls, caches):
-        """cache.py:446-492: left-pad single caches into one batch."""
+        """cache.py:446-492: single caches stacked into one batch, each
+        right-aligned at the longest (the shorter get left padding)."""
         if not caches:
             return cls([0])
-        bits = caches[0].bits
-        gs = caches[0].group_size
         lengths = [c.offset for c in caches]
-        max_len = max(lengths)
-        padding = [max_len - l for l in lengths]
-        batch = cls(padding, bits=bits, group_size=gs)
-        if all(c.empty() for c in caches):
+        width = max(lengths)
+        batch = cls([width - n for n in lengths], bits=caches[0].bits, group_size=caches[0].group_size)
+        filled = [c for c in caches if not c.empty()]
+        if not filled:
             return batch
-        B = len(caches)
-        ref = next(c for c in caches if not c.empty())
-        H = ref._keys[0].shape[1]
-
-        def alloc(tup):
-            return tuple(torch.zeros((B, H, max_len, t.shape[3]), dtype=t.dtype, device=t.device)
-                         for t in tup)
-
-        batch._keys = alloc(ref._keys)
-        batch._values = alloc(ref._values)
-        for i, (p, c) in enumerate(zip(padding, caches)):
+        rl = _Relayout((filled[0]._keys, filled[0]._values), len(caches), width)
+        for i, c in enumerate(caches):
             if c.empty():
-                continue
-            for j in range(3):
-                batch._keys[j][i:i + 1, :, p:p + c.offset] = c._keys[j][:, :, :c.offset]
-                batch._values[j][i:i + 1, :, p:p + c.offset] = c._values[j][:, :, :c.offset]
-        batch.offset = batch.offset + max_len
-        batch._idx = max_len
+                rl.row(i)
+            else:
+                rl.row(i, width - c.offset, (c._keys, c._values), 0, [(0, c.offset)])
+        batch._keys, batch._values = rl.run()
+        batch.offset = batch.offset + width
+        batch._idx = width
         return batch
 
 
@@ -529,6 +600,13 @@ class QuantizedRotatingSDPACache:
         self.offset -= num_to_trim
         self._idx -= num_to_trim
         return num_to_trim > 0
+
+    def _temporal_runs(self):
+        """Column runs of the window in temporal order."""
+        n = min(self.offset, self.max_size)
+        if self.offset > self.max_size:
+            return _ring_runs(self.keep, self._idx, n)
+        return [(0, n)] if n > 0 else []
 
     @property
     def state(self):
@@ -658,112 +736,108 @@ class BatchQuantizedRotatingSDPACache:
         return _create_causal_mask(N, offset=off, left_padding=self.left_padding,
                                    window_size=kwargs.get("window_size"), device=dev)
 
+    def _temporal_runs(self):
+        """Column runs of the window in temporal order (shared by all rows)."""
+        n = min(self._idx, self.max_size)
+        if self._idx > self.max_size:
+            return _ring_runs(self.keep, self._write_pos(), n)
+        return [(0, n)] if n > 0 else []
+
     def filter(self, batch_indices):
-        """cache.py:868-874."""
-        bi = torch.as_tensor(batch_indices, dtype=torch.int64)
+        """cache.py:868-874: keep the listed sequences, in that order (rows
+        move as they are: the ring layout is shared by the batch)."""
+        keep = _indices(batch_indices, self.offset.shape[0])
         if self._keys is not None:
-            dev_bi = bi.to(self._keys[0].device)
-            self._keys = tuple(t.index_select(0, dev_bi) for t in self._keys)
-            self._values = tuple(t.index_select(0, dev_bi) for t in self._values)
-        self.offset = self.offset[bi]
-        self.left_padding = self.left_padding[bi]
+            kv = (self._keys, self._values)
+            width = self._keys[0].shape[2]
+            rl = _Relayout(kv, len(keep), width)
+            for j, b in enumerate(keep):
+                rl.row(j, 0, kv, b, [(0, width)])
+            self._keys, self._values = rl.run()
+            self._spare = None
+        self.offset = self.offset[keep]
+        self.left_padding = self.left_padding[keep]
 
     def extend(self, other):
-        """cache.py:876-912."""
-        if self._keys is None and other._keys is None:
-            self.offset = torch.cat([self.offset, other.offset])
-            self.left_padding = torch.cat([self.left_padding, other.left_padding])
-            return
-        max_idx = max(self._idx, other._idx)
-
-        def pad_quant(tuples, c_idx):
-            left = max_idx - c_idx
-            if left == 0:
-                return tuples
-            return tuple(torch.nn.functional.pad(t, (0, 0, left, 0)) for t in tuples)
-
-        sk = pad_quant(self._keys, self._idx) if self._keys is not None else None
-        sv = pad_quant(self._values, self._idx) if self._values is not None else None
-        ok = pad_quant(other._keys, other._idx) if other._keys is not None else None
-        ov = pad_quant(other._values, other._idx) if other._values is not None else None
-        if sk is not None and ok is not None:
-            self._keys = tuple(torch.cat([s, o]) for s, o in zip(sk, ok))
-            self._values = tuple(torch.cat([s, o]) for s, o in zip(sv, ov))
-        elif ok is not None:
-            self._keys = ok
-            self._values = ov
-        s_left = max_idx - self._idx
-        o_left = max_idx - other._idx
+        """cache.py:876-912: other's sequences are appended after this
+        batch's.  Each side's window is laid out in temporal order and
+        right-aligned at the longer window n (the shorter side's shift joins
+        its left padding) in max_size-wide buffers, and the layout starts
+        unrotated (_idx = n).  While neither ring has wrapped this is the
+        reference's left shift by the _idx difference; the reference needs
+        equal buffer widths there, and after a wrap it shifts the ring as it
+        lies, out of temporal order.  A side without buffers contributes
+        zero rows."""
+        if other.max_size != self.max_size or other.keep != self.keep:
+            raise ValueError("extend needs caches with the same max_size and keep")
+        sides = (self, other)
+        vis = [min(c._idx, c.max_size) if c._keys is not None else 0 for c in sides]
+        n = max(vis)
+        filled = [c for c in sides if c._keys is not None]
+        if filled:
+            rl = _Relayout((filled[0]._keys, filled[0]._values), sum(c.offset.shape[0] for c in sides),
+                           self.max_size)
+            row = 0
+            for c, v in zip(sides, vis):
+                runs = c._temporal_runs() if c._keys is not None else []
+                for b in range(c.offset.shape[0]):
+                    if runs:
+                        rl.row(row, n - v, (c._keys, c._values), b, runs)
+                    else:
+                        rl.row(row)
+                    row += 1
+            self._keys, self._values = rl.run()
+            self._spare = None
         self.offset = torch.cat([self.offset, other.offset])
-        self.left_padding = torch.cat([self.left_padding + s_left, other.left_padding + o_left])
-        self._idx = max_idx
+        self.left_padding = torch.cat([self.left_padding + (n - vis[0]), other.left_padding + (n - vis[1])])
+        self._idx = n
 
     def extract(self, idx):
-        """cache.py:914-961: one sequence as a single rotating cache, temporal order."""
+        """cache.py:914-961: sequence idx as a QuantizedRotatingSDPACache:
+        its last min(offset[idx], max_size) tokens in temporal order (the
+        window without the sequence's left padding) in a max_size buffer."""
         cache = QuantizedRotatingSDPACache(max_size=self.max_size, keep=self.keep,
                                            bits=self.bits, group_size=self.group_size)
         if self._keys is None:
             return cache
-        visible = min(self._idx, self.max_size)
-        n_tokens = max(0, min(int(self.offset[idx]), self.max_size))
-        if n_tokens == 0:
+        (b,) = _indices([idx], self.offset.shape[0])
+        n = max(0, min(int(self.offset[b]), self.max_size))
+        if n == 0:
             return cache
-        ptr = self._write_pos()
-
-        def extract_temporal(tuples):
-            res = tuple(t[idx:idx + 1, :, :visible].contiguous() for t in tuples)
-            if self._idx > self.max_size:
-                res = tuple(_ring_temporal(t, self.keep, ptr, visible) for t in res)
-            padding = visible - n_tokens
-            if padding > 0:
-                res = tuple(t[:, :, padding:visible].contiguous() for t in res)
-            return res
-
-        cache._keys = extract_temporal(self._keys)
-        cache._values = extract_temporal(self._values)
-        cache.offset = n_tokens
-        cache._idx = n_tokens
-        if n_tokens < self.max_size:
-            pad_len = self.max_size - n_tokens
-            cache._keys = tuple(torch.nn.functional.pad(t, (0, 0, 0, pad_len)) for t in cache._keys)
-            cache._values = tuple(torch.nn.functional.pad(t, (0, 0, 0, pad_len))
-                                  for t in cache._values)
+        visible = min(self._idx, self.max_size)
+        kv = (self._keys, self._values)
+        rl = _Relayout(kv, 1, self.max_size)
+        rl.row(0, 0, kv, b, _drop_front(self._temporal_runs(), visible - n))
+        cache._keys, cache._values = rl.run()
+        cache.offset = n
+        cache._idx = n
         return cache
 
     @classmethod
     def merge(cls, caches):
-        """cache.py:963-1010."""
+        """cache.py:963-1010: single rotating caches stacked into one batch,
+        each window in temporal order and right-aligned at the longest (the
+        shorter get left padding).  The buffers are max_size wide, so the
+        merged batch can go on decoding (the reference allocates only the
+        longest window, which leaves the next decode no slot)."""
         if not caches:
             return cls([0], max_size=4096)
-        max_size = caches[0].max_size
-        bits = caches[0].bits
-        gs = caches[0].group_size
-        keep = caches[0].keep
+        c0 = caches[0]
         lengths = [c.size() for c in caches]
-        max_len = max(lengths)
-        padding = [max_len - l for l in lengths]
-        batch = cls(padding, max_size=max_size, keep=keep, bits=bits, group_size=gs)
-        if all(c.empty() for c in caches):
+        width = max(lengths)
+        batch = cls([width - n for n in lengths], max_size=c0.max_size, keep=c0.keep, bits=c0.bits,
+                    group_size=c0.group_size)
+        filled = [c for c in caches if not c.empty()]
+        if not filled:
             return batch
-        B = len(caches)
-        ref = next(c for c in caches if not c.empty())
-        H = ref._keys[0].shape[1]
-        ks_ref, vs_ref = ref.state
-
-        def alloc(tup):
-            return tuple(torch.zeros((B, H, max_len, t.shape[3]), dtype=t.dtype, device=t.device)
-                         for t in tup)
-
-        batch._keys = alloc(ks_ref)
-        batch._values = alloc(vs_ref)
-        for i, (p, c) in enumerate(zip(padding, caches)):
-            if c.empty():
-                continue
-            kst, vst = c.state
-            n = kst[0].shape[2]
-            for j in range(3):
-                batch._keys[j][i:i + 1, :, p:p + n] = kst[j]
-                batch._values[j][i:i + 1, :, p:p + n] = vst[j]
-        batch.offset = batch.offset + max_len
-        batch._idx = max_len
+        rl = _Relayout((filled[0]._keys, filled[0]._values), len(caches), c0.max_size)
+        for i, c in enumerate(caches):
+            runs = [] if c.empty() else c._temporal_runs()
+            if runs:
+                rl.row(i, width - c.size(), (c._keys, c._values), 0, runs)
+            else:
+                rl.row(i)
+        batch._keys, batch._values = rl.run()
+        batch.offset = batch.offset + width
+        batch._idx = width
         return batch

@@ -8,6 +8,7 @@ tensors raise (the library has no CPU implementation).
 from __future__ import annotations
 
 import ctypes
+from typing import NamedTuple, Optional
 
 import torch
 
@@ -180,6 +181,63 @@ def requant_window(old: tuple, new: tuple, dst: tuple, n_old: int, keep: int, ro
                                    _view(x), _view(d[0]), _view(d[1]), _view(d[2]))
     _lib.check(_lib.load().qsdpa_requant_window(jobs, 2, _stream(keys)))
     return total
+
+
+class RowMove(NamedTuple):
+    """Fill token columns [dst_col, dst_col + tokens) of batch row `dst_row` of
+    a (B, H, N, W) buffer, every head: the columns dst_col + [copy_begin,
+    copy_end) from `src` (batch row `src_row`, starting at column `src_col`),
+    the others with zeros (all of them when src is None)."""
+    dst: torch.Tensor
+    dst_row: int
+    dst_col: int
+    tokens: int
+    src: Optional[torch.Tensor] = None
+    src_row: int = 0
+    src_col: int = 0
+    copy_begin: int = 0
+    copy_end: int = 0
+
+
+def _check_rows(name, t, row, col, n):
+    if t.dim() != 4 or (t.shape[3] > 1 and t.stride(3) != 1):
+        raise ValueError(f"{name}: expected a (B, H, N, W) tensor with contiguous W, got {tuple(t.shape)}")
+    if not (0 <= row < t.shape[0] and 0 <= col and col + n <= t.shape[2]):
+        raise ValueError(f"{name}: rows {row}, columns [{col}, {col + n}) outside shape {tuple(t.shape)}")
+
+
+def move_rows(moves) -> None:
+    """Run RowMoves with qsdpa_move_rows (kernel-argument descriptors, one
+    launch per 48 moves, no synchronization).  Bounds, dtypes, head counts
+    and row widths are checked here; no destination may overlap another
+    destination or a source of the same call."""
+    moves = [m for m in moves if m.tokens > 0 and m.dst.shape[1] > 0]
+    if not moves:
+        return
+    dev = moves[0].dst.device
+    _require_device(*(m.dst for m in moves), *(m.src for m in moves))
+    arr = (_lib.RowMove * len(moves))()
+    for i, m in enumerate(moves):
+        d = m.dst
+        _check_rows("dst", d, m.dst_row, m.dst_col, m.tokens)
+        if d.device != dev:
+            raise ValueError("all moves of one call must be on one device")
+        es = d.element_size()
+        dst_ptr = d.data_ptr() + (m.dst_row * d.stride(0) + m.dst_col * d.stride(2)) * es
+        src_ptr, shs, sts, lo, hi = None, 0, 0, 0, 0
+        if m.src is not None and m.copy_end > m.copy_begin:
+            s = m.src
+            lo, hi = int(m.copy_begin), int(m.copy_end)
+            if not 0 <= lo < hi <= m.tokens:
+                raise ValueError(f"copy range [{lo}, {hi}) outside [0, {m.tokens})")
+            _check_rows("src", s, m.src_row, m.src_col, hi - lo)
+            if s.dtype != d.dtype or s.shape[1] != d.shape[1] or s.shape[3] != d.shape[3] or s.device != dev:
+                raise ValueError(f"src {tuple(s.shape)} {s.dtype} does not match dst {tuple(d.shape)} {d.dtype}")
+            src_ptr = s.data_ptr() + (m.src_row * s.stride(0) + m.src_col * s.stride(2)) * es
+            shs, sts = s.stride(1) * es, s.stride(2) * es
+        arr[i] = _lib.RowMove(src_ptr, dst_ptr, shs, sts, d.stride(1) * es, d.stride(2) * es,
+                              d.shape[1], int(m.tokens), d.shape[3] * es, lo, hi)
+    _lib.check(_lib.load().qsdpa_move_rows(arr, len(moves), _stream(moves[0].dst)))
 
 
 def dequantize(packed: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor | None = None,

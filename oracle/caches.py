@@ -58,6 +58,15 @@ def _dynamic_roll(x, shifts, axis):
     return np.take_along_axis(x, idx, axis=axis)
 
 
+def _from_end(idx, B):
+    """Extension: a negative sequence index counts from the end (the
+    reference's slice [idx:idx + 1] is empty for idx = -1)."""
+    idx = int(idx)
+    if not -B <= idx < B:
+        raise IndexError(idx)
+    return idx % B
+
+
 def _ring_temporal(t, keep, ptr, n_visible):
     """[0:keep] + [ptr:n_visible] + [keep:ptr]  (identity when ptr <= keep)."""
     if ptr <= keep or ptr >= n_visible:
@@ -229,23 +238,59 @@ class BatchQuantizedSDPACache:
                                   window_size=kw.get("window_size"))
 
     def filter(self, batch_indices):                                # cache.py:378-391
-        bi = np.asarray(batch_indices)
-        if self._keys is not None:
-            self._keys = tuple(t[bi] for t in self._keys)
-            self._values = tuple(t[bi] for t in self._values)
+        bi = np.asarray(batch_indices, dtype=np.int64).reshape(-1)
         self.offset = self.offset[bi]
         self.left_padding = self.left_padding[bi]
-        min_pad = int(self.left_padding.min())
+        if self._keys is None:      # (the reference would trim a None buffer)
+            return
+        self._keys = tuple(t[bi] for t in self._keys)
+        self._values = tuple(t[bi] for t in self._values)
+        min_pad = int(self.left_padding.min()) if bi.size else 0
         if min_pad > 0:
             self._keys = tuple(t[:, :, min_pad:] for t in self._keys)
             self._values = tuple(t[:, :, min_pad:] for t in self._values)
             self._idx -= min_pad
             self.left_padding = self.left_padding - min_pad
 
+    def extend(self, other):                                        # cache.py:393-427
+        """Other's rows after this batch's; both sides padded on the left by
+        max(_idx) - own _idx and on the right to the larger capacity (cut
+        when the left pad pushes columns past it).  Extension: a side
+        without buffers contributes zero rows (the reference needs both)."""
+        top = max(self._idx, other._idx)
+        sides = (self, other)
+        filled = [c for c in sides if c._keys is not None]
+        if filled:
+            cap = max(c._keys[0].shape[2] for c in filled)
+            like = filled[0]
+
+            def placed(c, tup, like_tup):
+                left = top - c._idx
+                out = []
+                for j, ref in enumerate(like_tup):
+                    B = c.offset.shape[0]
+                    z = np.zeros((B, ref.shape[1], cap, ref.shape[3]), ref.dtype)
+                    if tup is not None:
+                        t = tup[j]
+                        n = min(t.shape[2], cap - left)
+                        z[:, :, left:left + n] = t[:, :, :n]
+                    out.append(z)
+                return out
+
+            ks = [placed(c, c._keys, like._keys) for c in sides]
+            vs = [placed(c, c._values, like._values) for c in sides]
+            self._keys = tuple(np.concatenate([a, b], axis=0) for a, b in zip(*ks))
+            self._values = tuple(np.concatenate([a, b], axis=0) for a, b in zip(*vs))
+        self.offset = np.concatenate([self.offset, other.offset])
+        self.left_padding = np.concatenate([self.left_padding + (top - self._idx),
+                                            other.left_padding + (top - other._idx)])
+        self._idx = top
+
     def extract(self, idx):                                         # cache.py:429-444
         c = QuantizedSDPACache(bits=self.bits, group_size=self.group_size, dtype=self.dtype)
         if self._keys is None:
             return c
+        idx = _from_end(idx, self.offset.shape[0])
         pad = int(self.left_padding[idx])
         c._keys = tuple(t[idx:idx + 1, :, pad:self._idx].copy() for t in self._keys)
         c._values = tuple(t[idx:idx + 1, :, pad:self._idx].copy() for t in self._values)
@@ -485,12 +530,67 @@ class BatchQuantizedRotatingSDPACache:
         return create_causal_mask(N, offset=off, left_padding=self.left_padding,
                                   window_size=kw.get("window_size"))
 
+    def filter(self, batch_indices):                                # cache.py:868-874
+        bi = np.asarray(batch_indices, dtype=np.int64).reshape(-1)
+        if self._keys is not None:
+            self._keys = tuple(t[bi] for t in self._keys)
+            self._values = tuple(t[bi] for t in self._values)
+        self.offset = self.offset[bi]
+        self.left_padding = self.left_padding[bi]
+
+    def _temporal(self, tup):
+        """The visible window of every row, in temporal order."""
+        n_visible = min(self._idx, self.max_size)
+        res = tuple(t[:, :, :n_visible] for t in tup)
+        if self._idx > self.max_size:
+            res = tuple(_ring_temporal(t, self.keep, self._ring_ptr(), n_visible) for t in res)
+        return res
+
+    def extend(self, other):                                        # cache.py:876-912
+        """Other's rows after this batch's.  The reference pads each side on
+        the left by max(_idx) - own _idx and concatenates the buffers as
+        they lie.  Extension, for every pair of batches: each side's window
+        is first put in temporal order (the reference's shift of a wrapped
+        ring mixes old and new tokens) and right-aligned at the longer
+        window n in max_size-wide buffers (the reference's concatenation
+        fails on unequal widths); _idx = n, so the ring starts unrotated.
+        While neither side has wrapped, n - own visible = max(_idx) - own
+        _idx: the reference's shift.  A side without buffers contributes zero
+        rows (the reference keeps only the other side's)."""
+        sides = (self, other)
+        vis = [min(c._idx, c.max_size) if c._keys is not None else 0 for c in sides]
+        n = max(vis)
+        filled = [c for c in sides if c._keys is not None]
+        if filled:
+            like = filled[0]
+            W = self.max_size
+
+            def placed(c, v, tup, like_tup):
+                out = []
+                tt = c._temporal(tup) if tup is not None else None
+                for j, ref in enumerate(like_tup):
+                    z = np.zeros((c.offset.shape[0], ref.shape[1], W, ref.shape[3]), ref.dtype)
+                    if tt is not None:
+                        z[:, :, n - v:n] = tt[j]
+                    out.append(z)
+                return out
+
+            ks = [placed(c, v, c._keys, like._keys) for c, v in zip(sides, vis)]
+            vs = [placed(c, v, c._values, like._values) for c, v in zip(sides, vis)]
+            self._keys = tuple(np.concatenate([a, b], axis=0) for a, b in zip(*ks))
+            self._values = tuple(np.concatenate([a, b], axis=0) for a, b in zip(*vs))
+        self.offset = np.concatenate([self.offset, other.offset])
+        self.left_padding = np.concatenate([self.left_padding + (n - vis[0]),
+                                            other.left_padding + (n - vis[1])])
+        self._idx = n
+
     def extract(self, idx):                                         # cache.py:914-961
         c = QuantizedRotatingSDPACache(max_size=self.max_size, keep=self.keep,
                                        bits=self.bits, group_size=self.group_size,
                                        dtype=self.dtype)
         if self._keys is None:
             return c
+        idx = _from_end(idx, self.offset.shape[0])
         visible = min(self._idx, self.max_size)
         n_tokens = max(0, min(int(self.offset[idx]), self.max_size))
         if n_tokens == 0:
@@ -534,8 +634,10 @@ class BatchQuantizedRotatingSDPACache:
         ref = next(c for c in caches if not c.empty())
         H = ref._keys[0].shape[1]
         ks, vs = ref.state
-        batch._keys = tuple(np.zeros((B, H, max_len, t.shape[3]), t.dtype) for t in ks)
-        batch._values = tuple(np.zeros((B, H, max_len, t.shape[3]), t.dtype) for t in vs)
+        # Extension: max_size columns, not max_len, so the merged batch can
+        # take its next decode (at column max_len).
+        batch._keys = tuple(np.zeros((B, H, max_size, t.shape[3]), t.dtype) for t in ks)
+        batch._values = tuple(np.zeros((B, H, max_size, t.shape[3]), t.dtype) for t in vs)
         for i, (p, c) in enumerate(zip(padding, caches)):
             if c.empty():
                 continue

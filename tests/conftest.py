@@ -125,6 +125,27 @@ def _cpu_quantize_kv_into(keys, values, kdst, vdst, t0, bits, group_size):
     _cpu_quantize_into(values, vdst, t0, bits, group_size)
 
 
+def _cpu_move_rows(moves):
+    """CPU stand-in for kernels.move_rows (qsdpa_move_rows): the same
+    RowMove semantics with torch slicing, plus the wrapper's bounds checks."""
+    for m in moves:
+        if m.tokens <= 0:
+            continue
+        d = m.dst
+        if not (0 <= m.dst_row < d.shape[0] and 0 <= m.dst_col and m.dst_col + m.tokens <= d.shape[2]):
+            raise ValueError("dst rows out of range")
+        seg = d[m.dst_row, :, m.dst_col:m.dst_col + m.tokens]
+        seg.zero_()
+        if m.src is not None and m.copy_end > m.copy_begin:
+            n = m.copy_end - m.copy_begin
+            s = m.src
+            if not (0 <= m.src_row < s.shape[0] and 0 <= m.src_col and m.src_col + n <= s.shape[2]):
+                raise ValueError("src rows out of range")
+            if s.dtype != d.dtype or s.shape[1] != d.shape[1] or s.shape[3] != d.shape[3]:
+                raise ValueError("src does not match dst")
+            seg[:, m.copy_begin:m.copy_end] = s[m.src_row, :, m.src_col:m.src_col + n]
+
+
 @pytest.fixture
 def cpu_kernels(monkeypatch):
     from mlx_qsdpa_amd import kernels
@@ -132,6 +153,7 @@ def cpu_kernels(monkeypatch):
     monkeypatch.setattr(kernels, "quantize_kv_into", _cpu_quantize_kv_into)
     monkeypatch.setattr(kernels, "dequantize", _cpu_dequantize)
     monkeypatch.setattr(kernels, "requant_window", _cpu_requant_window)
+    monkeypatch.setattr(kernels, "move_rows", _cpu_move_rows)
     return kernels
 
 

@@ -43,6 +43,7 @@ _STRUCTS = {
     "qsdpa_quantize_args": _lib.QuantizeArgs,
     "qsdpa_dequantize_args": _lib.DequantizeArgs,
     "qsdpa_requant_args": _lib.RequantArgs,
+    "qsdpa_row_move": _lib.RowMove,
 }
 
 
@@ -97,6 +98,23 @@ def test_invalid_arguments_return_codes():
     assert lib.qsdpa_requant_window(r, 2, None) == _lib.QSDPA_ERR_INVALID
     assert b"share" in lib.qsdpa_last_error()
     assert lib.qsdpa_requant_window(r, 3, None) == _lib.QSDPA_ERR_INVALID
+    m = (_lib.RowMove * 2)()
+    for x in m:
+        x.dst, x.heads, x.tokens, x.row_bytes = 64, 2, 4, 16
+    assert lib.qsdpa_move_rows(m, -1, None) == _lib.QSDPA_ERR_INVALID
+    assert lib.qsdpa_move_rows(None, 1, None) == _lib.QSDPA_ERR_INVALID
+    assert lib.qsdpa_move_rows(None, 0, None) == _lib.QSDPA_OK  # nothing to do: no launch
+    m[1].src, m[1].copy_begin, m[1].copy_end = 128, 3, 5  # copy range past `tokens`
+    assert lib.qsdpa_move_rows(m, 2, None) == _lib.QSDPA_ERR_INVALID
+    assert b"copy range" in lib.qsdpa_last_error()
+    m[1].copy_end, m[1].src_token_stride = 4, -16
+    assert lib.qsdpa_move_rows(m, 2, None) == _lib.QSDPA_ERR_INVALID
+    assert b"negative stride" in lib.qsdpa_last_error()
+    m[1].src_token_stride, m[1].row_bytes = 16, 0
+    assert lib.qsdpa_move_rows(m, 2, None) == _lib.QSDPA_ERR_INVALID
+    m[1].row_bytes, m[1].dst = 16, None
+    assert lib.qsdpa_move_rows(m, 2, None) == _lib.QSDPA_ERR_INVALID
+    assert b"null dst" in lib.qsdpa_last_error()
     a = _lib.DecodeArgs()
     a.B = a.H_q = a.H_kv = a.N = 1
     a.D, a.bits, a.group_size = 100, 4, 32
