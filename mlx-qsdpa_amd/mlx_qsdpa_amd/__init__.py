@@ -51,6 +51,11 @@ def cache_sdpa(q, k_quant, v_quant, cache, scale=None, mask=None, crossover=None
                           group_size=cache.group_size, kv_start=kv_start)
 
 
+# The model side (needs cache_sdpa above): the router keyed on
+# _use_fused_sdpa, an attention layer calling it, cache save / load.
+from .attention import Attention, KVCache, scaled_dot_product_attention  # noqa: E402
+from .cache_io import load_cache, save_cache  # noqa: E402
+
 __all__ = [
     "quantized_sdpa",
     "QuantizedSDPACache",
@@ -60,4 +65,9 @@ __all__ = [
     "cache_sdpa",
     "quantize",
     "dequantize",
+    "scaled_dot_product_attention",
+    "Attention",
+    "KVCache",
+    "save_cache",
+    "load_cache",
 ]

@@ -51,7 +51,7 @@ def _create_causal_mask(N, offset, window_size=None, left_padding=None, device=N
         mask = q_idx[:, None] >= k_idx[None]
         if window_size is not None:
             mask = mask & (q_idx[:, None] - k_idx[None] < window_size)
-    return mask if device is None else mask.to(device)
+    return mask if device is None else kernels.to_device(mask, device)
 
 
 def _zeros_q(shape3, dim, bits, group_size, dtype, device):
@@ -215,12 +215,13 @@ class QuantizedSDPACache:
         return num_to_trim > 0
 
     def make_mask(self, N, return_array=False, window_size=None):
+        dev = self._keys[0].device if self._keys is not None else None
         if window_size is not None:
-            return _create_causal_mask(N, self.offset, window_size=window_size)
+            return _create_causal_mask(N, self.offset, window_size=window_size, device=dev)
         if N == 1:
             return None
         if return_array:
-            return _create_causal_mask(N, self.offset)
+            return _create_causal_mask(N, self.offset, device=dev)
         return "causal"
 
     @property
@@ -323,7 +324,7 @@ class BatchQuantizedSDPACache:
     def kv_start(self, device=None):
         """Per-sequence first valid slot (= left padding), int32 on `device`."""
         lp = self.left_padding.to(torch.int32)
-        return lp if device is None else lp.to(device, non_blocking=True)
+        return lp if device is None else kernels.to_device(lp, device)
 
     def update_and_fetch(self, keys, values):
         """cache.py:279-322: all sequences append at the shared column _idx."""
@@ -397,6 +398,24 @@ class BatchQuantizedSDPACache:
         self.offset = torch.as_tensor(self.offset, dtype=torch.int64).cpu()
         self.left_padding = torch.as_tensor(self.left_padding, dtype=torch.int64).cpu()
         self._idx = 0 if self._keys is None else self._keys[0].shape[2]
+
+    @property
+    def meta_state(self):
+        """Extension (the reference's batch cache has none): the settings a
+        saved state needs to come back (offsets travel in ``state``)."""
+        return tuple(map(str, (self.bits, self.group_size)))
+
+    @meta_state.setter
+    def meta_state(self, v):
+        self.bits, self.group_size = map(int, v)
+
+    @classmethod
+    def from_state(cls, state, meta_state):
+        obj = cls.__new__(cls)
+        obj._right_padding = None
+        obj.meta_state = meta_state
+        obj.state = state
+        return obj
 
     def make_mask(self, N, return_array=False, **kwargs):
         """cache.py:369-376 (logical offsets for queries, buffer index for keys)."""
@@ -629,6 +648,11 @@ class QuantizedRotatingSDPACache:
             self._values = None
             return
         n_visible = keys[0].shape[2]
+        # The snapshot is in temporal order: the ring restarts unrotated and
+        # the next write goes to slot n_visible, or to `keep` (the oldest
+        # token after the sinks) when the window is full.  (Extension: the
+        # reference leaves _idx to the caller.)
+        self._idx = n_visible
         pad_len = self.max_size - n_visible
         if pad_len <= 0:
             self._keys = keys
@@ -636,6 +660,25 @@ class QuantizedRotatingSDPACache:
             return
         self._keys = tuple(torch.nn.functional.pad(t, (0, 0, 0, pad_len)) for t in keys)
         self._values = tuple(torch.nn.functional.pad(t, (0, 0, 0, pad_len)) for t in values)
+
+    @property
+    def meta_state(self):
+        """Extension (the reference's rotating cache has none): the settings
+        and token count a saved temporal-order state needs to come back."""
+        return tuple(map(str, (self.keep, self.max_size, self.offset, self.bits, self.group_size)))
+
+    @meta_state.setter
+    def meta_state(self, v):
+        self.keep, self.max_size, self.offset, self.bits, self.group_size = map(int, v)
+
+    @classmethod
+    def from_state(cls, state, meta_state):
+        obj = cls.__new__(cls)
+        obj._keys = obj._values = None
+        obj.meta_state = meta_state
+        obj._idx = 0
+        obj.state = state
+        return obj
 
 
 class BatchQuantizedRotatingSDPACache:
@@ -735,6 +778,52 @@ class BatchQuantizedRotatingSDPACache:
         dev = self._keys[0].device if self._keys is not None else None
         return _create_causal_mask(N, offset=off, left_padding=self.left_padding,
                                    window_size=kwargs.get("window_size"), device=dev)
+
+    @property
+    def state(self):
+        """Extension (the reference's batched rotating cache has no state):
+        the window of every sequence in temporal order, offset and
+        left_padding -- the form a saved batch comes back from."""
+        if self._keys is None:
+            return None, None, self.offset, self.left_padding
+        n, ptr = min(self._idx, self.max_size), self._write_pos()
+        if self._idx > self.max_size:
+            return (tuple(_ring_temporal(t, self.keep, ptr, n) for t in self._keys),
+                    tuple(_ring_temporal(t, self.keep, ptr, n) for t in self._values),
+                    self.offset, self.left_padding)
+        return _sl(self._keys, 0, n), _sl(self._values, 0, n), self.offset, self.left_padding
+
+    @state.setter
+    def state(self, v):
+        """A temporal-order window back into max_size slots; the ring restarts
+        unrotated (_idx = the window length)."""
+        keys, values, offset, left_padding = v
+        self.offset = torch.as_tensor(offset, dtype=torch.int64).cpu()
+        self.left_padding = torch.as_tensor(left_padding, dtype=torch.int64).cpu()
+        if keys is None:
+            self._keys = self._values = None
+            self._idx = 0
+            return
+        n = keys[0].shape[2]
+        pad = self.max_size - n
+        self._keys = tuple(torch.nn.functional.pad(t, (0, 0, 0, pad)) if pad > 0 else t for t in keys)
+        self._values = tuple(torch.nn.functional.pad(t, (0, 0, 0, pad)) if pad > 0 else t for t in values)
+        self._idx = n
+
+    @property
+    def meta_state(self):
+        return tuple(map(str, (self.keep, self.max_size, self.bits, self.group_size)))
+
+    @meta_state.setter
+    def meta_state(self, v):
+        self.keep, self.max_size, self.bits, self.group_size = map(int, v)
+
+    @classmethod
+    def from_state(cls, state, meta_state):
+        obj = cls.__new__(cls)
+        obj.meta_state = meta_state
+        obj.state = state
+        return obj
 
     def _temporal_runs(self):
         """Column runs of the window in temporal order (shared by all rows)."""

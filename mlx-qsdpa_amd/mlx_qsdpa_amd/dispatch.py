@@ -156,6 +156,12 @@ def quantized_sdpa(
     # not 16-byte aligned is copied first, as the reference's kernel builder
     # copies every input (ensure_row_contiguous, kernels.py:190).
     packed_k, packed_v = _row_aligned(packed_k), _row_aligned(packed_v)
+    # A mask made on the host (as a cache's make_mask may make it) goes to
+    # the device in stream order, without waiting.
+    if isinstance(mask, torch.Tensor) and q.device.type == "cuda":
+        mask = kernels.to_device(mask, q.device)
+    if isinstance(kv_start, torch.Tensor) and q.device.type == "cuda":
+        kv_start = kernels.to_device(kv_start, q.device)
 
     if qL > 1 and not _fused_takes(q, packed_k, packed_v, k_scales, v_scales, k_biases,
                                    v_biases, scale, bits, group_size):

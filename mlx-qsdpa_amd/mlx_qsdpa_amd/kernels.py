@@ -59,6 +59,14 @@ def _rows_in_storage(t: torch.Tensor) -> int:
     return max(0, (elems - 1 - last_other) // sn + 1)
 
 
+def to_device(t: torch.Tensor, device) -> torch.Tensor:
+    """A small host tensor (mask, offsets) on a GPU `device`, copied in
+    stream order from pinned memory: the host does not wait for the GPU."""
+    if t.device.type == "cuda" or torch.device(device).type != "cuda":
+        return t.to(device)
+    return t.pin_memory().to(device, non_blocking=True)
+
+
 def _stream(t: torch.Tensor) -> int:
     return torch.cuda.current_stream(t.device).cuda_stream
 
