@@ -72,6 +72,9 @@ def parse_args(argv=None):
     ap.add_argument("--qlen", type=int, default=1,
                     help="query positions per call; > 1 times causal multi-query attention "
                          "(fused vs dequantize + attention) instead of the decode step")
+    ap.add_argument("--rotating-prefill", action="store_true",
+                    help="time C5's prefill chunk (--qlen, default 512) through the batched rotating "
+                         "cache: requant + attention")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="time budget of the CPU baseline sample (0 = skip)")
     ap.add_argument("--seed", type=int, default=0)
@@ -161,30 +164,41 @@ def make_sets(cfg, N, n_sets, device, seed):
     return sets
 
 
+def host_threads():
+    """Host threads for the CPU baseline: the cores this process may run on
+    (len(os.sched_getaffinity(0))), capped by OMP_NUM_THREADS when it is set
+    lower (the GPU boxes give one GPU's job a 16-core share)."""
+    cores = len(os.sched_getaffinity(0))
+    cap = os.environ.get("OMP_NUM_THREADS", "")
+    return (min(cores, int(cap)) if cap.isdigit() and int(cap) > 0 else cores), cores
+
+
 def cpu_baseline(cfg, N, host_set, budget_s):
-    """Oracle float32 decode (1 thread) on the first KV set, repeated within budget."""
+    """Oracle float32 decode on all host threads (key ranges split over
+    threads, log-sum-exp merge) on the first KV set, repeated within budget."""
     import numpy as np
-    from threadpoolctl import threadpool_limits
 
     from oracle import attention
 
     B, Hq, Hkv, D, bits, gs, dt, _, _ = cfg
     q, kq, vq = host_set
-    with threadpool_limits(limits=1):
-        times = []
-        t_end = time.perf_counter() + budget_s
-        while True:
-            t0 = time.perf_counter()
-            attention.decode_fp32(q, kq[0], vq[0], kq[1], vq[1], kq[2], vq[2], bits=bits,
-                                  group_size=gs)
-            times.append(time.perf_counter() - t0)
-            if time.perf_counter() > t_end or len(times) >= 50:
-                break
+    threads, cores = host_threads()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while True:
+        t0 = time.perf_counter()
+        attention.decode_fp32_threads(q, kq[0], vq[0], kq[1], vq[1], kq[2], vq[2], bits=bits,
+                                      group_size=gs, threads=threads)
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() > t_end or len(times) >= 50:
+            break
     us = float(np.median(times)) * 1e6
-    return {"value": round(us, 1), "unit": "us/step", "cores": 1, "kind": "port",
-            "sample": (f"{len(times)} full decode steps of the same workload (N={N}) on one "
-                       f"host core, numpy float32 dequantize + attention "
-                       f"(oracle.attention.decode_fp32), median")}
+    return {"value": round(us, 1), "unit": "us/step", "cores": threads, "kind": "port",
+            "sample": (f"{len(times)} full decode steps of the same workload (N={N}) on {threads} host "
+                       f"threads (sched_getaffinity: {cores} cores; OMP_NUM_THREADS cap "
+                       f"{os.environ.get('OMP_NUM_THREADS', 'unset')}), numpy float32 dequantize + "
+                       f"attention over key ranges per thread with a log-sum-exp merge "
+                       f"(oracle.attention.decode_fp32_threads), median")}
 
 
 # BASELINE config C4: continuous-batching decode through the batch cache's
@@ -278,6 +292,36 @@ def run_c4(args) -> int:
     kern_us = float(np.mean(kern_ms)) * 1e3
     hip.destroy(ev_b + ev_e)
 
+    # The API path: the same batch shape through BatchQuantizedSDPACache --
+    # update_and_fetch (quantize-on-append, growth by 256 slots when full)
+    # then cache_sdpa with kv_start = the left padding, per step.
+    import mlx_qsdpa_amd as mq
+
+    cache = mq.BatchQuantizedSDPACache((lmax - lengths).tolist(), bits=bits, group_size=gs)
+    for t0_ in range(0, lmax, chunk):
+        n_ = min(chunk, lmax - t0_)
+        kk = torch.randn((B, Hkv, n_, D), generator=g, device=device, dtype=torch.float32).to(T)
+        vv = torch.randn((B, Hkv, n_, D), generator=g, device=device, dtype=torch.float32).to(T)
+        cache.update_and_fetch(kk, vv)
+        del kk, vv
+    torch.cuda.synchronize()
+
+    def api_step():
+        kq, vq = cache.update_and_fetch(new[0], new[1])
+        return mq.cache_sdpa(q, kq, vq, cache, kv_start=cache.kv_start(device))
+
+    for _ in range(args.warmup):
+        api_step()
+    torch.cuda.synchronize()
+    cap0 = cache._keys[0].shape[2]
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        api_step()
+    torch.cuda.synchronize()
+    api_us = (time.perf_counter() - t0) / args.steps * 1e6
+    grew = cache._keys[0].shape[2] != cap0
+    del cache
+
     us_step = wall / args.steps * 1e6
     valid = lambda n_: int((lengths + (n_ + 1 - lmax)).sum())  # noqa: E731 (keys per sequence after the append)
     bytes_wall = np.mean([metric.decode_bytes(B, Hq, Hkv, D, bits, gs, valid(k))
@@ -287,7 +331,8 @@ def run_c4(args) -> int:
     step_gbps = bytes_wall / (us_step * 1e-6) / 1e9
     kern_gbps = bytes_kern / (kern_us * 1e-6) / 1e9
     print(f"bench: c4 {us_step:.2f} us/step wall (append + decode), decode kernel {kern_us:.2f} us "
-          f"({kern_gbps:.0f} GB/s), splits={splits}", file=sys.stderr, flush=True)
+          f"({kern_gbps:.0f} GB/s), splits={splits}; API path {api_us:.2f} us/step", file=sys.stderr,
+          flush=True)
     workload = (f"c4: batched decode B={B} H_q={Hq} H_kv={Hkv} D={D} {bits}-bit gs={gs} f16, lengths "
                 f"U[{c['len_lo']},{c['len_hi']}] left-padded, append + decode per step")
     line = {
@@ -300,6 +345,8 @@ def run_c4(args) -> int:
                    "num_splits": splits},
         "effective_gbps": round(step_gbps, 1),
         "pct_hbm_peak": round(100.0 * step_gbps / HBM_PEAK_GBPS, 2),
+        "api_path": {"us_per_step": round(api_us, 3), "cache_grew_in_timed_steps": grew,
+                     "call": "BatchQuantizedSDPACache.update_and_fetch + cache_sdpa(kv_start=left padding)"},
         "roofline": {"bound": "hbm", "achieved": round(kern_gbps, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(kern_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
                      "kernel_us": round(kern_us, 3), "kernel_us_p5_p50_p95": _pcts(kern_ms),
@@ -401,12 +448,106 @@ def run_multi_query(args) -> int:
     return 0
 
 
+def run_rotating_prefill(args) -> int:
+    """--rotating-prefill: C5's prefill chunk through the batched rotating
+    cache.  The window (max_size = C5's N, keep = 4 sinks) is filled and
+    advanced past its wrap; each step then takes one chunk of --qlen tokens
+    (default 512): update_and_fetch (the requant launch: the old window in
+    temporal order + the chunk, trimmed to the sinks and the newest tokens,
+    quantized again into the spare buffers, K and V in one launch) and
+    cache_sdpa with the causal mask (rows are unpadded, so "causal" is the
+    mask make_mask would build).  Reports the wall time per chunk and, from
+    torch events on the launch stream, the requant and the attention."""
+    import numpy as np
+    import torch
+
+    import mlx_qsdpa_amd as mq
+    from mlx_qsdpa_amd import metric
+
+    B, Hq, Hkv, D, bits, gs, dt, W, _ = CONFIGS["c5"]
+    L = args.qlen if args.qlen > 1 else 512
+    keep = 4
+    device = torch.device("cuda:0")
+    T = torch.bfloat16
+    g = torch.Generator(device=device)
+    g.manual_seed(args.seed)
+
+    def rnd(n, h=Hkv):
+        return torch.randn((B, h, n, D), generator=g, device=device, dtype=torch.float32).to(T)
+
+    cache = mq.BatchQuantizedRotatingSDPACache([0] * B, W, keep=keep, bits=bits, group_size=gs)
+    for _ in range(W // 1024):
+        cache.update_and_fetch(rnd(1024), rnd(1024))
+    for _ in range(37):  # past the wrap: the ring is rotated
+        cache.update_and_fetch(rnd(1), rnd(1))
+    chunks = [(rnd(L), rnd(L), rnd(L, Hq)) for _ in range(4)]
+    torch.cuda.synchronize()
+
+    def step(i, ev=None):
+        k, v, q = chunks[i % len(chunks)]
+        if ev is not None:
+            ev[0].record()
+        kq, vq = cache.update_and_fetch(k, v)
+        if ev is not None:
+            ev[1].record()
+        out = mq.cache_sdpa(q, kq, vq, cache, mask="causal")
+        if ev is not None:
+            ev[2].record()
+        return out
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(i)
+    torch.cuda.synchronize()
+    us = (time.perf_counter() - t0) / args.steps * 1e6
+    evs = [tuple(torch.cuda.Event(enable_timing=True) for _ in range(3)) for _ in range(args.steps)]
+    for i in range(args.steps):
+        step(i, evs[i])
+    torch.cuda.synchronize()
+    req_ms = [a.elapsed_time(b) for a, b, _ in evs]
+    att_ms = [b.elapsed_time(c) for _, b, c in evs]
+    req_us, att_us = float(np.mean(req_ms)) * 1e3, float(np.mean(att_ms)) * 1e3
+    # Requant bytes: the old window read once (quantized), the chunk read
+    # (raw T), the new window written (quantized); K and V.
+    per_tok = metric.kv_bytes_per_token(Hkv, D, bits, gs)
+    req_bytes = B * W * per_tok + 2 * B * Hkv * L * D * 2 + B * W * per_tok
+    req_gbps = req_bytes / (req_us * 1e-6) / 1e9
+    pairs = sum(max(0, min(W, W - L + i + 1)) for i in range(L))
+    flops = 4.0 * B * Hq * pairs * D
+    tflops = flops / (att_us * 1e-6) / 1e12
+    print(f"bench: c5 rotating prefill chunk L={L}: {us:.2f} us/chunk wall; requant {req_us:.2f} us "
+          f"({req_gbps:.0f} GB/s), attention {att_us:.2f} us ({tflops:.1f} TFLOP/s)", file=sys.stderr, flush=True)
+    workload = (f"c5-rot-q{L}: rotating prefill chunk B={B} H_q={Hq} H_kv={Hkv} D={D} {bits}-bit gs={gs} "
+                f"{dt} max_size={W} keep={keep}, wrapped window, requant + causal attention")
+    line = {
+        "metric": f"µs per rotating prefill chunk of {L} tokens (requant + attention), C5",
+        "value": round(us, 3), "unit": "us/chunk", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(us / 1e3, 6), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": dt, "data": "synthetic",
+        "config": {"workload": workload, "B": B, "H_q": Hq, "H_kv": Hkv, "D": D, "max_size": W,
+                   "keep": keep, "qL": L, "bits": bits, "group_size": gs},
+        "requant": {"us": round(req_us, 3), "us_p5_p50_p95": _pcts(req_ms), "bytes": req_bytes,
+                    "achieved_gbps": round(req_gbps, 1), "frac_hbm": round(req_gbps / HBM_PEAK_GBPS, 4)},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": 2500.0, "unit": "TFLOP/s",
+                     "frac": round(tflops / 2500.0, 4), "traffic": None, "kernel_us": round(att_us, 3),
+                     "kernel_us_p5_p50_p95": _pcts(att_ms), "flops": flops},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main(argv=None) -> int:
     args = parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the decode path is "
               "single-GPU in this build, see DESIGN.md for how it would shard.", file=sys.stderr)
         return 2
+    if args.rotating_prefill:
+        return run_rotating_prefill(args)
     if args.config == "c4":
         return run_c4(args)
     if args.qlen > 1:
@@ -462,13 +603,44 @@ def main(argv=None) -> int:
     kern_ms = [hip.elapsed_ms(ev_b[i], ev_e[i]) for i in range(args.steps)]
     hip.destroy(ev_b + ev_e)
 
+    # Whole step (decode kernel + split-K merge): torch events on the stream
+    # both launches go to.
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(args.steps)]
+    for i in range(args.steps):
+        evs[i][0].record()
+        plans[i % n_sets]()
+        evs[i][1].record()
+    torch.cuda.synchronize()
+    step_ms = [a.elapsed_time(b) for a, b in evs]
+
+    # The API path: mlx_qsdpa_amd.quantized_sdpa per step (argument blocks
+    # cached per tensor geometry), same KV sets.
+    import mlx_qsdpa_amd as mq
+
+    def api(i):
+        q, kq, vq = sets[i % n_sets]
+        return mq.quantized_sdpa(q, kq[0], vq[0], kq[1], vq[1], kq[2], vq[2], scale=D ** -0.5,
+                                 bits=bits, group_size=gs)
+
+    for i in range(max(args.warmup, 2)):
+        api(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        api(i)
+    torch.cuda.synchronize()
+    api_us = (time.perf_counter() - t0) / args.steps * 1e6
+
     us_step = wall / args.steps * 1e6
     kern_us = float(np.mean(kern_ms)) * 1e3
     alg_bytes = metric.decode_bytes(B, Hq, Hkv, D, bits, gs, B * N)
     step_gbps = alg_bytes / (us_step * 1e-6) / 1e9
     kern_gbps = alg_bytes / (kern_us * 1e-6) / 1e9
+    step_us = float(np.mean(step_ms)) * 1e3
     print(f"bench: {us_step:.2f} us/step wall, main kernel {kern_us:.2f} us "
-          f"({kern_gbps:.0f} GB/s), splits={splits}", file=sys.stderr, flush=True)
+          f"({kern_gbps:.0f} GB/s), whole step {step_us:.2f} us (events), API path {api_us:.2f} us/step, "
+          f"splits={splits}", file=sys.stderr, flush=True)
 
     cpu = None
     if args.cpu_seconds > 0:
@@ -505,6 +677,10 @@ def main(argv=None) -> int:
         },
         "effective_gbps": round(step_gbps, 1),
         "pct_hbm_peak": round(100.0 * step_gbps / HBM_PEAK_GBPS, 2),
+        "whole_step": {"us": round(step_us, 3), "us_p5_p50_p95": _pcts(step_ms),
+                       "what": "decode kernel + split-K merge, torch events on the launch stream"},
+        "api_path": {"us_per_step": round(api_us, 3),
+                     "call": "mlx_qsdpa_amd.quantized_sdpa per step (argument block cached per geometry)"},
         "roofline": {
             "bound": "hbm",
             "achieved": round(kern_gbps, 1),

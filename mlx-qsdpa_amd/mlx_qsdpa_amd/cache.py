@@ -30,28 +30,40 @@ from . import kernels
 
 
 def _create_causal_mask(N, offset, window_size=None, left_padding=None, device=None):
-    """cache.py:15-43.  Batched offsets give a bool (B, 1, N, max(offset)+N)."""
+    """cache.py:15-43.  Batched offsets give a bool (B, 1, N, max(offset)+N).
+
+    With a GPU `device` the mask is computed there from the (B,) offsets and
+    left padding, which are the only host-to-device copy (pinned, no wait)."""
+    on_gpu = device is not None and torch.device(device).type == "cuda"
     if isinstance(offset, torch.Tensor) and offset.dim() > 0:
         off = offset.to("cpu", torch.int64)
-        max_off = int(off.max())
-        total = max_off + N
-        q_pos = torch.arange(N)[None, :] + off[:, None]
-        k_pos = torch.arange(total)[None, :]
+        total = int(off.max()) + N
+        dev = device if on_gpu else None
+        if on_gpu:
+            lp = None if left_padding is None else left_padding.to("cpu", torch.int64)
+            both = off if lp is None else torch.stack([off, lp])
+            both = kernels.to_device(both, device)
+            off_d, lp_d = (both, None) if lp is None else (both[0], both[1])
+        else:
+            off_d = off
+            lp_d = None if left_padding is None else left_padding.to("cpu", torch.int64)
+        q_pos = torch.arange(N, device=dev)[None, :] + off_d[:, None]
+        k_pos = torch.arange(total, device=dev)[None, :]
         mask = q_pos[:, :, None] >= k_pos[:, None, :]
-        if left_padding is not None:
-            lp = left_padding.to("cpu", torch.int64)
-            mask = mask & (k_pos[:, None, :] >= lp[:, None, None])
+        if lp_d is not None:
+            mask = mask & (k_pos[:, None, :] >= lp_d[:, None, None])
         if window_size is not None:
             mask = mask & (q_pos[:, :, None] - k_pos[:, None, :] < window_size)
         mask = mask[:, None, :, :]
-    else:
-        offset = int(offset)
-        q_idx = torch.arange(offset, offset + N)
-        k_idx = torch.arange(offset + N)
-        mask = q_idx[:, None] >= k_idx[None]
-        if window_size is not None:
-            mask = mask & (q_idx[:, None] - k_idx[None] < window_size)
-    return mask if device is None else kernels.to_device(mask, device)
+        return mask if dev is not None or device is None else mask.to(device)
+    offset = int(offset)
+    dev = device if on_gpu else None
+    q_idx = torch.arange(offset, offset + N, device=dev)
+    k_idx = torch.arange(offset + N, device=dev)
+    mask = q_idx[:, None] >= k_idx[None]
+    if window_size is not None:
+        mask = mask & (q_idx[:, None] - k_idx[None] < window_size)
+    return mask if dev is not None or device is None else mask.to(device)
 
 
 def _zeros_q(shape3, dim, bits, group_size, dtype, device):
@@ -322,9 +334,17 @@ class BatchQuantizedSDPACache:
         return n
 
     def kv_start(self, device=None):
-        """Per-sequence first valid slot (= left padding), int32 on `device`."""
-        lp = self.left_padding.to(torch.int32)
-        return lp if device is None else kernels.to_device(lp, device)
+        """Per-sequence first valid slot (= left padding), int32 on `device`.
+        The device copy is kept until left_padding changes, so a decode loop
+        uploads it once."""
+        if device is None:
+            return self.left_padding.to(torch.int32)
+        tag = (id(self.left_padding), self.left_padding._version, str(device))
+        held = getattr(self, "_kv_start_dev", None)
+        if held is None or held[0] != tag:
+            held = (tag, kernels.to_device(self.left_padding.to(torch.int32), device), self.left_padding)
+            self._kv_start_dev = held
+        return held[1]
 
     def update_and_fetch(self, keys, values):
         """cache.py:279-322: all sequences append at the shared column _idx."""

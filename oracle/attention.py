@@ -135,3 +135,50 @@ def decode_fp32(q, k_packed, v_packed, k_scales, v_scales, k_biases, v_biases,
     s /= s.sum(axis=-1, keepdims=True)
     o = np.matmul(s, v)                                             # [B,Hkv,G,D]
     return o.reshape(B, Hq, 1, D)
+
+
+def decode_fp32_threads(q, k_packed, v_packed, k_scales, v_scales, k_biases, v_biases,
+                        *, bits, group_size, threads, scale=None):
+    """decode_fp32 on `threads` host threads: the keys are cut into `threads`
+    contiguous ranges, each thread dequantizes its range and computes its
+    partial softmax (row max m, sum l, unnormalised output a), and the
+    partials are merged as  o = sum_i exp(m_i - M) a_i / sum_i exp(m_i - M) l_i
+    (M = max_i m_i).  numpy releases the GIL inside its array operations,
+    so the ranges run in parallel; each thread's BLAS calls are limited to
+    one thread.  The CPU baseline of bench.py on all host cores; pinned to
+    decode_fp32 by tests/test_oracle_attention.py."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    from threadpoolctl import threadpool_limits
+
+    B, Hq, L, D = q.shape
+    Hkv, N = k_packed.shape[1], k_packed.shape[2]
+    G = Hq // Hkv
+    if scale is None:
+        scale = D ** -0.5
+    threads = max(1, min(int(threads), N))
+    cuts = np.linspace(0, N, threads + 1).astype(int)
+    qg = np.asarray(q, np.float32).reshape(B, Hkv, G, D) * np.float32(scale)
+
+    def deq(p, s, b, lo, hi):
+        codes = affine.unpack(p[:, :, lo:hi], bits).astype(np.float32)
+        out = codes * np.repeat(np.asarray(s[:, :, lo:hi], np.float32), group_size, axis=-1)
+        if b is not None:
+            out += np.repeat(np.asarray(b[:, :, lo:hi], np.float32), group_size, axis=-1)
+        return out
+
+    def part(i):
+        lo, hi = cuts[i], cuts[i + 1]
+        k = deq(k_packed, k_scales, k_biases, lo, hi)
+        v = deq(v_packed, v_scales, v_biases, lo, hi)
+        s = np.matmul(qg, np.swapaxes(k, -1, -2))                  # [B,Hkv,G,n]
+        m = s.max(axis=-1, keepdims=True)
+        np.exp(s - m, out=s)
+        return m, s.sum(axis=-1, keepdims=True), np.matmul(s, v)
+
+    with threadpool_limits(limits=1), ThreadPoolExecutor(max_workers=threads) as ex:
+        parts = list(ex.map(part, range(threads)))
+    M = np.max(np.stack([p[0] for p in parts]), axis=0)
+    num = sum(np.exp(p[0] - M) * p[2] for p in parts)
+    den = sum(np.exp(p[0] - M) * p[1] for p in parts)
+    return (num / den).reshape(B, Hq, 1, D)

@@ -498,3 +498,43 @@ def test_plan_grows_in_place_with_appends(device):
         assert_close(got, oracle_out(inp, mask=add), f"n={n + 1}")
     with pytest.raises(ValueError):
         plan.set_keys(cap + 1)
+
+
+def test_decode_argument_cache(device):
+    """kernels.decode re-launches a cached argument block for a repeated
+    tensor geometry (key count free): every cached call, over a growing key
+    count, with kv_start and on a second stream, equals the uncached call
+    bit for bit and the oracle to tolerance."""
+    rng = np.random.default_rng(61)
+    B, Hq, Hkv, D, bits, gs, cap = 2, 16, 2, 128, 4, 64, 3000
+    inp = make_inputs(rng, B, Hq, Hkv, cap, D, bits, gs)
+    g = to_dev(inp, device)
+    ks = torch.tensor([0, 37], dtype=torch.int32, device=device)
+    side = torch.cuda.Stream(device)
+
+    def call(n, kv_start, cached):
+        if not cached:
+            kernels._ARGS.d = {}
+        v = [g[k][:, :, :n] for k in ("kp", "vp", "ks", "vs", "kb", "vb")]
+        return kernels.decode(g["q"], *v, scale=D ** -0.5, bits=bits, group_size=gs, kv_start=kv_start)
+
+    for kv_start in (None, ks):
+        for n in (100, 2047, 2048, 3000, 64, 1):
+            print(f"argument cache n={n} kv_start={kv_start is not None}", flush=True)
+            want = call(n, kv_start, cached=False)
+            got = call(n, kv_start, cached=True)       # hit (cached by the call above)
+            nxt = call(min(n + 1, cap), kv_start, cached=True)  # hit with another key count
+            with torch.cuda.stream(side):
+                other = call(n, kv_start, cached=True)  # a new entry for the other stream
+            torch.cuda.synchronize()
+            assert torch.equal(got, want), f"n={n}: cached call differs"
+            assert torch.equal(other, want), f"n={n}: other stream differs"
+            sub = {k: (None if inp[k] is None else inp[k][:, :, :min(n + 1, cap)]) for k in inp
+                   if k in ("kp", "vp", "ks", "vs", "kb", "vb")}
+            ref_in = dict(inp, **sub)
+            mask = None
+            if kv_start is not None:
+                mask = np.arange(min(n + 1, cap))[None, None, None, :] >= np.array([0, 37])[:, None, None, None]
+                if min(n + 1, cap) <= 37:
+                    continue  # sequence 1 has no keys: its row is all-masked
+            assert_close(to_np(nxt), oracle_out(ref_in, mask=mask), f"n={n + 1} cached")

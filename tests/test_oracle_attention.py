@@ -176,3 +176,20 @@ def test_decode_fp32_close_to_reference(rng):
                                              dtype="f16")
     f32 = attention.decode_fp32(q, kp, vp, ks, vs, kb, vb, bits=4, group_size=gs)
     np.testing.assert_allclose(f32, ref, atol=2e-3)
+
+
+@pytest.mark.parametrize("threads", [1, 3, 8])
+def test_decode_fp32_threads_equals_single_thread(rng, threads):
+    """The key-range split + log-sum-exp merge of the multi-core CPU
+    baseline gives the single-pass float32 result (to float32 rounding),
+    including a range whose keys all score far below another's."""
+    B, Hq, Hkv, N, D, gs = 2, 8, 2, 301, 64, 32
+    q = affine.random_T(rng, (B, Hq, 1, D), "f16")
+    k = affine.random_T(rng, (B, Hkv, N, D), "f16")
+    k[:, :, 200:] *= 6.0  # the last range dominates the softmax
+    v = affine.random_T(rng, (B, Hkv, N, D), "f16")
+    kp, ks, kb = affine.quantize(k, gs, 4, "f16")
+    vp, vs, vb = affine.quantize(v, gs, 4, "f16")
+    one = attention.decode_fp32(q, kp, vp, ks, vs, kb, vb, bits=4, group_size=gs)
+    par = attention.decode_fp32_threads(q, kp, vp, ks, vs, kb, vb, bits=4, group_size=gs, threads=threads)
+    np.testing.assert_allclose(par, one, rtol=2e-5, atol=2e-6)
