@@ -1,0 +1,535 @@
+// Quantized attention for many query positions (prefill, chunked and
+// speculative decoding) on the gfx950 matrix cores.
+//
+// Reference: the reference sends every qL > 1 call through dequantize +
+// mx.fast.scaled_dot_product_attention (mlx_qsdpa/dispatch.py:68-83); the
+// decode kernel (decode_mfma.hip) takes such calls in blocks of 16 query rows,
+// each of which loads and dequantizes the kv head's whole K / V again.  Here
+// one workgroup takes 128 rows of a kv head -- 8 waves x 16 rows -- and every
+// 64-token K / V tile is loaded once per workgroup, dequantized once into
+// LDS, and read from LDS by all eight waves:
+//
+//   loads      the raw codes, scales and biases of tile j + 2 are in flight
+//              (two register sets) while tile j is computed;
+//   dequant    every thread turns its piece of tile j + 1 into T values
+//              (T(fma(scale, code, bias)), as mx.dequantize rounds them) in
+//              the LDS buffer the waves do not read during tile j: K
+//              row-major (token, dims), V transposed (dim, tokens) with the
+//              tokens of each 32-token half in the order of the S^T
+//              fragment, so that the P^T operand is a lane's own softmax
+//              values;
+//   compute    per wave and tile, S^T = K Q^T (A = K rows from LDS, B = Q^T
+//              in registers: 4 token blocks x D/32 steps of
+//              v_mfma_f32_16x16x32 per 16-row block), the online softmax of the decode kernel
+//              (log2 domain, rescale when the maximum grows by more than 8),
+//              then out^T += V^T P^T (A = V^T rows from LDS; bfloat16 splits
+//              P into hi + lo terms);
+//   barrier    one per tile: it orders this tile's reads before the next
+//              tile's writes of the same buffer.
+//
+// Rows of a kv head are (position v / G, head v % G) as in the decode
+// kernel; a causal mask (aligned to the last key), kv_start (keys before it
+// are skipped) and a bool / additive mask are applied per score.  The grid
+// maps the row groups of one (batch, kv head) to one XCD, so its K / V is
+// fetched into one L2.
+#include <type_traits>
+
+#include "mfma_common.h"
+
+namespace qsdpa {
+namespace {
+
+// Workgroup shape: 8 waves x 16 rows (about 190 registers, two waves per
+// SIMD).  Measured at the C5 chunk (B=4, H_q=16, H_kv=4, N=4096, q_len=512,
+// bf16 8-bit): 144 us; 4 waves x 32 rows (one wave per SIMD, 380
+// registers) 171-174 us; 4 waves x 16 rows (64-row groups, two per CU)
+// 172 us.  The build can override both for such comparisons.
+#ifndef QSDPA_PF_WAVES
+#define QSDPA_PF_WAVES 8
+#endif
+#ifndef QSDPA_PF_RB
+#define QSDPA_PF_RB 1
+#endif
+constexpr int kPWaves = QSDPA_PF_WAVES;  // waves per workgroup
+constexpr int kPThreads = kPWaves * 64;
+constexpr int kPTile = 64;               // tokens per tile
+constexpr int kRB = QSDPA_PF_RB;         // 16-row blocks per wave
+constexpr int kPRows = 16 * kRB;         // query rows per wave
+constexpr int kPGroupRows = kPWaves * kPRows;
+constexpr int kVPitch = kPTile * 2 + 16;  // bytes per V^T row (dim) in LDS
+
+template <int D>
+struct PGeo {
+  static constexpr int KPitch = D * 2 + 16;        // bytes per K row (token) in LDS
+  static constexpr int KBytes = kPTile * KPitch;
+  static constexpr int VBytes = D * kVPitch;
+  static constexpr int BufBytes = KBytes + VBytes;
+  static constexpr int NM = D / 32;                // QK k-steps
+  static constexpr int NB = D / 16;                // PV dim blocks
+};
+
+// Column of token t (0..63) of a tile in the V^T rows: within each 32-token
+// half, the slot order of the S^T fragment (lane quad q holds tokens
+// 16 * (j >> 2) + 4 q + (j & 3), j = 0..7, as its k slots 8 q + j).
+__device__ __forceinline__ int vcol(int t) {
+  const int u = t >> 5, tt = t & 31;
+  return 32 * u + 8 * ((tt >> 2) & 3) + 4 * (tt >> 4) + (tt & 3);
+}
+
+// Element pair i of a dequantized 8-dim slice (dequant_k's output): the two
+// dims it holds (float16 4-bit: i and i + 4; otherwise 2i and 2i + 1).
+template <typename Tag, int BITS>
+__device__ __forceinline__ int pair_dim(int i, int half) {
+  if constexpr (Tag::kId == QSDPA_F16 && BITS == 4) return i + 4 * half;
+  else return 2 * i + half;
+}
+
+// The workgroup's threads split a tile: K token tid / KPT, dims
+// [c D / KPT, (c + 1) D / KPT) with c = tid % KPT; V tokens 2 (tid % 32) + e
+// (e = 0, 1), dims [cv D / VPT, (cv + 1) D / VPT) with cv = tid / 32.
+constexpr int kKPT = kPThreads / kPTile;
+constexpr int kVPT = kPThreads / (kPTile / 2);
+
+template <int W>
+__device__ __forceinline__ void load_words(rsrc_t rs, uint32_t off, uint32_t* w) {
+  typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+  if constexpr (W % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < W / 4; ++i) {
+      const u4 x = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16 * i, 0, 0);
+      w[4 * i] = x[0]; w[4 * i + 1] = x[1]; w[4 * i + 2] = x[2]; w[4 * i + 3] = x[3];
+    }
+  } else if constexpr (W == 2) {
+    const u2 x = __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0);
+    w[0] = x[0]; w[1] = x[1];
+  } else {
+    static_assert(W == 1, "piece size");
+    w[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0);
+  }
+}
+
+// Raw registers of one tile for one thread (the split above).
+template <int D, int BITS>
+struct PRaw {
+  static constexpr int KW = D / kKPT * BITS / 32;
+  static constexpr int VW = D / kVPT * BITS / 32;
+  uint32_t k[KW];
+  uint32_t ks, kb;      // the K quarter's scale / bias half-words (two groups: both)
+  uint32_t v[2][VW];
+  uint32_t vs[2], vb[2];
+};
+
+template <typename Tag, int D, int BITS, int GS>
+struct Prefill {
+  using PG = PGeo<D>;
+  using Raw = PRaw<D, BITS>;
+  static constexpr int kQD = D / kKPT;                    // K dims per thread
+  static constexpr int kKG = kQD > GS ? kQD / GS : 1;     // groups per K quarter (1 or 2)
+  static constexpr int kVD = D / kVPT;                    // V dims per thread and token
+  static_assert(kKG <= 2, "groups per K quarter");
+  static_assert(kVD <= GS, "a V piece lies in one group");
+
+  struct Src {
+    rsrc_t k, v, ks, vs, kb, vb;
+    uint32_t k_sn, v_sn, ks_sn, vs_sn, kb_sn, vb_sn;  // bytes per token
+  };
+
+  // Issue the loads of the tile whose first token is `rel0` tokens past the
+  // sequence's first key (rows past the end read as zero).
+  static __device__ __forceinline__ void load(Raw& R, const Src& s, int rel0, int tid) {
+    const uint32_t kt = static_cast<uint32_t>(rel0 + tid / kKPT);
+    const int c = tid % kKPT;
+    load_words<Raw::KW>(s.k, kt * s.k_sn + static_cast<uint32_t>(c * Raw::KW * 4), R.k);
+    const uint32_t g0 = static_cast<uint32_t>(c * kQD / GS);
+    if constexpr (kKG == 2) {
+      R.ks = __builtin_amdgcn_raw_buffer_load_b32(s.ks, kt * s.ks_sn + g0 * 2, 0, 0);
+      R.kb = __builtin_amdgcn_raw_buffer_load_b32(s.kb, kt * s.kb_sn + g0 * 2, 0, 0);
+    } else {
+      R.ks = __builtin_amdgcn_raw_buffer_load_b16(s.ks, kt * s.ks_sn + g0 * 2, 0, 0);
+      R.kb = __builtin_amdgcn_raw_buffer_load_b16(s.kb, kt * s.kb_sn + g0 * 2, 0, 0);
+    }
+    const int pr = tid & 31, cv = tid >> 5;
+    const uint32_t gv = static_cast<uint32_t>(cv * kVD / GS);
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const uint32_t vt = static_cast<uint32_t>(rel0 + 2 * pr + e);
+      load_words<Raw::VW>(s.v, vt * s.v_sn + static_cast<uint32_t>(cv * Raw::VW * 4), R.v[e]);
+      R.vs[e] = __builtin_amdgcn_raw_buffer_load_b16(s.vs, vt * s.vs_sn + gv * 2, 0, 0);
+      R.vb[e] = __builtin_amdgcn_raw_buffer_load_b16(s.vb, vt * s.vb_sn + gv * 2, 0, 0);
+    }
+  }
+
+  // Dequantize the thread's piece of a tile into the LDS buffer `buf`.
+  static __device__ __forceinline__ void stage(const Raw& R, uint8_t* buf, int tid) {
+    // K: token tid / KPT, dims [c D/KPT, (c + 1) D/KPT), row-major.
+    {
+      const int t = tid / kKPT, c = tid % kKPT;
+      uint8_t* dst = buf + t * PG::KPitch + c * kQD * 2;
+#pragma unroll
+      for (int s = 0; s < kQD / 8; ++s) {
+        const int g = kKG == 2 ? (8 * s) / GS : 0;
+        const uint32_t sw = g ? (R.ks >> 16) : R.ks;
+        const uint32_t bw = g ? (R.kb >> 16) : R.kb;
+        uint32_t a[4];
+        dequant_k<Tag, BITS>(R.k + s * (BITS / 4), splat_lo(sw), splat_lo(bw), to_f32<Tag>(static_cast<uint16_t>(sw)),
+                             to_f32<Tag>(static_cast<uint16_t>(bw)), a);
+        *reinterpret_cast<u4*>(dst + s * 16) = u4{a[0], a[1], a[2], a[3]};
+      }
+    }
+    // V: tokens 2 pr, 2 pr + 1, dims [cv D/VPT, (cv + 1) D/VPT), transposed.
+    {
+      const int pr = tid & 31, cv = tid >> 5;
+      uint8_t* vt = buf + PG::KBytes + vcol(2 * pr) * 2;
+      uint32_t a[2][4];
+#pragma unroll
+      for (int s = 0; s < kVD / 8; ++s) {
+#pragma unroll
+        for (int e = 0; e < 2; ++e)
+          dequant_k<Tag, BITS>(R.v[e] + s * (BITS / 4), splat_lo(R.vs[e]), splat_lo(R.vb[e]),
+                               to_f32<Tag>(static_cast<uint16_t>(R.vs[e])),
+                               to_f32<Tag>(static_cast<uint16_t>(R.vb[e])), a[e]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int d0 = cv * kVD + 8 * s;
+          *reinterpret_cast<uint32_t*>(vt + (d0 + pair_dim<Tag, BITS>(i, 0)) * kVPitch) =
+              perm(a[1][i], a[0][i], 0x05040100u);
+          *reinterpret_cast<uint32_t*>(vt + (d0 + pair_dim<Tag, BITS>(i, 1)) * kVPitch) =
+              perm(a[1][i], a[0][i], 0x07060302u);
+        }
+      }
+    }
+  }
+};
+
+// Parameters beyond the decode's: none; the same MfmaParams (q_len > 1).
+template <typename Tag, int D, int BITS, int GS>
+__global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(MfmaParams p, int groups_per_head) {
+  using PG = PGeo<D>;
+  using P = Prefill<Tag, D, BITS, GS>;
+  __shared__ __attribute__((aligned(16))) uint8_t s_buf[2 * PG::BufBytes];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int quad = lane >> 4;
+  const int r = lane & 15;
+
+  // XCD-aware work order: workgroups are dispatched to the 8 XCDs round
+  // robin, so the work of workgroup id w goes to XCD w % 8 in consecutive
+  // runs: the row groups of one (batch, kv head) share one XCD's L2.
+  const int total = gridDim.x;
+  int w = blockIdx.x;
+  if (total % 8 == 0) w = (w % 8) * (total / 8) + w / 8;
+  const int grp = w % groups_per_head;
+  const int kvh = (w / groups_per_head) % p.Hkv;
+  const int b = w / (groups_per_head * p.Hkv);
+
+  const int rows = p.G * p.qL;
+  const int v_first = grp * kPGroupRows;
+  const int nrows = min(kPGroupRows, rows - v_first);    // real rows of the group
+  // Keys: [s0, n_end) of this sequence; causal: the group's last position's limit.
+  const int s0 = p.kv_start ? min(max(p.kv_start[b], 0), p.N) : 0;
+  const int n_end = p.causal ? min(p.N, max(0, p.N - p.qL + (v_first + nrows - 1) / p.G + 1)) : p.N;
+  const int len = max(n_end - s0, 0);
+  const int T = (len + kPTile - 1) / kPTile;
+
+  // The wave's rows: block rb, lane row r -> v = v_first + 32 wave + 16 rb + r.
+  int n_lane[kRB], n_wave[kRB];  // a lane's key limit; the wave's smallest
+  int64_t mrow[kRB];
+  uint32_t qt[kRB][PG::NM][4];
+  {
+    const uint8_t* q0 = reinterpret_cast<const uint8_t*>(p.q) +
+                        (static_cast<int64_t>(b) * p.q_sb + static_cast<int64_t>(kvh) * p.G * p.q_sh) * 2;
+    const rsrc_t rq = make_rsrc(
+        q0, static_cast<uint32_t>(((p.G - 1) * p.q_sh + static_cast<int64_t>(p.qL - 1) * p.q_sq) * 2 + D * 2));
+#pragma unroll
+    for (int rb = 0; rb < kRB; ++rb) {
+      const int v = v_first + min(kPRows * wave + 16 * rb + r, nrows - 1);
+      const int hq = kvh * p.G + v % p.G, iq = v / p.G;
+      n_lane[rb] = p.causal ? min(n_end, max(0, p.N - p.qL + iq + 1)) : n_end;
+      mrow[rb] = static_cast<int64_t>(b) * p.m_sb + static_cast<int64_t>(hq) * p.m_sh +
+                 static_cast<int64_t>(iq) * p.m_sq;
+      const uint32_t off = static_cast<uint32_t>((static_cast<int64_t>(v % p.G) * p.q_sh +
+                                                  static_cast<int64_t>(iq) * p.q_sq) * 2);
+#pragma unroll
+      for (int m = 0; m < PG::NM; ++m) {
+        const u4 x = __builtin_amdgcn_raw_buffer_load_b128(rq, off + (32 * m + 8 * quad) * 2, 0, 0);
+        uint32_t d0 = x[0], d1 = x[1], d2 = x[2], d3 = x[3];
+        if constexpr (Tag::kId == QSDPA_F16 && BITS == 4) {  // the K slice order: dims 0, 4, 1, 5, ...
+          qt[rb][m][0] = perm(d2, d0, 0x05040100u);
+          qt[rb][m][1] = perm(d2, d0, 0x07060302u);
+          qt[rb][m][2] = perm(d3, d1, 0x05040100u);
+          qt[rb][m][3] = perm(d3, d1, 0x07060302u);
+        } else {
+          qt[rb][m][0] = d0; qt[rb][m][1] = d1; qt[rb][m][2] = d2; qt[rb][m][3] = d3;
+        }
+      }
+    }
+  }
+
+#pragma unroll
+  for (int rb = 0; rb < kRB; ++rb) {
+    int m = n_lane[rb];
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) m = min(m, __shfl_xor(m, o));
+    n_wave[rb] = __builtin_amdgcn_readfirstlane(m);
+  }
+
+  // K / V descriptors over rows [s0, N) of this (batch, kv head).
+  typename P::Src src;
+  {
+    const int64_t tok0 = s0;
+    const int avail = p.N - s0;
+    auto rsrc = [&](const void* base, int64_t sb, int64_t sh, int64_t sn, int esz, int row_bytes, bool present) {
+      const uint8_t* p0 = static_cast<const uint8_t*>(base) +
+                          (static_cast<int64_t>(b) * sb + static_cast<int64_t>(kvh) * sh + tok0 * sn) * esz;
+      const uint32_t bytes =
+          (present && avail > 0) ? static_cast<uint32_t>((avail - 1) * sn * esz + row_bytes) : 0u;
+      return make_rsrc(p0, bytes);
+    };
+    constexpr int kRow = D * BITS / 8, kMeta = D / GS * 2;
+    src.k = rsrc(p.kp, p.kp_sb, p.kp_sh, p.kp_sn, 4, kRow, true);
+    src.v = rsrc(p.vp, p.vp_sb, p.vp_sh, p.vp_sn, 4, kRow, true);
+    src.ks = rsrc(p.ks, p.ks_sb, p.ks_sh, p.ks_sn, 2, kMeta, true);
+    src.vs = rsrc(p.vs, p.vs_sb, p.vs_sh, p.vs_sn, 2, kMeta, true);
+    src.kb = rsrc(p.has_bias ? p.kb : p.ks, p.kb_sb, p.kb_sh, p.kb_sn, 2, kMeta, p.has_bias);
+    src.vb = rsrc(p.has_bias ? p.vb : p.vs, p.vb_sb, p.vb_sh, p.vb_sn, 2, kMeta, p.has_bias);
+    src.k_sn = static_cast<uint32_t>(p.kp_sn * 4);
+    src.v_sn = static_cast<uint32_t>(p.vp_sn * 4);
+    src.ks_sn = static_cast<uint32_t>(p.ks_sn * 2);
+    src.vs_sn = static_cast<uint32_t>(p.vs_sn * 2);
+    src.kb_sn = static_cast<uint32_t>(p.kb_sn * 2);
+    src.vb_sn = static_cast<uint32_t>(p.vb_sn * 2);
+  }
+
+  f4 acc[kRB][PG::NB];
+  float mrun[kRB], lrun[kRB];
+#pragma unroll
+  for (int rb = 0; rb < kRB; ++rb) {
+#pragma unroll
+    for (int i = 0; i < PG::NB; ++i) acc[rb][i] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    mrun[rb] = kNegBig;
+    lrun[rb] = 0.0f;
+  }
+
+  // One tile from LDS buffer `buf`, first key s0 + tb0.
+  auto compute = [&](const uint8_t* buf, int tb0) {
+    const uint8_t* kb = buf;
+    const uint8_t* vt = buf + PG::KBytes;
+    // ---- S^T = K Q^T: 4 token blocks x kRB row blocks ----
+    // Steps outer, token blocks inner: consecutive MFMAs feed 4 kRB
+    // independent accumulators instead of waiting on each other's results.
+    f4 S[4][kRB];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int rb = 0; rb < kRB; ++rb) S[t][rb] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int m = 0; m < PG::NM; ++m)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const u4 x = *reinterpret_cast<const u4*>(kb + (16 * t + r) * PG::KPitch + (32 * m + 8 * quad) * 2);
+        const uint32_t a[4] = {x[0], x[1], x[2], x[3]};
+#pragma unroll
+        for (int rb = 0; rb < kRB; ++rb) S[t][rb] = mfma<Tag>(a, qt[rb][m], S[t][rb]);
+      }
+    // ---- scores: lane (quad, r) holds tokens 16 t + 4 quad + i of row r ----
+    const int tb = s0 + tb0;
+    uint32_t pb[2][kRB][4], pl[2][kRB][4];  // [half u][row block][pair]
+#pragma unroll
+    for (int rb = 0; rb < kRB; ++rb) {
+      float sc[16];
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sc[4 * t + i] = S[t][rb][i] * p.qscale;
+      if (p.mask) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int key = min(tb + 16 * t + 4 * quad + i, p.N - 1);
+            sc[4 * t + i] += mask_value(p, mrow[rb] + static_cast<int64_t>(key) * p.m_sn);
+          }
+      }
+      if (tb + kPTile > n_wave[rb]) {  // keys past a row's limit (causal, or the sequence's end)
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (tb + 16 * t + 4 * quad + i >= n_lane[rb]) sc[4 * t + i] = -__builtin_huge_valf();
+      }
+      float tmax = sc[0];
+#pragma unroll
+      for (int e = 1; e < 16; ++e) tmax = fmaxf(tmax, sc[e]);
+      tmax = fmaxf(tmax, shfl_xor_f32(tmax, 16));
+      tmax = fmaxf(tmax, shfl_xor_f32(tmax, 32));
+      const bool grow = tmax > mrun[rb] + kRescale;
+      if (__builtin_amdgcn_ballot_w64(grow)) {
+        const float mnew = grow ? tmax : mrun[rb];
+        const float f = fast_exp2(mrun[rb] - mnew);
+        mrun[rb] = mnew;
+        lrun[rb] *= f;
+#pragma unroll
+        for (int i = 0; i < PG::NB; ++i) acc[rb][i] *= f;
+      }
+      float pr[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) pr[e] = fast_exp2(sc[e] - mrun[rb]);
+      float sum = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sum += pr[e];
+      lrun[rb] += sum;
+      // P^T of half u: k slots 2i, 2i + 1 = tokens tau(quad, 2i), tau(quad, 2i + 1):
+      // blocks 2u (i = 0, 1) and 2u + 1 (i = 2, 3).
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float x0 = pr[4 * (2 * u + (i >> 1)) + 2 * (i & 1)];
+          const float x1 = pr[4 * (2 * u + (i >> 1)) + 2 * (i & 1) + 1];
+          pb[u][rb][i] = pack_T2<Tag>(x0, x1);
+          if constexpr (Tag::kId == QSDPA_BF16)
+            pl[u][rb][i] = pack_T2<Tag>(x0 - unpack_T2_lo<Tag>(pb[u][rb][i]), x1 - unpack_T2_hi<Tag>(pb[u][rb][i]));
+        }
+    }
+    // ---- out^T += V^T P^T: the half's V^T operands held, then the hi terms
+    // of all dim blocks, then (bfloat16) the lo terms, so no MFMA waits on
+    // the one before it ----
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      uint32_t a[PG::NB][4];
+#pragma unroll
+      for (int db = 0; db < PG::NB; ++db) {
+        const u4 x = *reinterpret_cast<const u4*>(vt + (16 * db + r) * kVPitch + (32 * u + 8 * quad) * 2);
+        a[db][0] = x[0]; a[db][1] = x[1]; a[db][2] = x[2]; a[db][3] = x[3];
+      }
+#pragma unroll
+      for (int db = 0; db < PG::NB; ++db)
+#pragma unroll
+        for (int rb = 0; rb < kRB; ++rb) acc[rb][db] = mfma<Tag>(a[db], pb[u][rb], acc[rb][db]);
+      if constexpr (Tag::kId == QSDPA_BF16) {
+#pragma unroll
+        for (int db = 0; db < PG::NB; ++db)
+#pragma unroll
+          for (int rb = 0; rb < kRB; ++rb) acc[rb][db] = mfma<Tag>(a[db], pl[u][rb], acc[rb][db]);
+      }
+    }
+  };
+
+  // ---- the tile pipeline: loads two tiles ahead, one barrier per tile ----
+  typename P::Raw R0, R1;
+  uint8_t* buf0 = s_buf;
+  uint8_t* buf1 = s_buf + PG::BufBytes;
+  const int oob = len + 2 * kPTile;  // rows past every descriptor: the loads read zero
+  auto row_of = [&](int j) { return j < T ? j * kPTile : oob; };
+  if (T > 0) {
+    P::load(R0, src, row_of(0), tid);
+    P::load(R1, src, row_of(1), tid);
+    P::stage(R0, buf0, tid);
+    P::load(R0, src, row_of(2), tid);
+    __syncthreads();
+    for (int j = 0; j < T; j += 2) {
+      // tile j in buf0; R1 holds tile j + 1, R0 tile j + 2.
+      if (j + 1 < T) {
+        P::stage(R1, buf1, tid);
+        P::load(R1, src, row_of(j + 3), tid);
+      }
+      compute(buf0, j * kPTile);
+      __syncthreads();
+      if (j + 1 >= T) break;
+      // tile j + 1 in buf1; R0 holds tile j + 2, R1 tile j + 3.
+      if (j + 2 < T) {
+        P::stage(R0, buf0, tid);
+        P::load(R0, src, row_of(j + 4), tid);
+      }
+      compute(buf1, (j + 1) * kPTile);
+      __syncthreads();
+    }
+  }
+
+  // ---- normalise and store: lane (quad, r) holds dims 16 db + 4 quad + i of row r ----
+#pragma unroll
+  for (int rb = 0; rb < kRB; ++rb) {
+    float l = lrun[rb];
+    l += shfl_xor_f32(l, 16);
+    l += shfl_xor_f32(l, 32);
+    const int vr = kPRows * wave + 16 * rb + r;
+    if (vr >= nrows) continue;
+    const int v = v_first + vr;
+    const int hq = kvh * p.G + v % p.G, iq = v / p.G;
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    uint16_t* dst = p.out + static_cast<int64_t>(b) * p.o_sb + static_cast<int64_t>(hq) * p.o_sh +
+                    static_cast<int64_t>(iq) * p.o_sq + 4 * quad;
+#pragma unroll
+    for (int db = 0; db < PG::NB; ++db) {
+      const uint32_t lo = pack_T2<Tag>(acc[rb][db][0] * inv, acc[rb][db][1] * inv);
+      const uint32_t hi = pack_T2<Tag>(acc[rb][db][2] * inv, acc[rb][db][3] * inv);
+      uint16_t* o = dst + 16 * db;
+      o[0] = static_cast<uint16_t>(lo);
+      o[1] = static_cast<uint16_t>(lo >> 16);
+      o[2] = static_cast<uint16_t>(hi);
+      o[3] = static_cast<uint16_t>(hi >> 16);
+    }
+  }
+}
+
+template <typename Tag, int D, int BITS>
+void launch_prefill_gs(const MfmaParams& p, int gs, int groups, hipStream_t stream, const qsdpa_decode_args* a) {
+  const dim3 grid(groups * p.Hkv * p.B);
+  void (*k)(MfmaParams, int) = gs == 32 ? prefill_mfma_kernel<Tag, D, BITS, 32>
+                               : gs == 64 ? prefill_mfma_kernel<Tag, D, BITS, 64>
+                                          : prefill_mfma_kernel<Tag, D, BITS, 128>;
+  if (a->prof_begin || a->prof_end)
+    hipExtLaunchKernelGGL(k, grid, dim3(kPThreads), 0, stream, static_cast<hipEvent_t>(a->prof_begin),
+                          static_cast<hipEvent_t>(a->prof_end), 0, p, groups);
+  else
+    hipLaunchKernelGGL(k, grid, dim3(kPThreads), 0, stream, p, groups);
+}
+
+}  // namespace
+
+bool mfma_supports(const qsdpa_decode_args* a);
+
+// The prefill kernel takes q_len > 1 calls on the MFMA path's layouts whose
+// kv heads have at least 64 query rows and that fill at least a quarter of
+// the GPU with 128-row groups; others stay on the decode kernel's split-K
+// blocks.  K / V rows are read in 16-byte pieces (8-byte V pieces at D = 128,
+// 4-bit), so the packed views must be 16-byte aligned.
+bool prefill_supports(const qsdpa_decode_args* a, int cus) {
+  // D = 256 would need more than the 512 registers of a wave (its
+  // accumulators and Q rows double): those calls keep the decode kernel.
+  if (a->q_len <= 1 || a->D != 128 || !mfma_supports(a)) return false;
+  const int64_t rows = static_cast<int64_t>(a->H_q / a->H_kv) * a->q_len;
+  if (rows < 64) return false;
+  const int64_t groups = (rows + kPGroupRows - 1) / kPGroupRows;
+  if (groups * a->H_kv * a->B < cus / 4) return false;
+  if (groups * a->H_kv * a->B >= (int64_t(1) << 31)) return false;
+  const int kq_bytes = a->D / 4 * a->bits / 8, vp_bytes = a->D / 8 * a->bits / 8;
+  if (!aligned_view(a->k_packed, std::min(kq_bytes, 16), 4)) return false;
+  if (!aligned_view(a->v_packed, std::min(vp_bytes, 16), 4)) return false;
+  if (a->D / 4 > a->group_size && !aligned_view(a->k_scales, 4, 2)) return false;
+  if (a->D / 4 > a->group_size && a->k_biases.ptr && !aligned_view(a->k_biases, 4, 2)) return false;
+  // Row byte offsets up to 4 tiles past the last key stay within 32 bits.
+  const int64_t max_sn = std::max({a->k_packed.stride_n * 4, a->v_packed.stride_n * 4, a->k_scales.stride_n * 2,
+                                   a->v_scales.stride_n * 2, a->k_biases.stride_n * 2, a->v_biases.stride_n * 2});
+  if (max_sn < 0 || max_sn * (static_cast<int64_t>(a->N) + 4 * kPTile) >= (int64_t(1) << 31)) return false;
+  return true;
+}
+
+int launch_prefill_mfma(const qsdpa_decode_args* a, hipStream_t stream) {
+  MfmaParams p = mfma_params(a, 1, nullptr, nullptr);
+  const int groups = (p.G * p.qL + kPGroupRows - 1) / kPGroupRows;
+  const bool f16 = a->dtype == QSDPA_F16;
+  auto bits = [&](auto tag, auto dim) {
+    using Tag = decltype(tag);
+    constexpr int D = decltype(dim)::value;
+    if (a->bits == 4) launch_prefill_gs<Tag, D, 4>(p, a->group_size, groups, stream, a);
+    else launch_prefill_gs<Tag, D, 8>(p, a->group_size, groups, stream, a);
+  };
+  if (f16) bits(F16{}, std::integral_constant<int, 128>{});
+  else bits(BF16{}, std::integral_constant<int, 128>{});
+  return check_launch("prefill_mfma");
+}
+
+}  // namespace qsdpa

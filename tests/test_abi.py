@@ -128,3 +128,33 @@ def test_invalid_arguments_return_codes():
     assert lib.qsdpa_decode(ctypes.byref(a), None) == _lib.QSDPA_ERR_INVALID  # null pointers
     with pytest.raises(_lib.QsdpaError):
         _lib.check(lib.qsdpa_decode(ctypes.byref(a), None))
+
+
+def test_prefill_routing_rule():
+    """Calls with many query rows per kv head (and enough 128-row groups to
+    fill a quarter of 256 CUs) run the one-pass prefill kernel: no split-K
+    workspace.  Smaller multi-query calls keep the split-K decode kernel.
+    (Planning only validates arguments; nothing is launched or read.)"""
+    lib = _lib.load()
+
+    def plan(B, Hq, Hkv, N, D, L, bits=8, gs=128):
+        a = _lib.DecodeArgs()
+        a.B, a.H_q, a.H_kv, a.N, a.D = B, Hq, Hkv, N, D
+        a.bits, a.group_size, a.dtype, a.scale = bits, gs, _lib.QSDPA_BF16, 0.1
+        a.q_len, a.causal = L, 1
+        W, G = D * bits // 32, D // gs
+        base = 1 << 20  # 16-byte aligned stand-in addresses (never dereferenced)
+        a.q = _lib.View(base, Hq * L * D, L * D, D)
+        a.out = _lib.View(base, Hq * L * D, L * D, D)
+        a.k_packed = a.v_packed = _lib.View(base, Hkv * N * W, N * W, W)
+        a.k_scales = a.v_scales = a.k_biases = a.v_biases = _lib.View(base, Hkv * N * G, N * G, G)
+        n = ctypes.c_int32(0)
+        ws = lib.qsdpa_decode_workspace_size(ctypes.byref(a), ctypes.byref(n))
+        assert ws >= 0, lib.qsdpa_last_error()
+        return n.value, ws
+
+    assert plan(4, 16, 4, 4096, 128, 512) == (1, 0)       # the C5 chunk: prefill kernel
+    splits, ws = plan(1, 16, 4, 4096, 128, 8)              # 32 rows per kv head: decode kernel
+    assert splits > 1 and ws > 0
+    splits, ws = plan(1, 16, 4, 4096, 256, 512)             # D = 256: decode kernel
+    assert splits >= 1 and (splits == 1 or ws > 0)

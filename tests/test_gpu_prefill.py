@@ -1,0 +1,113 @@
+"""The prefill kernel (many query positions per kv head, D = 128) against the
+float64 oracle (tests/torch_oracle.py, pinned to the numpy oracle by
+tests/test_gpu_parity_full.py).
+
+Shapes are chosen so the library routes them to the prefill kernel: at
+least 64 query rows per kv head (H_q / H_kv x q_len) and at least 64
+128-row groups in the grid.  Covered: both dtypes, 4- and 8-bit codes, all
+group sizes, the symmetric format, causal and full attention, kv_start
+(left padding), bool and additive masks, a partial last row group, a
+partial last key tile, keys that start inside a tile, and the C5 chunk.
+Tolerance: |out - ref| <= 2e-3 + 1e-2 |ref|.
+"""
+
+import pytest
+import torch
+
+import torch_oracle as to
+
+from mlx_qsdpa_amd import kernels
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 2e-3, 1e-2
+
+
+def _inputs(B, Hq, Hkv, N, L, bits, gs, dtype, seed, symmetric=False, D=128):
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    dev = torch.device("cuda:0")
+    q = torch.randn(B, Hq, L, D, generator=g).to(dtype).to(dev)
+    kw = torch.randn(B, Hkv, N, D, generator=g)
+    kw[..., :3] *= 6.0  # a few large channels: scores with a spread
+    vw = torch.randn(B, Hkv, N, D, generator=g)
+    kq = kernels.quantize(kw.to(dtype).to(dev), gs, bits)
+    vq = kernels.quantize(vw.to(dtype).to(dev), gs, bits)
+    if symmetric:
+        kq, vq = (kq[0], kq[1], None), (vq[0], vq[1], None)
+    return q, kq, vq
+
+
+def _check(q, kq, vq, bits, gs, ctx, mask=None, causal=False, kv_start=None):
+    D = q.shape[-1]
+    out = kernels.decode(q, kq[0], vq[0], kq[1], vq[1], kq[2], vq[2], scale=D ** -0.5, bits=bits,
+                         group_size=gs, mask=mask, kv_start=kv_start, causal=causal)
+    ref_mask = mask
+    N, L = kq[0].shape[2], q.shape[2]
+    keep = None
+    if causal:
+        keep = torch.arange(N, device=q.device)[None, :] <= (N - L) + torch.arange(L, device=q.device)[:, None]
+        keep = keep[None, None]
+    if kv_start is not None:
+        ks = torch.arange(N, device=q.device)[None, :] >= kv_start.to(q.device).long()[:, None]
+        ks = ks[:, None, None, :]
+        keep = ks if keep is None else keep & ks
+    if keep is not None:
+        if ref_mask is None:
+            ref_mask = keep
+        elif ref_mask.dtype == torch.bool:
+            ref_mask = ref_mask & keep
+        else:
+            ref_mask = ref_mask.float().masked_fill(~keep, float("-inf"))
+    want = to.quantized_sdpa(q, kq, vq, bits=bits, group_size=gs, scale=D ** -0.5, mask=ref_mask)
+    torch.cuda.synchronize()
+    err = (out.double() - want).abs()
+    bound = ATOL + RTOL * want.abs()
+    bad = err > bound
+    assert not bool(bad.any()), f"{ctx}: {int(bad.sum())} outside tolerance, max err {float(err.max()):.3e}"
+    assert bool(torch.isfinite(out).all()), ctx
+
+
+CASES = [  # (B, Hq, Hkv, N, L, bits, gs, dtype, causal, symmetric)
+    (2, 32, 8, 1000, 256, 4, 64, torch.float16, True, False),
+    (2, 32, 8, 777, 256, 4, 32, torch.float16, True, False),
+    (2, 32, 8, 1024, 200, 8, 128, torch.bfloat16, True, False),   # last row group partial
+    (4, 16, 4, 4096, 512, 8, 128, torch.bfloat16, True, False),   # the C5 chunk
+    (4, 16, 4, 2111, 512, 4, 128, torch.bfloat16, False, False),
+    (2, 32, 8, 700, 256, 8, 32, torch.float16, False, True),
+    (1, 64, 8, 600, 512, 4, 64, torch.bfloat16, True, True),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: "B{}_H{}x{}_N{}_L{}_b{}_g{}_{}_{}{}".format(
+    *c[:7], str(c[7]).split(".")[-1], "causal" if c[8] else "full", "_sym" if c[9] else ""))
+def test_prefill_matches_oracle(device, case):
+    B, Hq, Hkv, N, L, bits, gs, dtype, causal, sym = case
+    print(f"prefill case {case}", flush=True)
+    q, kq, vq = _inputs(B, Hq, Hkv, N, L, bits, gs, dtype, seed=N + L, symmetric=sym)
+    _check(q, kq, vq, bits, gs, f"case {case}", causal=causal)
+
+
+def test_prefill_kv_start_and_masks(device):
+    B, Hq, Hkv, N, L, bits, gs = 2, 32, 8, 900, 256, 4, 64
+    for dtype in (torch.float16, torch.bfloat16):
+        q, kq, vq = _inputs(B, Hq, Hkv, N, L, bits, gs, dtype, seed=11)
+        ks = torch.tensor([37, 300], dtype=torch.int32, device=device)  # starts inside a tile
+        print(f"prefill kv_start {dtype}", flush=True)
+        _check(q, kq, vq, bits, gs, f"kv_start {dtype}", kv_start=ks, causal=True)
+        g = torch.Generator(device="cpu").manual_seed(12)
+        keep = torch.rand(B, 1, L, N, generator=g) < 0.8
+        keep[..., -1] = True  # no all-masked rows
+        print(f"prefill bool mask {dtype}", flush=True)
+        _check(q, kq, vq, bits, gs, f"bool mask {dtype}", mask=keep.to(device), causal=True)
+        add = (torch.randn(1, Hq, L, N, generator=g) * 3).to(dtype).to(device)
+        print(f"prefill additive mask {dtype}", flush=True)
+        _check(q, kq, vq, bits, gs, f"additive mask {dtype}", mask=add)
+
+
+def test_prefill_repeatable(device):
+    """Repeated calls give bit-identical outputs."""
+    q, kq, vq = _inputs(4, 16, 4, 4096, 512, 8, 128, torch.bfloat16, seed=5)
+    outs = [kernels.decode(q, kq[0], vq[0], kq[1], vq[1], kq[2], vq[2], scale=128 ** -0.5, bits=8,
+                           group_size=128, causal=True) for _ in range(3)]
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
