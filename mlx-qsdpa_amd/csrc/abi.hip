@@ -43,8 +43,10 @@ int mfma_num_splits(const qsdpa_decode_args* a, int cus);
 int launch_decode_mfma(const qsdpa_decode_args* a, int num_splits, float* part_acc, float* part_ml,
                        int units, int* sched, hipStream_t stream);
 // Defined in prefill_mfma.hip.
-bool prefill_supports(const qsdpa_decode_args* a, int cus);
-int launch_prefill_mfma(const qsdpa_decode_args* a, hipStream_t stream);
+bool prefill_supports(const qsdpa_decode_args* a);
+int prefill_num_splits(const qsdpa_decode_args* a, int cus);
+int launch_prefill_mfma(const qsdpa_decode_args* a, int splits, float* part_acc, float* part_ml,
+                        hipStream_t stream);
 
 
 namespace {
@@ -130,15 +132,12 @@ int validate_decode(const qsdpa_decode_args* a) {
 // Split count: enough workgroups to cover every CU twice, but never fewer
 // than 64 keys per split, and no more than kMaxSplits.
 int decode_plan(const qsdpa_decode_args* a, int* num_splits, int64_t* workspace_bytes) {
-  // Many query positions per kv head: the prefill kernel, one pass.
-  if (prefill_supports(a, compute_units())) {
-    *num_splits = 1;
-    *workspace_bytes = 0;
-    return QSDPA_OK;
-  }
-  int splits = a->num_splits;
+  // Many query positions per kv head: the prefill kernel, with key splits
+  // where its row groups alone would leave CUs idle.
+  const bool prefill = prefill_supports(a);
+  int splits = prefill ? prefill_num_splits(a, compute_units()) : a->num_splits;
   const bool mfma = mfma_supports(a);
-  if (splits == 0) {
+  if (splits == 0 && !prefill) {
     if (mfma) {
       splits = mfma_num_splits(a, compute_units());
     } else {
@@ -185,11 +184,12 @@ int run_decode(const qsdpa_decode_args* args, int splits, void* workspace, hipSt
     sched = reinterpret_cast<int*>(part_ml + rows * (splits + 1) * 2);
   }
   // (prof_begin / prof_end ride on the main kernel's own dispatch)
-  if (prefill_supports(args, compute_units())) return launch_prefill_mfma(args, s);
+  const bool prefill = prefill_supports(args);
   const bool mfma = mfma_supports(args);
-  const int units = streamk_units(args, splits);
+  const int units = prefill ? 0 : streamk_units(args, splits);
   int rc;
-  if (mfma) rc = launch_decode_mfma(args, splits, part_acc, part_ml, units, sched, s);
+  if (prefill) rc = launch_prefill_mfma(args, splits, part_acc, part_ml, s);
+  else if (mfma) rc = launch_decode_mfma(args, splits, part_acc, part_ml, units, sched, s);
   else rc = launch_decode_valu(args, splits, part_acc, part_ml, s);
   if (rc) return rc;
   // The MFMA kernel stores float16 inputs' partials as normalised float16

@@ -1,12 +1,15 @@
 // Log-sum-exp merge of split-K partials (pass 2 of the two-pass decode).
 //
 // Reference: mlx_qsdpa/kernels.py:342-418 (online merge over blocks at
-// 369-386, zero-sum guard at 408).  Partials here are float32 (the reference
-// stores them in T, dispatch.py:235-239):
-//   part_acc[(b*H_q + h)*splits + s][D]   unnormalised sum of p * v
-//   part_ml [(b*H_q + h)*splits + s][2]   (m, l): running max (log2 domain)
-//                                          and sum of p = exp2(score - m)
-// out[b, h, :] = sum_s acc_s * exp2(m_s - M) / sum_s l_s * exp2(m_s - M),
+// 369-386, zero-sum guard at 408).  The reference stores partials in T
+// (dispatch.py:235-239); here, per row r = (b*H_q + h)*qL + i and split s:
+//   part_acc[r*splits + s][D]   float32 unnormalised sum of p * v, or (the
+//                               MFMA kernels with float16 inputs, HALF) the
+//                               normalised row acc / l as float16, in the
+//                               first half of the same area
+//   part_ml [r*splits + s][2]   (m, l): running max (log2 domain) and sum of
+//                               p = exp2(score - m)
+// out[b, h, i, :] = sum_s acc_s * exp2(m_s - M) / sum_s l_s * exp2(m_s - M),
 // M = max_s m_s, and 0 when every split is empty (l = 0).
 //
 // Launch: grid (B*H_q, D/32), 256 threads = 32 split groups x 8 dim
@@ -129,6 +132,69 @@ __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ pa
   }
 }
 
+// Many rows with few splits each (prefill partials): one thread per (row,
+// 4 dims), the splits in order with the same online rescaling as above,
+// four splits' loads in flight at a time.  Rows numbered as above, no
+// stream-K schedule.
+template <typename Tag, bool HALF>
+__global__ __launch_bounds__(256) void merge_rows_kernel(const float* __restrict__ part_acc,
+                                                         const float* __restrict__ part_ml, int D, int splits,
+                                                         int Hq, int qL, int64_t rows, uint16_t* __restrict__ out,
+                                                         int64_t o_sb, int64_t o_sh, int64_t o_sq) {
+  const int quads = D / 4;
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (idx >= rows * quads) return;
+  const int64_t bh = idx / quads;
+  const int d = static_cast<int>(idx % quads) * 4;
+  const int64_t first = bh * splits;
+  const float2* ml = reinterpret_cast<const float2*>(part_ml) + first;
+  const float* pa = part_acc + first * D + d;
+  const uint16_t* ph = reinterpret_cast<const uint16_t*>(part_acc) + first * D + d;
+  float m = kNegBig, l = 0.0f;
+  float4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int s0 = 0; s0 < splits; s0 += kPer) {
+    float4 x[kPer];
+    float2 w[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int s = s0 + k;
+      const bool ok = s < splits;
+      if constexpr (HALF) {
+        const uint2 hv = ok ? *reinterpret_cast<const uint2*>(ph + static_cast<int64_t>(s) * D) : uint2{0u, 0u};
+        x[k] = float4{f16_bits_to_f32(static_cast<uint16_t>(hv.x)), f16_bits_to_f32(static_cast<uint16_t>(hv.x >> 16)),
+                      f16_bits_to_f32(static_cast<uint16_t>(hv.y)), f16_bits_to_f32(static_cast<uint16_t>(hv.y >> 16))};
+      } else {
+        x[k] = ok ? *reinterpret_cast<const float4*>(pa + static_cast<int64_t>(s) * D) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+      w[k] = ok ? ml[s] : float2{kNegBig, 0.0f};
+    }
+    float mr = m;
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) mr = fmaxf(mr, w[k].x);
+    const float f = fast_exp2(m - mr);
+    l *= f;
+    acc.x *= f; acc.y *= f; acc.z *= f; acc.w *= f;
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const float e = fast_exp2(w[k].x - mr);
+      l = fmaf(w[k].y, e, l);
+      const float ex = HALF ? w[k].y * e : e;
+      acc.x = fmaf(x[k].x, ex, acc.x); acc.y = fmaf(x[k].y, ex, acc.y);
+      acc.z = fmaf(x[k].z, ex, acc.z); acc.w = fmaf(x[k].w, ex, acc.w);
+    }
+    m = mr;
+  }
+  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+  const int rows_b = Hq * qL;
+  const int64_t b = bh / rows_b;
+  const int h = static_cast<int>((bh % rows_b) / qL), i = static_cast<int>(bh % qL);
+  uint16_t* dst = out + b * o_sb + static_cast<int64_t>(h) * o_sh + static_cast<int64_t>(i) * o_sq + d;
+  dst[0] = from_f32<Tag>(acc.x * inv);
+  dst[1] = from_f32<Tag>(acc.y * inv);
+  dst[2] = from_f32<Tag>(acc.z * inv);
+  dst[3] = from_f32<Tag>(acc.w * inv);
+}
+
 }  // namespace
 
 int launch_merge(const qsdpa_decode_args* a, int num_splits, const float* part_acc,
@@ -138,6 +204,21 @@ int launch_merge(const qsdpa_decode_args* a, int num_splits, const float* part_a
   uint16_t* out = static_cast<uint16_t*>(const_cast<void*>(a->out.ptr));
   const int qL = a->q_len > 1 ? a->q_len : 1;
   const int64_t o_sq = qL > 1 ? a->out.stride_n : 0;
+  const int64_t rows = static_cast<int64_t>(a->B) * a->H_q * qL;
+  if (!sched && num_splits <= 16 && rows >= 2048) {
+    const int64_t threads = rows * (a->D / 4);
+    const dim3 g(static_cast<unsigned>((threads + 255) / 256));
+    if (a->dtype == QSDPA_F16 && half_parts)
+      merge_rows_kernel<F16, true><<<g, dim3(256), 0, stream>>>(part_acc, part_ml, a->D, num_splits, a->H_q, qL, rows,
+                                                                out, a->out.stride_b, a->out.stride_h, o_sq);
+    else if (a->dtype == QSDPA_F16)
+      merge_rows_kernel<F16, false><<<g, dim3(256), 0, stream>>>(part_acc, part_ml, a->D, num_splits, a->H_q, qL, rows,
+                                                                 out, a->out.stride_b, a->out.stride_h, o_sq);
+    else
+      merge_rows_kernel<BF16, false><<<g, dim3(256), 0, stream>>>(part_acc, part_ml, a->D, num_splits, a->H_q, qL,
+                                                                  rows, out, a->out.stride_b, a->out.stride_h, o_sq);
+    return check_launch("merge_rows");
+  }
   const dim3 grid(a->B * a->H_q * qL, a->D / 32);
   if (a->dtype == QSDPA_F16 && half_parts)
     merge_kernel<F16, true><<<grid, dim3(256), 0, stream>>>(part_acc, part_ml, a->D, num_splits, a->H_q, qL,

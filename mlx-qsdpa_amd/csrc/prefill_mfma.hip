@@ -32,8 +32,6 @@
 // are skipped) and a bool / additive mask are applied per score.  The grid
 // maps the row groups of one (batch, kv head) to one XCD, so its K / V is
 // fetched into one L2.
-#include <type_traits>
-
 #include "mfma_common.h"
 
 namespace qsdpa {
@@ -57,6 +55,7 @@ constexpr int kRB = QSDPA_PF_RB;         // 16-row blocks per wave
 constexpr int kPRows = 16 * kRB;         // query rows per wave
 constexpr int kPGroupRows = kPWaves * kPRows;
 constexpr int kVPitch = kPTile * 2 + 16;  // bytes per V^T row (dim) in LDS
+constexpr int kMaxPrefillSplits = 64;
 
 template <int D>
 struct PGeo {
@@ -204,6 +203,8 @@ struct Prefill {
 // Parameters beyond the decode's: none; the same MfmaParams (q_len > 1).
 template <typename Tag, int D, int BITS, int GS>
 __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(MfmaParams p, int groups_per_head) {
+  // p.num_splits: key splits per row group (1: the output; more: split-K
+  // partials in the decode's layout, merged by merge_kernel).
   using PG = PGeo<D>;
   using P = Prefill<Tag, D, BITS, GS>;
   __shared__ __attribute__((aligned(16))) uint8_t s_buf[2 * PG::BufBytes];
@@ -220,6 +221,9 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(MfmaParams p, i
   const int total = gridDim.x;
   int w = blockIdx.x;
   if (total % 8 == 0) w = (w % 8) * (total / 8) + w / 8;
+  const int S = p.num_splits;
+  const int split = w % S;
+  w /= S;
   const int grp = w % groups_per_head;
   const int kvh = (w / groups_per_head) % p.Hkv;
   const int b = w / (groups_per_head * p.Hkv);
@@ -231,7 +235,10 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(MfmaParams p, i
   const int s0 = p.kv_start ? min(max(p.kv_start[b], 0), p.N) : 0;
   const int n_end = p.causal ? min(p.N, max(0, p.N - p.qL + (v_first + nrows - 1) / p.G + 1)) : p.N;
   const int len = max(n_end - s0, 0);
-  const int T = (len + kPTile - 1) / kPTile;
+  const int T_all = (len + kPTile - 1) / kPTile;
+  // This split's tiles: [j_base, j_base + T) of the group's T_all.
+  const int j_base = static_cast<int>(static_cast<int64_t>(split) * T_all / S);
+  const int T = static_cast<int>(static_cast<int64_t>(split + 1) * T_all / S) - j_base;
 
   // The wave's rows: block rb, lane row r -> v = v_first + 32 wave + 16 rb + r.
   int n_lane[kRB], n_wave[kRB];  // a lane's key limit; the wave's smallest
@@ -422,7 +429,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(MfmaParams p, i
   uint8_t* buf0 = s_buf;
   uint8_t* buf1 = s_buf + PG::BufBytes;
   const int oob = len + 2 * kPTile;  // rows past every descriptor: the loads read zero
-  auto row_of = [&](int j) { return j < T ? j * kPTile : oob; };
+  auto row_of = [&](int j) { return j < T ? (j_base + j) * kPTile : oob; };
   if (T > 0) {
     P::load(R0, src, row_of(0), tid);
     P::load(R1, src, row_of(1), tid);
@@ -435,7 +442,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(MfmaParams p, i
         P::stage(R1, buf1, tid);
         P::load(R1, src, row_of(j + 3), tid);
       }
-      compute(buf0, j * kPTile);
+      compute(buf0, (j_base + j) * kPTile);
       __syncthreads();
       if (j + 1 >= T) break;
       // tile j + 1 in buf1; R0 holds tile j + 2, R1 tile j + 3.
@@ -443,7 +450,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(MfmaParams p, i
         P::stage(R0, buf0, tid);
         P::load(R0, src, row_of(j + 4), tid);
       }
-      compute(buf1, (j + 1) * kPTile);
+      compute(buf1, (j_base + j + 1) * kPTile);
       __syncthreads();
     }
   }
@@ -459,24 +466,47 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(MfmaParams p, i
     const int v = v_first + vr;
     const int hq = kvh * p.G + v % p.G, iq = v / p.G;
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-    uint16_t* dst = p.out + static_cast<int64_t>(b) * p.o_sb + static_cast<int64_t>(hq) * p.o_sh +
-                    static_cast<int64_t>(iq) * p.o_sq + 4 * quad;
+    if (S == 1) {
+      uint16_t* dst = p.out + static_cast<int64_t>(b) * p.o_sb + static_cast<int64_t>(hq) * p.o_sh +
+                      static_cast<int64_t>(iq) * p.o_sq + 4 * quad;
 #pragma unroll
-    for (int db = 0; db < PG::NB; ++db) {
-      const uint32_t lo = pack_T2<Tag>(acc[rb][db][0] * inv, acc[rb][db][1] * inv);
-      const uint32_t hi = pack_T2<Tag>(acc[rb][db][2] * inv, acc[rb][db][3] * inv);
-      uint16_t* o = dst + 16 * db;
-      o[0] = static_cast<uint16_t>(lo);
-      o[1] = static_cast<uint16_t>(lo >> 16);
-      o[2] = static_cast<uint16_t>(hi);
-      o[3] = static_cast<uint16_t>(hi >> 16);
+      for (int db = 0; db < PG::NB; ++db) {
+        const uint32_t lo = pack_T2<Tag>(acc[rb][db][0] * inv, acc[rb][db][1] * inv);
+        const uint32_t hi = pack_T2<Tag>(acc[rb][db][2] * inv, acc[rb][db][3] * inv);
+        uint16_t* o = dst + 16 * db;  // out rows are only 2-byte aligned in general
+        o[0] = static_cast<uint16_t>(lo);
+        o[1] = static_cast<uint16_t>(lo >> 16);
+        o[2] = static_cast<uint16_t>(hi);
+        o[3] = static_cast<uint16_t>(hi >> 16);
+      }
+    } else {
+      // The split's partial of row (b, hq, iq), column `split`, as the
+      // decode kernel stores it: float16 inputs the normalised row acc / l
+      // as float16, bfloat16 inputs the float32 row; then (m, l).
+      const int64_t slot = ((static_cast<int64_t>(b) * p.Hq + hq) * p.qL + iq) * S + split;
+#pragma unroll
+      for (int db = 0; db < PG::NB; ++db) {
+        const int d = 16 * db + 4 * quad;
+        if constexpr (Tag::kId == QSDPA_F16) {
+          typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+          *reinterpret_cast<u2*>(reinterpret_cast<uint16_t*>(p.part_acc) + slot * D + d) =
+              u2{pack_T2<Tag>(acc[rb][db][0] * inv, acc[rb][db][1] * inv),
+                 pack_T2<Tag>(acc[rb][db][2] * inv, acc[rb][db][3] * inv)};
+        } else {
+          __builtin_nontemporal_store(acc[rb][db], reinterpret_cast<f4*>(p.part_acc + slot * D + d));
+        }
+      }
+      if (quad == 0) {
+        p.part_ml[slot * 2] = mrun[rb];
+        p.part_ml[slot * 2 + 1] = l;
+      }
     }
   }
 }
 
 template <typename Tag, int D, int BITS>
 void launch_prefill_gs(const MfmaParams& p, int gs, int groups, hipStream_t stream, const qsdpa_decode_args* a) {
-  const dim3 grid(groups * p.Hkv * p.B);
+  const dim3 grid(groups * p.Hkv * p.B * p.num_splits);
   void (*k)(MfmaParams, int) = gs == 32 ? prefill_mfma_kernel<Tag, D, BITS, 32>
                                : gs == 64 ? prefill_mfma_kernel<Tag, D, BITS, 64>
                                           : prefill_mfma_kernel<Tag, D, BITS, 128>;
@@ -492,19 +522,18 @@ void launch_prefill_gs(const MfmaParams& p, int gs, int groups, hipStream_t stre
 bool mfma_supports(const qsdpa_decode_args* a);
 
 // The prefill kernel takes q_len > 1 calls on the MFMA path's layouts whose
-// kv heads have at least 64 query rows and that fill at least a quarter of
-// the GPU with 128-row groups; others stay on the decode kernel's split-K
-// blocks.  K / V rows are read in 16-byte pieces (8-byte V pieces at D = 128,
-// 4-bit), so the packed views must be 16-byte aligned.
-bool prefill_supports(const qsdpa_decode_args* a, int cus) {
+// kv heads have at least one full 128-row group (D = 128); others stay on
+// the decode kernel's 16-row blocks (a half-empty group would leave half its
+// waves computing padding rows).  K / V rows are read in 16-byte pieces (8-byte V
+// pieces at 4-bit), so the packed views must be aligned to the pieces.
+bool prefill_supports(const qsdpa_decode_args* a) {
   // D = 256 would need more than the 512 registers of a wave (its
   // accumulators and Q rows double): those calls keep the decode kernel.
   if (a->q_len <= 1 || a->D != 128 || !mfma_supports(a)) return false;
   const int64_t rows = static_cast<int64_t>(a->H_q / a->H_kv) * a->q_len;
-  if (rows < 64) return false;
+  if (rows < kPGroupRows) return false;
   const int64_t groups = (rows + kPGroupRows - 1) / kPGroupRows;
-  if (groups * a->H_kv * a->B < cus / 4) return false;
-  if (groups * a->H_kv * a->B >= (int64_t(1) << 31)) return false;
+  if (groups * a->H_kv * a->B * kMaxPrefillSplits >= (int64_t(1) << 31)) return false;
   const int kq_bytes = a->D / 4 * a->bits / 8, vp_bytes = a->D / 8 * a->bits / 8;
   if (!aligned_view(a->k_packed, std::min(kq_bytes, 16), 4)) return false;
   if (!aligned_view(a->v_packed, std::min(vp_bytes, 16), 4)) return false;
@@ -517,18 +546,32 @@ bool prefill_supports(const qsdpa_decode_args* a, int cus) {
   return true;
 }
 
-int launch_prefill_mfma(const qsdpa_decode_args* a, hipStream_t stream) {
-  MfmaParams p = mfma_params(a, 1, nullptr, nullptr);
+// Key splits of the prefill kernel: enough workgroups for every CU, each
+// split at least 4 tiles (an explicit num_splits > 0 is kept, up to the
+// same bounds).  At the C5 chunk (256 row groups) one split; with
+// q_len = 128 (64 groups) 4 splits: 38 against 126 us in one.
+int prefill_num_splits(const qsdpa_decode_args* a, int cus) {
+  const int64_t rows = static_cast<int64_t>(a->H_q / a->H_kv) * a->q_len;
+  const int64_t grid = (rows + kPGroupRows - 1) / kPGroupRows * a->H_kv * a->B;
+  const int64_t tiles = (static_cast<int64_t>(a->N) + kPTile - 1) / kPTile;
+  int64_t s = a->num_splits > 0 ? a->num_splits : (cus + grid - 1) / grid;
+  s = std::min<int64_t>(s, std::max<int64_t>(1, tiles / 4));
+  s = std::min<int64_t>(s, kMaxPrefillSplits);
+  return static_cast<int>(std::max<int64_t>(s, 1));
+}
+
+int launch_prefill_mfma(const qsdpa_decode_args* a, int splits, float* part_acc, float* part_ml,
+                        hipStream_t stream) {
+  MfmaParams p = mfma_params(a, splits, part_acc, part_ml);
   const int groups = (p.G * p.qL + kPGroupRows - 1) / kPGroupRows;
   const bool f16 = a->dtype == QSDPA_F16;
-  auto bits = [&](auto tag, auto dim) {
+  auto bits = [&](auto tag) {
     using Tag = decltype(tag);
-    constexpr int D = decltype(dim)::value;
-    if (a->bits == 4) launch_prefill_gs<Tag, D, 4>(p, a->group_size, groups, stream, a);
-    else launch_prefill_gs<Tag, D, 8>(p, a->group_size, groups, stream, a);
+    if (a->bits == 4) launch_prefill_gs<Tag, 128, 4>(p, a->group_size, groups, stream, a);
+    else launch_prefill_gs<Tag, 128, 8>(p, a->group_size, groups, stream, a);
   };
-  if (f16) bits(F16{}, std::integral_constant<int, 128>{});
-  else bits(BF16{}, std::integral_constant<int, 128>{});
+  if (f16) bits(F16{});
+  else bits(BF16{});
   return check_launch("prefill_mfma");
 }
 

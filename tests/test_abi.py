@@ -131,10 +131,11 @@ def test_invalid_arguments_return_codes():
 
 
 def test_prefill_routing_rule():
-    """Calls with many query rows per kv head (and enough 128-row groups to
-    fill a quarter of 256 CUs) run the one-pass prefill kernel: no split-K
-    workspace.  Smaller multi-query calls keep the split-K decode kernel.
-    (Planning only validates arguments; nothing is launched or read.)"""
+    """Calls with at least one full 128-row group per kv head (D = 128) run
+    the prefill kernel: one pass where its groups fill the 256 CUs, key
+    splits (a merge workspace) where they would not.  Smaller multi-query
+    calls and D = 256 keep the split-K decode kernel.  (Planning only
+    validates arguments; nothing is launched or read.)"""
     lib = _lib.load()
 
     def plan(B, Hq, Hkv, N, D, L, bits=8, gs=128):
@@ -153,7 +154,10 @@ def test_prefill_routing_rule():
         assert ws >= 0, lib.qsdpa_last_error()
         return n.value, ws
 
-    assert plan(4, 16, 4, 4096, 128, 512) == (1, 0)       # the C5 chunk: prefill kernel
+    assert plan(4, 16, 4, 4096, 128, 512) == (1, 0)       # the C5 chunk: prefill kernel, one pass
+    splits, ws = plan(4, 16, 4, 4096, 128, 128)            # 64 groups: 4 key splits of 16 tiles
+    assert splits == 4 and ws > 0
+    assert plan(1, 64, 8, 256, 128, 16)[0] == 1             # 8 groups, 4 tiles: one split each
     splits, ws = plan(1, 16, 4, 4096, 128, 8)              # 32 rows per kv head: decode kernel
     assert splits > 1 and ws > 0
     splits, ws = plan(1, 16, 4, 4096, 256, 512)             # D = 256: decode kernel

@@ -3,8 +3,9 @@ float64 oracle (tests/torch_oracle.py, pinned to the numpy oracle by
 tests/test_gpu_parity_full.py).
 
 Shapes are chosen so the library routes them to the prefill kernel: at
-least 64 query rows per kv head (H_q / H_kv x q_len) and at least 64
-128-row groups in the grid.  Covered: both dtypes, 4- and 8-bit codes, all
+least one full 128-row group per kv head (H_q / H_kv x q_len), with one
+pass where the groups fill the GPU and key splits (merged by the split-K
+merge kernel) where they do not.  Covered: both dtypes, 4- and 8-bit codes, all
 group sizes, the symmetric format, causal and full attention, kv_start
 (left padding), bool and additive masks, a partial last row group, a
 partial last key tile, keys that start inside a tile, and the C5 chunk.
@@ -85,6 +86,27 @@ def test_prefill_matches_oracle(device, case):
     print(f"prefill case {case}", flush=True)
     q, kq, vq = _inputs(B, Hq, Hkv, N, L, bits, gs, dtype, seed=N + L, symmetric=sym)
     _check(q, kq, vq, bits, gs, f"case {case}", causal=causal)
+
+
+SPLIT_CASES = [  # small grids: the planner gives each row group several key splits
+    (1, 32, 8, 4000, 256, 4, 64, torch.float16, True, False),     # 64 groups: 4 splits
+    (1, 16, 4, 3000, 128, 8, 128, torch.bfloat16, True, False),   # 16 groups: 11 splits
+    (2, 16, 4, 2500, 128, 4, 32, torch.float16, False, True),     # 32 groups, full attention
+]
+
+
+@pytest.mark.parametrize("case", SPLIT_CASES, ids=lambda c: "B{}_H{}x{}_N{}_L{}_b{}_g{}".format(*c[:7]))
+def test_prefill_key_splits(device, case):
+    B, Hq, Hkv, N, L, bits, gs, dtype, causal, sym = case
+    q, kq, vq = _inputs(B, Hq, Hkv, N, L, bits, gs, dtype, seed=N + 7, symmetric=sym)
+    splits, ws = kernels.decode_plan(q, kq[0], vq[0], kq[1], vq[1], kq[2], vq[2], scale=128 ** -0.5, bits=bits,
+                                     group_size=gs)
+    print(f"prefill split case {case}: {splits} splits", flush=True)
+    assert splits > 1 and ws > 0
+    _check(q, kq, vq, bits, gs, f"split case {case}", causal=causal)
+    if causal:
+        ks = torch.tensor([0, 611][:B], dtype=torch.int32, device=device)
+        _check(q, kq, vq, bits, gs, f"split case {case} kv_start", causal=True, kv_start=ks)
 
 
 def test_prefill_kv_start_and_masks(device):
