@@ -55,6 +55,7 @@
 // partials for the merge kernel (merge.hip): float16 inputs store the
 // normalised row acc / l as float16 (half the bytes), bfloat16 float32 rows.
 #include "mfma_tile.h"
+#include "wave_split.h"
 
 // Timeline probe (a build with -DQSDPA_TIMELINE only; the default build has
 // none of it): each wave stamps s_memrealtime (100 MHz) at fixed points of
@@ -116,25 +117,10 @@ __device__ __forceinline__ void decode_segment(const MfmaParams& p, float* s_acc
   const int len = max(n_end - s0, 0);
   const int T = (len + kTile - 1) / kTile;
   const int J = T > t_lo ? min(jmax, (T - t_lo + stride - 1) / stride) : 0;
-  // Positions below J - E go round-robin to the 8 waves; the last E go to
-  // waves 0-3 only.  Waves 4-7 share their SIMDs with waves 0-3, and the
-  // older waves' loads are served first, so equal shares would leave 0-3
-  // idle at the end.  D = 256 (HBM-bound): E = J / 2 (in whole rounds of 8)
-  // gives 0-3 three tiles for every one of 4-7 (C3 24.6 against 25.9 us per
-  // step with five for three, C2 33.5 against 34.2); D = 128 (VALU-bound):
-  // E = J / 4, five for three (C4 62.5 against 65.5 us with three for one).
-  // Every wave's first position (its index) must lie in the round-robin part
-  // (J - E >= 8 whenever E > 0), or the waves' position sequences would
-  // overlap; both ratios keep E <= J / 2 with E = 0 below 16 positions, and
-  // the guard keeps it so.
-  const int E0 = D == 256 ? 8 * (J / 16) : 8 * (J / 32);
-  const int E = J - E0 >= kWaves ? E0 : 0;
-  const int J8 = J - E;
-  auto next_pos = [&](int j) -> int {
-    if (j + kWaves < J8) return j + kWaves;
-    if (wave >= 4) return J;
-    return j < J8 ? J8 + wave : j + 4;
-  };
+  // The waves' shares of the J positions (wave_split.h).
+  static_assert(kWaves == kSplitWaves, "the tile split is for 8 waves");
+  const int J8 = wave_split_rr_end(J, D);
+  auto next_pos = [&](int j) -> int { return wave_split_next(j, J, J8, wave); };
   // Rows of a position relative to s0; past the end, rows outside every
   // descriptor (the loads read zero without touching memory).  Every tile
   // issues the same loads, so the compiler's vmcnt waits stay exact.

@@ -1,0 +1,41 @@
+// How the 8 waves of a decode workgroup share the J tile positions of their
+// split (decode_mfma.hip).  Plain C++ as well as device code, so that a host
+// program can check the invariant the kernel relies on: every position in
+// [0, J) is visited by exactly one wave.
+//
+// Positions below J - E go round-robin to the 8 waves; the last E go to
+// waves 0-3 only.  Waves 4-7 share their SIMDs with waves 0-3, and the older
+// waves' loads are served first, so equal shares would leave 0-3 idle at the
+// end.  D = 256 (HBM-bound): E = 8 (J / 16), three tiles for waves 0-3 for
+// every one of 4-7; D = 128 (VALU-bound): E = 8 (J / 32), five for three.
+// Every wave's first position (its index) must lie in the round-robin part
+// (J - E >= 8 whenever E > 0), or the waves' position sequences would
+// overlap; E is 0 otherwise.
+#pragma once
+
+#if defined(__HIPCC__)
+#define QSDPA_HD __host__ __device__ __forceinline__
+#else
+#define QSDPA_HD inline
+#endif
+
+namespace qsdpa {
+
+constexpr int kSplitWaves = 8;
+
+// Positions [0, J8) are round-robin; [J8, J) belong to waves 0-3.
+QSDPA_HD int wave_split_rr_end(int J, int D) {
+  const int E0 = D == 256 ? 8 * (J / 16) : 8 * (J / 32);
+  const int E = J - E0 >= kSplitWaves ? E0 : 0;
+  return J - E;
+}
+
+// The position wave `wave` takes after position j (J or more: none).  A
+// wave starts at position `wave`.
+QSDPA_HD int wave_split_next(int j, int J, int J8, int wave) {
+  if (j + kSplitWaves < J8) return j + kSplitWaves;
+  if (wave >= 4) return J;
+  return j < J8 ? J8 + wave : j + 4;
+}
+
+}  // namespace qsdpa

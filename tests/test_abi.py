@@ -162,3 +162,39 @@ def test_prefill_routing_rule():
     assert splits > 1 and ws > 0
     splits, ws = plan(1, 16, 4, 4096, 256, 512)             # D = 256: decode kernel
     assert splits >= 1 and (splits == 1 or ws > 0)
+
+
+@pytest.mark.skipif(shutil.which("g++") is None, reason="g++ not available")
+def test_wave_split_covers_every_position_once(tmp_path):
+    """The decode kernel's share of a split's tile positions among its 8
+    waves (csrc/wave_split.h, compiled here for the host): for every J up
+    to 1024 and both ratios, each position in [0, J) is visited by exactly
+    one wave, and waves 4-7 take no positions of the tail."""
+    header = HEADER.parent.parent / "mlx-qsdpa_amd" / "csrc" / "wave_split.h"
+    src = tmp_path / "split.cc"
+    src.write_text(f"""
+#include <cstdio>
+#include <vector>
+#include "{header}"
+int main() {{
+  for (int D : {{128, 256}})
+    for (int J = 0; J <= 1024; ++J) {{
+      const int J8 = qsdpa::wave_split_rr_end(J, D);
+      if (J8 < 0 || J8 > J) {{ std::printf("J8 %d of %d\\n", J8, J); return 1; }}
+      std::vector<int> seen(J, 0);
+      for (int w = 0; w < 8; ++w)
+        for (int j = w; j < J; j = qsdpa::wave_split_next(j, J, J8, w)) {{
+          seen[j]++;
+          if (w >= 4 && j >= J8) {{ std::printf("wave %d in the tail at %d (J=%d)\\n", w, j, J); return 1; }}
+        }}
+      for (int j = 0; j < J; ++j)
+        if (seen[j] != 1) {{ std::printf("D=%d J=%d position %d seen %d times\\n", D, J, j, seen[j]); return 1; }}
+    }}
+  std::printf("ok\\n");
+  return 0;
+}}
+""")
+    exe = tmp_path / "split"
+    subprocess.run(["g++", "-std=c++17", "-O1", "-Wall", "-Werror", str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True)
+    assert out.returncode == 0 and out.stdout.strip() == "ok", out.stdout
