@@ -422,6 +422,44 @@ int launch_decode_mfma(const qsdpa_decode_args* a, int num_splits, float* part_a
 }  // namespace qsdpa
 
 #ifdef QSDPA_TIMELINE
+namespace qsdpa {
+namespace {
+// Read-only streaming probe (probe build only): workgroup w of `gridDim.x`
+// reads its contiguous share of the buffer in 16-byte pieces, 8 pieces per
+// thread in flight, with the decode's non-temporal policy, and writes one
+// word -- the time of one launch that only reads that many bytes.
+__global__ __launch_bounds__(512) void stream_read_kernel(const u4* src, uint64_t n16, uint32_t* sink) {
+  const uint64_t share = (n16 + gridDim.x - 1) / gridDim.x;
+  const uint64_t lo = blockIdx.x * share;
+  const uint64_t hi = lo + share < n16 ? lo + share : n16;
+  uint32_t acc = 0;
+  for (uint64_t i = lo + threadIdx.x; i < hi; i += 8 * 512) {
+    u4 x[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint64_t j = i + static_cast<uint64_t>(k) * 512;
+      x[k] = j < hi ? __builtin_nontemporal_load(src + j) : u4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) acc ^= x[k][0] ^ x[k][1] ^ x[k][2] ^ x[k][3];
+  }
+  if (acc == 0x9e3779b9u) sink[blockIdx.x] = acc;  // keeps the loads; the sink is almost never written
+}
+}  // namespace
+}  // namespace qsdpa
+
+// Launch the streaming probe over `bytes` (a multiple of 16) with `blocks`
+// workgroups of 512 threads; ev_begin / ev_end (hipEvent_t) ride on the dispatch.
+extern "C" int qsdpa_debug_stream_read(const void* src, uint64_t bytes, void* sink, int blocks, void* stream,
+                                       void* ev_begin, void* ev_end) {
+  if (!src || !sink || blocks < 1 || bytes % 16) return -1;
+  hipExtLaunchKernelGGL(qsdpa::stream_read_kernel, dim3(blocks), dim3(512), 0, static_cast<hipStream_t>(stream),
+                        static_cast<hipEvent_t>(ev_begin), static_cast<hipEvent_t>(ev_end), 0,
+                        static_cast<const qsdpa::u4*>(src), static_cast<uint64_t>(bytes / 16),
+                        static_cast<uint32_t*>(sink));
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
 // Copy the timeline stamps (uint64 [2048 workgroups][8 waves][18 slots]).
 extern "C" int qsdpa_debug_timeline(void* dst, size_t bytes) {
   if (bytes > sizeof(g_timeline)) bytes = sizeof(g_timeline);

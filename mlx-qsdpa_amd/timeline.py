@@ -1,7 +1,8 @@
 """Per-phase timeline of the matrix-core decode kernel on one GPU.
 
-  python mlx-qsdpa_amd/timeline.py build            # here (hipcc): the probe library
-  python mlx-qsdpa_amd/timeline.py run [--config c3] # on the GPU
+  python mlx-qsdpa_amd/timeline.py build               # here (hipcc): the probe library
+  python mlx-qsdpa_amd/timeline.py run [--config c3]    # on the GPU
+  python mlx-qsdpa_amd/timeline.py stream [--config c3] # on the GPU: a read-only launch of the same bytes
 
 ``build`` compiles the library with -DQSDPA_TIMELINE into
 mlx_qsdpa_amd/libqsdpa_timeline.so: the same kernels, plus an s_memrealtime
@@ -95,9 +96,53 @@ def run(config: str, n: int | None, calls: int, lib_path: Path = LIB) -> None:
           f"{np.median(ev_us):.2f}); stamps span {span:.2f} us (first entry to last store complete)")
 
 
+def stream(config: str, n: int | None, calls: int, lib_path: Path = LIB, blocks=(256, 512, 1024, 2048)) -> None:
+    """Time a launch that only reads the decode's bytes (the probe library's
+    stream_read kernel): the floor of one kernel moving that much from HBM,
+    over the same number of distinct buffers as the decode's sets."""
+    for p in (ROOT, HERE):
+        sys.path.insert(0, str(p))
+    import numpy as np
+    import torch
+
+    import bench
+    from mlx_qsdpa_amd import _lib, metric
+
+    lib = _lib.load(lib_path)
+    lib.qsdpa_debug_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_int,
+                                            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+    lib.qsdpa_debug_stream_read.restype = ctypes.c_int
+    cfg = bench.CONFIGS[config]
+    B, Hq, Hkv, D, bits, gs, dt, N0, _ = cfg
+    N = n or N0
+    nbytes = metric.decode_bytes(B, Hq, Hkv, D, bits, gs, B * N) // 16 * 16
+    n_sets = max(2, int(1.2e9 // nbytes) + 1)
+    dev = torch.device("cuda:0")
+    bufs = [torch.ones(nbytes, dtype=torch.uint8, device=dev) for _ in range(n_sets)]
+    sink = torch.zeros(4096, dtype=torch.int32, device=dev)
+    stream_h = torch.cuda.current_stream(dev).cuda_stream
+    hip = bench.HipEvents()
+    print(f"# {config}: {nbytes} bytes read per launch, {n_sets} buffers cycled")
+    print("| workgroups | median us | p10 us | TB/s (median) | % of 8 TB/s |")
+    print("|---|---|---|---|---|")
+    for nb in blocks:
+        ev = hip.create(2 * calls)
+        for i in range(calls + 5):
+            e = (ev[2 * (i - 5)], ev[2 * (i - 5) + 1]) if i >= 5 else (None, None)
+            rc = lib.qsdpa_debug_stream_read(bufs[i % n_sets].data_ptr(), nbytes, sink.data_ptr(), nb, stream_h, *e)
+            if rc != 0:
+                raise SystemExit("qsdpa_debug_stream_read failed")
+        torch.cuda.synchronize()
+        us = np.array([hip.elapsed_ms(ev[2 * i], ev[2 * i + 1]) * 1e3 for i in range(calls)])
+        hip.destroy(ev)
+        med = float(np.median(us))
+        print(f"| {nb} | {med:.2f} | {np.percentile(us, 10):.2f} | {nbytes / med / 1e6:.2f} | "
+              f"{100 * nbytes / med / 1e6 / 8:.1f} |")
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
-    ap.add_argument("what", choices=["build", "run"])
+    ap.add_argument("what", choices=["build", "run", "stream"])
     ap.add_argument("--config", default="c3", choices=["c1", "c2", "c3", "c5"])
     ap.add_argument("--n", type=int, default=None)
     ap.add_argument("--calls", type=int, default=40)
@@ -105,6 +150,8 @@ def main(argv=None) -> int:
     a = ap.parse_args(argv)
     if a.what == "build":
         build()
+    elif a.what == "stream":
+        stream(a.config, a.n, a.calls, Path(a.lib))
     else:
         run(a.config, a.n, a.calls, Path(a.lib))
     return 0
