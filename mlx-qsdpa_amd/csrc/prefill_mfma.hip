@@ -7,55 +7,67 @@
 // each of which loads and dequantizes the kv head's whole K / V again.  Here
 // one workgroup takes 128 rows of a kv head -- 8 waves x 16 rows -- and every
 // 64-token K / V tile is loaded once per workgroup, dequantized once into
-// LDS, and read from LDS by all eight waves:
+// LDS, and read from LDS by all eight waves.  Per tile j, in each wave:
 //
-//   loads      the raw codes, scales and biases of tile j + 2 are in flight
-//              (two register sets) while tile j is computed;
-//   dequant    every thread turns its piece of tile j + 1 into T values
-//              (T(fma(scale, code, bias)), as mx.dequantize rounds them) in
-//              the LDS buffer the waves do not read during tile j: K
-//              row-major (token, dims), V transposed (dim, tokens) with the
-//              tokens of each 32-token half in the order of the S^T
-//              fragment, so that the P^T operand is a lane's own softmax
-//              values;
-//   compute    per wave and tile, S^T = K Q^T (A = K rows from LDS, B = Q^T
-//              in registers: 4 token blocks x D/32 steps of
-//              v_mfma_f32_16x16x32 per 16-row block), the online softmax of the decode kernel
-//              (log2 domain, rescale when the maximum grows by more than 8),
-//              then out^T += V^T P^T (A = V^T rows from LDS; bfloat16 splits
-//              P into hi + lo terms);
-//   barrier    one per tile: it orders this tile's reads before the next
-//              tile's writes of the same buffer.
+//   QK         S^T = K Q^T (A = K rows from LDS buffer j % 2, B = Q^T in
+//              registers): 4 token blocks x D/32 steps of v_mfma_f32_16x16x32
+//              in the input type T, steps outer so that consecutive MFMAs
+//              feed four independent accumulators;
+//   dequant    every thread turns its piece of tile j + 1 (raw codes, scales
+//              and biases loaded two tiles ahead into one of two register
+//              sets) into values in the other LDS buffer -- K row-major
+//              (token, dims) in T, V transposed (dim, tokens) as float16,
+//              with the tokens of each 32-token half in the order of the S^T
+//              fragment so that the P^T operand is a lane's own softmax
+//              values -- and reissues that register set's loads for tile
+//              j + 3; the dequantization's VALU work has no dependence on
+//              the QK MFMAs and runs beside them;
+//   softmax    online, in the log2 domain, rescaled when the maximum grows
+//              by more than 8 (the decode kernel's); without a mask tensor
+//              the score scale is applied inside the exponent's fma;
+//   PV         out^T += V^T P^T in float16 (A = V^T rows from LDS, B = P^T);
+//   barrier    one per tile: it orders this tile's reads of buffer j % 2
+//              before the next tile's writes of it.
+//
+// P.V runs in float16 for bfloat16 inputs too.  V is rounded to bfloat16
+// exactly as mx.dequantize rounds it, then scaled by 2^-k and converted to
+// float16, which is exact for magnitudes from 2^-17 up (below that the error
+// is at most 2^-25 * 2^k).  A scan of the workgroup's V scales and biases
+// gives max |V| (at code 0 or 2^bits - 1 of each group): k is 0 unless it
+// reaches kVBound (the output is scaled back by 2^k), and P (in [0, 256])
+// enters as one float16 term -- the float16 path's 11 significant bits, one
+// MFMA per block -- while max |V| is at most kPVSingle, as two terms (hi +
+// lo, 22 bits) above it.
 //
 // Rows of a kv head are (position v / G, head v % G) as in the decode
 // kernel; a causal mask (aligned to the last key), kv_start (keys before it
 // are skipped) and a bool / additive mask are applied per score.  The grid
 // maps the row groups of one (batch, kv head) to one XCD, so its K / V is
 // fetched into one L2.
+#include <type_traits>
+
 #include "mfma_common.h"
 
 namespace qsdpa {
 namespace {
 
-// Workgroup shape: 8 waves x 16 rows (about 190 registers, two waves per
-// SIMD).  Measured at the C5 chunk (B=4, H_q=16, H_kv=4, N=4096, q_len=512,
-// bf16 8-bit): 144 us; 4 waves x 32 rows (one wave per SIMD, 380
+// Workgroup shape: 8 waves x 16 rows (two waves per SIMD).  Measured at the
+// C5 chunk (B=4, H_q=16, H_kv=4, N=4096, q_len=512, bf16 8-bit) with
+// bfloat16 P.V: 144 us; 4 waves x 32 rows (one wave per SIMD, about 380
 // registers) 171-174 us; 4 waves x 16 rows (64-row groups, two per CU)
-// 172 us.  The build can override both for such comparisons.
-#ifndef QSDPA_PF_WAVES
-#define QSDPA_PF_WAVES 8
-#endif
-#ifndef QSDPA_PF_RB
-#define QSDPA_PF_RB 1
-#endif
-constexpr int kPWaves = QSDPA_PF_WAVES;  // waves per workgroup
+// 172 us.
+constexpr int kPWaves = 8;
 constexpr int kPThreads = kPWaves * 64;
-constexpr int kPTile = 64;               // tokens per tile
-constexpr int kRB = QSDPA_PF_RB;         // 16-row blocks per wave
-constexpr int kPRows = 16 * kRB;         // query rows per wave
-constexpr int kPGroupRows = kPWaves * kPRows;
-constexpr int kVPitch = kPTile * 2 + 16;  // bytes per V^T row (dim) in LDS
+constexpr int kPTile = 64;                   // tokens per tile
+constexpr int kPGroupRows = kPWaves * 16;    // query rows per workgroup
+constexpr int kVPitch = kPTile * 2 + 16;     // bytes per V^T row (dim) in LDS
 constexpr int kMaxPrefillSplits = 64;
+constexpr float kVBound = 64000.0f;          // largest |V| staged in float16 unscaled
+// bfloat16 inputs: the largest max |V| for which P enters the P.V MFMAs as
+// one float16 term (11 significant bits); above it, as two (hi + lo, 22
+// bits).  P's rounding moves an output by up to 2^-11 max|V| (about 2^-12
+// max|V| in the random tests), so one term keeps 2e-3 for |V| <= 8.
+constexpr float kPVSingle = 8.0f;
 
 template <int D>
 struct PGeo {
@@ -107,21 +119,29 @@ __device__ __forceinline__ void load_words(rsrc_t rs, uint32_t off, uint32_t* w)
   }
 }
 
-// Raw registers of one tile for one thread (the split above).
-template <int D, int BITS>
+// Raw registers of one tile for one thread (the split above).  Single
+// scale / bias half-words stay 16-bit values: widened, the compiler masks
+// them as soon as they arrive, and that mask waits for every load in flight.
+template <int D, int BITS, int GS>
 struct PRaw {
   static constexpr int KW = D / kKPT * BITS / 32;
   static constexpr int VW = D / kVPT * BITS / 32;
+  using KMeta = std::conditional_t<(D / kKPT > GS), uint32_t, uint16_t>;  // two groups: both half-words
   uint32_t k[KW];
-  uint32_t ks, kb;      // the K quarter's scale / bias half-words (two groups: both)
+  KMeta ks, kb;
   uint32_t v[2][VW];
-  uint32_t vs[2], vb[2];
+  uint16_t vs[2], vb[2];
 };
+
+// Two bfloat16 values (a packed pair) -> the float16 pair of the same values.
+__device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t x) {
+  return pack_T2<F16>(__builtin_bit_cast(float, x << 16), __builtin_bit_cast(float, x & 0xFFFF0000u));
+}
 
 template <typename Tag, int D, int BITS, int GS>
 struct Prefill {
   using PG = PGeo<D>;
-  using Raw = PRaw<D, BITS>;
+  using Raw = PRaw<D, BITS, GS>;
   static constexpr int kQD = D / kKPT;                    // K dims per thread
   static constexpr int kKG = kQD > GS ? kQD / GS : 1;     // groups per K quarter (1 or 2)
   static constexpr int kVD = D / kVPT;                    // V dims per thread and token
@@ -158,8 +178,9 @@ struct Prefill {
     }
   }
 
-  // Dequantize the thread's piece of a tile into the LDS buffer `buf`.
-  static __device__ __forceinline__ void stage(const Raw& R, uint8_t* buf, int tid) {
+  // Dequantize the thread's piece of a tile into the LDS buffer `buf`: K in
+  // T, V in float16 (bfloat16 inputs: the bfloat16 values times vsc = 2^-k).
+  static __device__ __forceinline__ void stage(const Raw& R, uint8_t* buf, int tid, float vsc) {
     // K: token tid / KPT, dims [c D/KPT, (c + 1) D/KPT), row-major.
     {
       const int t = tid / kKPT, c = tid % kKPT;
@@ -167,8 +188,8 @@ struct Prefill {
 #pragma unroll
       for (int s = 0; s < kQD / 8; ++s) {
         const int g = kKG == 2 ? (8 * s) / GS : 0;
-        const uint32_t sw = g ? (R.ks >> 16) : R.ks;
-        const uint32_t bw = g ? (R.kb >> 16) : R.kb;
+        const uint32_t sw = g ? static_cast<uint32_t>(R.ks >> 16) : static_cast<uint32_t>(R.ks);
+        const uint32_t bw = g ? static_cast<uint32_t>(R.kb >> 16) : static_cast<uint32_t>(R.kb);
         uint32_t a[4];
         dequant_k<Tag, BITS>(R.k + s * (BITS / 4), splat_lo(sw), splat_lo(bw), to_f32<Tag>(static_cast<uint16_t>(sw)),
                              to_f32<Tag>(static_cast<uint16_t>(bw)), a);
@@ -183,10 +204,19 @@ struct Prefill {
 #pragma unroll
       for (int s = 0; s < kVD / 8; ++s) {
 #pragma unroll
-        for (int e = 0; e < 2; ++e)
-          dequant_k<Tag, BITS>(R.v[e] + s * (BITS / 4), splat_lo(R.vs[e]), splat_lo(R.vb[e]),
-                               to_f32<Tag>(static_cast<uint16_t>(R.vs[e])),
-                               to_f32<Tag>(static_cast<uint16_t>(R.vb[e])), a[e]);
+        for (int e = 0; e < 2; ++e) {
+          if constexpr (Tag::kId == QSDPA_F16) {
+            dequant_k<Tag, BITS>(R.v[e] + s * (BITS / 4), splat_lo(R.vs[e]), splat_lo(R.vb[e]), to_f32<Tag>(R.vs[e]),
+                                 to_f32<Tag>(R.vb[e]), a[e]);
+          } else {
+            // bfloat16(fma(s, c, b)) * 2^-k = bfloat16(fma(s 2^-k, c, b 2^-k)).
+            uint32_t t[4];
+            dequant_k<Tag, BITS>(R.v[e] + s * (BITS / 4), 0u, 0u, to_f32<Tag>(R.vs[e]) * vsc,
+                                 to_f32<Tag>(R.vb[e]) * vsc, t);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) a[e][i] = bf16x2_to_f16x2(t[i]);
+          }
+        }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int d0 = cv * kVD + 8 * s;
@@ -200,6 +230,47 @@ struct Prefill {
   }
 };
 
+// Mask values (log2 domain) of the lane's 16 scores of a tile: keys
+// key0 + 16 t + i (clamped to the last key) of the lane's mask row, all
+// loads issued before any is used.
+__device__ __forceinline__ void load_mask16(const MfmaParams& p, int64_t mrow, int key0, float mv[16]) {
+  int64_t o[16];
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[4 * t + i] = mrow + static_cast<int64_t>(min(key0 + 16 * t + i, p.N - 1)) * p.m_sn;
+  switch (p.mask_kind) {
+    case QSDPA_BOOL: {
+      const uint8_t* m = static_cast<const uint8_t*>(p.mask);
+      uint8_t x[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) x[e] = m[o[e]];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) mv[e] = x[e] ? 0.0f : -__builtin_huge_valf();
+      break;
+    }
+    case QSDPA_F16:
+    case QSDPA_BF16: {
+      const uint16_t* m = static_cast<const uint16_t*>(p.mask);
+      uint16_t x[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) x[e] = m[o[e]];
+      const bool h = p.mask_kind == QSDPA_F16;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) mv[e] = (h ? f16_bits_to_f32(x[e]) : bf16_bits_to_f32(x[e])) * kLog2e;
+      break;
+    }
+    default: {
+      const float* m = static_cast<const float*>(p.mask);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) mv[e] = m[o[e]];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) mv[e] *= kLog2e;
+      break;
+    }
+  }
+}
+
 // Parameters beyond the decode's: none; the same MfmaParams (q_len > 1).
 template <typename Tag, int D, int BITS, int GS>
 __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(MfmaParams p, int groups_per_head) {
@@ -208,6 +279,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(MfmaParams p, i
   using PG = PGeo<D>;
   using P = Prefill<Tag, D, BITS, GS>;
   __shared__ __attribute__((aligned(16))) uint8_t s_buf[2 * PG::BufBytes];
+  __shared__ float s_red[kPWaves];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -240,46 +312,38 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(MfmaParams p, i
   const int j_base = static_cast<int>(static_cast<int64_t>(split) * T_all / S);
   const int T = static_cast<int>(static_cast<int64_t>(split + 1) * T_all / S) - j_base;
 
-  // The wave's rows: block rb, lane row r -> v = v_first + 32 wave + 16 rb + r.
-  int n_lane[kRB], n_wave[kRB];  // a lane's key limit; the wave's smallest
-  int64_t mrow[kRB];
-  uint32_t qt[kRB][PG::NM][4];
+  // The lane's row: v = v_first + 16 wave + r (clamped to the last real row).
+  int n_lane, n_wave;  // the lane's key limit; the wave's smallest
+  int64_t mrow;
+  uint32_t qt[PG::NM][4];
   {
     const uint8_t* q0 = reinterpret_cast<const uint8_t*>(p.q) +
                         (static_cast<int64_t>(b) * p.q_sb + static_cast<int64_t>(kvh) * p.G * p.q_sh) * 2;
     const rsrc_t rq = make_rsrc(
         q0, static_cast<uint32_t>(((p.G - 1) * p.q_sh + static_cast<int64_t>(p.qL - 1) * p.q_sq) * 2 + D * 2));
+    const int v = v_first + min(16 * wave + r, nrows - 1);
+    const int hq = kvh * p.G + v % p.G, iq = v / p.G;
+    n_lane = p.causal ? min(n_end, max(0, p.N - p.qL + iq + 1)) : n_end;
+    mrow = static_cast<int64_t>(b) * p.m_sb + static_cast<int64_t>(hq) * p.m_sh + static_cast<int64_t>(iq) * p.m_sq;
+    const uint32_t off =
+        static_cast<uint32_t>((static_cast<int64_t>(v % p.G) * p.q_sh + static_cast<int64_t>(iq) * p.q_sq) * 2);
 #pragma unroll
-    for (int rb = 0; rb < kRB; ++rb) {
-      const int v = v_first + min(kPRows * wave + 16 * rb + r, nrows - 1);
-      const int hq = kvh * p.G + v % p.G, iq = v / p.G;
-      n_lane[rb] = p.causal ? min(n_end, max(0, p.N - p.qL + iq + 1)) : n_end;
-      mrow[rb] = static_cast<int64_t>(b) * p.m_sb + static_cast<int64_t>(hq) * p.m_sh +
-                 static_cast<int64_t>(iq) * p.m_sq;
-      const uint32_t off = static_cast<uint32_t>((static_cast<int64_t>(v % p.G) * p.q_sh +
-                                                  static_cast<int64_t>(iq) * p.q_sq) * 2);
-#pragma unroll
-      for (int m = 0; m < PG::NM; ++m) {
-        const u4 x = __builtin_amdgcn_raw_buffer_load_b128(rq, off + (32 * m + 8 * quad) * 2, 0, 0);
-        uint32_t d0 = x[0], d1 = x[1], d2 = x[2], d3 = x[3];
-        if constexpr (Tag::kId == QSDPA_F16 && BITS == 4) {  // the K slice order: dims 0, 4, 1, 5, ...
-          qt[rb][m][0] = perm(d2, d0, 0x05040100u);
-          qt[rb][m][1] = perm(d2, d0, 0x07060302u);
-          qt[rb][m][2] = perm(d3, d1, 0x05040100u);
-          qt[rb][m][3] = perm(d3, d1, 0x07060302u);
-        } else {
-          qt[rb][m][0] = d0; qt[rb][m][1] = d1; qt[rb][m][2] = d2; qt[rb][m][3] = d3;
-        }
+    for (int m = 0; m < PG::NM; ++m) {
+      const u4 x = __builtin_amdgcn_raw_buffer_load_b128(rq, off + (32 * m + 8 * quad) * 2, 0, 0);
+      uint32_t d0 = x[0], d1 = x[1], d2 = x[2], d3 = x[3];
+      if constexpr (Tag::kId == QSDPA_F16 && BITS == 4) {  // the K slice order: dims 0, 4, 1, 5, ...
+        qt[m][0] = perm(d2, d0, 0x05040100u);
+        qt[m][1] = perm(d2, d0, 0x07060302u);
+        qt[m][2] = perm(d3, d1, 0x05040100u);
+        qt[m][3] = perm(d3, d1, 0x07060302u);
+      } else {
+        qt[m][0] = d0; qt[m][1] = d1; qt[m][2] = d2; qt[m][3] = d3;
       }
     }
-  }
-
-#pragma unroll
-  for (int rb = 0; rb < kRB; ++rb) {
-    int m = n_lane[rb];
+    int m = n_lane;
 #pragma unroll
     for (int o = 1; o < 16; o <<= 1) m = min(m, __shfl_xor(m, o));
-    n_wave[rb] = __builtin_amdgcn_readfirstlane(m);
+    n_wave = __builtin_amdgcn_readfirstlane(m);
   }
 
   // K / V descriptors over rows [s0, N) of this (batch, kv head).
@@ -309,100 +373,115 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(MfmaParams p, i
     src.vb_sn = static_cast<uint32_t>(p.vb_sn * 2);
   }
 
-  f4 acc[kRB][PG::NB];
-  float mrun[kRB], lrun[kRB];
+  f4 acc[PG::NB];
 #pragma unroll
-  for (int rb = 0; rb < kRB; ++rb) {
-#pragma unroll
-    for (int i = 0; i < PG::NB; ++i) acc[rb][i] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-    mrun[rb] = kNegBig;
-    lrun[rb] = 0.0f;
-  }
+  for (int i = 0; i < PG::NB; ++i) acc[i] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  float mrun = kNegBig, lrun = 0.0f;
+  float vsc = 1.0f, osc = 1.0f;  // V scale 2^-k in LDS, output scale 2^k (bfloat16)
 
-  // One tile from LDS buffer `buf`, first key s0 + tb0.
-  auto compute = [&](const uint8_t* buf, int tb0) {
-    const uint8_t* kb = buf;
-    const uint8_t* vt = buf + PG::KBytes;
-    // ---- S^T = K Q^T: 4 token blocks x kRB row blocks ----
-    // Steps outer, token blocks inner: consecutive MFMAs feed 4 kRB
-    // independent accumulators instead of waiting on each other's results.
-    f4 S[4][kRB];
+  // Without a mask tensor and with a positive scale, the scale goes inside
+  // the exponent's fma (max(S) q = max(S q) for q > 0).
+  const bool fold = !p.mask && p.qscale > 0.0f;
+  const float ea = fold ? p.qscale : 1.0f;
+
+  // One tile: S^T from buffer `cur` (first key s0 + tb0), the next tile's
+  // dequantization from the register set `Rn` into `nxt` and that set's
+  // reload from row `nrow`, the softmax, then P.V from `cur`.
+  // two_c: P as two float16 terms (std::true_type) or one.
+  auto tile = [&](auto two_c, const uint8_t* cur, uint8_t* nxt, typename P::Raw& Rn, int nrow,
+                  int tb0) __attribute__((always_inline)) {
+    constexpr bool kTwo = decltype(two_c)::value;
+    const int tb = s0 + tb0;
+    float mv[16];
+    if (p.mask) load_mask16(p, mrow, tb + 4 * quad, mv);
+    // ---- S^T = K Q^T ----
+    // The A operands of step m + 1 are read while the MFMAs of step m run
+    // (scheduling fences keep that order: left to itself the compiler
+    // reuses one register set and waits for each read).
+    f4 S4[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) S4[t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    u4 ka[2][4];
+    auto read_k = [&](u4* x, int m) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        x[t] = *reinterpret_cast<const u4*>(cur + (16 * t + r) * PG::KPitch + (32 * m + 8 * quad) * 2);
+    };
+    read_k(ka[0], 0);
+#pragma unroll
+    for (int m = 0; m < PG::NM; ++m) {
+      __builtin_amdgcn_sched_barrier(0);
+      if (m + 1 < PG::NM) read_k(ka[(m + 1) & 1], m + 1);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const u4 x = ka[m & 1][t];
+        const uint32_t a[4] = {x[0], x[1], x[2], x[3]};
+        S4[t] = mfma<Tag>(a, qt[m], S4[t]);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // ---- the next tile: dequantize into the other buffer, reissue its loads ----
+    P::stage(Rn, nxt, tid, vsc);
+    P::load(Rn, src, nrow, tid);
+    // ---- scores: lane (quad, r) holds keys tb + 16 t + 4 quad + i of row r ----
+    float sc[16];
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
-      for (int rb = 0; rb < kRB; ++rb) S[t][rb] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+      for (int i = 0; i < 4; ++i) sc[4 * t + i] = S4[t][i];
+    if (!fold) {
 #pragma unroll
-    for (int m = 0; m < PG::NM; ++m)
+      for (int e = 0; e < 16; ++e) sc[e] *= p.qscale;
+      if (p.mask) {
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const u4 x = *reinterpret_cast<const u4*>(kb + (16 * t + r) * PG::KPitch + (32 * m + 8 * quad) * 2);
-        const uint32_t a[4] = {x[0], x[1], x[2], x[3]};
-#pragma unroll
-        for (int rb = 0; rb < kRB; ++rb) S[t][rb] = mfma<Tag>(a, qt[rb][m], S[t][rb]);
+        for (int e = 0; e < 16; ++e) sc[e] += mv[e];
       }
-    // ---- scores: lane (quad, r) holds tokens 16 t + 4 quad + i of row r ----
-    const int tb = s0 + tb0;
-    uint32_t pb[2][kRB][4], pl[2][kRB][4];  // [half u][row block][pair]
-#pragma unroll
-    for (int rb = 0; rb < kRB; ++rb) {
-      float sc[16];
+    }
+    if (tb + kPTile > n_wave) {  // keys past a row's limit (causal, or the sequence's end)
+      const int lim = n_lane - tb - 4 * quad;  // key tb + 4 quad + k is past the limit when k >= lim
 #pragma unroll
       for (int t = 0; t < 4; ++t)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sc[4 * t + i] = S[t][rb][i] * p.qscale;
-      if (p.mask) {
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int key = min(tb + 16 * t + 4 * quad + i, p.N - 1);
-            sc[4 * t + i] += mask_value(p, mrow[rb] + static_cast<int64_t>(key) * p.m_sn);
-          }
-      }
-      if (tb + kPTile > n_wave[rb]) {  // keys past a row's limit (causal, or the sequence's end)
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            if (tb + 16 * t + 4 * quad + i >= n_lane[rb]) sc[4 * t + i] = -__builtin_huge_valf();
-      }
-      float tmax = sc[0];
-#pragma unroll
-      for (int e = 1; e < 16; ++e) tmax = fmaxf(tmax, sc[e]);
-      tmax = fmaxf(tmax, shfl_xor_f32(tmax, 16));
-      tmax = fmaxf(tmax, shfl_xor_f32(tmax, 32));
-      const bool grow = tmax > mrun[rb] + kRescale;
-      if (__builtin_amdgcn_ballot_w64(grow)) {
-        const float mnew = grow ? tmax : mrun[rb];
-        const float f = fast_exp2(mrun[rb] - mnew);
-        mrun[rb] = mnew;
-        lrun[rb] *= f;
-#pragma unroll
-        for (int i = 0; i < PG::NB; ++i) acc[rb][i] *= f;
-      }
-      float pr[16];
-#pragma unroll
-      for (int e = 0; e < 16; ++e) pr[e] = fast_exp2(sc[e] - mrun[rb]);
-      float sum = 0.0f;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) sum += pr[e];
-      lrun[rb] += sum;
-      // P^T of half u: k slots 2i, 2i + 1 = tokens tau(quad, 2i), tau(quad, 2i + 1):
-      // blocks 2u (i = 0, 1) and 2u + 1 (i = 2, 3).
-#pragma unroll
-      for (int u = 0; u < 2; ++u)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float x0 = pr[4 * (2 * u + (i >> 1)) + 2 * (i & 1)];
-          const float x1 = pr[4 * (2 * u + (i >> 1)) + 2 * (i & 1) + 1];
-          pb[u][rb][i] = pack_T2<Tag>(x0, x1);
-          if constexpr (Tag::kId == QSDPA_BF16)
-            pl[u][rb][i] = pack_T2<Tag>(x0 - unpack_T2_lo<Tag>(pb[u][rb][i]), x1 - unpack_T2_hi<Tag>(pb[u][rb][i]));
-        }
+        for (int i = 0; i < 4; ++i)
+          if (16 * t + i >= lim) sc[4 * t + i] = -__builtin_huge_valf();
     }
-    // ---- out^T += V^T P^T: the half's V^T operands held, then the hi terms
-    // of all dim blocks, then (bfloat16) the lo terms, so no MFMA waits on
-    // the one before it ----
+    float tmax = sc[0];
+#pragma unroll
+    for (int e = 1; e < 16; ++e) tmax = fmaxf(tmax, sc[e]);
+    tmax = fmaxf(tmax, shfl_xor_f32(tmax, 16));
+    tmax = fmaxf(tmax, shfl_xor_f32(tmax, 32));
+    tmax *= ea;
+    const bool grow = tmax > mrun + kRescale;
+    if (__builtin_amdgcn_ballot_w64(grow)) {
+      const float mnew = grow ? tmax : mrun;
+      const float f = fast_exp2(mrun - mnew);
+      mrun = mnew;
+      lrun *= f;
+#pragma unroll
+      for (int i = 0; i < PG::NB; ++i) acc[i] *= f;
+    }
+    const float nm = -mrun;
+    float pr[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) pr[e] = fast_exp2(fmaf(sc[e], ea, nm));
+    float s4[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) s4[t] = (pr[4 * t] + pr[4 * t + 1]) + (pr[4 * t + 2] + pr[4 * t + 3]);
+    lrun += (s4[0] + s4[1]) + (s4[2] + s4[3]);
+    // P^T of half u: k slots 2i, 2i + 1 = tokens tau(quad, 2i), tau(quad, 2i + 1):
+    // blocks 2u (i = 0, 1) and 2u + 1 (i = 2, 3).
+    uint32_t pb[2][4], pl[2][4];
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int e = 4 * (2 * u + (i >> 1)) + 2 * (i & 1);
+        pb[u][i] = pack_T2<F16>(pr[e], pr[e + 1]);
+        if constexpr (kTwo)
+          pl[u][i] = pack_T2<F16>(pr[e] - unpack_T2_lo<F16>(pb[u][i]), pr[e + 1] - unpack_T2_hi<F16>(pb[u][i]));
+      }
+    // ---- out^T += V^T P^T (two terms: the hi terms of all dim blocks, then the lo terms) ----
+    const uint8_t* vt = cur + PG::KBytes;
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       uint32_t a[PG::NB][4];
@@ -410,16 +489,11 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(MfmaParams p, i
       for (int db = 0; db < PG::NB; ++db) {
         const u4 x = *reinterpret_cast<const u4*>(vt + (16 * db + r) * kVPitch + (32 * u + 8 * quad) * 2);
         a[db][0] = x[0]; a[db][1] = x[1]; a[db][2] = x[2]; a[db][3] = x[3];
+        acc[db] = mfma<F16>(a[db], pb[u], acc[db]);
       }
+      if constexpr (kTwo) {
 #pragma unroll
-      for (int db = 0; db < PG::NB; ++db)
-#pragma unroll
-        for (int rb = 0; rb < kRB; ++rb) acc[rb][db] = mfma<Tag>(a[db], pb[u][rb], acc[rb][db]);
-      if constexpr (Tag::kId == QSDPA_BF16) {
-#pragma unroll
-        for (int db = 0; db < PG::NB; ++db)
-#pragma unroll
-          for (int rb = 0; rb < kRB; ++rb) acc[rb][db] = mfma<Tag>(a[db], pl[u][rb], acc[rb][db]);
+        for (int db = 0; db < PG::NB; ++db) acc[db] = mfma<F16>(a[db], pl[u], acc[db]);
       }
     }
   };
@@ -430,76 +504,108 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(MfmaParams p, i
   uint8_t* buf1 = s_buf + PG::BufBytes;
   const int oob = len + 2 * kPTile;  // rows past every descriptor: the loads read zero
   auto row_of = [&](int j) { return j < T ? (j_base + j) * kPTile : oob; };
+  // Keys of tile j; past the split's tiles, the sequence end (every score
+  // masked: an odd tile count's last pair computes one empty tile).
+  auto keys_of = [&](int j) { return j < T ? (j_base + j) * kPTile : len; };
+  auto run = [&](auto two_c) __attribute__((always_inline)) {
+    for (int j = 0; j < T; j += 2) {
+      // tile j in buf0; R1 holds tile j + 1, R0 tile j + 2.
+      tile(two_c, buf0, buf1, R1, row_of(j + 3), keys_of(j));
+      __syncthreads();
+      // tile j + 1 in buf1; R0 holds tile j + 2, R1 tile j + 3.
+      tile(two_c, buf1, buf0, R0, row_of(j + 4), keys_of(j + 1));
+      __syncthreads();
+    }
+  };
   if (T > 0) {
     P::load(R0, src, row_of(0), tid);
     P::load(R1, src, row_of(1), tid);
-    P::stage(R0, buf0, tid);
+    bool two = false;
+    if constexpr (Tag::kId == QSDPA_BF16) {
+      // max |V| of this workgroup's keys: a group's values are affine in
+      // the code, so its largest magnitude is at code 0 or 2^bits - 1.
+      constexpr int NG = D / GS;
+      constexpr float kCodeMax = static_cast<float>((1 << BITS) - 1);
+      float bound = 0.0f;
+      const int t_hi = min((j_base + T) * kPTile, len);
+      for (int t = j_base * kPTile + tid; t < t_hi; t += kPThreads) {
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+          const float sv = bf16_bits_to_f32(
+              __builtin_amdgcn_raw_buffer_load_b16(src.vs, static_cast<uint32_t>(t) * src.vs_sn + 2 * g, 0, 0));
+          const float bv = bf16_bits_to_f32(
+              __builtin_amdgcn_raw_buffer_load_b16(src.vb, static_cast<uint32_t>(t) * src.vb_sn + 2 * g, 0, 0));
+          bound = fmaxf(bound, fmaxf(fabsf(bv), fabsf(fmaf(sv, kCodeMax, bv))));
+        }
+      }
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) bound = fmaxf(bound, shfl_xor_f32(bound, o));
+      if (lane == 0) s_red[wave] = bound;
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < kPWaves; ++i) bound = fmaxf(bound, s_red[i]);
+      two = !(bound <= kPVSingle);
+      if (bound > kVBound) {
+        // k = 1 + floor(log2(bound / kVBound)), so that bound 2^-k < kVBound.
+        const float x = fminf(bound * (1.0f / kVBound), 0x1p100f);
+        const int k = static_cast<int>((__builtin_bit_cast(uint32_t, x) >> 23) & 0xFFu) - 126;
+        vsc = __builtin_bit_cast(float, static_cast<uint32_t>(127 - k) << 23);
+        osc = __builtin_bit_cast(float, static_cast<uint32_t>(127 + k) << 23);
+      }
+    }
+    P::stage(R0, buf0, tid, vsc);
     P::load(R0, src, row_of(2), tid);
     __syncthreads();
-    for (int j = 0; j < T; j += 2) {
-      // tile j in buf0; R1 holds tile j + 1, R0 tile j + 2.
-      if (j + 1 < T) {
-        P::stage(R1, buf1, tid);
-        P::load(R1, src, row_of(j + 3), tid);
-      }
-      compute(buf0, (j_base + j) * kPTile);
-      __syncthreads();
-      if (j + 1 >= T) break;
-      // tile j + 1 in buf1; R0 holds tile j + 2, R1 tile j + 3.
-      if (j + 2 < T) {
-        P::stage(R0, buf0, tid);
-        P::load(R0, src, row_of(j + 4), tid);
-      }
-      compute(buf1, (j_base + j + 1) * kPTile);
-      __syncthreads();
+    if constexpr (Tag::kId == QSDPA_BF16) {
+      if (two) run(std::true_type{});
+      else run(std::false_type{});
+    } else {
+      run(std::false_type{});
     }
   }
 
   // ---- normalise and store: lane (quad, r) holds dims 16 db + 4 quad + i of row r ----
+  float l = lrun;
+  l += shfl_xor_f32(l, 16);
+  l += shfl_xor_f32(l, 32);
+  const int vr = 16 * wave + r;
+  if (vr >= nrows) return;
+  const int v = v_first + vr;
+  const int hq = kvh * p.G + v % p.G, iq = v / p.G;
+  if (S == 1) {
+    const float inv = (l > 0.0f ? 1.0f / l : 0.0f) * osc;
+    uint16_t* dst = p.out + static_cast<int64_t>(b) * p.o_sb + static_cast<int64_t>(hq) * p.o_sh +
+                    static_cast<int64_t>(iq) * p.o_sq + 4 * quad;
 #pragma unroll
-  for (int rb = 0; rb < kRB; ++rb) {
-    float l = lrun[rb];
-    l += shfl_xor_f32(l, 16);
-    l += shfl_xor_f32(l, 32);
-    const int vr = kPRows * wave + 16 * rb + r;
-    if (vr >= nrows) continue;
-    const int v = v_first + vr;
-    const int hq = kvh * p.G + v % p.G, iq = v / p.G;
+    for (int db = 0; db < PG::NB; ++db) {
+      const uint32_t lo = pack_T2<Tag>(acc[db][0] * inv, acc[db][1] * inv);
+      const uint32_t hi = pack_T2<Tag>(acc[db][2] * inv, acc[db][3] * inv);
+      uint16_t* o = dst + 16 * db;  // out rows are only 2-byte aligned in general
+      o[0] = static_cast<uint16_t>(lo);
+      o[1] = static_cast<uint16_t>(lo >> 16);
+      o[2] = static_cast<uint16_t>(hi);
+      o[3] = static_cast<uint16_t>(hi >> 16);
+    }
+  } else {
+    // The split's partial of row (b, hq, iq), column `split`, as the decode
+    // kernel stores it: float16 inputs the normalised row acc / l as
+    // float16, bfloat16 inputs the float32 row; then (m, l).
+    const int64_t slot = ((static_cast<int64_t>(b) * p.Hq + hq) * p.qL + iq) * S + split;
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-    if (S == 1) {
-      uint16_t* dst = p.out + static_cast<int64_t>(b) * p.o_sb + static_cast<int64_t>(hq) * p.o_sh +
-                      static_cast<int64_t>(iq) * p.o_sq + 4 * quad;
 #pragma unroll
-      for (int db = 0; db < PG::NB; ++db) {
-        const uint32_t lo = pack_T2<Tag>(acc[rb][db][0] * inv, acc[rb][db][1] * inv);
-        const uint32_t hi = pack_T2<Tag>(acc[rb][db][2] * inv, acc[rb][db][3] * inv);
-        uint16_t* o = dst + 16 * db;  // out rows are only 2-byte aligned in general
-        o[0] = static_cast<uint16_t>(lo);
-        o[1] = static_cast<uint16_t>(lo >> 16);
-        o[2] = static_cast<uint16_t>(hi);
-        o[3] = static_cast<uint16_t>(hi >> 16);
+    for (int db = 0; db < PG::NB; ++db) {
+      const int d = 16 * db + 4 * quad;
+      if constexpr (Tag::kId == QSDPA_F16) {
+        typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+        *reinterpret_cast<u2*>(reinterpret_cast<uint16_t*>(p.part_acc) + slot * D + d) =
+            u2{pack_T2<Tag>(acc[db][0] * inv, acc[db][1] * inv), pack_T2<Tag>(acc[db][2] * inv, acc[db][3] * inv)};
+      } else {
+        __builtin_nontemporal_store(acc[db] * osc, reinterpret_cast<f4*>(p.part_acc + slot * D + d));
       }
-    } else {
-      // The split's partial of row (b, hq, iq), column `split`, as the
-      // decode kernel stores it: float16 inputs the normalised row acc / l
-      // as float16, bfloat16 inputs the float32 row; then (m, l).
-      const int64_t slot = ((static_cast<int64_t>(b) * p.Hq + hq) * p.qL + iq) * S + split;
-#pragma unroll
-      for (int db = 0; db < PG::NB; ++db) {
-        const int d = 16 * db + 4 * quad;
-        if constexpr (Tag::kId == QSDPA_F16) {
-          typedef uint32_t u2 __attribute__((ext_vector_type(2)));
-          *reinterpret_cast<u2*>(reinterpret_cast<uint16_t*>(p.part_acc) + slot * D + d) =
-              u2{pack_T2<Tag>(acc[rb][db][0] * inv, acc[rb][db][1] * inv),
-                 pack_T2<Tag>(acc[rb][db][2] * inv, acc[rb][db][3] * inv)};
-        } else {
-          __builtin_nontemporal_store(acc[rb][db], reinterpret_cast<f4*>(p.part_acc + slot * D + d));
-        }
-      }
-      if (quad == 0) {
-        p.part_ml[slot * 2] = mrun[rb];
-        p.part_ml[slot * 2 + 1] = l;
-      }
+    }
+    if (quad == 0) {
+      p.part_ml[slot * 2] = mrun;
+      p.part_ml[slot * 2 + 1] = l;
     }
   }
 }

@@ -126,6 +126,44 @@ def test_prefill_kv_start_and_masks(device):
         _check(q, kq, vq, bits, gs, f"additive mask {dtype}", mask=add)
 
 
+@pytest.mark.parametrize("case", [
+    # (shape B, H_q, H_kv, N, L; V scale; scale of 4 outlier channels; tolerance)
+    ((2, 32, 8, 900, 256), 1.0, 8.0, "parity"),          # max |V| ~ 40: P in two float16 terms
+    ((2, 32, 8, 900, 256), 2.0e4, 40.0, "scaled"),       # max |V| ~ 3e6: V staged at 2^-6
+    ((1, 16, 4, 3000, 128), 2.0e4, 40.0, "scaled"),      # the same through key splits
+], ids=["outliers", "beyond_f16", "beyond_f16_splits"])
+def test_prefill_bf16_large_values(device, case):
+    """bfloat16 V with large values.  Past max |V| = 8 the kernel feeds P to
+    the P.V MFMAs as two float16 terms (22 significant bits), and past
+    64000 it stages V in float16 scaled by 2^-k and scales the output (or the
+    float32 partials) back by 2^k.  With outlier channels the parity bar
+    holds; at |V| ~ 1e6 no float P meets an absolute 2e-3 where outputs
+    cancel, so the bar there is 2^-20 max|V| (22-bit P moves an output by up to
+    2^-22 max|V|) plus the relative 1e-2: a wrong scale would miss it by
+    orders of magnitude."""
+    (B, Hq, Hkv, N, L), vmul, omul, tol = case
+    g = torch.Generator(device="cpu").manual_seed(21)
+    q = torch.randn(B, Hq, L, 128, generator=g).bfloat16().to(device)
+    kw = torch.randn(B, Hkv, N, 128, generator=g)
+    vw = torch.randn(B, Hkv, N, 128, generator=g) * vmul
+    vw[..., :4] *= omul
+    kq = kernels.quantize(kw.bfloat16().to(device), 64, 8)
+    vq = kernels.quantize(vw.bfloat16().to(device), 64, 8)
+    print(f"prefill bf16 large V {case}", flush=True)
+    if tol == "parity":
+        _check(q, kq, vq, 8, 64, f"large V {case}", causal=True)
+        return
+    out = kernels.decode(q, kq[0], vq[0], kq[1], vq[1], kq[2], vq[2], scale=128 ** -0.5, bits=8, group_size=64,
+                         causal=True)
+    keep = torch.arange(N, device=device)[None, :] <= (N - L) + torch.arange(L, device=device)[:, None]
+    want = to.quantized_sdpa(q, kq, vq, bits=8, group_size=64, scale=128 ** -0.5, mask=keep[None, None])
+    vmax = float(kernels.dequantize(vq[0], vq[1], vq[2], 64, 8).float().abs().max())
+    err = (out.double() - want).abs()
+    bound = 2.0 ** -20 * vmax + RTOL * want.abs()
+    assert bool(torch.isfinite(out).all())
+    assert bool((err <= bound).all()), f"{case}: max err {float(err.max()):.4g} (max |V| {vmax:.3g})"
+
+
 def test_prefill_repeatable(device):
     """Repeated calls give bit-identical outputs."""
     q, kq, vq = _inputs(4, 16, 4, 4096, 512, 8, 128, torch.bfloat16, seed=5)
