@@ -20,8 +20,9 @@
 //              with the tokens of each 32-token half in the order of the S^T
 //              fragment so that the P^T operand is a lane's own softmax
 //              values -- and reissues that register set's loads for tile
-//              j + 3; the dequantization's VALU work has no dependence on
-//              the QK MFMAs and runs beside them;
+//              j + 3.  Waves 4-7 do this after their QK MFMAs, waves 0-3
+//              after their P.V, so that the two waves of a SIMD alternate
+//              MFMA and VALU phases (120 against 124 us at the C5 chunk);
 //   softmax    online, in the log2 domain, rescaled when the maximum grows
 //              by more than 8 (the decode kernel's); without a mask tensor
 //              the score scale is applied inside the exponent's fma;
@@ -60,7 +61,7 @@ constexpr int kPWaves = 8;
 constexpr int kPThreads = kPWaves * 64;
 constexpr int kPTile = 64;                   // tokens per tile
 constexpr int kPGroupRows = kPWaves * 16;    // query rows per workgroup
-constexpr int kVPitch = kPTile * 2 + 16;     // bytes per V^T row (dim) in LDS
+constexpr int kVPitch = kPTile * 2 + 32;     // bytes per V^T row (dim) in LDS
 constexpr int kMaxPrefillSplits = 64;
 constexpr float kVBound = 64000.0f;          // largest |V| staged in float16 unscaled
 // bfloat16 inputs: the largest max |V| for which P enters the P.V MFMAs as
@@ -69,9 +70,14 @@ constexpr float kVBound = 64000.0f;          // largest |V| staged in float16 un
 // max|V| in the random tests), so one term keeps 2e-3 for |V| <= 8.
 constexpr float kPVSingle = 8.0f;
 
+// LDS rows are padded by 32 bytes.  Measured at the C5 chunk: with 16-byte
+// padding (K 272 B, V^T 144 B per row) the 16-byte operand reads of the 16
+// rows of an MFMA block spend 1.8e7 bank-conflict cycles per call, with 32
+// bytes 2.0e6, and the kernel takes 121-123 us instead of 129-130; 48 and
+// 64 bytes conflict like 16.
 template <int D>
 struct PGeo {
-  static constexpr int KPitch = D * 2 + 16;        // bytes per K row (token) in LDS
+  static constexpr int KPitch = D * 2 + 32;        // bytes per K row (token) in LDS
   static constexpr int KBytes = kPTile * KPitch;
   static constexpr int VBytes = D * kVPitch;
   static constexpr int BufBytes = KBytes + VBytes;
@@ -156,25 +162,28 @@ struct Prefill {
   // Issue the loads of the tile whose first token is `rel0` tokens past the
   // sequence's first key (rows past the end read as zero).
   static __device__ __forceinline__ void load(Raw& R, const Src& s, int rel0, int tid) {
-    const uint32_t kt = static_cast<uint32_t>(rel0 + tid / kKPT);
+    // Offsets: the tile's row times the row stride (uniform, scalar) plus
+    // the thread's fixed part.
+    const uint32_t row = static_cast<uint32_t>(rel0);
+    const uint32_t kt = static_cast<uint32_t>(tid / kKPT);
     const int c = tid % kKPT;
-    load_words<Raw::KW>(s.k, kt * s.k_sn + static_cast<uint32_t>(c * Raw::KW * 4), R.k);
+    load_words<Raw::KW>(s.k, row * s.k_sn + (kt * s.k_sn + static_cast<uint32_t>(c * Raw::KW * 4)), R.k);
     const uint32_t g0 = static_cast<uint32_t>(c * kQD / GS);
     if constexpr (kKG == 2) {
-      R.ks = __builtin_amdgcn_raw_buffer_load_b32(s.ks, kt * s.ks_sn + g0 * 2, 0, 0);
-      R.kb = __builtin_amdgcn_raw_buffer_load_b32(s.kb, kt * s.kb_sn + g0 * 2, 0, 0);
+      R.ks = __builtin_amdgcn_raw_buffer_load_b32(s.ks, row * s.ks_sn + (kt * s.ks_sn + g0 * 2), 0, 0);
+      R.kb = __builtin_amdgcn_raw_buffer_load_b32(s.kb, row * s.kb_sn + (kt * s.kb_sn + g0 * 2), 0, 0);
     } else {
-      R.ks = __builtin_amdgcn_raw_buffer_load_b16(s.ks, kt * s.ks_sn + g0 * 2, 0, 0);
-      R.kb = __builtin_amdgcn_raw_buffer_load_b16(s.kb, kt * s.kb_sn + g0 * 2, 0, 0);
+      R.ks = __builtin_amdgcn_raw_buffer_load_b16(s.ks, row * s.ks_sn + (kt * s.ks_sn + g0 * 2), 0, 0);
+      R.kb = __builtin_amdgcn_raw_buffer_load_b16(s.kb, row * s.kb_sn + (kt * s.kb_sn + g0 * 2), 0, 0);
     }
     const int pr = tid & 31, cv = tid >> 5;
     const uint32_t gv = static_cast<uint32_t>(cv * kVD / GS);
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
-      const uint32_t vt = static_cast<uint32_t>(rel0 + 2 * pr + e);
-      load_words<Raw::VW>(s.v, vt * s.v_sn + static_cast<uint32_t>(cv * Raw::VW * 4), R.v[e]);
-      R.vs[e] = __builtin_amdgcn_raw_buffer_load_b16(s.vs, vt * s.vs_sn + gv * 2, 0, 0);
-      R.vb[e] = __builtin_amdgcn_raw_buffer_load_b16(s.vb, vt * s.vb_sn + gv * 2, 0, 0);
+      const uint32_t vt = static_cast<uint32_t>(2 * pr + e);
+      load_words<Raw::VW>(s.v, row * s.v_sn + (vt * s.v_sn + static_cast<uint32_t>(cv * Raw::VW * 4)), R.v[e]);
+      R.vs[e] = __builtin_amdgcn_raw_buffer_load_b16(s.vs, row * s.vs_sn + (vt * s.vs_sn + gv * 2), 0, 0);
+      R.vb[e] = __builtin_amdgcn_raw_buffer_load_b16(s.vb, row * s.vb_sn + (vt * s.vb_sn + gv * 2), 0, 0);
     }
   }
 
@@ -420,9 +429,13 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(MfmaParams p, i
       }
     }
     __builtin_amdgcn_sched_barrier(0);
-    // ---- the next tile: dequantize into the other buffer, reissue its loads ----
-    P::stage(Rn, nxt, tid, vsc);
-    P::load(Rn, src, nrow, tid);
+    // ---- the next tile: dequantize into the other buffer, reissue its loads
+    // (waves 4-7 here, waves 0-3 after the P.V: the two waves of a SIMD then
+    // alternate MFMA and VALU phases) ----
+    if (wave >= 4) {
+      P::stage(Rn, nxt, tid, vsc);
+      P::load(Rn, src, nrow, tid);
+    }
     // ---- scores: lane (quad, r) holds keys tb + 16 t + 4 quad + i of row r ----
     float sc[16];
 #pragma unroll
@@ -495,6 +508,10 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(MfmaParams p, i
 #pragma unroll
         for (int db = 0; db < PG::NB; ++db) acc[db] = mfma<F16>(a[db], pl[u], acc[db]);
       }
+    }
+    if (wave < 4) {
+      P::stage(Rn, nxt, tid, vsc);
+      P::load(Rn, src, nrow, tid);
     }
   };
 
