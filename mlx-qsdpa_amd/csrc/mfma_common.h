@@ -149,16 +149,40 @@ __device__ __forceinline__ f4 mfma(const uint32_t a[4], const uint32_t b[4], f4 
                                                    0, 0, 0);
 }
 
-__device__ __forceinline__ float mask_value(const MfmaParams& p, int64_t o) {
+// Mask values (log2 domain) at element offsets o[0..N) of the mask tensor:
+// every load is issued before any is used, so a caller that issues them
+// ahead of its next tile's loads waits for them alone.
+template <int N>
+__device__ __forceinline__ void mask_values(const MfmaParams& p, const int64_t (&o)[N], float (&mv)[N]) {
   switch (p.mask_kind) {
-    case QSDPA_BOOL:
-      return static_cast<const uint8_t*>(p.mask)[o] ? 0.0f : -__builtin_huge_valf();
+    case QSDPA_BOOL: {
+      const uint8_t* m = static_cast<const uint8_t*>(p.mask);
+      uint8_t x[N];
+#pragma unroll
+      for (int e = 0; e < N; ++e) x[e] = m[o[e]];
+#pragma unroll
+      for (int e = 0; e < N; ++e) mv[e] = x[e] ? 0.0f : -__builtin_huge_valf();
+      break;
+    }
     case QSDPA_F16:
-      return f16_bits_to_f32(static_cast<const uint16_t*>(p.mask)[o]) * kLog2e;
-    case QSDPA_BF16:
-      return bf16_bits_to_f32(static_cast<const uint16_t*>(p.mask)[o]) * kLog2e;
-    default:
-      return static_cast<const float*>(p.mask)[o] * kLog2e;
+    case QSDPA_BF16: {
+      const uint16_t* m = static_cast<const uint16_t*>(p.mask);
+      uint16_t x[N];
+#pragma unroll
+      for (int e = 0; e < N; ++e) x[e] = m[o[e]];
+      const bool h = p.mask_kind == QSDPA_F16;
+#pragma unroll
+      for (int e = 0; e < N; ++e) mv[e] = (h ? f16_bits_to_f32(x[e]) : bf16_bits_to_f32(x[e])) * kLog2e;
+      break;
+    }
+    default: {
+      const float* m = static_cast<const float*>(p.mask);
+#pragma unroll
+      for (int e = 0; e < N; ++e) mv[e] = m[o[e]];
+#pragma unroll
+      for (int e = 0; e < N; ++e) mv[e] *= kLog2e;
+      break;
+    }
   }
 }
 

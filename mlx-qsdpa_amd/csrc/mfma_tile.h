@@ -231,6 +231,15 @@ struct Kernel {
                                                       f4 (&acc)[G::NB], float& mrun, float& lrun, int tb, int n0,
                                                       int n1, int quad, int64_t mrow, const VMetaLane& vm,
                                                       IK&& issue_k, IV&& issue_v) {
+    // Mask values of the lane's 8 keys, loaded before the next tile's K
+    // loads are issued, so waiting for them does not wait for those.
+    float mv[8];
+    if (p.mask) {
+      int64_t o[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[j] = mrow + static_cast<int64_t>(min(tb + tau(quad, j), p.N - 1)) * p.m_sn;
+      mask_values<8>(p, o, mv);
+    }
     // ---- S^T = K Q^T (Q^T operand m: 16 B per lane, in registers) ----
     f4 S[2];
 #pragma unroll
@@ -244,10 +253,7 @@ struct Kernel {
     for (int j = 0; j < 8; ++j) sc[j] = S[j >> 2][j & 3] * p.qscale;
     if (p.mask) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int t = min(tb + tau(quad, j), p.N - 1);
-        sc[j] += mask_value(p, mrow + static_cast<int64_t>(t) * p.m_sn);
-      }
+      for (int j = 0; j < 8; ++j) sc[j] += mv[j];
     }
     if (__builtin_expect(tb + kTile > n1 || tb < n0, 0)) {  // a partial tile
 #pragma unroll

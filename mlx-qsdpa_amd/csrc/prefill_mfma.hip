@@ -240,44 +240,14 @@ struct Prefill {
 };
 
 // Mask values (log2 domain) of the lane's 16 scores of a tile: keys
-// key0 + 16 t + i (clamped to the last key) of the lane's mask row, all
-// loads issued before any is used.
+// key0 + 16 t + i (clamped to the last key) of the lane's mask row.
 __device__ __forceinline__ void load_mask16(const MfmaParams& p, int64_t mrow, int key0, float mv[16]) {
   int64_t o[16];
 #pragma unroll
   for (int t = 0; t < 4; ++t)
 #pragma unroll
     for (int i = 0; i < 4; ++i) o[4 * t + i] = mrow + static_cast<int64_t>(min(key0 + 16 * t + i, p.N - 1)) * p.m_sn;
-  switch (p.mask_kind) {
-    case QSDPA_BOOL: {
-      const uint8_t* m = static_cast<const uint8_t*>(p.mask);
-      uint8_t x[16];
-#pragma unroll
-      for (int e = 0; e < 16; ++e) x[e] = m[o[e]];
-#pragma unroll
-      for (int e = 0; e < 16; ++e) mv[e] = x[e] ? 0.0f : -__builtin_huge_valf();
-      break;
-    }
-    case QSDPA_F16:
-    case QSDPA_BF16: {
-      const uint16_t* m = static_cast<const uint16_t*>(p.mask);
-      uint16_t x[16];
-#pragma unroll
-      for (int e = 0; e < 16; ++e) x[e] = m[o[e]];
-      const bool h = p.mask_kind == QSDPA_F16;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) mv[e] = (h ? f16_bits_to_f32(x[e]) : bf16_bits_to_f32(x[e])) * kLog2e;
-      break;
-    }
-    default: {
-      const float* m = static_cast<const float*>(p.mask);
-#pragma unroll
-      for (int e = 0; e < 16; ++e) mv[e] = m[o[e]];
-#pragma unroll
-      for (int e = 0; e < 16; ++e) mv[e] *= kLog2e;
-      break;
-    }
-  }
+  mask_values<16>(p, o, *reinterpret_cast<float(*)[16]>(mv));
 }
 
 // Parameters beyond the decode's: none; the same MfmaParams (q_len > 1).
