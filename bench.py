@@ -72,6 +72,9 @@ def parse_args(argv=None):
     ap.add_argument("--qlen", type=int, default=1,
                     help="query positions per call; > 1 times causal multi-query attention "
                          "(fused vs dequantize + attention) instead of the decode step")
+    ap.add_argument("--mask", default="none", choices=["none", "bool", "additive"],
+                    help="with --qlen: pass the causal mask as a [B, 1, qL, N] tensor (bool, or additive "
+                         "in the input type with random values on the kept keys) instead of the flag")
     ap.add_argument("--rotating-prefill", action="store_true",
                     help="time C5's prefill chunk (--qlen, default 512) through the batched rotating "
                          "cache: requant + attention")
@@ -380,15 +383,26 @@ def run_multi_query(args) -> int:
     g.manual_seed(args.seed + 1)
     qs = [torch.randn((B, Hq, L, D), generator=g, device=device, dtype=torch.float32).to(T)
           for _ in range(n_sets)]
+    # The causal mask as a flag, or (--mask) as a tensor the kernels read per score.
+    mask = None
+    if args.mask != "none":
+        keep = torch.arange(N, device=device)[None, :] <= (N - L) + torch.arange(L, device=device)[:, None]
+        keep = keep[None, None].expand(B, 1, L, N)
+        if args.mask == "bool":
+            mask = keep.contiguous()
+        else:
+            noise = torch.randn((B, 1, L, N), generator=g, device=device, dtype=torch.float32)
+            mask = torch.where(keep, noise, torch.full_like(noise, float("-inf"))).to(T)
     plans = [kernels.DecodePlan(qq, kq[0], vq[0], kq[1], vq[1], kq[2], vq[2], scale=D ** -0.5,
-                                bits=bits, group_size=gs, num_splits=args.splits, causal=True)
+                                bits=bits, group_size=gs, num_splits=args.splits, mask=mask,
+                                causal=mask is None)
              for qq, (_, kq, vq) in zip(qs, sets)]
     splits = plans[0].num_splits
 
     def fallback(i):
         _, kq, vq = sets[i]
         return dispatch.fallback_sdpa(qs[i], kq, vq, bits=bits, group_size=gs, scale=D ** -0.5,
-                                      mask="causal")
+                                      mask="causal" if mask is None else mask)
 
     got = plans[0]().float()
     want = fallback(0).float()
@@ -424,11 +438,12 @@ def run_multi_query(args) -> int:
     flops = 4.0 * B * Hq * pairs * D
     tflops = flops / (kern_us * 1e-6) / 1e12
     peak = 2500.0  # dense fp16 / bf16 MFMA
-    print(f"bench: {args.config} qL={L} causal: fused {us:.2f} us/call wall, kernel {kern_us:.2f} us "
+    mname = "causal" if mask is None else f"causal, {args.mask} mask tensor"
+    print(f"bench: {args.config} qL={L} {mname}: fused {us:.2f} us/call wall, kernel {kern_us:.2f} us "
           f"({tflops:.1f} TFLOP/s); dequantize + attention {fb_us:.2f} us; max |diff| {max_diff:.2e}",
           file=sys.stderr, flush=True)
     workload = (f"{args.config}-q{L}: causal attention B={B} H_q={Hq} H_kv={Hkv} D={D} {bits}-bit "
-                f"gs={gs} {dt} N={N} qL={L}")
+                f"gs={gs} {dt} N={N} qL={L}" + ("" if mask is None else f" ({args.mask} mask tensor)"))
     line = {
         "metric": f"µs per attention call, {L} causal query positions (fused vs dequantize + attention)",
         "value": round(us, 3), "unit": "us/call", "n_gpus": 1, "steps": args.steps,
@@ -566,8 +581,17 @@ def main(argv=None) -> int:
     print(f"bench: config={args.config} N={N} sets={n_sets} ({kv_set_bytes / 1e6:.1f} MB each)",
           file=sys.stderr, flush=True)
     sets = make_sets(cfg, N, n_sets, device, args.seed)
+    # --mask: a [B, 1, 1, N] mask tensor the kernel reads per score (bool: 10% of the keys
+    # dropped; additive: random values in the input type).
+    mask = None
+    if args.mask != "none":
+        gm = torch.Generator(device=device)
+        gm.manual_seed(args.seed + 2)
+        r = torch.rand((B, 1, 1, N), generator=gm, device=device)
+        T = torch.float16 if dt == "f16" else torch.bfloat16
+        mask = (r >= 0.1) if args.mask == "bool" else torch.randn((B, 1, 1, N), generator=gm, device=device).to(T)
     plans = [kernels.DecodePlan(q, kq[0], vq[0], kq[1], vq[1], kq[2], vq[2], scale=D ** -0.5,
-                                bits=bits, group_size=gs, num_splits=args.splits)
+                                bits=bits, group_size=gs, num_splits=args.splits, mask=mask)
              for q, kq, vq in sets]
     splits = plans[0].num_splits
 
@@ -621,7 +645,7 @@ def main(argv=None) -> int:
     def api(i):
         q, kq, vq = sets[i % n_sets]
         return mq.quantized_sdpa(q, kq[0], vq[0], kq[1], vq[1], kq[2], vq[2], scale=D ** -0.5,
-                                 bits=bits, group_size=gs)
+                                 bits=bits, group_size=gs, mask=mask)
 
     for i in range(max(args.warmup, 2)):
         api(i)
@@ -643,7 +667,7 @@ def main(argv=None) -> int:
           f"splits={splits}", file=sys.stderr, flush=True)
 
     cpu = None
-    if args.cpu_seconds > 0:
+    if args.cpu_seconds > 0 and mask is None:  # the CPU baseline times the unmasked workload
         host = tuple(x.cpu().numpy() if x.dtype == torch.uint32 else x.float().cpu().numpy()
                      for x in (sets[0][0],))
         kq = tuple(x.cpu().numpy() if x.dtype == torch.uint32 else x.float().cpu().numpy()
@@ -652,8 +676,10 @@ def main(argv=None) -> int:
                    for x in sets[0][2])
         cpu = cpu_baseline(cfg, N, (host[0], kq, vq), args.cpu_seconds)
 
-    ref_us = REFERENCE_US.get(N) if args.config == "c3" else None
+    ref_us = REFERENCE_US.get(N) if args.config == "c3" and mask is None else None
     workload = f"{args.config}: decode B={B} H_q={Hq} H_kv={Hkv} D={D} {bits}-bit gs={gs} {dt} N={N}"
+    if mask is not None:
+        workload += f" ({args.mask} mask tensor)"
     traffic = measured_traffic(workload)
     line = {
         "metric": METRIC,

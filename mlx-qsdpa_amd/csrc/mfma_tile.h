@@ -223,10 +223,11 @@ struct Kernel {
 
   // One tile: QK, online softmax, PV.  Keys t of the tile (first key tb)
   // outside [n0, n1) are masked (the sequence's first and last tiles may be
-  // partial).  The next tile's K loads are issued (issue_k) as soon as this
+  // partial); MASK: a mask tensor adds its values (a kernel of its own, so
+  // the unmasked kernel carries none of its code).  The next tile's K loads are issued (issue_k) as soon as this
   // tile's K has been consumed, and its V loads (issue_v) once V is in the PV
   // operands' pre-permuted form, so one register set suffices.
-  template <typename IK, typename IV>
+  template <bool MASK, typename IK, typename IV>
   static __device__ __forceinline__ void compute_tile(Regs& R, const MfmaParams& p, const uint32_t (&qt)[G::NM][4],
                                                       f4 (&acc)[G::NB], float& mrun, float& lrun, int tb, int n0,
                                                       int n1, int quad, int64_t mrow, const VMetaLane& vm,
@@ -234,7 +235,7 @@ struct Kernel {
     // Mask values of the lane's 8 keys, loaded before the next tile's K
     // loads are issued, so waiting for them does not wait for those.
     float mv[8];
-    if (p.mask) {
+    if constexpr (MASK) {
       int64_t o[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) o[j] = mrow + static_cast<int64_t>(min(tb + tau(quad, j), p.N - 1)) * p.m_sn;
@@ -251,7 +252,7 @@ struct Kernel {
     float sc[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) sc[j] = S[j >> 2][j & 3] * p.qscale;
-    if (p.mask) {
+    if constexpr (MASK) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) sc[j] += mv[j];
     }
