@@ -453,8 +453,57 @@ __global__ __launch_bounds__(512) void stream_read_kernel(const u4* src, uint64_
   }
   if (acc == 0x9e3779b9u) sink[blockIdx.x] = acc;  // keeps the loads; the sink is almost never written
 }
+
+// The same with W-byte loads (4, 8 or 16 per lane) and P of them per thread
+// in flight: equal bytes in flight with more, narrower load instructions.
+template <int W, int P>
+__global__ __launch_bounds__(512) void stream_read_w_kernel(const uint8_t* src, uint64_t n, uint32_t* sink) {
+  typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+  const uint64_t share = (n + gridDim.x - 1) / gridDim.x;
+  const uint64_t lo = blockIdx.x * share;
+  const uint64_t hi = lo + share < n ? lo + share : n;
+  uint32_t acc = 0;
+  for (uint64_t i = lo + threadIdx.x; i < hi; i += static_cast<uint64_t>(P) * 512) {
+    uint32_t x[P];
+#pragma unroll
+    for (int k = 0; k < P; ++k) {
+      const uint64_t j = i + static_cast<uint64_t>(k) * 512;
+      if constexpr (W == 16) {
+        const u4 v = j < hi ? __builtin_nontemporal_load(reinterpret_cast<const u4*>(src) + j) : u4{0u, 0u, 0u, 0u};
+        x[k] = v[0] ^ v[1] ^ v[2] ^ v[3];
+      } else if constexpr (W == 8) {
+        const u2 v = j < hi ? __builtin_nontemporal_load(reinterpret_cast<const u2*>(src) + j) : u2{0u, 0u};
+        x[k] = v[0] ^ v[1];
+      } else {
+        x[k] = j < hi ? __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(src) + j) : 0u;
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < P; ++k) acc ^= x[k];
+  }
+  if (acc == 0x9e3779b9u) sink[blockIdx.x] = acc;
+}
 }  // namespace
 }  // namespace qsdpa
+
+// W-byte variant: `bytes` a multiple of 16, width 4 / 8 / 16, per 4 / 8 / 16 / 32.
+extern "C" int qsdpa_debug_stream_read_w(const void* src, uint64_t bytes, void* sink, int blocks, int width, int per,
+                                         void* stream, void* ev_begin, void* ev_end) {
+  if (!src || !sink || blocks < 1 || bytes % 16) return -1;
+  void (*k)(const uint8_t*, uint64_t, uint32_t*) = nullptr;
+#define QSDPA_SRW(w, p) \
+  if (width == w && per == p) k = qsdpa::stream_read_w_kernel<w, p>;
+  QSDPA_SRW(4, 4) QSDPA_SRW(4, 8) QSDPA_SRW(4, 16) QSDPA_SRW(4, 32)
+  QSDPA_SRW(8, 4) QSDPA_SRW(8, 8) QSDPA_SRW(8, 16) QSDPA_SRW(8, 32)
+  QSDPA_SRW(16, 4) QSDPA_SRW(16, 8) QSDPA_SRW(16, 16) QSDPA_SRW(16, 32)
+#undef QSDPA_SRW
+  if (!k) return -1;
+  hipExtLaunchKernelGGL(k, dim3(blocks), dim3(512), 0, static_cast<hipStream_t>(stream),
+                        static_cast<hipEvent_t>(ev_begin), static_cast<hipEvent_t>(ev_end), 0,
+                        static_cast<const uint8_t*>(src), static_cast<uint64_t>(bytes / width),
+                        static_cast<uint32_t*>(sink));
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
 
 // Launch the streaming probe over `bytes` (a multiple of 16) with `blocks`
 // workgroups of 512 threads; ev_begin / ev_end (hipEvent_t) ride on the dispatch.

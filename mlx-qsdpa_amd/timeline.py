@@ -140,9 +140,52 @@ def stream(config: str, n: int | None, calls: int, lib_path: Path = LIB, blocks=
               f"{100 * nbytes / med / 1e6 / 8:.1f} |")
 
 
+def stream_width(config: str, n: int | None, calls: int, lib_path: Path = LIB, blocks: int = 256) -> None:
+    """Equal bytes in flight per thread, read with 16-, 8- or 4-byte loads
+    (the probe library's stream_read_w kernel): does the read rate follow
+    the bytes or the load instructions in flight?"""
+    for p in (ROOT, HERE):
+        sys.path.insert(0, str(p))
+    import numpy as np
+    import torch
+
+    import bench
+    from mlx_qsdpa_amd import _lib, metric
+
+    lib = _lib.load(lib_path)
+    f = lib.qsdpa_debug_stream_read_w
+    f.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                  ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+    f.restype = ctypes.c_int
+    cfg = bench.CONFIGS[config]
+    B, Hq, Hkv, D, bits, gs, dt, N0, _ = cfg
+    N = n or N0
+    nbytes = metric.decode_bytes(B, Hq, Hkv, D, bits, gs, B * N) // 16 * 16
+    n_sets = max(2, int(1.2e9 // nbytes) + 1)
+    dev = torch.device("cuda:0")
+    bufs = [torch.ones(nbytes, dtype=torch.uint8, device=dev) for _ in range(n_sets)]
+    sink = torch.zeros(4096, dtype=torch.int32, device=dev)
+    stream_h = torch.cuda.current_stream(dev).cuda_stream
+    hip = bench.HipEvents()
+    print(f"# {config}: {nbytes} bytes read per launch, {n_sets} buffers cycled, {blocks} workgroups x 512 threads")
+    print("| load bytes | loads per thread in flight | KB in flight per workgroup | median us | TB/s |")
+    print("|---|---|---|---|---|")
+    for width, per in ((16, 4), (8, 8), (4, 16), (16, 8), (8, 16), (4, 32), (16, 16), (8, 32)):
+        ev = hip.create(2 * calls)
+        for i in range(calls + 5):
+            e = (ev[2 * (i - 5)], ev[2 * (i - 5) + 1]) if i >= 5 else (None, None)
+            if f(bufs[i % n_sets].data_ptr(), nbytes, sink.data_ptr(), blocks, width, per, stream_h, *e) != 0:
+                raise SystemExit("qsdpa_debug_stream_read_w failed")
+        torch.cuda.synchronize()
+        us = np.array([hip.elapsed_ms(ev[2 * i], ev[2 * i + 1]) * 1e3 for i in range(calls)])
+        hip.destroy(ev)
+        med = float(np.median(us))
+        print(f"| {width} | {per} | {512 * width * per // 1024} | {med:.2f} | {nbytes / med / 1e6:.2f} |", flush=True)
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
-    ap.add_argument("what", choices=["build", "run", "stream"])
+    ap.add_argument("what", choices=["build", "run", "stream", "stream-width"])
     ap.add_argument("--config", default="c3", choices=["c1", "c2", "c3", "c5"])
     ap.add_argument("--n", type=int, default=None)
     ap.add_argument("--calls", type=int, default=40)
@@ -152,6 +195,8 @@ def main(argv=None) -> int:
         build()
     elif a.what == "stream":
         stream(a.config, a.n, a.calls, Path(a.lib))
+    elif a.what == "stream-width":
+        stream_width(a.config, a.n, a.calls, Path(a.lib))
     else:
         run(a.config, a.n, a.calls, Path(a.lib))
     return 0
