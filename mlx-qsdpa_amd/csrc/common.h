@@ -69,6 +69,28 @@ __device__ __forceinline__ float shfl_xor_f32(float x, int mask) {
       float, __builtin_amdgcn_ds_bpermute((lane ^ mask) << 2, __builtin_bit_cast(int, x)));
 }
 
+// Max of x over lanes i, i ^ 16, i ^ 32 and i ^ 48 (the four 16-lane rows)
+// with gfx950's row swaps: VALU instructions, where a ds_bpermute goes
+// through the LDS and waits for it.  Inline assembly, because this compiler
+// has folded both halves of its permlane swap builtin's result into one
+// register when both inputs were one value.  The s_nops give each swap two wait states after a
+// VALU write of its operands and each v_max two after the swap.
+__device__ __forceinline__ float max_over_rows(float x) {
+  float a = x, b = x;
+  asm volatile(
+      "s_nop 1\n\t"
+      "v_permlane16_swap_b32 %0, %1\n\t"
+      "s_nop 1\n\t"
+      "v_max_f32 %0, %0, %1\n\t"
+      "v_mov_b32 %1, %0\n\t"
+      "s_nop 1\n\t"
+      "v_permlane32_swap_b32 %0, %1\n\t"
+      "s_nop 1\n\t"
+      "v_max_f32 %0, %0, %1"
+      : "+v"(a), "+v"(b));
+  return a;
+}
+
 // Sum over aligned groups of G consecutive lanes; every lane of a group gets
 // the bitwise-identical total (each step adds symmetric partners).
 template <int G>

@@ -22,10 +22,17 @@
 //              values -- and reissues that register set's loads for tile
 //              j + 3.  Waves 4-7 do this after their QK MFMAs, waves 0-3
 //              after their P.V, so that the two waves of a SIMD alternate
-//              MFMA and VALU phases (120 against 124 us at the C5 chunk);
+//              MFMA and VALU phases (120 against 124 us at the C5 chunk).
+//              The SIMD's arbiter favours the older wave (0-3), which left
+//              waves 4-7 the longer path per tile (their dequantization
+//              contends with the other wave's softmax): they raise their
+//              priority from their dequantization to the end of the tile
+//              (117 against 121 us);
 //   softmax    online, in the log2 domain, rescaled when the maximum grows
 //              by more than 8 (the decode kernel's); without a mask tensor
-//              the score scale is applied inside the exponent's fma;
+//              the score scale is applied inside the exponent's fma; the
+//              tile maximum over a row's four lanes by row swaps (VALU)
+//              rather than LDS permutes;
 //   PV         out^T += V^T P^T in float16 (A = V^T rows from LDS, B = P^T);
 //   barrier    one per tile: it orders this tile's reads of buffer j % 2
 //              before the next tile's writes of it.
@@ -403,6 +410,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(MfmaParams p, i
     // (waves 4-7 here, waves 0-3 after the P.V: the two waves of a SIMD then
     // alternate MFMA and VALU phases) ----
     if (wave >= 4) {
+      __builtin_amdgcn_s_setprio(1);  // back to 0 at the end of the tile
       P::stage(Rn, nxt, tid, vsc);
       P::load(Rn, src, nrow, tid);
     }
@@ -431,9 +439,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(MfmaParams p, i
     float tmax = sc[0];
 #pragma unroll
     for (int e = 1; e < 16; ++e) tmax = fmaxf(tmax, sc[e]);
-    tmax = fmaxf(tmax, shfl_xor_f32(tmax, 16));
-    tmax = fmaxf(tmax, shfl_xor_f32(tmax, 32));
-    tmax *= ea;
+    tmax = max_over_rows(tmax) * ea;
     const bool grow = tmax > mrun + kRescale;
     if (__builtin_amdgcn_ballot_w64(grow)) {
       const float mnew = grow ? tmax : mrun;
@@ -482,6 +488,8 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(MfmaParams p, i
     if (wave < 4) {
       P::stage(Rn, nxt, tid, vsc);
       P::load(Rn, src, nrow, tid);
+    } else {
+      __builtin_amdgcn_s_setprio(0);
     }
   };
 
