@@ -186,6 +186,27 @@ __device__ __forceinline__ void mask_values(const MfmaParams& p, const int64_t (
   }
 }
 
+// Mask values of a lane's keys key0 + off(e), e < N (off: a pattern of
+// constants), clamped to the last key.  `whole`: every key of the tile is
+// below N.  Then, with adjacent keys in the mask (key stride 1), the offsets
+// are one base plus constants, which the loads carry as immediate offsets;
+// otherwise every key's offset is computed and clamped (64-bit products).
+template <int N, typename Off>
+__device__ __forceinline__ void mask_tile(const MfmaParams& p, int64_t mrow, int key0, bool whole, Off&& off,
+                                          float (&mv)[N]) {
+  int64_t o[N];
+  if (whole && p.m_sn == 1) {
+    const int64_t o0 = mrow + key0;
+#pragma unroll
+    for (int e = 0; e < N; ++e) o[e] = o0 + off(e);
+    mask_values<N>(p, o, mv);
+  } else {
+#pragma unroll
+    for (int e = 0; e < N; ++e) o[e] = mrow + static_cast<int64_t>(min(key0 + off(e), p.N - 1)) * p.m_sn;
+    mask_values<N>(p, o, mv);
+  }
+}
+
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 
 // Raw buffer descriptor (gfx9 dword3: 32-bit data format, no swizzle).

@@ -235,12 +235,8 @@ struct Kernel {
     // Mask values of the lane's 8 keys, loaded before the next tile's K
     // loads are issued, so waiting for them does not wait for those.
     float mv[8];
-    if constexpr (MASK) {
-      int64_t o[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) o[j] = mrow + static_cast<int64_t>(min(tb + tau(quad, j), p.N - 1)) * p.m_sn;
-      mask_values<8>(p, o, mv);
-    }
+    if constexpr (MASK)
+      mask_tile<8>(p, mrow, tb + 4 * quad, tb + kTile <= p.N, [](int j) { return tau(0, j); }, mv);
     // ---- S^T = K Q^T (Q^T operand m: 16 B per lane, in registers) ----
     f4 S[2];
 #pragma unroll
