@@ -222,7 +222,8 @@ int qsdpa_dequantize(const qsdpa_dequantize_args* args, void* stream);
  *   dequantized as qsdpa_dequantize does (T(fmaf(scale, q, bias)));
  *   new token i is src row i;
  *   each kept row is quantized as qsdpa_quantize does.
- * The destination must not overlap the old window.
+ * The destination must not overlap the old window.  The jobs of one call
+ * share B, H, bits, group_size and dtype.
  * Replaces the dequantize + concatenate + trim + quantize of
  * mlx_qsdpa/cache.py:593-634 (QuantizedRotatingSDPACache._update_prefill,
  * _dequant_temporal) and cache.py:813-857 (the batched cache's).

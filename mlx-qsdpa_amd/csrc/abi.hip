@@ -327,8 +327,9 @@ int qsdpa_requant_window(const qsdpa_requant_args* jobs, int32_t count, void* st
   if (!jobs) return fail(QSDPA_ERR_INVALID, "null args");
   if (count < 1 || count > 2) return fail(QSDPA_ERR_INVALID, "count must be 1 or 2, got %d", count);
   for (int i = 1; i < count; ++i)
-    if (jobs[i].bits != jobs[0].bits || jobs[i].group_size != jobs[0].group_size || jobs[i].dtype != jobs[0].dtype)
-      return fail(QSDPA_ERR_INVALID, "requant jobs of one call must share bits, group_size and dtype");
+    if (jobs[i].bits != jobs[0].bits || jobs[i].group_size != jobs[0].group_size || jobs[i].dtype != jobs[0].dtype ||
+        jobs[i].B != jobs[0].B || jobs[i].H != jobs[0].H)
+      return fail(QSDPA_ERR_INVALID, "requant jobs of one call must share B, H, bits, group_size and dtype");
   const qsdpa_requant_args* ptrs[2];
   for (int i = 0; i < count; ++i) {
     const qsdpa_requant_args* a = jobs + i;

@@ -257,27 +257,33 @@ struct RequantJobs {
 
 template <typename Tag, int BITS, int GS>
 __global__ __launch_bounds__(256) void requant_kernel(RequantJobs jobs) {
+  // Grid: x over the rows' (row, group, lane) triples of one (batch, head),
+  // y = batch * H + head, z = job; the launcher keeps x's count in 32 bits.
   constexpr int L = GS / 8;  // lanes per group, 8 values each
   constexpr int PER = 32 / BITS;
   constexpr uint32_t kMask = (1u << BITS) - 1u;
-  const RequantParams& p = jobs.p[blockIdx.y];
-  const int ng = p.D / GS;
-  const int64_t groups = static_cast<int64_t>(p.B) * p.H * p.total * ng;
-  const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const int64_t grp = gid / L;
+  const RequantParams& p = jobs.p[blockIdx.z];
+  const uint32_t ng = static_cast<uint32_t>(p.D / GS);
+  const uint32_t gid = blockIdx.x * 256u + threadIdx.x;
+  const uint32_t grp = gid / L;
   const int part = static_cast<int>(gid % L);
-  if (grp >= groups) return;
+  if (grp >= static_cast<uint32_t>(p.total) * ng) return;
   const int g = static_cast<int>(grp % ng);
-  int64_t row = grp / ng;
-  const int t = static_cast<int>(row % p.total);
-  row /= p.total;
-  const int h = static_cast<int>(row % p.H);
-  const int b = static_cast<int>(row / p.H);
+  const int t = static_cast<int>(grp / ng);
+  const int b = static_cast<int>(blockIdx.y) / p.H;
+  const int h = static_cast<int>(blockIdx.y) % p.H;
   const int c = t < p.keep ? t : t + p.drop;
   const int d0 = g * GS + part * 8;  // the lane's first dim
   uint16_t raw[8];
   if (c < p.n_old) {
-    const int u = (c < p.keep || p.rot == 0) ? c : p.keep + (c - p.keep + p.rot) % (p.n_old - p.keep);
+    // Ring row of combined token c: c - keep + rot < 2 (n_old - keep), so one
+    // conditional subtraction is the modulo.
+    int u = c;
+    if (c >= p.keep && p.rot != 0) {
+      u = c - p.keep + p.rot;
+      if (u >= p.n_old - p.keep) u -= p.n_old - p.keep;
+      u += p.keep;
+    }
     const float sc = to_f32<Tag>(p.os[off3(b, h, u, p.os_sb, p.os_sh, p.os_sn) + g]);
     const float bi = p.ob ? to_f32<Tag>(p.ob[off3(b, h, u, p.ob_sb, p.ob_sh, p.ob_sn) + g]) : 0.0f;
     const uint32_t* words = p.op + off3(b, h, u, p.op_sb, p.op_sh, p.op_sn) + d0 / PER;
@@ -388,13 +394,15 @@ int launch_requant(const qsdpa_requant_args* const* jobs, int count, hipStream_t
     p.c_sb = a->dst_scales.stride_b; p.c_sh = a->dst_scales.stride_h; p.c_sn = a->dst_scales.stride_n;
     p.db = static_cast<uint16_t*>(const_cast<void*>(a->dst_biases.ptr));
     p.z_sb = a->dst_biases.stride_b; p.z_sh = a->dst_biases.stride_h; p.z_sn = a->dst_biases.stride_n;
-    most = std::max<int64_t>(most, static_cast<int64_t>(a->B) * a->H * p.total * (a->D / a->group_size));
+    most = std::max<int64_t>(most, static_cast<int64_t>(p.total) * (a->D / a->group_size));
   }
-  if (most == 0) return QSDPA_OK;
-  const int lanes = a0->group_size / 8;
-  const int64_t blocks = (most * lanes + 255) / 256;
-  if (blocks >= (int64_t(1) << 31)) return fail(QSDPA_ERR_UNSUPPORTED, "requant: window too large");
-  const dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>(count));
+  if (most == 0 || a0->B * a0->H == 0) return QSDPA_OK;
+  // Lanes of one (batch, head): rows x groups x GS / 8.
+  const int64_t lanes = most * (a0->group_size / 8);
+  if (lanes + 255 >= (int64_t(1) << 32) || a0->B * a0->H > 65535)
+    return fail(QSDPA_ERR_UNSUPPORTED, "requant: window too large");
+  const dim3 grid(static_cast<unsigned>((lanes + 255) / 256), static_cast<unsigned>(a0->B * a0->H),
+                  static_cast<unsigned>(count));
   auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, dim3(256), 0, stream, j); };
   const bool f16 = a0->dtype == QSDPA_F16;
   const int gs = a0->group_size, bits = a0->bits;

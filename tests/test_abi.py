@@ -98,6 +98,9 @@ def test_invalid_arguments_return_codes():
     assert lib.qsdpa_requant_window(r, 2, None) == _lib.QSDPA_ERR_INVALID
     assert b"share" in lib.qsdpa_last_error()
     assert lib.qsdpa_requant_window(r, 3, None) == _lib.QSDPA_ERR_INVALID
+    r[1].bits, r[1].H = 4, 2  # K and V of one cache: same batch and heads
+    assert lib.qsdpa_requant_window(r, 2, None) == _lib.QSDPA_ERR_INVALID
+    assert b"share B, H" in lib.qsdpa_last_error()
     m = (_lib.RowMove * 2)()
     for x in m:
         x.dst, x.heads, x.tokens, x.row_bytes = 64, 2, 4, 16
