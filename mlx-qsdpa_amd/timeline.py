@@ -3,6 +3,8 @@
   python mlx-qsdpa_amd/timeline.py build               # here (hipcc): the probe library
   python mlx-qsdpa_amd/timeline.py run [--config c3]    # on the GPU
   python mlx-qsdpa_amd/timeline.py stream [--config c3] # on the GPU: a read-only launch of the same bytes
+  python mlx-qsdpa_amd/timeline.py prefill [--qlen 512] # on the GPU: the prefill kernel's phases at C5
+  python mlx-qsdpa_amd/timeline.py lds                  # on the GPU: LDS read rate of the prefill pattern
 
 ``build`` compiles the library with -DQSDPA_TIMELINE into
 mlx_qsdpa_amd/libqsdpa_timeline.so: the same kernels, plus an s_memrealtime
@@ -11,6 +13,12 @@ qsdpa_debug_timeline().  ``run`` times the bench.py workload of a config
 (synthetic K/V cycled over enough sets to stream from HBM) and prints, for
 each point, the spread over the grid's waves in microseconds from the first
 wave's entry, plus the median per wave slot (0-7) of the workgroup.
+
+``prefill`` runs C5's causal chunk (bench.py's workload, the causal flag) on the
+probe build's prefill kernel and prints, per wave slot, the mean shader-clock
+cycles per tile of its three phases (start of tile to row maxima, row maxima to
+end of tile, barrier); ``lds`` times the probe build's LDS read kernel (the
+prefill kernel's K / V^T operand reads, one workgroup per CU).
 
 Points: entry; Q staged in LDS (after the workgroup barrier); k-th tile
 done; stream end (the wave's last tile); partials merged in LDS (after the
@@ -183,12 +191,101 @@ def stream_width(config: str, n: int | None, calls: int, lib_path: Path = LIB, b
         print(f"| {width} | {per} | {512 * width * per // 1024} | {med:.2f} | {nbytes / med / 1e6:.2f} |", flush=True)
 
 
+def prefill(qlen: int, calls: int, lib_path: Path = LIB) -> None:
+    """Per-wave phase cycles of the prefill kernel at C5's causal chunk."""
+    for p in (ROOT, HERE):
+        sys.path.insert(0, str(p))
+    import numpy as np
+    import torch
+
+    import bench
+    from mlx_qsdpa_amd import _lib, kernels, metric
+
+    lib = _lib.load(lib_path)
+    _lib._lib = lib  # the kernels module launches through this library
+    lib.qsdpa_debug_prefill_phases.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+    lib.qsdpa_debug_prefill_phases.restype = ctypes.c_int
+    cfg = bench.CONFIGS["c5"]
+    B, Hq, Hkv, D, bits, gs, dt, N, _ = cfg
+    dev = torch.device("cuda:0")
+    n_sets = max(2, int(1.2e9 // (B * N * metric.kv_bytes_per_token(Hkv, D, bits, gs))) + 1)
+    sets = bench.make_sets(cfg, N, n_sets, dev, 0)
+    g = torch.Generator(device=dev)
+    g.manual_seed(1)
+    plans = [kernels.DecodePlan(torch.randn((B, Hq, qlen, D), generator=g, device=dev).bfloat16(), kq[0], vq[0],
+                                kq[1], vq[1], kq[2], vq[2], scale=D ** -0.5, bits=bits, group_size=gs, causal=True)
+             for _, kq, vq in sets]
+    hip = bench.HipEvents()
+    ev = hip.create(2 * calls)
+    for i in range(calls):
+        plans[i % n_sets]((ev[2 * i], ev[2 * i + 1]))
+    torch.cuda.synchronize()
+    ev_us = [hip.elapsed_ms(ev[2 * i], ev[2 * i + 1]) * 1e3 for i in range(calls)]
+    hip.destroy(ev)
+    groups = (Hq // Hkv * qlen + 127) // 128
+    nwg = groups * Hkv * B * plans[0].num_splits
+    buf = np.zeros(4096 * 8 * 4, dtype=np.uint64)
+    if lib.qsdpa_debug_prefill_phases(buf.ctypes.data, buf.nbytes) != 0:
+        raise SystemExit("qsdpa_debug_prefill_phases failed")
+    t = buf[: nwg * 32].reshape(nwg, 8, 4).astype(np.float64)
+    n = t[:, :, 3]
+    ok = n > 1
+    print(f"# c5 causal chunk qL={qlen}: {nwg} workgroups x 8 waves, last of {calls} calls; kernel "
+          f"{ev_us[-1]:.1f} us (median {np.median(ev_us):.1f}); tiles per wave {n[ok].mean():.1f}")
+    print("| wave | start -> row maxima | row maxima -> end | barrier | cycles per tile |")
+    print("|---|---|---|---|---|")
+    for w in range(8):
+        m = ok[:, w]
+        a = (t[m, w, 0] / n[m, w]).mean()
+        c = (t[m, w, 1] / n[m, w]).mean()
+        d = (t[m, w, 2] / (n[m, w] - 1)).mean()
+        print(f"| {w} | {a:.0f} | {c:.0f} | {d:.0f} | {a + c + d:.0f} |")
+
+
+def lds(calls: int, lib_path: Path = LIB, blocks: int = 256, iters: int = 2000) -> None:
+    """LDS read rate of the prefill kernel's operand pattern."""
+    for p in (ROOT, HERE):
+        sys.path.insert(0, str(p))
+    import numpy as np
+    import torch
+
+    import bench
+    from mlx_qsdpa_amd import _lib
+
+    lib = _lib.load(lib_path)
+    f = lib.qsdpa_debug_lds_read
+    f.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                  ctypes.c_void_p]
+    f.restype = ctypes.c_int
+    dev = torch.device("cuda:0")
+    sink = torch.zeros(blocks, dtype=torch.int32, device=dev)
+    cyc = torch.zeros(1, dtype=torch.int64, device=dev)
+    stream_h = torch.cuda.current_stream(dev).cuda_stream
+    hip = bench.HipEvents()
+    ev = hip.create(2 * calls)
+    for i in range(calls + 2):
+        e = (ev[2 * (i - 2)], ev[2 * (i - 2) + 1]) if i >= 2 else (None, None)
+        if f(blocks, iters, sink.data_ptr(), cyc.data_ptr(), stream_h, *e) != 0:
+            raise SystemExit("qsdpa_debug_lds_read failed")
+    torch.cuda.synchronize()
+    us = float(np.median([hip.elapsed_ms(ev[2 * i], ev[2 * i + 1]) * 1e3 for i in range(calls)]))
+    hip.destroy(ev)
+    per_wg = iters * 8 * 32 * 1024  # bytes one workgroup reads: 8 waves x 32 KB per iteration
+    cycles = int(cyc.item())
+    print(f"# {blocks} workgroups x 512 threads, {iters} iterations of 32 KB per wave (16 K + 16 V^T reads of "
+          f"16 B per lane)")
+    print(f"median {us:.1f} us per launch: {per_wg / us / 1e3:.1f} GB/s per CU, {per_wg * blocks / us / 1e6:.1f} TB/s "
+          f"chip; workgroup 0: {cycles} s_memtime cycles, {per_wg / cycles:.1f} B per cycle "
+          f"({cycles / iters:.0f} cycles per 256 KB iteration)")
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
-    ap.add_argument("what", choices=["build", "run", "stream", "stream-width"])
+    ap.add_argument("what", choices=["build", "run", "stream", "stream-width", "prefill", "lds"])
     ap.add_argument("--config", default="c3", choices=["c1", "c2", "c3", "c5"])
     ap.add_argument("--n", type=int, default=None)
     ap.add_argument("--calls", type=int, default=40)
+    ap.add_argument("--qlen", type=int, default=512, help="prefill: query positions of the chunk")
     ap.add_argument("--lib", default=str(LIB), help="probe library to run (default: the one `build` makes)")
     a = ap.parse_args(argv)
     if a.what == "build":
@@ -197,6 +294,10 @@ def main(argv=None) -> int:
         stream(a.config, a.n, a.calls, Path(a.lib))
     elif a.what == "stream-width":
         stream_width(a.config, a.n, a.calls, Path(a.lib))
+    elif a.what == "prefill":
+        prefill(a.qlen, a.calls, Path(a.lib))
+    elif a.what == "lds":
+        lds(a.calls, Path(a.lib))
     else:
         run(a.config, a.n, a.calls, Path(a.lib))
     return 0
