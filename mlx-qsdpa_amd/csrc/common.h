@@ -91,6 +91,19 @@ __device__ __forceinline__ float max_over_rows(float x) {
   return a;
 }
 
+// Max of 8 floats in four instructions (three v_max3_f32, one v_max_f32).
+// Inline assembly: in IEEE mode the compiler puts a canonicalizing v_max in
+// front of fmaxf for every input it cannot prove canonical (MFMA results,
+// selects), which more than doubles the count.
+__device__ __forceinline__ float max8(const float (&x)[8]) {
+  float a, b, c, m;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(a) : "v"(x[0]), "v"(x[1]), "v"(x[2]));
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(b) : "v"(x[3]), "v"(x[4]), "v"(x[5]));
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(c) : "v"(x[6]), "v"(x[7]), "v"(a));
+  asm("v_max_f32 %0, %1, %2" : "=v"(m) : "v"(b), "v"(c));
+  return m;
+}
+
 // Sum over aligned groups of G consecutive lanes; every lane of a group gets
 // the bitwise-identical total (each step adds symmetric partners).
 template <int G>

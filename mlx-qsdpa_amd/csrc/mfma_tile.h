@@ -259,10 +259,7 @@ struct Kernel {
         if (t >= n1 || t < n0) sc[j] = -__builtin_huge_valf();
       }
     }
-    float tmax = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])),
-                       fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
-    tmax = fmaxf(tmax, shfl_xor_f32(tmax, 16));
-    tmax = fmaxf(tmax, shfl_xor_f32(tmax, 32));
+    const float tmax = max_over_rows(max8(sc));
     const bool grow = tmax > mrun + kRescale;
     if (__builtin_amdgcn_ballot_w64(grow)) {
       const float mnew = grow ? tmax : mrun;
