@@ -166,6 +166,10 @@ __device__ __forceinline__ void decode_segment(const MfmaParams& p, float* s_acc
   L.v_r = r * G::VW * 4 + 4 * quad * rs.v_sn;
   L.vs_r = vword * 4 + r * rs.vs_sn;
   L.vb_r = vword * 4 + r * rs.vb_sn;
+  // Opaque to the optimizer: seeing r * stride inside, it folds a load's
+  // uniform row * stride + L into a per-lane (row + r) * stride, one
+  // quarter-rate v_mul_lo_u32 per load and tile.
+  asm("" : "+v"(L.k_r), "+v"(L.ks_r), "+v"(L.kb_r), "+v"(L.v_r), "+v"(L.vs_r), "+v"(L.vb_r));
   // Token tau(quad, j) of a half sits in row 4*quad + (j & 3); its meta word
   // gv / 2 was loaded by quad gv / 2.
   VMetaLane vm;

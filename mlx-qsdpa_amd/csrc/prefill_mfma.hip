@@ -188,33 +188,52 @@ struct Prefill {
   struct Src {
     rsrc_t k, v, ks, vs, kb, vb;
     uint32_t k_sn, v_sn, ks_sn, vs_sn, kb_sn, vb_sn;  // bytes per token
+    uint32_t k_l, ks_l, kb_l, v_l[2], vs_l[2], vb_l[2];  // the thread's fixed byte offsets
   };
 
-  // Issue the loads of the tile whose first token is `rel0` tokens past the
-  // sequence's first key (rows past the end read as zero).
-  static __device__ __forceinline__ void load(Raw& R, const Src& s, int rel0, int tid) {
-    // Offsets: the tile's row times the row stride (uniform, scalar) plus
-    // the thread's fixed part.
-    const uint32_t row = static_cast<uint32_t>(rel0);
+  // The thread's fixed part of every load offset (its token in the tile
+  // times the stride, plus its dims), once per kernel.  Opaque to the
+  // optimizer: seeing token * stride inside, it folds a load's uniform
+  // row * stride + offset into a per-lane (row + token) * stride, one
+  // quarter-rate v_mul_lo_u32 per load and tile.
+  static __device__ __forceinline__ void lanes(Src& s, int tid) {
     const uint32_t kt = static_cast<uint32_t>(tid / kKPT);
     const int c = tid % kKPT;
-    load_words<Raw::KW>(s.k, row * s.k_sn + (kt * s.k_sn + static_cast<uint32_t>(c * Raw::KW * 4)), R.k);
     const uint32_t g0 = static_cast<uint32_t>(c * kQD / GS);
-    if constexpr (kKG == 2) {
-      R.ks = __builtin_amdgcn_raw_buffer_load_b32(s.ks, row * s.ks_sn + (kt * s.ks_sn + g0 * 2), 0, 0);
-      R.kb = __builtin_amdgcn_raw_buffer_load_b32(s.kb, row * s.kb_sn + (kt * s.kb_sn + g0 * 2), 0, 0);
-    } else {
-      R.ks = __builtin_amdgcn_raw_buffer_load_b16(s.ks, row * s.ks_sn + (kt * s.ks_sn + g0 * 2), 0, 0);
-      R.kb = __builtin_amdgcn_raw_buffer_load_b16(s.kb, row * s.kb_sn + (kt * s.kb_sn + g0 * 2), 0, 0);
-    }
+    s.k_l = kt * s.k_sn + static_cast<uint32_t>(c * Raw::KW * 4);
+    s.ks_l = kt * s.ks_sn + g0 * 2;
+    s.kb_l = kt * s.kb_sn + g0 * 2;
     const int pr = tid & 31, cv = tid >> 5;
     const uint32_t gv = static_cast<uint32_t>(cv * kVD / GS);
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
       const uint32_t vt = static_cast<uint32_t>(2 * pr + e);
-      load_words<Raw::VW>(s.v, row * s.v_sn + (vt * s.v_sn + static_cast<uint32_t>(cv * Raw::VW * 4)), R.v[e]);
-      R.vs[e] = __builtin_amdgcn_raw_buffer_load_b16(s.vs, row * s.vs_sn + (vt * s.vs_sn + gv * 2), 0, 0);
-      R.vb[e] = __builtin_amdgcn_raw_buffer_load_b16(s.vb, row * s.vb_sn + (vt * s.vb_sn + gv * 2), 0, 0);
+      s.v_l[e] = vt * s.v_sn + static_cast<uint32_t>(cv * Raw::VW * 4);
+      s.vs_l[e] = vt * s.vs_sn + gv * 2;
+      s.vb_l[e] = vt * s.vb_sn + gv * 2;
+    }
+    asm("" : "+v"(s.k_l), "+v"(s.ks_l), "+v"(s.kb_l), "+v"(s.v_l[0]), "+v"(s.v_l[1]));
+    asm("" : "+v"(s.vs_l[0]), "+v"(s.vs_l[1]), "+v"(s.vb_l[0]), "+v"(s.vb_l[1]));
+  }
+
+  // Issue the loads of the tile whose first token is `rel0` tokens past the
+  // sequence's first key (rows past the end read as zero): the tile's row
+  // times the row stride (uniform, scalar) plus the thread's fixed part.
+  static __device__ __forceinline__ void load(Raw& R, const Src& s, int rel0) {
+    const uint32_t row = static_cast<uint32_t>(rel0);
+    load_words<Raw::KW>(s.k, row * s.k_sn + s.k_l, R.k);
+    if constexpr (kKG == 2) {
+      R.ks = __builtin_amdgcn_raw_buffer_load_b32(s.ks, row * s.ks_sn + s.ks_l, 0, 0);
+      R.kb = __builtin_amdgcn_raw_buffer_load_b32(s.kb, row * s.kb_sn + s.kb_l, 0, 0);
+    } else {
+      R.ks = __builtin_amdgcn_raw_buffer_load_b16(s.ks, row * s.ks_sn + s.ks_l, 0, 0);
+      R.kb = __builtin_amdgcn_raw_buffer_load_b16(s.kb, row * s.kb_sn + s.kb_l, 0, 0);
+    }
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      load_words<Raw::VW>(s.v, row * s.v_sn + s.v_l[e], R.v[e]);
+      R.vs[e] = __builtin_amdgcn_raw_buffer_load_b16(s.vs, row * s.vs_sn + s.vs_l[e], 0, 0);
+      R.vb[e] = __builtin_amdgcn_raw_buffer_load_b16(s.vb, row * s.vb_sn + s.vb_l[e], 0, 0);
     }
   }
 
@@ -372,6 +391,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(MfmaParams p, i
     src.vs_sn = static_cast<uint32_t>(p.vs_sn * 2);
     src.kb_sn = static_cast<uint32_t>(p.kb_sn * 2);
     src.vb_sn = static_cast<uint32_t>(p.vb_sn * 2);
+    P::lanes(src, tid);
   }
 
   f4 acc[PG::NB];
@@ -435,7 +455,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(MfmaParams p, i
     if (wave >= 4) {
       __builtin_amdgcn_s_setprio(1);  // back to 0 at the end of the tile
       P::stage(Rn, nxt, tid, vsc);
-      P::load(Rn, src, nrow, tid);
+      P::load(Rn, src, nrow);
     }
     // ---- scores: lane (quad, r) holds keys tb + 16 t + 4 quad + i of row r ----
     float sc[16];
@@ -514,7 +534,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(MfmaParams p, i
     }
     if (wave < 4) {
       P::stage(Rn, nxt, tid, vsc);
-      P::load(Rn, src, nrow, tid);
+      P::load(Rn, src, nrow);
     } else {
       __builtin_amdgcn_s_setprio(0);
     }
@@ -545,8 +565,8 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(MfmaParams p, i
     }
   };
   if (T > 0) {
-    P::load(R0, src, row_of(0), tid);
-    P::load(R1, src, row_of(1), tid);
+    P::load(R0, src, row_of(0));
+    P::load(R1, src, row_of(1));
     bool two = false;
     if constexpr (Tag::kId == QSDPA_BF16) {
       // max |V| of this workgroup's keys: a group's values are affine in
@@ -581,7 +601,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(MfmaParams p, i
       }
     }
     P::stage(R0, buf0, tid, vsc);
-    P::load(R0, src, row_of(2), tid);
+    P::load(R0, src, row_of(2));
     __syncthreads();
     if constexpr (Tag::kId == QSDPA_BF16) {
       if (two) run(std::true_type{});
