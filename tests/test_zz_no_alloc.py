@@ -25,16 +25,16 @@ pytestmark = pytest.mark.gpu
 ATOL, RTOL = 2e-3, 1e-2
 
 
-def _inputs(rng, B, Hq, Hkv, N, D, bits, gs, dt, device):
+def _inputs(rng, B, Hq, Hkv, N, D, bits, gs, dt, device, qL=1):
     T = torch_dtype(dt)
-    q = affine.random_T(rng, (B, Hq, 1, D), dt)
+    q = affine.random_T(rng, (B, Hq, qL, D), dt)
     kq = affine.quantize(affine.random_T(rng, (B, Hkv, N, D), dt), gs, bits, dt)
     vq = affine.quantize(affine.random_T(rng, (B, Hkv, N, D), dt), gs, bits, dt)
     dev = lambda x: from_np(x, T, device)  # noqa: E731  (uint32 arrays keep their type)
     return (q, kq, vq), (dev(q), tuple(map(dev, kq)), tuple(map(dev, vq)))
 
 
-def _run_both(host, devt, bits, gs, dt, kv_start=None, num_splits=0):
+def _run_both(host, devt, bits, gs, dt, kv_start=None, num_splits=0, causal=False):
     """qsdpa_decode (with a workspace) and qsdpa_decode_noalloc on the same
     inputs; returns both outputs and the split count."""
     lib = _lib.load()
@@ -44,7 +44,7 @@ def _run_both(host, devt, bits, gs, dt, kv_start=None, num_splits=0):
     for noalloc in (False, True):
         out = torch.full_like(q, float("nan"))
         a, keep = kernels._decode_args(q, kq[0], vq[0], kq[1], vq[1], kq[2], vq[2], out, D ** -0.5, bits, gs,
-                                       None, kv_start, num_splits)
+                                       None, kv_start, num_splits, causal=causal)
         n = ctypes.c_int32(0)
         ws = _lib.check(lib.qsdpa_decode_workspace_size(ctypes.byref(a), ctypes.byref(n)))
         stream = torch.cuda.current_stream(q.device).cuda_stream
@@ -102,6 +102,27 @@ def test_noalloc_streamk_schedule_and_single_pass(device):
     assert np.all(np.abs(got - want) <= ATOL + RTOL * np.abs(want))
     ref, got, splits = _run_both(host, devt, bits, gs, dt, num_splits=1)
     assert splits == 1 and np.array_equal(got, ref)
+
+
+def test_noalloc_prefill_key_splits(device):
+    """Several query positions per kv head on the prefill kernel with key
+    splits (float32 partials of many rows in the scratch, merged by the row
+    merge), then a smaller chunk on the same scratch."""
+    rng = np.random.default_rng(125)
+    cases = [
+        # (B, Hq, Hkv, N, qL, D, bits, gs, dtype)
+        (1, 16, 4, 3000, 128, 128, 8, 128, "bf16"),   # 16 row groups: 11 key splits
+        (1, 8, 2, 1500, 64, 128, 4, 64, "f16"),       # smaller: 4 row groups, float16 partial rows
+    ]
+    for case in cases:
+        B, Hq, Hkv, N, qL, D, bits, gs, dt = case
+        host, devt = _inputs(rng, B, Hq, Hkv, N, D, bits, gs, dt, device, qL=qL)
+        ref, got, splits = _run_both(host, devt, bits, gs, dt, causal=True)
+        assert splits > 1, f"{case}: expected key splits"
+        assert np.array_equal(got, ref), f"{case}: noalloc output differs from qsdpa_decode"
+        want = _oracle(host, bits, gs, dt, mask="causal")  # aligned to the last key
+        err = np.abs(got - want)
+        assert np.all(err <= ATOL + RTOL * np.abs(want)), f"{case}: max err {err.max():.3e}"
 
 
 def test_noalloc_refuses_partials_beyond_the_scratch(device):
