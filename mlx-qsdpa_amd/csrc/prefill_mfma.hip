@@ -573,17 +573,29 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(MfmaParams p, i
       // the code, so its largest magnitude is at code 0 or 2^bits - 1.
       constexpr int NG = D / GS;
       constexpr float kCodeMax = static_cast<float>((1 << BITS) - 1);
+      // Eight rows per thread in flight (rows past the range read the
+      // range's first row again: no effect on the maximum).
+      constexpr int kRows = 8;
       float bound = 0.0f;
-      const int t_hi = min((j_base + T) * kPTile, len);
-      for (int t = j_base * kPTile + tid; t < t_hi; t += kPThreads) {
+      const int t_lo = j_base * kPTile, t_hi = min((j_base + T) * kPTile, len);
+      for (int t0 = t_lo + tid; t0 < t_hi; t0 += kRows * kPThreads) {
+        uint16_t sv[kRows][NG], bv[kRows][NG];
 #pragma unroll
-        for (int g = 0; g < NG; ++g) {
-          const float sv = bf16_bits_to_f32(
-              __builtin_amdgcn_raw_buffer_load_b16(src.vs, static_cast<uint32_t>(t) * src.vs_sn + 2 * g, 0, 0));
-          const float bv = bf16_bits_to_f32(
-              __builtin_amdgcn_raw_buffer_load_b16(src.vb, static_cast<uint32_t>(t) * src.vb_sn + 2 * g, 0, 0));
-          bound = fmaxf(bound, fmaxf(fabsf(bv), fabsf(fmaf(sv, kCodeMax, bv))));
+        for (int u = 0; u < kRows; ++u) {
+          const int t = t0 + u * kPThreads < t_hi ? t0 + u * kPThreads : t_lo;
+#pragma unroll
+          for (int g = 0; g < NG; ++g) {
+            sv[u][g] = __builtin_amdgcn_raw_buffer_load_b16(src.vs, static_cast<uint32_t>(t) * src.vs_sn + 2 * g, 0, 0);
+            bv[u][g] = __builtin_amdgcn_raw_buffer_load_b16(src.vb, static_cast<uint32_t>(t) * src.vb_sn + 2 * g, 0, 0);
+          }
         }
+#pragma unroll
+        for (int u = 0; u < kRows; ++u)
+#pragma unroll
+          for (int g = 0; g < NG; ++g) {
+            const float s = bf16_bits_to_f32(sv[u][g]), b = bf16_bits_to_f32(bv[u][g]);
+            bound = fmaxf(bound, fmaxf(fabsf(b), fabsf(fmaf(s, kCodeMax, b))));
+          }
       }
 #pragma unroll
       for (int o = 1; o < 64; o <<= 1) bound = fmaxf(bound, shfl_xor_f32(bound, o));
