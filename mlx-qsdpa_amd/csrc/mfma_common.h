@@ -137,6 +137,48 @@ __device__ __forceinline__ void dequant_k(const uint32_t* w, uint32_t s2, uint32
   }
 }
 
+// bfloat16 inputs: the 8 values (dims in order, float32, not yet rounded to
+// T) of an 8-dim slice.  A 16-bit half whose bits are a code c < 1024 is the
+// float16 value c 2^-24 (a subnormal), so one mask or v_perm_b32 places two
+// codes, and v_fma_mix_f32 (float32 fma of a float16 half, widened exactly)
+// gives (c 2^-24)(s 2^24) + b, the value and the one rounding of fmaf(c, s,
+// b), without a v_cvt_f32_ubyte per code.  S = s 2^24, and for 4-bit codes
+// S16 = s 2^20 (the odd nibbles of a byte are read as 16 c).  Exact while S
+// is finite: callers keep |s| below kMixScaleMax.
+constexpr float kMixScaleMax = 0x1p100f;
+
+template <int H>
+__device__ __forceinline__ float fma_half(uint32_t t, float S, float B) {
+  return fmaf(static_cast<float>(__builtin_bit_cast(f16x2, t)[H]), S, B);
+}
+template <int BITS>
+__device__ __forceinline__ void mix_dequant8(const uint32_t* w, float S, float S16, float B, float (&y)[8]) {
+  if constexpr (BITS == 8) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t x = w[h];
+      const uint32_t e = x & 0x00FF00FFu;          // codes of dims 0 and 2
+      const uint32_t o = perm(x, x, 0x0C030C01u);  // dims 1 and 3
+      y[4 * h + 0] = fma_half<0>(e, S, B);
+      y[4 * h + 1] = fma_half<0>(o, S, B);
+      y[4 * h + 2] = fma_half<1>(e, S, B);
+      y[4 * h + 3] = fma_half<1>(o, S, B);
+    }
+  } else {
+    static_assert(BITS == 4, "code width");
+    const uint32_t x = w[0], x8 = x >> 8;
+    const uint32_t a = x & kNib, c = x & kNib1, e = x8 & kNib, g = x8 & kNib1;  // dims (0,4) (1,5) (2,6) (3,7)
+    y[0] = fma_half<0>(a, S, B);
+    y[1] = fma_half<0>(c, S16, B);
+    y[2] = fma_half<0>(e, S, B);
+    y[3] = fma_half<0>(g, S16, B);
+    y[4] = fma_half<1>(a, S, B);
+    y[5] = fma_half<1>(c, S16, B);
+    y[6] = fma_half<1>(e, S, B);
+    y[7] = fma_half<1>(g, S16, B);
+  }
+}
+
 template <typename Tag>
 __device__ __forceinline__ f4 mfma(const uint32_t a[4], const uint32_t b[4], f4 c) {
   const uint4 av = {a[0], a[1], a[2], a[3]};

@@ -138,21 +138,24 @@ __device__ __forceinline__ int pair_dim(int i, int half) {
 constexpr int kKPT = kPThreads / kPTile;
 constexpr int kVPT = kPThreads / (kPTile / 2);
 
+// Loads at the thread's byte offset `voff` plus the uniform `soff` (the
+// buffer instruction's scalar offset, which the range check includes: words
+// past the descriptor's size read as zero either way).
 template <int W>
-__device__ __forceinline__ void load_words(rsrc_t rs, uint32_t off, uint32_t* w) {
+__device__ __forceinline__ void load_words(rsrc_t rs, uint32_t voff, uint32_t soff, uint32_t* w) {
   typedef uint32_t u2 __attribute__((ext_vector_type(2)));
   if constexpr (W % 4 == 0) {
 #pragma unroll
     for (int i = 0; i < W / 4; ++i) {
-      const u4 x = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16 * i, 0, 0);
+      const u4 x = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 16 * i, soff, 0);
       w[4 * i] = x[0]; w[4 * i + 1] = x[1]; w[4 * i + 2] = x[2]; w[4 * i + 3] = x[3];
     }
   } else if constexpr (W == 2) {
-    const u2 x = __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0);
+    const u2 x = __builtin_amdgcn_raw_buffer_load_b64(rs, voff, soff, 0);
     w[0] = x[0]; w[1] = x[1];
   } else {
     static_assert(W == 1, "piece size");
-    w[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0);
+    w[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, voff, soff, 0);
   }
 }
 
@@ -217,23 +220,24 @@ struct Prefill {
   }
 
   // Issue the loads of the tile whose first token is `rel0` tokens past the
-  // sequence's first key (rows past the end read as zero): the tile's row
-  // times the row stride (uniform, scalar) plus the thread's fixed part.
+  // sequence's first key (rows past the end read as zero): the thread's
+  // fixed part as the vector offset, the tile's row times the row stride
+  // (uniform) as the scalar offset, so that no load takes a VALU add.
   static __device__ __forceinline__ void load(Raw& R, const Src& s, int rel0) {
     const uint32_t row = static_cast<uint32_t>(rel0);
-    load_words<Raw::KW>(s.k, row * s.k_sn + s.k_l, R.k);
+    load_words<Raw::KW>(s.k, s.k_l, row * s.k_sn, R.k);
     if constexpr (kKG == 2) {
-      R.ks = __builtin_amdgcn_raw_buffer_load_b32(s.ks, row * s.ks_sn + s.ks_l, 0, 0);
-      R.kb = __builtin_amdgcn_raw_buffer_load_b32(s.kb, row * s.kb_sn + s.kb_l, 0, 0);
+      R.ks = __builtin_amdgcn_raw_buffer_load_b32(s.ks, s.ks_l, row * s.ks_sn, 0);
+      R.kb = __builtin_amdgcn_raw_buffer_load_b32(s.kb, s.kb_l, row * s.kb_sn, 0);
     } else {
-      R.ks = __builtin_amdgcn_raw_buffer_load_b16(s.ks, row * s.ks_sn + s.ks_l, 0, 0);
-      R.kb = __builtin_amdgcn_raw_buffer_load_b16(s.kb, row * s.kb_sn + s.kb_l, 0, 0);
+      R.ks = __builtin_amdgcn_raw_buffer_load_b16(s.ks, s.ks_l, row * s.ks_sn, 0);
+      R.kb = __builtin_amdgcn_raw_buffer_load_b16(s.kb, s.kb_l, row * s.kb_sn, 0);
     }
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
-      load_words<Raw::VW>(s.v, row * s.v_sn + s.v_l[e], R.v[e]);
-      R.vs[e] = __builtin_amdgcn_raw_buffer_load_b16(s.vs, row * s.vs_sn + s.vs_l[e], 0, 0);
-      R.vb[e] = __builtin_amdgcn_raw_buffer_load_b16(s.vb, row * s.vb_sn + s.vb_l[e], 0, 0);
+      load_words<Raw::VW>(s.v, s.v_l[e], row * s.v_sn, R.v[e]);
+      R.vs[e] = __builtin_amdgcn_raw_buffer_load_b16(s.vs, s.vs_l[e], row * s.vs_sn, 0);
+      R.vb[e] = __builtin_amdgcn_raw_buffer_load_b16(s.vb, s.vb_l[e], row * s.vb_sn, 0);
     }
   }
 
@@ -244,45 +248,81 @@ struct Prefill {
     {
       const int t = tid / kKPT, c = tid % kKPT;
       uint8_t* dst = buf + t * PG::KPitch + c * kQD * 2;
+      auto k_scale = [&](int g) { return g ? static_cast<uint32_t>(R.ks >> 16) : static_cast<uint32_t>(R.ks); };
+      auto k_bias = [&](int g) { return g ? static_cast<uint32_t>(R.kb >> 16) : static_cast<uint32_t>(R.kb); };
+      bool mix = false;
+      if constexpr (Tag::kId == QSDPA_BF16) {
+        // Wave-uniform: every scale of the wave's slices below kMixScaleMax
+        // (NaN and infinities included in the other path).
+        bool ok = fabsf(to_f32<Tag>(static_cast<uint16_t>(k_scale(0)))) < kMixScaleMax;
+        if constexpr (kKG == 2) ok = ok && fabsf(to_f32<Tag>(static_cast<uint16_t>(k_scale(1)))) < kMixScaleMax;
+        mix = __builtin_amdgcn_ballot_w64(!ok) == 0;
+      }
+      if (mix) {
 #pragma unroll
-      for (int s = 0; s < kQD / 8; ++s) {
-        const int g = kKG == 2 ? (8 * s) / GS : 0;
-        const uint32_t sw = g ? static_cast<uint32_t>(R.ks >> 16) : static_cast<uint32_t>(R.ks);
-        const uint32_t bw = g ? static_cast<uint32_t>(R.kb >> 16) : static_cast<uint32_t>(R.kb);
-        uint32_t a[4];
-        dequant_k<Tag, BITS>(R.k + s * (BITS / 4), splat_lo(sw), splat_lo(bw), to_f32<Tag>(static_cast<uint16_t>(sw)),
-                             to_f32<Tag>(static_cast<uint16_t>(bw)), a);
-        *reinterpret_cast<u4*>(dst + s * 16) = u4{a[0], a[1], a[2], a[3]};
+        for (int s = 0; s < kQD / 8; ++s) {
+          const int g = kKG == 2 ? (8 * s) / GS : 0;
+          const float sf = to_f32<Tag>(static_cast<uint16_t>(k_scale(g)));
+          float y[8];
+          mix_dequant8<BITS>(R.k + s * (BITS / 4), sf * 0x1p24f, sf * 0x1p20f, to_f32<Tag>(static_cast<uint16_t>(k_bias(g))),
+                             y);
+          *reinterpret_cast<u4*>(dst + s * 16) = u4{pack_T2<Tag>(y[0], y[1]), pack_T2<Tag>(y[2], y[3]),
+                                                    pack_T2<Tag>(y[4], y[5]), pack_T2<Tag>(y[6], y[7])};
+        }
+      } else {
+#pragma unroll
+        for (int s = 0; s < kQD / 8; ++s) {
+          const int g = kKG == 2 ? (8 * s) / GS : 0;
+          const uint32_t sw = k_scale(g), bw = k_bias(g);
+          uint32_t a[4];
+          dequant_k<Tag, BITS>(R.k + s * (BITS / 4), splat_lo(sw), splat_lo(bw), to_f32<Tag>(static_cast<uint16_t>(sw)),
+                               to_f32<Tag>(static_cast<uint16_t>(bw)), a);
+          *reinterpret_cast<u4*>(dst + s * 16) = u4{a[0], a[1], a[2], a[3]};
+        }
       }
     }
     // V: tokens 2 pr, 2 pr + 1, dims [cv D/VPT, (cv + 1) D/VPT), transposed.
     {
       const int pr = tid & 31, cv = tid >> 5;
       uint8_t* vt = buf + PG::KBytes + vcol(2 * pr) * 2;
-      uint32_t a[2][4];
+      if constexpr (Tag::kId == QSDPA_F16) {
+        uint32_t a[2][4];
 #pragma unroll
-      for (int s = 0; s < kVD / 8; ++s) {
+        for (int s = 0; s < kVD / 8; ++s) {
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          if constexpr (Tag::kId == QSDPA_F16) {
+          for (int e = 0; e < 2; ++e)
             dequant_k<Tag, BITS>(R.v[e] + s * (BITS / 4), splat_lo(R.vs[e]), splat_lo(R.vb[e]), to_f32<Tag>(R.vs[e]),
                                  to_f32<Tag>(R.vb[e]), a[e]);
-          } else {
-            // bfloat16(fma(s, c, b)) * 2^-k = bfloat16(fma(s 2^-k, c, b 2^-k)).
-            uint32_t t[4];
-            dequant_k<Tag, BITS>(R.v[e] + s * (BITS / 4), 0u, 0u, to_f32<Tag>(R.vs[e]) * vsc,
-                                 to_f32<Tag>(R.vb[e]) * vsc, t);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) a[e][i] = bf16x2_to_f16x2(t[i]);
+          for (int i = 0; i < 4; ++i) {
+            const int d0 = cv * kVD + 8 * s;
+            *reinterpret_cast<uint32_t*>(vt + (d0 + pair_dim<Tag, BITS>(i, 0)) * kVPitch) =
+                perm(a[1][i], a[0][i], 0x05040100u);
+            *reinterpret_cast<uint32_t*>(vt + (d0 + pair_dim<Tag, BITS>(i, 1)) * kVPitch) =
+                perm(a[1][i], a[0][i], 0x07060302u);
           }
         }
+      } else {
+        // bfloat16(fma(s, c, b)) * 2^-k = bfloat16(fma(s 2^-k, c, b 2^-k)),
+        // by mix_dequant8: the scan that chose k bounds |s| 2^-k by
+        // 2 kVBound / (2^bits - 1), far below kMixScaleMax.  The two tokens'
+        // values of a dim are rounded as one pair, which is the V^T word.
+        float S[2], S16[2], Bv[2];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int e = 0; e < 2; ++e) {
+          S[e] = to_f32<Tag>(R.vs[e]) * (vsc * 0x1p24f);
+          S16[e] = to_f32<Tag>(R.vs[e]) * (vsc * 0x1p20f);
+          Bv[e] = to_f32<Tag>(R.vb[e]) * vsc;
+        }
+#pragma unroll
+        for (int s = 0; s < kVD / 8; ++s) {
+          float y[2][8];
+#pragma unroll
+          for (int e = 0; e < 2; ++e) mix_dequant8<BITS>(R.v[e] + s * (BITS / 4), S[e], S16[e], Bv[e], y[e]);
           const int d0 = cv * kVD + 8 * s;
-          *reinterpret_cast<uint32_t*>(vt + (d0 + pair_dim<Tag, BITS>(i, 0)) * kVPitch) =
-              perm(a[1][i], a[0][i], 0x05040100u);
-          *reinterpret_cast<uint32_t*>(vt + (d0 + pair_dim<Tag, BITS>(i, 1)) * kVPitch) =
-              perm(a[1][i], a[0][i], 0x07060302u);
+#pragma unroll
+          for (int d = 0; d < 8; ++d)
+            *reinterpret_cast<uint32_t*>(vt + (d0 + d) * kVPitch) = bf16x2_to_f16x2(pack_T2<Tag>(y[0][d], y[1][d]));
         }
       }
     }

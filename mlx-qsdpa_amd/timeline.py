@@ -5,6 +5,7 @@
   python mlx-qsdpa_amd/timeline.py stream [--config c3] # on the GPU: a read-only launch of the same bytes
   python mlx-qsdpa_amd/timeline.py prefill [--qlen 512] # on the GPU: the prefill kernel's phases at C5
   python mlx-qsdpa_amd/timeline.py lds                  # on the GPU: LDS read rate of the prefill pattern
+  python mlx-qsdpa_amd/timeline.py rates                # on the GPU: VALU issue interval per instruction
 
 ``build`` compiles the library with -DQSDPA_TIMELINE into
 mlx_qsdpa_amd/libqsdpa_timeline.so: the same kernels, plus an s_memrealtime
@@ -18,7 +19,9 @@ wave's entry, plus the median per wave slot (0-7) of the workgroup.
 probe build's prefill kernel and prints, per wave slot, the mean shader-clock
 cycles per tile of its three phases (start of tile to row maxima, row maxima to
 end of tile, barrier); ``lds`` times the probe build's LDS read kernel (the
-prefill kernel's K / V^T operand reads, one workgroup per CU).
+prefill kernel's K / V^T operand reads, one workgroup per CU); ``rates`` times
+one instruction at a time (8 independent chains per lane, 8 waves per SIMD)
+and prints its issue interval per SIMD, in ns and relative to v_fma_f32.
 
 Points: entry; Q staged in LDS (after the workgroup barrier); k-th tile
 done; stream end (the wave's last tile); partials merged in LDS (after the
@@ -279,9 +282,51 @@ def lds(calls: int, lib_path: Path = LIB, blocks: int = 256, iters: int = 2000) 
           f"({cycles / iters:.0f} cycles per 256 KB iteration)")
 
 
+def rates(calls: int, lib_path: Path = LIB, blocks: int = 2048, iters: int = 2048) -> None:
+    """Issue interval of the dequantization's and softmax's VALU instructions."""
+    for p in (ROOT, HERE):
+        sys.path.insert(0, str(p))
+    import numpy as np
+    import torch
+
+    import bench
+    from mlx_qsdpa_amd import _lib
+
+    lib = _lib.load(lib_path)
+    lib.qsdpa_debug_valu_rate_count.restype = ctypes.c_int
+    lib.qsdpa_debug_valu_rate_name.argtypes = [ctypes.c_int]
+    lib.qsdpa_debug_valu_rate_name.restype = ctypes.c_char_p
+    f = lib.qsdpa_debug_valu_rate
+    f.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                  ctypes.c_void_p]
+    f.restype = ctypes.c_int
+    dev = torch.device("cuda:0")
+    sink = torch.zeros(blocks * 256, dtype=torch.int32, device=dev)
+    stream_h = torch.cuda.current_stream(dev).cuda_stream
+    simds = torch.cuda.get_device_properties(dev).multi_processor_count * 4
+    per_simd = blocks * 4 * iters * 8 / simds  # wave instructions issued per SIMD
+    hip = bench.HipEvents()
+    ev = hip.create(2 * calls)
+    print(f"# {blocks} workgroups x 4 waves, {iters} x 8 chained instructions per lane, {simds} SIMDs")
+    print("| instruction | ns per wave instruction per SIMD | relative to v_fma_f32 |")
+    print("|---|---|---|")
+    base = None
+    for w in range(lib.qsdpa_debug_valu_rate_count()):
+        for i in range(calls + 1):
+            e = (ev[2 * (i - 1)], ev[2 * (i - 1) + 1]) if i >= 1 else (None, None)
+            if f(w, blocks, iters, sink.data_ptr(), stream_h, *e) != 0:
+                raise SystemExit("qsdpa_debug_valu_rate failed")
+        torch.cuda.synchronize()
+        us = float(np.median([hip.elapsed_ms(ev[2 * i], ev[2 * i + 1]) * 1e3 for i in range(calls)]))
+        ns = us * 1e3 / per_simd
+        base = base or ns
+        print(f"| {lib.qsdpa_debug_valu_rate_name(w).decode()} | {ns:.2f} | {ns / base:.2f} |")
+    hip.destroy(ev)
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
-    ap.add_argument("what", choices=["build", "run", "stream", "stream-width", "prefill", "lds"])
+    ap.add_argument("what", choices=["build", "run", "stream", "stream-width", "prefill", "lds", "rates"])
     ap.add_argument("--config", default="c3", choices=["c1", "c2", "c3", "c5"])
     ap.add_argument("--n", type=int, default=None)
     ap.add_argument("--calls", type=int, default=40)
@@ -298,6 +343,8 @@ def main(argv=None) -> int:
         prefill(a.qlen, a.calls, Path(a.lib))
     elif a.what == "lds":
         lds(a.calls, Path(a.lib))
+    elif a.what == "rates":
+        rates(min(a.calls, 5), Path(a.lib))
     else:
         run(a.config, a.n, a.calls, Path(a.lib))
     return 0

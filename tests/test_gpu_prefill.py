@@ -164,6 +164,34 @@ def test_prefill_bf16_large_values(device, case):
     assert bool((err <= bound).all()), f"{case}: max err {float(err.max()):.4g} (max |V| {vmax:.3g})"
 
 
+@pytest.mark.parametrize("bits,gs", [(8, 64), (4, 128)])
+def test_prefill_bf16_huge_k_scales(device, bits, gs):
+    """bfloat16 K groups with scales of 2^101 and more.  The kernel's
+    dequantization multiplies each scale by 2^24 (codes read as float16
+    subnormals); a wave with a scale at or above 2^100 takes the plain
+    float32 path instead, whose values are finite where the scaled one would
+    overflow.  Keys 64-127 (whole waves of a tile) and every seventh key
+    (most waves) carry such groups, with values near 2^109 (8-bit) or 2^105
+    (4-bit); queries scaled to match keep their scores near 1, so the
+    softmax mixes them and the normal keys (scores near 0): a wrong K value
+    shows as a wrong output or a NaN."""
+    B, Hq, Hkv, N, L = 2, 32, 8, 900, 256
+    q, kq, vq = _inputs(B, Hq, Hkv, N, L, bits, gs, torch.bfloat16, seed=31)
+    q = (q.float() * 2.0 ** (-108 if bits == 8 else -104)).bfloat16()
+    huge = torch.zeros(N, dtype=torch.bool)
+    huge[64:128] = True
+    huge[::7] = True
+    g = torch.Generator(device="cpu").manual_seed(32)
+    ks, kb = kq[1].clone(), kq[2].clone()
+    shape = (B, Hkv, int(huge.sum()), ks.shape[-1])
+    s = (2.0 ** 101 * (1.0 + torch.rand(shape, generator=g))).bfloat16().to(device)
+    ks[:, :, huge.to(device)] = s
+    kb[:, :, huge.to(device)] = (-(2 ** (bits - 1)) * s.float()).bfloat16()
+    kq = (kq[0], ks, kb)
+    print(f"prefill huge K scales bits={bits} gs={gs}", flush=True)
+    _check(q, kq, vq, bits, gs, f"huge K scales {bits}-bit", causal=True)
+
+
 def test_prefill_repeatable(device):
     """Repeated calls give bit-identical outputs."""
     q, kq, vq = _inputs(4, 16, 4, 4096, 512, 8, 128, torch.bfloat16, seed=5)
