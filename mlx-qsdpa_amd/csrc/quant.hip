@@ -1,10 +1,12 @@
 // Quantize-on-append and dequantize kernels (MLX affine format).
 //
-// quantize: GS / 8 lanes per (row, group), 8 values per lane.  The per-group rule is the float32
-// edge-snapped affine quantizer (see oracle/affine.py for the written
+// quantize: GS / 8 lanes per (row, group) with 8 values each for small jobs,
+// GS / 32 lanes with 32 values for large ones.  The per-group rule is the
+// float32 edge-snapped affine quantizer (see oracle/affine.py for the written
 // contract); every operation is spelled with an explicitly rounded intrinsic
-// so the compiler can neither contract nor reassociate it, which keeps the
-// output bit-identical to the numpy restatement.
+// (the one fma is written out), and each code's division goes through the
+// group's reciprocal with an exact fallback near ties, which keeps the output
+// bit-identical to the numpy restatement.
 //
 // dequantize: one thread per packed word; value = round_T(fmaf(s, q, b)).
 // Replaces mx.quantize + slice assignment (mlx_qsdpa/cache.py:186-192) and
@@ -29,15 +31,17 @@ struct QuantParams {
   int64_t z_sb, z_sh, z_sn;
 };
 
-// Min / max over aligned groups of L consecutive lanes (L in {1, 4, 8,
+// Min / max over aligned groups of L consecutive lanes (L in {1, 2, 4, 8,
 // 16}); every lane of a group gets the result.  Exact in any order.
 template <int L>
 __device__ __forceinline__ void group_minmax(float& lo, float& hi) {
   if constexpr (L == 1) return;
   lo = fminf(lo, dpp_f32<0xB1>(lo));
   hi = fmaxf(hi, dpp_f32<0xB1>(hi));
-  lo = fminf(lo, dpp_f32<0x4E>(lo));
-  hi = fmaxf(hi, dpp_f32<0x4E>(hi));
+  if constexpr (L >= 4) {
+    lo = fminf(lo, dpp_f32<0x4E>(lo));
+    hi = fmaxf(hi, dpp_f32<0x4E>(hi));
+  }
   if constexpr (L >= 8) {
     lo = fminf(lo, dpp_f32<0x141>(lo));
     hi = fmaxf(hi, dpp_f32<0x141>(hi));
@@ -48,26 +52,57 @@ __device__ __forceinline__ void group_minmax(float& lo, float& hi) {
   }
 }
 
+// Codes through the group's reciprocal.  A value's code is q = rint(fl(x /
+// scale)), x = fl(v - bias).  inv = v_rcp_f32(scale) is within one ulp
+// (relative error below 2^-23; scale is a normal number, at least about
+// 5e-8 in magnitude).  With p = x inv (exact product) and z = x / scale,
+// |p - z| <= |z| 2^-23 and |fl(z) - z| <= |z| 2^-24, so |p - fl(z)| <= 1.5
+// |z| 2^-23.  q = rint(fl(p)) and e = fl(p - q) (one fma, within 2^-25 of p
+// - q): when |e| < 1/2 - (|fl(p)| 2^-21 + 2^-24), fl(z) lies closer to q
+// than 1/2, so rint(fl(z)) = q.  Otherwise -- within about |z| 2^-21 of a
+// half-integer (one value in ten thousand at |z| ~ 100), or not finite --
+// the exactly rounded quotient decides.  The check is per value, the branch
+// to the divisions once per wave: an exact division costs about ten VALU
+// instructions, one of them an 8-cycle v_rcp_f32, and a per-value branch
+// about as much again.  (The fma is written out: this compiler contracts a
+// multiply and a subtract even when both are spelled __fmul_rn / __fsub_rn.)
+__device__ __forceinline__ float code_near(float x, float inv, bool& tie) {
+  const float r = __fmul_rn(x, inv);
+  const float q = rintf(r);
+  const float e = __builtin_fmaf(x, inv, -q);
+  tie = !(fabsf(e) < __builtin_fmaf(fabsf(r), -0x1p-21f, 0.5f - 0x1p-24f));
+  return q;
+}
+
+// Code j of a word set to q (an integral float or NaN), clamped to [0,
+// 2^BITS - 1] with NaN to 0.  8-bit: one v_cvt_pk_u8_f32 (round to nearest
+// even, saturating to [0, 255], NaN to 0: measured, the same as fminf(fmaxf(q,
+// 0), 255) for the integral q here).
+template <int BITS>
+__device__ __forceinline__ uint32_t put_code(uint32_t word, float q, int j) {
+  if constexpr (BITS == 8) {
+    return __builtin_amdgcn_cvt_pk_u8_f32(q, static_cast<uint32_t>(j), word);
+  } else {
+    constexpr float kBins = static_cast<float>((1 << BITS) - 1);
+    const uint32_t mask = ((1u << BITS) - 1u) << (j * BITS);
+    return (word & ~mask) | (static_cast<uint32_t>(fminf(fmaxf(q, 0.0f), kBins)) << (j * BITS));
+  }
+}
+
 // Quantize one group of GS values spread over L consecutive lanes (VALS =
-// GS / L T values per lane, as raw 16-bit patterns): min / max across the
-// lanes, then the edge-snapped affine rule, every operation an explicitly
-// rounded intrinsic; each lane packs its own VALS codes to `dst` and lane 0
-// of the group stores the scale and bias.  Shared by quantize_kernel and
+// GS / L values per lane, val(i) the lane's i-th T value as float; lo / hi:
+// the min / max of the lane's own values): min / max across the lanes, then
+// the edge-snapped affine rule, every operation an explicitly rounded
+// intrinsic; each lane packs its own VALS codes to `dst` and lane 0 of the
+// group stores the scale and bias.  Shared by quantize_kernel and
 // requant_kernel so the two stay bit-identical.
-template <typename Tag, int BITS, int GS, int L>
-__device__ __forceinline__ void quantize_group(const uint16_t (&raw)[GS / L], int part, uint32_t* dst,
+template <typename Tag, int BITS, int GS, int L, bool DST16 = false, typename Val>
+__device__ __forceinline__ void quantize_group(Val&& val, float w_min, float w_max, int part, uint32_t* dst,
                                                uint16_t* scale_dst, uint16_t* bias_dst) {
   constexpr int VALS = GS / L;
   constexpr int PER = 32 / BITS;
   constexpr int WORDS = VALS / PER;
   constexpr float kBins = static_cast<float>((1 << BITS) - 1);
-  float w_min = __builtin_huge_valf(), w_max = -__builtin_huge_valf();
-#pragma unroll
-  for (int i = 0; i < VALS; ++i) {
-    const float v = to_f32<Tag>(raw[i]);
-    w_min = fminf(w_min, v);
-    w_max = fmaxf(w_max, v);
-  }
   group_minmax<L>(w_min, w_max);
   float scale = fmaxf(__fdiv_rn(__fsub_rn(w_max, w_min), kBins), 1e-7f);
   const bool side = fabsf(w_min) > fabsf(w_max);
@@ -77,21 +112,58 @@ __device__ __forceinline__ void quantize_group(const uint16_t (&raw)[GS / L], in
   const bool nz = q0 != 0.0f;
   if (nz) scale = __fdiv_rn(edge, q0);
   const float bias = nz ? edge : 0.0f;
+  const float inv = __builtin_amdgcn_rcpf(scale);
+  uint32_t words[WORDS];
+  bool tie = false;
 #pragma unroll
   for (int w = 0; w < WORDS; ++w) {
     uint32_t word = 0;
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
-      const float v = to_f32<Tag>(raw[w * PER + j]);
-      float q = rintf(__fdiv_rn(__fsub_rn(v, bias), scale));
-      q = fminf(fmaxf(q, 0.0f), kBins);
-      word |= static_cast<uint32_t>(q) << (j * BITS);
+      bool t;
+      word = put_code<BITS>(word, code_near(__fsub_rn(val(w * PER + j), bias), inv, t), j);
+      tie |= t;
     }
-    dst[w] = word;
+    words[w] = word;
+  }
+  if (__builtin_amdgcn_ballot_w64(tie)) {
+#pragma unroll
+    for (int w = 0; w < WORDS; ++w)
+#pragma unroll
+      for (int j = 0; j < PER; ++j) {
+        const float x = __fsub_rn(val(w * PER + j), bias);
+        bool t;
+        code_near(x, inv, t);
+        if (t) words[w] = put_code<BITS>(words[w], rintf(__fdiv_rn(x, scale)), j);
+      }
+  }
+  // DST16: dst is 16-byte aligned, one 16-byte store per 4 words (the
+  // requant kernel measured 15.4 against 19.2 us at the C5 chunk with
+  // single-word stores).
+  if constexpr (DST16) {
+    static_assert(WORDS % 4 == 0, "16-byte code stores");
+#pragma unroll
+    for (int w = 0; w < WORDS; w += 4)
+      *reinterpret_cast<uint4*>(dst + w) = uint4{words[w], words[w + 1], words[w + 2], words[w + 3]};
+  } else {
+#pragma unroll
+    for (int w = 0; w < WORDS; ++w) dst[w] = words[w];
   }
   if (part == 0) {
     *scale_dst = from_f32<Tag>(scale);
     *bias_dst = from_f32<Tag>(bias);
+  }
+}
+
+// Min / max of a lane's N values val(i) (fminf / fmaxf: a NaN is ignored).
+template <int N, typename Val>
+__device__ __forceinline__ void lane_minmax(Val&& val, float& lo, float& hi) {
+  lo = __builtin_huge_valf();
+  hi = -__builtin_huge_valf();
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    lo = fminf(lo, val(i));
+    hi = fmaxf(hi, val(i));
   }
 }
 
@@ -107,9 +179,9 @@ struct QuantJobs {
 // per lane (16-byte pieces when VEC, i.e. the rows are 16-byte aligned); the
 // group's min / max are reduced across the L lanes and every lane quantizes
 // and packs its own values.  L = GS / 8 for small jobs (a one-row append:
-// its latency is that of 8 values, not GS); L = 1 for large ones, which
-// fill the GPU anyway and then do not repeat the scale's divisions in every
-// lane.  A group's lanes are all in range or all out of it, so the
+// its latency is that of 8 values, not GS); L = GS / 32 for large ones,
+// which fill the GPU anyway: a lane's group work (min / max reductions,
+// scale divisions) is then shared by 32 values.  A group's lanes are all in range or all out of it, so the
 // cross-lane steps never read an exited lane.  I is the index type: 32-bit
 // whenever the launch's thread count fits.
 template <typename Tag, int BITS, int GS, int L, bool VEC, typename I>
@@ -148,8 +220,11 @@ __global__ __launch_bounds__(256) void quantize_kernel(QuantJobs jobs) {
     for (int i = 0; i < VALS; ++i) raw[i] = src[i];
   }
 
+  auto val = [&](int i) { return to_f32<Tag>(raw[i]); };
+  float lo, hi;
+  lane_minmax<VALS>(val, lo, hi);
   const int t = p.t0 + s;
-  quantize_group<Tag, BITS, GS, L>(raw, part, p.dp + off3(b, h, t, p.p_sb, p.p_sh, p.p_sn) + (g * GS + part * VALS) / PER,
+  quantize_group<Tag, BITS, GS, L>(val, lo, hi, part, p.dp + off3(b, h, t, p.p_sb, p.p_sh, p.p_sn) + (g * GS + part * VALS) / PER,
                                    p.ds + off3(b, h, t, p.c_sb, p.c_sh, p.c_sn) + g,
                                    p.db + off3(b, h, t, p.z_sb, p.z_sh, p.z_sn) + g);
 }
@@ -172,7 +247,7 @@ void launch_quantize_l(const QuantJobs& j, bool vec, int64_t groups, int count, 
 
 template <typename Tag, int BITS, int GS>
 void launch_quantize_gs(const QuantJobs& j, bool vec, int64_t groups, int count, hipStream_t stream) {
-  if (groups >= kWideJobGroups) launch_quantize_l<Tag, BITS, GS, 1>(j, vec, groups, count, stream);
+  if (groups >= kWideJobGroups) launch_quantize_l<Tag, BITS, GS, GS / 32>(j, vec, groups, count, stream);
   else launch_quantize_l<Tag, BITS, GS, GS / 8>(j, vec, groups, count, stream);
 }
 
@@ -232,8 +307,10 @@ __global__ __launch_bounds__(256) void dequantize_kernel(DequantParams p) {
 // c < keep, else keep + (c - keep + rot) % (n_old - keep): dequantized
 // exactly as dequantize_kernel does, value = T(fmaf(s, q, b)); otherwise it
 // is chunk row c - n_old.  The row is then quantized as quantize_kernel
-// does (quantize_group), 8 values per lane, GS / 8 lanes per group, into
-// the destination buffers, which must not alias the old window.
+// does (quantize_group), 32 values per lane, GS / 32 lanes per group (the
+// group's min / max reductions and scale divisions shared by 32 values, not
+// 8: the kernel was VALU-bound at 8), into the destination buffers, which
+// must not alias the old window.
 struct RequantParams {
   int B, H, D, n_old, keep, rot, total, drop;
   const uint32_t* op;
@@ -255,26 +332,38 @@ struct RequantJobs {
   RequantParams p[2];
 };
 
-template <typename Tag, int BITS, int GS>
+template <typename Tag, int BITS, int GS, bool DST16>
 __global__ __launch_bounds__(256) void requant_kernel(RequantJobs jobs) {
-  // Grid: x over the rows' (row, group, lane) triples of one (batch, head),
-  // y = batch * H + head, z = job; the launcher keeps x's count in 32 bits.
-  constexpr int L = GS / 8;  // lanes per group, 8 values each
+  // Grid: x over the (row, lane) pairs of one group column of one (batch,
+  // head), y = (batch * H + head) * ng + group, z = job: the group, batch and
+  // head are uniform.  Within a (batch, head) every offset fits in 32 bits
+  // (the launcher checks), so the lanes' row offsets are 32-bit products.
+  constexpr int VALS = 32;         // values per lane
+  constexpr int L = GS / VALS;     // lanes per group
   constexpr int PER = 32 / BITS;
   constexpr uint32_t kMask = (1u << BITS) - 1u;
   const RequantParams& p = jobs.p[blockIdx.z];
-  const uint32_t ng = static_cast<uint32_t>(p.D / GS);
+  // (The compiler divides in vector registers; readfirstlane keeps the
+  // slice bases' 64-bit products scalar.)
+  const int ng = p.D / GS;
+  const int g = __builtin_amdgcn_readfirstlane(static_cast<int>(blockIdx.y) % ng);
+  const int bh = static_cast<int>(blockIdx.y) / ng;
+  const int b = __builtin_amdgcn_readfirstlane(bh / p.H), h = __builtin_amdgcn_readfirstlane(bh % p.H);
   const uint32_t gid = blockIdx.x * 256u + threadIdx.x;
-  const uint32_t grp = gid / L;
+  const int t = static_cast<int>(gid / L);
   const int part = static_cast<int>(gid % L);
-  if (grp >= static_cast<uint32_t>(p.total) * ng) return;
-  const int g = static_cast<int>(grp % ng);
-  const int t = static_cast<int>(grp / ng);
-  const int b = static_cast<int>(blockIdx.y) / p.H;
-  const int h = static_cast<int>(blockIdx.y) % p.H;
+  if (t >= p.total) return;
+  auto rows = [&](auto* base, int64_t sb, int64_t sh) {
+    return base + (static_cast<int64_t>(b) * sb + static_cast<int64_t>(h) * sh);
+  };
+  uint32_t* const dst_p = rows(p.dp, p.p_sb, p.p_sh);
+  uint16_t* const dst_s = rows(p.ds, p.c_sb, p.c_sh);
+  uint16_t* const dst_b = rows(p.db, p.z_sb, p.z_sh);
+  auto at = [](int row, int64_t sn) { return static_cast<uint32_t>(row) * static_cast<uint32_t>(sn); };
   const int c = t < p.keep ? t : t + p.drop;
-  const int d0 = g * GS + part * 8;  // the lane's first dim
-  uint16_t raw[8];
+  const int d0 = g * GS + part * VALS;  // the lane's first dim
+  float val[VALS];  // T values as float
+  float lo, hi;     // their min / max
   if (c < p.n_old) {
     // Ring row of combined token c: c - keep + rot < 2 (n_old - keep), so one
     // conditional subtraction is the modulo.
@@ -284,24 +373,41 @@ __global__ __launch_bounds__(256) void requant_kernel(RequantJobs jobs) {
       if (u >= p.n_old - p.keep) u -= p.n_old - p.keep;
       u += p.keep;
     }
-    const float sc = to_f32<Tag>(p.os[off3(b, h, u, p.os_sb, p.os_sh, p.os_sn) + g]);
-    const float bi = p.ob ? to_f32<Tag>(p.ob[off3(b, h, u, p.ob_sb, p.ob_sh, p.ob_sn) + g]) : 0.0f;
-    const uint32_t* words = p.op + off3(b, h, u, p.op_sb, p.op_sh, p.op_sn) + d0 / PER;
+    const float sc = to_f32<Tag>(rows(p.os, p.os_sb, p.os_sh)[at(u, p.os_sn) + g]);
+    const float bi = p.ob ? to_f32<Tag>(rows(p.ob, p.ob_sb, p.ob_sh)[at(u, p.ob_sn) + g]) : 0.0f;
+    const uint32_t* words = rows(p.op, p.op_sb, p.op_sh) + (at(u, p.op_sn) + d0 / PER);
+    // T(fmaf(s, q, b)) as dequantize_kernel stores it, rounded two values
+    // at a time (v_cvt_pk_*_f32: the same rounding, and a NaN still reads
+    // as NaN, which the quantizer maps to code 0 whatever its bits).
+    float y[VALS];
 #pragma unroll
-    for (int w = 0; w < 8 / PER; ++w) {
+    for (int w = 0; w < VALS / PER; ++w) {
       const uint32_t word = words[w];
 #pragma unroll
       for (int j = 0; j < PER; ++j)
-        raw[w * PER + j] = from_f32<Tag>(__fmaf_rn(sc, static_cast<float>((word >> (j * BITS)) & kMask), bi));
+        y[w * PER + j] = __fmaf_rn(sc, static_cast<float>((word >> (j * BITS)) & kMask), bi);
     }
-  } else {
-    const uint16_t* src = p.src + off3(b, h, c - p.n_old, p.s_sb, p.s_sh, p.s_sn) + d0;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) raw[i] = src[i];
+    for (int i = 0; i < VALS; i += 2) {
+      const uint32_t pr = pack_T2<Tag>(y[i], y[i + 1]);
+      val[i] = unpack_T2_lo<Tag>(pr);
+      val[i + 1] = unpack_T2_hi<Tag>(pr);
+    }
+    // The min / max of the rounded values are the rounded min / max of the
+    // fma results (rounding is monotone), which the compiler knows to be
+    // canonical floats: no quieting v_max per value.
+    lane_minmax<VALS>([&](int i) { return y[i]; }, lo, hi);
+    const uint32_t m = pack_T2<Tag>(lo, hi);
+    lo = unpack_T2_lo<Tag>(m);
+    hi = unpack_T2_hi<Tag>(m);
+  } else {
+    const uint16_t* src = rows(p.src, p.s_sb, p.s_sh) + (at(c - p.n_old, p.s_sn) + d0);
+#pragma unroll
+    for (int i = 0; i < VALS; ++i) val[i] = to_f32<Tag>(src[i]);
+    lane_minmax<VALS>([&](int i) { return val[i]; }, lo, hi);
   }
-  quantize_group<Tag, BITS, GS, L>(raw, part, p.dp + off3(b, h, t, p.p_sb, p.p_sh, p.p_sn) + d0 / PER,
-                                   p.ds + off3(b, h, t, p.c_sb, p.c_sh, p.c_sn) + g,
-                                   p.db + off3(b, h, t, p.z_sb, p.z_sh, p.z_sn) + g);
+  quantize_group<Tag, BITS, GS, L, DST16>([&](int i) { return val[i]; }, lo, hi, part, dst_p + (at(t, p.p_sn) + d0 / PER),
+                                          dst_s + (at(t, p.c_sn) + g), dst_b + (at(t, p.z_sn) + g));
 }
 
 }  // namespace
@@ -373,6 +479,7 @@ int launch_dequantize(const qsdpa_dequantize_args* a, hipStream_t stream) {
 int launch_requant(const qsdpa_requant_args* const* jobs, int count, hipStream_t stream) {
   RequantJobs j{};
   int64_t most = 0;
+  bool dst16 = true;
   const qsdpa_requant_args* a0 = jobs[0];
   for (int i = 0; i < count; ++i) {
     const qsdpa_requant_args* a = jobs[i];
@@ -394,20 +501,42 @@ int launch_requant(const qsdpa_requant_args* const* jobs, int count, hipStream_t
     p.c_sb = a->dst_scales.stride_b; p.c_sh = a->dst_scales.stride_h; p.c_sn = a->dst_scales.stride_n;
     p.db = static_cast<uint16_t*>(const_cast<void*>(a->dst_biases.ptr));
     p.z_sb = a->dst_biases.stride_b; p.z_sh = a->dst_biases.stride_h; p.z_sn = a->dst_biases.stride_n;
+    // A lane's first code word is a multiple of 4 words into its row.
+    dst16 = dst16 && aligned(a->dst_packed.ptr, 16) && p.p_sb % 4 == 0 && p.p_sh % 4 == 0 && p.p_sn % 4 == 0;
     most = std::max<int64_t>(most, static_cast<int64_t>(p.total) * (a->D / a->group_size));
   }
   if (most == 0 || a0->B * a0->H == 0) return QSDPA_OK;
-  // Lanes of one (batch, head): rows x groups x GS / 8.
-  const int64_t lanes = most * (a0->group_size / 8);
-  if (lanes + 255 >= (int64_t(1) << 32) || a0->B * a0->H > 65535)
+  // Lanes of one group column of one (batch, head): rows x GS / 32; one
+  // grid row per (batch, head, group).
+  const int64_t ng = a0->D / a0->group_size;
+  const int64_t lanes = most / ng * (a0->group_size / 32);
+  if (lanes + 255 >= (int64_t(1) << 32) || static_cast<int64_t>(a0->B) * a0->H * ng > 65535)
     return fail(QSDPA_ERR_UNSUPPORTED, "requant: window too large");
-  const dim3 grid(static_cast<unsigned>((lanes + 255) / 256), static_cast<unsigned>(a0->B * a0->H),
+  // Offsets within a (batch, head) are 32-bit in the kernel: rows x row
+  // stride plus the row's extent must stay below 2^31 elements.
+  for (int i = 0; i < count; ++i) {
+    const qsdpa_requant_args* a = jobs[i];
+    const int per = 32 / a->bits;
+    auto fits = [](int64_t rows, int64_t stride_n, int64_t extent) {
+      return stride_n >= 0 && (rows <= 0 || (rows - 1) * stride_n + extent < (int64_t(1) << 31));
+    };
+    const int64_t total = j.p[i].total;
+    if (!fits(a->n_old, a->old_packed.stride_n, a->D / per) || !fits(a->n_old, a->old_scales.stride_n, ng) ||
+        (a->old_biases.ptr && !fits(a->n_old, a->old_biases.stride_n, ng)) ||
+        !fits(a->S, a->src.stride_n, a->D) || !fits(total, a->dst_packed.stride_n, a->D / per) ||
+        !fits(total, a->dst_scales.stride_n, ng) || !fits(total, a->dst_biases.stride_n, ng))
+      return fail(QSDPA_ERR_UNSUPPORTED, "requant: a (batch, head) slice spans 2^31 elements or more");
+  }
+  const dim3 grid(static_cast<unsigned>((lanes + 255) / 256), static_cast<unsigned>(a0->B * a0->H * ng),
                   static_cast<unsigned>(count));
   auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, dim3(256), 0, stream, j); };
   const bool f16 = a0->dtype == QSDPA_F16;
   const int gs = a0->group_size, bits = a0->bits;
-#define QSDPA_REQUANT_CASE(T, B_, G_) \
-  if (bits == B_ && gs == G_) go(requant_kernel<T, B_, G_>);
+#define QSDPA_REQUANT_CASE(T, B_, G_)                \
+  if (bits == B_ && gs == G_) {                       \
+    if (dst16) go(requant_kernel<T, B_, G_, true>);   \
+    else go(requant_kernel<T, B_, G_, false>);        \
+  }
   if (f16) {
     QSDPA_REQUANT_CASE(F16, 4, 32) QSDPA_REQUANT_CASE(F16, 4, 64) QSDPA_REQUANT_CASE(F16, 4, 128)
     QSDPA_REQUANT_CASE(F16, 8, 32) QSDPA_REQUANT_CASE(F16, 8, 64) QSDPA_REQUANT_CASE(F16, 8, 128)

@@ -65,6 +65,31 @@ def test_quantize_bulk_matches_oracle(device, dtype, bits, gs):
     assert _bits_equal(to_np(got[2]), want[2], dtype)
 
 
+@pytest.mark.parametrize("bulk", [False, True], ids=["append", "bulk"])
+@pytest.mark.parametrize("dtype,bits", [("f16", 4), ("bf16", 8), ("bf16", 4), ("f16", 8)])
+def test_quantize_ties_round_half_to_even(device, dtype, bits, bulk):
+    """Groups spanning [0, 2^bits - 1] with values at half-integers: the
+    snapped scale is -1 (times a power of two), so every such value's code
+    is an exact tie, which the kernel's reciprocal path must hand to the
+    exactly rounded quotient (round half to even).  Small jobs (8 values per
+    lane) and bulk ones (32 values per lane)."""
+    gs, D = 128, 128
+    bins = (1 << bits) - 1
+    top = min(bins, 127)  # k + 1/2 exact in bf16 for k < 128
+    row = np.array([0.0, float(bins)] + [k + 0.5 for k in range(top)] * (D // top + 1), np.float32)[:D]
+    S = (1 << 18) // 8 if bulk else 5  # bulk: 8 heads x S rows x one group = 2^18 groups
+    heads = np.float32([1.0, 0.25, 4.0, 0.5, 2.0, 1.0, 8.0, 0.125])  # exact scalings, one per head
+    w = np.ascontiguousarray(np.broadcast_to(row, (1, 8, S, D)) * heads[None, :, None, None])
+    assert np.array_equal(affine.to_T(w, dtype), w)  # every value exact in T
+    want = affine.quantize(w, gs, bits, dtype)
+    codes = affine.unpack(want[0], bits)
+    assert np.any(codes[..., 2:] % 2 == 0)  # the ties went to even codes
+    got = kernels.quantize(from_np(w, torch_dtype(dtype), device), gs, bits)
+    assert np.array_equal(to_np(got[0]), want[0])
+    assert _bits_equal(to_np(got[1]), want[1], dtype)
+    assert _bits_equal(to_np(got[2]), want[2], dtype)
+
+
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
 def test_quantize_into_strided_destination(device, dtype):
     """Writes land at [t0, t0+S) of a capacity-padded buffer; nothing else changes."""
