@@ -9,33 +9,38 @@
 // 64-token K / V tile is loaded once per workgroup, dequantized once into
 // LDS, and read from LDS by all eight waves.  Per tile j, in each wave:
 //
-//   QK         S^T = K Q^T (A = K rows from LDS buffer j % 2, B = Q^T in
+//   QK         S^T = K Q^T (A = K rows from LDS buffer j % 4, B = Q^T in
 //              registers): 4 token blocks x D/32 steps of v_mfma_f32_16x16x32
 //              in the input type T, steps outer so that consecutive MFMAs
 //              feed four independent accumulators;
-//   dequant    every thread turns its piece of tile j + 1 (raw codes, scales
+//   dequant    every thread turns its piece of tile j + 2 (raw codes, scales
 //              and biases loaded two tiles ahead into one of two register
-//              sets) into values in the other LDS buffer -- K row-major
+//              sets) into values in LDS buffer (j + 2) % 4 -- K row-major
 //              (token, dims) in T, V transposed (dim, tokens) as float16,
 //              with the tokens of each 32-token half in the order of the S^T
 //              fragment so that the P^T operand is a lane's own softmax
 //              values -- and reissues that register set's loads for tile
-//              j + 3.  Waves 4-7 do this after their QK MFMAs, waves 0-3
+//              j + 4.  Waves 4-7 do this after their QK MFMAs, waves 0-3
 //              after their P.V, so that the two waves of a SIMD alternate
 //              MFMA and VALU phases (120 against 124 us at the C5 chunk).
 //              The SIMD's arbiter favours the older wave (0-3), which left
 //              waves 4-7 the longer path per tile (their dequantization
 //              contends with the other wave's softmax): they raise their
 //              priority from their dequantization to the end of the tile
-//              (117 against 121 us);
+//              (117 against 121 us; without it 113-115 against 108-109 us
+//              with four buffers, where the other placements lose 1.5-3.5 us);
 //   softmax    online, in the log2 domain, rescaled when the maximum grows
 //              by more than 8 (the decode kernel's); without a mask tensor
 //              the score scale is applied inside the exponent's fma; the
 //              tile maximum over a row's four lanes by row swaps (VALU)
 //              rather than LDS permutes;
 //   PV         out^T += V^T P^T in float16 (A = V^T rows from LDS, B = P^T);
-//   barrier    one per tile: it orders this tile's reads of buffer j % 2
-//              before the next tile's writes of it.
+//   barrier    one per pair of tiles (four buffers, 155,648 B of LDS): a
+//              buffer is rewritten two tiles after its last reads, and read
+//              two tiles after its writes, so one barrier after every odd
+//              tile orders both, and the waves drift by up to two tiles
+//              between barriers (108.4-108.9 against 109.9-110.1 us at the
+//              C5 chunk with a barrier per tile and two buffers).
 //
 // P.V runs in float16 for bfloat16 inputs too.  V is rounded to bfloat16
 // exactly as mx.dequantize rounds it, then scaled by 2^-k and converted to
@@ -338,7 +343,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(MfmaParams p, i
   // partials in the decode's layout, merged by merge_kernel).
   using PG = PGeo<D>;
   using P = Prefill<Tag, D, BITS, GS>;
-  __shared__ __attribute__((aligned(16))) uint8_t s_buf[2 * PG::BufBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t s_buf[4 * PG::BufBytes];
   __shared__ float s_red[kPWaves];
 
   const int tid = threadIdx.x;
@@ -585,10 +590,15 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(MfmaParams p, i
 #endif
   };
 
-  // ---- the tile pipeline: loads two tiles ahead, one barrier per tile ----
+  // ---- the tile pipeline: four LDS buffers, tile j in buffer j % 4,
+  // dequantized two tiles ahead from raw registers loaded two tiles before
+  // that; one barrier per pair of tiles.  Tile j writes buffer (j + 2) % 4,
+  // last read by tile j - 2, which every wave left before the barrier after
+  // tile j - 1 or j - 2 (the last odd tile); tile j reads what tile j - 2
+  // wrote, before that same barrier.  Between barriers the waves drift by up
+  // to two tiles. ----
   typename P::Raw R0, R1;
-  uint8_t* buf0 = s_buf;
-  uint8_t* buf1 = s_buf + PG::BufBytes;
+  auto buf = [&](int j) { return s_buf + (j & 3) * PG::BufBytes; };
   const int oob = len + 2 * kPTile;  // rows past every descriptor: the loads read zero
   auto row_of = [&](int j) { return j < T ? (j_base + j) * kPTile : oob; };
   // Keys of tile j; past the split's tiles, the sequence end (every score
@@ -596,11 +606,9 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(MfmaParams p, i
   auto keys_of = [&](int j) { return j < T ? (j_base + j) * kPTile : len; };
   auto run = [&](auto two_c) __attribute__((always_inline)) {
     for (int j = 0; j < T; j += 2) {
-      // tile j in buf0; R1 holds tile j + 1, R0 tile j + 2.
-      tile(two_c, buf0, buf1, R1, row_of(j + 3), keys_of(j));
-      __syncthreads();
-      // tile j + 1 in buf1; R0 holds tile j + 2, R1 tile j + 3.
-      tile(two_c, buf1, buf0, R0, row_of(j + 4), keys_of(j + 1));
+      // tiles j, j + 1 in buf(j), buf(j + 1); R0 holds tile j + 2, R1 tile j + 3.
+      tile(two_c, buf(j), buf(j + 2), R0, row_of(j + 4), keys_of(j));
+      tile(two_c, buf(j + 1), buf(j + 3), R1, row_of(j + 5), keys_of(j + 1));
       __syncthreads();
     }
   };
@@ -652,8 +660,10 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(MfmaParams p, i
         osc = __builtin_bit_cast(float, static_cast<uint32_t>(127 + k) << 23);
       }
     }
-    P::stage(R0, buf0, tid, vsc);
+    P::stage(R0, buf(0), tid, vsc);
     P::load(R0, src, row_of(2));
+    P::stage(R1, buf(1), tid, vsc);
+    P::load(R1, src, row_of(3));
     __syncthreads();
     if constexpr (Tag::kId == QSDPA_BF16) {
       if (two) run(std::true_type{});
