@@ -61,21 +61,24 @@ struct Rsrcs {
   uint32_t k_sn, ks_sn, kb_sn, v_sn, vs_sn, vb_sn;
 };
 
+// Words at the lane's byte offset `voff` plus the uniform `soff` (the buffer
+// instruction's scalar offset, which the range check includes: a uniform row
+// offset costs no VALU add).
 template <int WORDS, int AUX>
-__device__ __forceinline__ void buffer_words(rsrc_t rs, uint32_t off, uint32_t* w) {
+__device__ __forceinline__ void buffer_words(rsrc_t rs, uint32_t voff, uint32_t soff, uint32_t* w) {
   typedef uint32_t u4 __attribute__((ext_vector_type(4)));
   typedef uint32_t u2 __attribute__((ext_vector_type(2)));
   if constexpr (WORDS % 4 == 0) {
 #pragma unroll
     for (int i = 0; i < WORDS / 4; ++i) {
-      const u4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16 * i, 0, AUX);
+      const u4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 16 * i, soff, AUX);
       w[4 * i] = v[0]; w[4 * i + 1] = v[1]; w[4 * i + 2] = v[2]; w[4 * i + 3] = v[3];
     }
   } else if constexpr (WORDS == 2) {
-    const u2 v = __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, AUX);
+    const u2 v = __builtin_amdgcn_raw_buffer_load_b64(rs, voff, soff, AUX);
     w[0] = v[0]; w[1] = v[1];
   } else {
-    w[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, AUX);
+    w[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, voff, soff, AUX);
   }
 }
 
@@ -112,15 +115,15 @@ struct Kernel {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const uint32_t row = static_cast<uint32_t>(rel0 + 16 * u);
-      buffer_words<G::KW, kAux>(rs.k, row * rs.k_sn + L.k_r, R.kw[u]);
+      buffer_words<G::KW, kAux>(rs.k, L.k_r, row * rs.k_sn, R.kw[u]);
       if constexpr (G::KG == 2)
-        R.ks[u] = __builtin_amdgcn_raw_buffer_load_b32(rs.ks, row * rs.ks_sn + L.ks_r, 0, kAux);
+        R.ks[u] = __builtin_amdgcn_raw_buffer_load_b32(rs.ks, L.ks_r, row * rs.ks_sn, kAux);
       else
-        R.ks[u] = __builtin_amdgcn_raw_buffer_load_b16(rs.ks, row * rs.ks_sn + L.ks_r, 0, kAux);
+        R.ks[u] = __builtin_amdgcn_raw_buffer_load_b16(rs.ks, L.ks_r, row * rs.ks_sn, kAux);
       if constexpr (G::KG == 2) {
-        R.kb[u] = __builtin_amdgcn_raw_buffer_load_b32(rs.kb, row * rs.kb_sn + L.kb_r, 0, kAux);
+        R.kb[u] = __builtin_amdgcn_raw_buffer_load_b32(rs.kb, L.kb_r, row * rs.kb_sn, kAux);
       } else {
-        R.kb[u] = __builtin_amdgcn_raw_buffer_load_b16(rs.kb, row * rs.kb_sn + L.kb_r, 0, kAux);
+        R.kb[u] = __builtin_amdgcn_raw_buffer_load_b16(rs.kb, L.kb_r, row * rs.kb_sn, kAux);
       }
     }
   }
@@ -130,17 +133,17 @@ struct Kernel {
     for (int u = 0; u < 2; ++u) {
       const uint32_t row = static_cast<uint32_t>(rel0 + 16 * u);
       if constexpr (G::NG >= 2) {
-        R.vs[u] = __builtin_amdgcn_raw_buffer_load_b32(rs.vs, row * rs.vs_sn + L.vs_r, 0, kAux);
-        R.vb[u] = __builtin_amdgcn_raw_buffer_load_b32(rs.vb, row * rs.vb_sn + L.vb_r, 0, kAux);
+        R.vs[u] = __builtin_amdgcn_raw_buffer_load_b32(rs.vs, L.vs_r, row * rs.vs_sn, kAux);
+        R.vb[u] = __builtin_amdgcn_raw_buffer_load_b32(rs.vb, L.vb_r, row * rs.vb_sn, kAux);
       } else {
-        R.vs[u] = __builtin_amdgcn_raw_buffer_load_b16(rs.vs, row * rs.vs_sn + L.vs_r, 0, kAux);
-        R.vb[u] = __builtin_amdgcn_raw_buffer_load_b16(rs.vb, row * rs.vb_sn + L.vb_r, 0, kAux);
+        R.vs[u] = __builtin_amdgcn_raw_buffer_load_b16(rs.vs, L.vs_r, row * rs.vs_sn, kAux);
+        R.vb[u] = __builtin_amdgcn_raw_buffer_load_b16(rs.vb, L.vb_r, row * rs.vb_sn, kAux);
       }
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const uint32_t row = static_cast<uint32_t>(rel0 + 16 * (j >> 2) + (j & 3));
-      buffer_words<G::VW, kAux>(rs.v, row * rs.v_sn + L.v_r, R.vw[j]);
+      buffer_words<G::VW, kAux>(rs.v, L.v_r, row * rs.v_sn, R.vw[j]);
     }
   }
 
@@ -245,9 +248,18 @@ struct Kernel {
 
     // ---- scores of (the lane's row, tokens tau(quad, j)), online softmax ----
     // n1: this lane's end of keys (the sequence's, or its causal limit).
+    // Without a mask tensor and with a positive scale, the scale goes into
+    // the exponent's fma (max(S) q = max(S q) for q > 0): no multiply per
+    // score.
+    const bool fold = !MASK && p.qscale > 0.0f;
+    const float ea = fold ? p.qscale : 1.0f;
     float sc[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) sc[j] = S[j >> 2][j & 3] * p.qscale;
+    for (int j = 0; j < 8; ++j) sc[j] = S[j >> 2][j & 3];
+    if (!fold) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) sc[j] *= p.qscale;
+    }
     if constexpr (MASK) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) sc[j] += mv[j];
@@ -259,7 +271,7 @@ struct Kernel {
         if (t >= n1 || t < n0) sc[j] = -__builtin_huge_valf();
       }
     }
-    const float tmax = max_over_rows(max8(sc));
+    const float tmax = max_over_rows(max8(sc)) * ea;
     const bool grow = tmax > mrun + kRescale;
     if (__builtin_amdgcn_ballot_w64(grow)) {
       const float mnew = grow ? tmax : mrun;
@@ -271,7 +283,7 @@ struct Kernel {
     }
     float pr[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) pr[j] = fast_exp2(sc[j] - mrun);
+    for (int j = 0; j < 8; ++j) pr[j] = fast_exp2(fmaf(sc[j], ea, -mrun));
     lrun += ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
 
     // ---- P^T operand: k slot 2i, 2i+1 = tokens tau(quad, 2i), tau(quad, 2i+1) ----
