@@ -149,6 +149,18 @@ def quantized_sdpa(
         num_splits: optional explicit split count (overrides threshold)
     Returns (B, H_q, qL, D) in q's dtype.
     """
+    # A decode step that repeats an earlier call's geometry relaunches that
+    # call's argument block (the checks below held for it; its shapes and
+    # strides are the block's key).
+    if mask is None and kv_start is None and threshold is None and num_splits is None and q.dim() == 4 \
+            and q.shape[2] == 1 and bits in (4, 8):
+        both = k_biases is not None and v_biases is not None
+        out = kernels.decode_repeat(q, packed_k, packed_v, k_scales, v_scales, k_biases if both else None,
+                                    v_biases if both else None,
+                                    scale=q.shape[3] ** -0.5 if scale is None else scale, bits=bits,
+                                    group_size=group_size)
+        if out is not None:
+            return out
     B, H_q, qL, D, H_kv, N = _validate(q, packed_k, packed_v, bits, group_size)
     if scale is None:
         scale = D ** -0.5                                          # dispatch.py:86-87

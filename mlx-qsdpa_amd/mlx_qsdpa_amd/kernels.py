@@ -22,7 +22,7 @@ _MASK_CODE = {torch.float16: _lib.QSDPA_F16, torch.bfloat16: _lib.QSDPA_BF16,
 
 def _require_device(*tensors):
     for t in tensors:
-        if t is not None and t.device.type != "cuda":
+        if t is not None and not t.is_cuda:
             raise RuntimeError(
                 "mlx_qsdpa_amd kernels run on a ROCm GPU only; got a tensor on "
                 f"{t.device} (there is no CPU implementation)")
@@ -68,7 +68,13 @@ def to_device(t: torch.Tensor, device) -> torch.Tensor:
     return t.pin_memory().to(device, non_blocking=True)
 
 
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream(t: torch.Tensor) -> int:
+    """The current stream of t's device (raw handle)."""
+    if _RAW_STREAM is not None:
+        return _RAW_STREAM(t.get_device())
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
@@ -417,26 +423,33 @@ _ARGS = threading.local()
 _ARGS_MAX = 32
 
 
-def _geo(t):
-    """Shape without the key dimension, strides and dtype of a [B, H, N, .] tensor."""
-    return None if t is None else (t.shape[:2], t.shape[3:], t.stride(), t.dtype)
+def _cache_key(q, pk, pv, ks, vs, kb, vb, kv_start, scale, bits, group_size, num_splits, causal, stream):
+    """The argument block's key: everything the block encodes except the key
+    count N and the data pointers, plus the device and stream, or None when
+    the tensors disagree with one another (the full path then raises).  pv
+    must have pk's shape, the scales and biases one shape with pk's (B, H,
+    N)."""
+    sk, ss = pk.shape, ks.shape
+    if pv.shape != sk or vs.shape != ss or ss[:3] != sk[:3] or (kb is not None and kb.shape != ss) \
+            or (vb is not None and vb.shape != ss):
+        return None
+    return (q.shape, q.stride(), q.dtype, sk[0], sk[1], sk[3], pk.dtype, pv.dtype, pk.stride(), pv.stride(), ss[3],
+            ks.dtype, vs.dtype, ks.stride(), vs.stride(), None if kb is None else (kb.dtype, kb.stride()),
+            None if vb is None else (vb.dtype, vb.stride()), None if kv_start is None else kv_start.shape,
+            float(scale), bits, group_size, int(num_splits), bool(causal), q.get_device(), stream)
 
 
 def _cached_decode(q, pk, pv, ks, vs, kb, vb, scale, bits, group_size, kv_start, num_splits,
                    causal, prof_events):
     """The decode through a cached argument block; (None, slot) when this
     geometry has not been seen (the caller then takes the full path and
-    stores its block in `slot`)."""
-    if q.device.type != "cuda":
+    stores its block in `slot`), (None, None) when it cannot be cached."""
+    if not q.is_cuda:
         return None, None
-    N = pk.shape[2]
-    if pv.shape[2] != N or ks.shape[2] != N or vs.shape[2] != N or (kb is not None and kb.shape[2] != N) \
-            or (vb is not None and vb.shape[2] != N):
-        return None, None  # inconsistent key counts: the full path raises
     stream = _stream(q)
-    key = (q.shape, q.stride(), q.dtype, _geo(pk), _geo(pv), _geo(ks), _geo(vs), _geo(kb), _geo(vb),
-           None if kv_start is None else kv_start.shape, float(scale), bits, group_size, int(num_splits),
-           bool(causal), q.device.index, stream)
+    key = _cache_key(q, pk, pv, ks, vs, kb, vb, kv_start, scale, bits, group_size, num_splits, causal, stream)
+    if key is None:
+        return None, None  # inconsistent shapes: the full path raises
     cache = getattr(_ARGS, "d", None)
     if cache is None:
         cache = _ARGS.d = {}
@@ -445,23 +458,37 @@ def _cached_decode(q, pk, pv, ks, vs, kb, vb, scale, bits, group_size, kv_start,
         return None, (cache, key)
     a = hit[0]
     lib = _lib.load()
-    a.N = N
+    N = pk.shape[2]
     a.q.ptr = q.data_ptr()
     a.k_packed.ptr, a.v_packed.ptr = pk.data_ptr(), pv.data_ptr()
     a.k_scales.ptr, a.v_scales.ptr = ks.data_ptr(), vs.data_ptr()
     a.k_biases.ptr = None if kb is None else kb.data_ptr()
     a.v_biases.ptr = None if vb is None else vb.data_ptr()
     a.kv_start = None if kv_start is None else kv_start.data_ptr()
-    a.num_splits = int(num_splits)
-    ws = _lib.check(lib.qsdpa_decode_workspace_size(ctypes.byref(a), None))
-    if ws > a.workspace_bytes:
-        hit[1] = torch.empty(ws, dtype=torch.uint8, device=q.device)
-        a.workspace, a.workspace_bytes = hit[1].data_ptr(), ws
+    if N != hit[2]:  # the workspace depends on the geometry and N alone
+        a.N = N
+        ws = _lib.check(lib.qsdpa_decode_workspace_size(ctypes.byref(a), None))
+        if ws > a.workspace_bytes:
+            hit[1] = torch.empty(ws, dtype=torch.uint8, device=q.device)
+            a.workspace, a.workspace_bytes = hit[1].data_ptr(), ws
+        hit[2] = N
     out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     a.out.ptr = out.data_ptr()
     a.prof_begin, a.prof_end = prof_events if prof_events is not None else (None, None)
     _lib.check(lib.qsdpa_decode(ctypes.byref(a), stream))
     return out, None
+
+
+def decode_repeat(q, pk, pv, ks, vs, kb, vb, *, scale, bits, group_size):
+    """A decode (no mask, kv_start or explicit split count) that repeats an
+    earlier call's geometry, through its argument block; None when there is
+    no such block or a packed row is not 16-byte aligned (the caller then
+    takes the full path).  Every tensor must be on the GPU (checked)."""
+    if q.is_cuda and pk.is_cuda and pv.is_cuda and ks.is_cuda and vs.is_cuda and (kb is None or kb.is_cuda) \
+            and (vb is None or vb.is_cuda) and q.stride(-1) == 1 and not (pk.data_ptr() | pv.data_ptr()) & 15:
+        out, _ = _cached_decode(q, pk, pv, ks, vs, kb, vb, scale, bits, group_size, None, 0, False, None)
+        return out
+    return None
 
 
 def decode(q, pk, pv, ks, vs, kb, vb, *, scale, bits, group_size, mask=None, kv_start=None,
@@ -514,5 +541,5 @@ def decode(q, pk, pv, ks, vs, kb, vb, *, scale, bits, group_size, mask=None, kv_
             cache.pop(next(iter(cache)))
         if ws <= 0:
             a.workspace, a.workspace_bytes, workspace = None, 0, None
-        cache[key] = [a, workspace]
+        cache[key] = [a, workspace, a.N]
     return out
