@@ -223,7 +223,10 @@ int qsdpa_dequantize(const qsdpa_dequantize_args* args, void* stream);
  *   new token i is src row i;
  *   each kept row is quantized as qsdpa_quantize does.
  * The destination must not overlap the old window.  The jobs of one call
- * share B, H, bits, group_size and dtype.
+ * share B, H, bits, group_size and dtype.  Every view's rows within one
+ * (batch, head) must span fewer than 2^31 elements (offsets there are
+ * 32-bit; QSDPA_ERR_UNSUPPORTED otherwise), and its strides must not be
+ * negative.
  * Replaces the dequantize + concatenate + trim + quantize of
  * mlx_qsdpa/cache.py:593-634 (QuantizedRotatingSDPACache._update_prefill,
  * _dequant_temporal) and cache.py:813-857 (the batched cache's).

@@ -13,6 +13,7 @@ import shutil
 import subprocess
 
 import pytest
+import torch
 
 from conftest import ROOT
 from mlx_qsdpa_amd import _lib
@@ -101,6 +102,15 @@ def test_invalid_arguments_return_codes():
     r[1].bits, r[1].H = 4, 2  # K and V of one cache: same batch and heads
     assert lib.qsdpa_requant_window(r, 2, None) == _lib.QSDPA_ERR_INVALID
     assert b"share B, H" in lib.qsdpa_last_error()
+    if not torch.cuda.is_available():  # dummy pointers: never where a launch could reach a GPU
+        r[1].H = 1
+        for x in r:
+            for i, v in enumerate((x.old_packed, x.old_scales, x.src, x.dst_packed, x.dst_scales, x.dst_biases)):
+                v.ptr = (1 + i) << 20  # stand-in addresses, never dereferenced
+                v.stride_n, v.stride_h, v.stride_b = 16, 64, 64
+        r[1].old_packed.stride_n = 1 << 31  # two old rows 2^31 words apart: 32-bit offsets cannot reach
+        assert lib.qsdpa_requant_window(r, 2, None) == _lib.QSDPA_ERR_UNSUPPORTED
+        assert b"2^31" in lib.qsdpa_last_error()
     m = (_lib.RowMove * 2)()
     for x in m:
         x.dst, x.heads, x.tokens, x.row_bytes = 64, 2, 4, 16
