@@ -8,7 +8,8 @@ pass where the groups fill the GPU and key splits (merged by the split-K
 merge kernel) where they do not.  Covered: both dtypes, 4- and 8-bit codes, all
 group sizes, the symmetric format, causal and full attention, kv_start
 (left padding), bool and additive masks, a partial last row group, a
-partial last key tile, keys that start inside a tile, and the C5 chunk.
+partial last key tile, keys that start inside a tile, key ranges of one to
+three tiles, huge K scales, and the C5 chunk.
 Tolerance: |out - ref| <= 2e-3 + 1e-2 |ref|.
 """
 
@@ -107,6 +108,20 @@ def test_prefill_key_splits(device, case):
     if causal:
         ks = torch.tensor([0, 611][:B], dtype=torch.int32, device=device)
         _check(q, kq, vq, bits, gs, f"split case {case} kv_start", causal=True, kv_start=ks)
+
+
+@pytest.mark.parametrize("N", [1, 63, 64, 65, 130, 191])
+def test_prefill_short_key_ranges(device, N):
+    """One to three 64-key tiles (full and partial): the pipeline dequantizes
+    two tiles ahead into four LDS buffers, so the first pair's stages and
+    loads reach past the last tile.  Full attention and causal, where qL > N
+    leaves the first positions without keys (rows of zeros)."""
+    B, Hq, Hkv, L, bits, gs = 1, 16, 4, 128, 8, 128
+    for dtype in (torch.bfloat16, torch.float16):
+        q, kq, vq = _inputs(B, Hq, Hkv, N, L, bits, gs, dtype, seed=N)
+        print(f"prefill short N={N} {dtype}", flush=True)
+        _check(q, kq, vq, bits, gs, f"short N={N} {dtype}")
+        _check(q, kq, vq, bits, gs, f"short N={N} {dtype} causal", causal=True)
 
 
 def test_prefill_kv_start_and_masks(device):
