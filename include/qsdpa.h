@@ -45,7 +45,7 @@
 extern "C" {
 #endif
 
-#define QSDPA_ABI_VERSION 4
+#define QSDPA_ABI_VERSION 5
 
 enum {
   QSDPA_OK = 0,
@@ -116,7 +116,11 @@ typedef struct {
    * (a run may cross sequences; a sequence with no keys gets none).       */
   int32_t num_splits;
 
-  /* Scratch for split-K partials, from qsdpa_decode_workspace_size().    */
+  /* Scratch for split-K partials, from qsdpa_decode_workspace_size().
+   * Its first 64 KiB hold the counters of the split merge that runs inside
+   * the decode launch: zero-fill a workspace before its first use; every
+   * call leaves them zero again, so a workspace can be re-used by later
+   * calls (in stream order) of any shape.                                 */
   void* workspace;
   size_t workspace_bytes;
 

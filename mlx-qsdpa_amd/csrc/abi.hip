@@ -41,7 +41,7 @@ int launch_merge(const qsdpa_decode_args* a, int num_splits, const float* part_a
 bool mfma_supports(const qsdpa_decode_args* a);
 int mfma_num_splits(const qsdpa_decode_args* a, int cus);
 int launch_decode_mfma(const qsdpa_decode_args* a, int num_splits, float* part_acc, float* part_ml,
-                       int units, int* sched, hipStream_t stream);
+                       int units, int* sched, unsigned* tickets, hipStream_t stream);
 // Defined in prefill_mfma.hip.
 bool prefill_supports(const qsdpa_decode_args* a);
 int prefill_num_splits(const qsdpa_decode_args* a, int cus);
@@ -129,6 +129,55 @@ int validate_decode(const qsdpa_decode_args* a) {
 
 }  // namespace
 
+namespace {
+
+// Where a split-K call keeps its scratch in the workspace, in bytes from
+// its start: the split merge's counters (kTicketBytes, zero between calls),
+// the partial rows, their (m, l), and the stream-K schedule.
+struct WorkspaceLayout {
+  int64_t acc, ml, sched, total;
+};
+
+WorkspaceLayout workspace_layout(const qsdpa_decode_args* a, int splits) {
+  const int64_t rows = static_cast<int64_t>(a->B) * a->H_q * std::max(a->q_len, 1);
+  WorkspaceLayout w;
+  w.acc = kTicketBytes;
+  w.ml = w.acc + rows * (splits + 1) * a->D * 4;
+  w.sched = w.ml + rows * (splits + 1) * 2 * 4;
+  w.total = w.sched + ((8LL * a->B + 255) / 256) * 256;
+  return w;
+}
+
+}  // namespace
+
+// A left-padded batch on the MFMA path runs splits * B equal units of the
+// stream-K schedule (common.h) over its sequences laid end to end, instead
+// of giving every sequence `splits`; 0 = uniform splits.
+int streamk_units(const qsdpa_decode_args* a, int splits) {
+  if (!a->kv_start || a->B < 2 || splits < 2 || !mfma_supports(a)) return 0;
+  // D = 256, 8-bit codes with a mask tensor: the stream-K instantiation
+  // would need more than 256 VGPRs (it spilled to scratch); uniform splits
+  // handle kv_start as well.
+  if (a->mask.ptr && a->D == 256 && a->bits == 8) return 0;
+  const int64_t units = static_cast<int64_t>(splits) * a->B;
+  if (units >= (int64_t(1) << 31) / 2) return 0;
+  if (static_cast<int64_t>(a->B) * (a->N / kSchedTile + 1) >= (int64_t(1) << 31)) return 0;
+  return static_cast<int>(units);
+}
+
+// A split-K decode on the matrix-core kernel with uniform splits merges its
+// partials inside the launch (decode_mfma.hip::split_merge) when it has at
+// most kFusedSplits splits, its blocks of 16 query rows have counters (at
+// most kTicketBlocks) and a block's partial rows span less than 2^31 bytes;
+// otherwise the merge kernel combines them.
+bool fused_merge(const qsdpa_decode_args* a, int splits, bool prefill, bool mfma, int units) {
+  if (prefill || !mfma || units > 0 || splits < 2 || splits > kFusedSplits) return false;
+  const int64_t qL = std::max(a->q_len, 1);
+  const int64_t G = a->H_q / a->H_kv;
+  const int64_t blocks = static_cast<int64_t>(a->B) * a->H_kv * ((G * qL + 15) / 16);
+  return blocks <= kTicketBlocks && G * qL * splits * a->D * 4 < (int64_t(1) << 31);
+}
+
 // Split count: enough workgroups to cover every CU twice, but never fewer
 // than 64 keys per split, and no more than kMaxSplits.
 int decode_plan(const qsdpa_decode_args* a, int* num_splits, int64_t* workspace_bytes) {
@@ -155,46 +204,38 @@ int decode_plan(const qsdpa_decode_args* a, int* num_splits, int64_t* workspace_
   // Partial slots per query row: splits, or splits + 1 columns per sequence
   // (U + B, U = splits * B) under the stream-K schedule of a left-padded
   // batch; then that schedule's (first column, count) per sequence.
-  const int64_t rows = static_cast<int64_t>(a->B) * a->H_q * std::max(a->q_len, 1);
-  *workspace_bytes = splits > 1 ? rows * (splits + 1) * (a->D + 2) * 4 + 8LL * a->B + 256 : 0;
+  *workspace_bytes = splits > 1 ? workspace_layout(a, splits).total : 0;
   return QSDPA_OK;
-}
-
-// A left-padded batch on the MFMA path runs splits * B equal units of the
-// stream-K schedule (common.h) over its sequences laid end to end, instead
-// of giving every sequence `splits`; 0 = uniform splits.
-int streamk_units(const qsdpa_decode_args* a, int splits) {
-  if (!a->kv_start || a->B < 2 || splits < 2 || !mfma_supports(a)) return 0;
-  const int64_t units = static_cast<int64_t>(splits) * a->B;
-  if (units >= (int64_t(1) << 31) / 2) return 0;
-  if (static_cast<int64_t>(a->B) * (a->N / kSchedTile + 1) >= (int64_t(1) << 31)) return 0;
-  return static_cast<int>(units);
 }
 
 // Launch the decode for validated arguments: the main kernel, then (split-K)
 // the merge, with the partials in `workspace` (decode_plan's layout).
 int run_decode(const qsdpa_decode_args* args, int splits, void* workspace, hipStream_t s) {
-  float* part_acc = nullptr;
-  float* part_ml = nullptr;
-  int* sched = nullptr;
-  if (splits > 1) {
-    const int64_t rows = static_cast<int64_t>(args->B) * args->H_q * std::max(args->q_len, 1);
-    part_acc = static_cast<float*>(workspace);
-    part_ml = part_acc + rows * (splits + 1) * args->D;
-    sched = reinterpret_cast<int*>(part_ml + rows * (splits + 1) * 2);
-  }
   // (prof_begin / prof_end ride on the main kernel's own dispatch)
   const bool prefill = prefill_supports(args);
   const bool mfma = mfma_supports(args);
   const int units = prefill ? 0 : streamk_units(args, splits);
+  const bool fused = fused_merge(args, splits, prefill, mfma, units);
+  float* part_acc = nullptr;
+  float* part_ml = nullptr;
+  int* sched = nullptr;
+  if (splits > 1) {
+    const WorkspaceLayout w = workspace_layout(args, splits);
+    uint8_t* base = static_cast<uint8_t*>(workspace);
+    part_acc = reinterpret_cast<float*>(base + w.acc);
+    part_ml = reinterpret_cast<float*>(base + w.ml);
+    sched = reinterpret_cast<int*>(base + w.sched);
+  }
   int rc;
   if (prefill) rc = launch_prefill_mfma(args, splits, part_acc, part_ml, s);
-  else if (mfma) rc = launch_decode_mfma(args, splits, part_acc, part_ml, units, sched, s);
+  else if (mfma)
+    rc = launch_decode_mfma(args, splits, part_acc, part_ml, units, sched,
+                            fused ? static_cast<unsigned*>(workspace) : nullptr, s);
   else rc = launch_decode_valu(args, splits, part_acc, part_ml, s);
   if (rc) return rc;
   // The MFMA kernel stores float16 inputs' partials as normalised float16
   // rows (in the first half of the float32 area).
-  if (splits > 1)
+  if (splits > 1 && !fused)
     rc = launch_merge(args, splits, part_acc, part_ml, mfma && args->dtype == QSDPA_F16, units ? sched : nullptr,
                       units + args->B, s);
   return rc;
@@ -205,8 +246,10 @@ int run_decode(const qsdpa_decode_args* args, int splits, void* workspace, hipSt
 // name to a kernel (on the host it is only a stand-in): each device's address
 // comes from hipGetSymbolAddress on the first call on that device.  Every
 // call on one GPU shares that GPU's array, so calls that overlap on one GPU
-// (two streams, or two host threads) race on it.  Nothing in it needs to
-// start at zero: every partial the merge reads is written by the same call.
+// (two streams, or two host threads) race on it.  Its first kTicketBytes
+// hold the split merge's counters: zero when the code object is loaded (a
+// static array without initializer is zero-filled) and zero again after
+// every call; every partial a merge reads is written by the same call.
 constexpr size_t kScratchBytes = QSDPA_NOALLOC_SCRATCH_BYTES;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 

@@ -15,6 +15,18 @@ void clear_error();
 // Map hipGetLastError() after a launch to QSDPA_OK / QSDPA_ERR_LAUNCH.
 int check_launch(const char* what);
 
+// The decode workspace starts with the split merge's counters: kTicketWords
+// uint32 per block of 16 query rows (batch, kv head, row block), for at
+// most kTicketBlocks blocks.  They must be zero before a workspace's first
+// use, and every call leaves them zero.
+constexpr int kTicketWords = 32;
+constexpr int kTicketBlocks = 512;
+constexpr int64_t kTicketBytes = int64_t(kTicketWords) * kTicketBlocks * 4;
+// Most splits a matrix-core decode launch merges itself (one level, the
+// last workgroup of a block: decode_mfma.hip::split_merge); more splits go
+// to the merge kernel.
+constexpr int kFusedSplits = 16;
+
 inline bool aligned(const void* p, int bytes) {
   return (reinterpret_cast<uintptr_t>(p) % static_cast<uintptr_t>(bytes)) == 0;
 }

@@ -57,28 +57,6 @@
 #include "mfma_tile.h"
 #include "wave_split.h"
 
-// Timeline probe (a build with -DQSDPA_TIMELINE only; the default build has
-// none of it): each wave stamps s_memrealtime (100 MHz) at fixed points of
-// the kernel into a device array that qsdpa_debug_timeline() copies out.
-// Slots per wave: 0 entry, 1 Q staged, 2 + k the k-th tile done (k < 12),
-// 14 stream end, 15 partials merged in LDS, 16 stores issued, 17 stores
-// complete.
-#ifdef QSDPA_TIMELINE
-constexpr int kTlWgs = 2048, kTlSlots = 18;
-__device__ unsigned long long g_timeline[kTlWgs * 8 * kTlSlots];
-#define QSDPA_TS(k)                                                                                      \
-  do {                                                                                                   \
-    const int slot_ = (k);                                                                               \
-    const int wg_ = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);                     \
-    if (wg_ < kTlWgs && slot_ < kTlSlots && (threadIdx.x & 63) == 0)                                    \
-      g_timeline[(wg_ * 8 + (threadIdx.x >> 6)) * kTlSlots + slot_] = __builtin_amdgcn_s_memrealtime(); \
-  } while (0)
-#else
-#define QSDPA_TS(k) \
-  do {              \
-  } while (0)
-#endif
-
 namespace qsdpa {
 
 namespace {
@@ -87,7 +65,7 @@ namespace {
 // most jmax of them) of sequence b for the block's 16 query rows.  Writes the
 // normalised output (one split) or the partials at column `col` of the rows'
 // partial slots.  Called by the whole workgroup.
-template <typename Tag, int D, int BITS, int GS, bool MASK>
+template <typename Tag, int D, int BITS, int GS, bool MASK, bool SK, bool FUSED>
 __device__ __forceinline__ void decode_segment(const MfmaParams& p, float* s_acc, float (*s_ml)[16][2],
                                                uint8_t* s_q, int lane, int wave, int quad, int r, int hblk,
                                                int kvh, int b, int t_lo, int stride, int jmax, int col) {
@@ -202,7 +180,6 @@ __device__ __forceinline__ void decode_segment(const MfmaParams& p, float* s_acc
   // grid's first tiles (20 MB at C3) would queue in front of it.
   if (qh < 16) *reinterpret_cast<u4*>(s_q + qh * kQRow + qc * 16) = qh < nh ? qv : u4{0u, 0u, 0u, 0u};
   __syncthreads();
-  QSDPA_TS(1);
   typename K::Regs R;
   int j = wave;
   K::load_k(R, rs, L, row_of(j));
@@ -238,17 +215,14 @@ __device__ __forceinline__ void decode_segment(const MfmaParams& p, float* s_acc
   float mrun = kNegBig;
   float lrun = 0.0f;
 
-  int tile_ = 0;
   while (j < J) {
     const int nj = next_pos(j);
     const int nrow = row_of(nj);
     auto ik = [&](typename K::Regs& X) { K::load_k(X, rs, L, nrow); };
     auto iv = [&](typename K::Regs& X) { K::load_v(X, rs, L, nrow); };
     K::template compute_tile<MASK>(R, p, qt, acc, mrun, lrun, s0 + row_of(j), s0, n_lane, quad, mrow, vm, ik, iv);
-    QSDPA_TS(2 + min(tile_++, 11));
     j = nj;
   }
-  QSDPA_TS(14);
 
   // ---- per-head totals over the four quads ----
   lrun += shfl_xor_f32(lrun, 16);
@@ -269,16 +243,108 @@ __device__ __forceinline__ void decode_segment(const MfmaParams& p, float* s_acc
       *reinterpret_cast<f4*>(dst + nb) = f4{acc[nb][i], acc[nb + 1][i], acc[nb + 2][i], acc[nb + 3][i]};
   }
   __syncthreads();
-  QSDPA_TS(15);
 
-  merge_store<Tag, D, kWaves>(
+  merge_store<Tag, D, kWaves, FUSED>(
       p, [&](int w, int h) { return s_acc + (w * 16 + h) * kRowF; },
       [&](int w, int h) { return f32x2{s_ml[w][h][0], s_ml[w][h][1]}; }, nh, v0, kvh, b, col, kThreads);
-  QSDPA_TS(16);
-#ifdef QSDPA_TIMELINE
+}
+
+// The split merge inside the launch (the FUSED instantiation: uniform
+// splits, at most kFusedSplits of them), after decode_segment stored this
+// split's partial rows.  Every workgroup waits until its partial stores are
+// complete, then takes a ticket of its block (batch, kv head, row block): an
+// agent-scope atomic increment that wraps to zero at the split count, so the
+// counter is zero again after every call.  The workgroup that draws the last
+// ticket merges the block's partials in split order and writes the output;
+// the others exit.  No workgroup waits for another, and the order of every
+// sum is fixed, so repeated calls give identical bits whichever workgroup
+// merges.  The partials cross XCDs through agent-coherent loads and stores
+// (kCoherent).  Thread t merges dims [8 (t % (D / 8)), +8) of row t / (D / 8).
+//
+// One level only: with more splits, a second level (the last of a group of
+// 16 merging into a group sum, the last group merging the sums) puts two
+// rounds of store, ticket and load on the path of the last workgroup, about
+// 2.9 us each on MI355X; measured at C3 (128 splits) that made the step
+// 30.2 us against 25.2 us with the merge kernel, so larger split counts keep
+// the merge kernel.
+template <typename Tag, int D>
+__device__ __forceinline__ void split_merge(const MfmaParams& p, int* s_flag, int b, int kvh, int hblk) {
+  constexpr bool kHalf = Tag::kId == QSDPA_F16;  // float16 normalised partial rows
+  constexpr int kPer = 8, kRowT = D / kPer;
+  constexpr uint32_t kPast = 0x80000000u;  // an offset past every descriptor: reads zero
+  typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+  const int S = p.num_splits;
+  unsigned* tk = p.tickets + static_cast<int64_t>(blockIdx.z * gridDim.y + blockIdx.y) * kTicketWords;
+  // Every partial store of this workgroup is complete before its ticket.
   __builtin_amdgcn_s_waitcnt(0);
-  QSDPA_TS(17);
-#endif
+  __syncthreads();
+  if (threadIdx.x == 0)
+    *s_flag = __builtin_amdgcn_atomic_inc32(tk, static_cast<unsigned>(S - 1), __ATOMIC_RELAXED, "agent") ==
+              static_cast<unsigned>(S - 1);
+  __syncthreads();
+  if (!*s_flag) return;
+
+  const int v0 = hblk * 16, nh = min(16, p.G * p.qL - v0);
+  const int t = threadIdx.x, h = t / kRowT, d = (t % kRowT) * kPer;
+  if (t >= 16 * kRowT || h >= nh) return;
+  const int v = v0 + h;
+  const int hh = kvh * p.G + v % p.G, iq = v / p.G;
+  const PartRows<Tag, D> pr(p, b, kvh);
+  const uint32_t row0 = PartRows<Tag, D>::local(p, v);  // slot of split 0 of the row
+  // All S partials' loads are issued before the first wait (S <= 16;
+  // slots past S read zero through an offset past the descriptor).
+  u2 m2[kFusedSplits];
+  u4 w[kFusedSplits][kHalf ? 1 : 2];
+#pragma unroll
+  for (int k = 0; k < kFusedSplits; ++k) {
+    const bool ok = k < S;
+    const uint32_t slot = row0 + static_cast<uint32_t>(k);
+    m2[k] = __builtin_amdgcn_raw_buffer_load_b64(pr.ml, ok ? slot * 8 : kPast, 0, kCoherent);
+#pragma unroll
+    for (int q = 0; q < (kHalf ? 1 : 2); ++q)
+      w[k][q] = __builtin_amdgcn_raw_buffer_load_b128(
+          pr.acc, ok ? (slot * D + d + 4 * q) * PartRows<Tag, D>::kEsz : kPast, 0, kCoherent);
+  }
+  // Whole-vector bit casts: this compiler reads element 0 for a bit cast of
+  // any single element of a vector.
+  f32x2 ml[kFusedSplits];
+  float M = kNegBig;
+#pragma unroll
+  for (int k = 0; k < kFusedSplits; ++k) {
+    ml[k] = k < S ? __builtin_bit_cast(f32x2, m2[k]) : f32x2{kNegBig, 0.0f};
+    M = fmaxf(M, ml[k][0]);
+  }
+  // out = sum_s w_s x_s / sum_s l_s 2^(m_s - M), w_s = l_s 2^(m_s - M) for
+  // normalised rows, 2^(m_s - M) for float32 sums (the merge kernel's
+  // equations, merge.hip).
+  float L = 0.0f, acc[kPer];
+#pragma unroll
+  for (int e = 0; e < kPer; ++e) acc[e] = 0.0f;
+#pragma unroll
+  for (int k = 0; k < kFusedSplits; ++k) {
+    const float wk = fast_exp2(ml[k][0] - M);
+    L = fmaf(ml[k][1], wk, L);
+    const float we = kHalf ? ml[k][1] * wk : wk;
+    float xv[kPer];
+    if constexpr (kHalf) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t u = w[k][0][e];
+        xv[2 * e] = f16_bits_to_f32(static_cast<uint16_t>(u));
+        xv[2 * e + 1] = f16_bits_to_f32(static_cast<uint16_t>(u >> 16));
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const f4 f = __builtin_bit_cast(f4, w[k][q]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xv[4 * q + e] = f[e];
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < kPer; ++e) acc[e] = fmaf(xv[e], we, acc[e]);
+  }
+  store_out8<Tag>(p, b, hh, iq, d, acc, L);
 }
 
 // SK: the stream-K schedule of a left-padded batch (a loop over segments);
@@ -286,15 +352,14 @@ __device__ __forceinline__ void decode_segment(const MfmaParams& p, float* s_acc
 // register pressure stays out of the common case).  MASK: a mask tensor
 // (its own instantiation: with the mask code in the unmasked kernel, C3
 // took 23.2 instead of 22.3 us).
-template <typename Tag, int D, int BITS, int GS, bool SK, bool MASK>
+template <typename Tag, int D, int BITS, int GS, bool SK, bool MASK, bool FUSED>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_mfma_kernel(MfmaParams p) {
   constexpr int kRowF = D + 4;  // LDS floats per (wave, head) row
   __shared__ __attribute__((aligned(16))) float s_acc[kWaves * 16 * kRowF];
   __shared__ float s_ml[kWaves][16][2];
   constexpr int kQRow = D * 2 + 16;  // bytes per staged Q row
   __shared__ __attribute__((aligned(16))) uint8_t s_q[16 * kQRow];
-
-  QSDPA_TS(0);
+  __shared__ int s_flag;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int quad = lane >> 4;
@@ -303,8 +368,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int kvh = blockIdx.y / p.hb_count;
   if constexpr (!SK) {
     // Uniform splits: grid (S, H_kv * row blocks, B); split x of sequence z.
-    decode_segment<Tag, D, BITS, GS, MASK>(p, s_acc, s_ml, s_q, lane, wave, quad, r, hblk, kvh, blockIdx.z, blockIdx.x,
+    decode_segment<Tag, D, BITS, GS, MASK, false, FUSED>(p, s_acc, s_ml, s_q, lane, wave, quad, r, hblk, kvh, blockIdx.z, blockIdx.x,
                                      p.num_splits, 0x7FFFFFFF, blockIdx.x);
+    if constexpr (FUSED) split_merge<Tag, D>(p, &s_flag, blockIdx.z, kvh, hblk);
   } else {
     // Left-padded batch: grid (U, H_kv * row blocks, 1), unit x of the
     // stream-K schedule (common.h) owns global tiles [x * C, (x + 1) * C) of
@@ -321,7 +387,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       const int Tb = seq_tiles(p.kv_start, b, p.N);
       const int hi = min(g_end, P + Tb);
       if (hi > g) {
-        decode_segment<Tag, D, BITS, GS, MASK>(p, s_acc, s_ml, s_q, lane, wave, quad, r, hblk, kvh, b, g - P, 1, hi - g,
+        decode_segment<Tag, D, BITS, GS, MASK, true, false>(p, s_acc, s_ml, s_q, lane, wave, quad, r, hblk, kvh, b, g - P, 1, hi - g,
                                          static_cast<int>(blockIdx.x) + b);
         __syncthreads();  // the next segment reuses the LDS
         g = hi;
@@ -335,16 +401,24 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 template <typename Tag, int D, int BITS, bool MASK>
 void launch_mask(const MfmaParams& p, int gs, hipStream_t stream, const qsdpa_decode_args* a) {
   const dim3 grid(p.units ? p.units : p.num_splits, p.Hkv * p.hb_count, p.units ? 1 : p.B);
-  void (*k)(MfmaParams);
-  if (p.units)
-    k = gs == 32 ? decode_mfma_kernel<Tag, D, BITS, 32, true, MASK>
-      : gs == 64 ? decode_mfma_kernel<Tag, D, BITS, 64, true, MASK>
-                 : decode_mfma_kernel<Tag, D, BITS, 128, true, MASK>;
+  void (*k)(MfmaParams) = nullptr;
+  // No stream-K instantiation for D = 256, 8-bit codes with a mask tensor
+  // (the launcher gives such calls uniform splits: abi.hip streamk_units).
+  constexpr bool kStreamK = !(MASK && D == 256 && BITS == 8);
+  if (p.units) {
+    if constexpr (kStreamK)
+      k = gs == 32 ? decode_mfma_kernel<Tag, D, BITS, 32, true, MASK, false>
+        : gs == 64 ? decode_mfma_kernel<Tag, D, BITS, 64, true, MASK, false>
+                   : decode_mfma_kernel<Tag, D, BITS, 128, true, MASK, false>;
+  } else if (p.tickets)
+    k = gs == 32 ? decode_mfma_kernel<Tag, D, BITS, 32, false, MASK, true>
+      : gs == 64 ? decode_mfma_kernel<Tag, D, BITS, 64, false, MASK, true>
+                 : decode_mfma_kernel<Tag, D, BITS, 128, false, MASK, true>;
   else
-    k = gs == 32 ? decode_mfma_kernel<Tag, D, BITS, 32, false, MASK>
-      : gs == 64 ? decode_mfma_kernel<Tag, D, BITS, 64, false, MASK>
-                 : decode_mfma_kernel<Tag, D, BITS, 128, false, MASK>;
-  launch_profiled(k, grid, dim3(kThreads), stream, a->prof_begin, a->prof_end, p);
+    k = gs == 32 ? decode_mfma_kernel<Tag, D, BITS, 32, false, MASK, false>
+      : gs == 64 ? decode_mfma_kernel<Tag, D, BITS, 64, false, MASK, false>
+                 : decode_mfma_kernel<Tag, D, BITS, 128, false, MASK, false>;
+  if (k) launch_profiled(k, grid, dim3(kThreads), stream, a->prof_begin, a->prof_end, p);
 }
 
 template <typename Tag, int D, int BITS>
@@ -416,10 +490,13 @@ int mfma_num_splits(const qsdpa_decode_args* a, int cus) {
 }
 
 int launch_decode_mfma(const qsdpa_decode_args* a, int num_splits, float* part_acc, float* part_ml,
-                       int units, int* sched, hipStream_t stream) {
+                       int units, int* sched, unsigned* tickets, hipStream_t stream) {
   MfmaParams p = mfma_params(a, num_splits, part_acc, part_ml);
   p.units = units;
   p.sched = sched;
+  p.tickets = tickets;
+  if (units && a->mask.ptr && a->D == 256 && a->bits == 8)
+    return fail(QSDPA_ERR_UNSUPPORTED, "decode_mfma: no stream-K kernel for D=256 8-bit codes with a mask");
   const bool f16 = a->dtype == QSDPA_F16;
   if (a->D == 128) {
     if (f16) launch_bits<F16, 128>(p, a->bits, a->group_size, stream, a);
@@ -433,97 +510,3 @@ int launch_decode_mfma(const qsdpa_decode_args* a, int num_splits, float* part_a
 
 }  // namespace qsdpa
 
-#ifdef QSDPA_TIMELINE
-namespace qsdpa {
-namespace {
-// Read-only streaming probe (probe build only): workgroup w of `gridDim.x`
-// reads its contiguous share of the buffer in 16-byte pieces, 8 pieces per
-// thread in flight, with the decode's non-temporal policy, and writes one
-// word -- the time of one launch that only reads that many bytes.
-__global__ __launch_bounds__(512) void stream_read_kernel(const u4* src, uint64_t n16, uint32_t* sink) {
-  const uint64_t share = (n16 + gridDim.x - 1) / gridDim.x;
-  const uint64_t lo = blockIdx.x * share;
-  const uint64_t hi = lo + share < n16 ? lo + share : n16;
-  uint32_t acc = 0;
-  for (uint64_t i = lo + threadIdx.x; i < hi; i += 8 * 512) {
-    u4 x[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const uint64_t j = i + static_cast<uint64_t>(k) * 512;
-      x[k] = j < hi ? __builtin_nontemporal_load(src + j) : u4{0u, 0u, 0u, 0u};
-    }
-#pragma unroll
-    for (int k = 0; k < 8; ++k) acc ^= x[k][0] ^ x[k][1] ^ x[k][2] ^ x[k][3];
-  }
-  if (acc == 0x9e3779b9u) sink[blockIdx.x] = acc;  // keeps the loads; the sink is almost never written
-}
-
-// The same with W-byte loads (4, 8 or 16 per lane) and P of them per thread
-// in flight: equal bytes in flight with more, narrower load instructions.
-template <int W, int P>
-__global__ __launch_bounds__(512) void stream_read_w_kernel(const uint8_t* src, uint64_t n, uint32_t* sink) {
-  typedef uint32_t u2 __attribute__((ext_vector_type(2)));
-  const uint64_t share = (n + gridDim.x - 1) / gridDim.x;
-  const uint64_t lo = blockIdx.x * share;
-  const uint64_t hi = lo + share < n ? lo + share : n;
-  uint32_t acc = 0;
-  for (uint64_t i = lo + threadIdx.x; i < hi; i += static_cast<uint64_t>(P) * 512) {
-    uint32_t x[P];
-#pragma unroll
-    for (int k = 0; k < P; ++k) {
-      const uint64_t j = i + static_cast<uint64_t>(k) * 512;
-      if constexpr (W == 16) {
-        const u4 v = j < hi ? __builtin_nontemporal_load(reinterpret_cast<const u4*>(src) + j) : u4{0u, 0u, 0u, 0u};
-        x[k] = v[0] ^ v[1] ^ v[2] ^ v[3];
-      } else if constexpr (W == 8) {
-        const u2 v = j < hi ? __builtin_nontemporal_load(reinterpret_cast<const u2*>(src) + j) : u2{0u, 0u};
-        x[k] = v[0] ^ v[1];
-      } else {
-        x[k] = j < hi ? __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(src) + j) : 0u;
-      }
-    }
-#pragma unroll
-    for (int k = 0; k < P; ++k) acc ^= x[k];
-  }
-  if (acc == 0x9e3779b9u) sink[blockIdx.x] = acc;
-}
-}  // namespace
-}  // namespace qsdpa
-
-// W-byte variant: `bytes` a multiple of 16, width 4 / 8 / 16, per 4 / 8 / 16 / 32.
-extern "C" int qsdpa_debug_stream_read_w(const void* src, uint64_t bytes, void* sink, int blocks, int width, int per,
-                                         void* stream, void* ev_begin, void* ev_end) {
-  if (!src || !sink || blocks < 1 || bytes % 16) return -1;
-  void (*k)(const uint8_t*, uint64_t, uint32_t*) = nullptr;
-#define QSDPA_SRW(w, p) \
-  if (width == w && per == p) k = qsdpa::stream_read_w_kernel<w, p>;
-  QSDPA_SRW(4, 4) QSDPA_SRW(4, 8) QSDPA_SRW(4, 16) QSDPA_SRW(4, 32)
-  QSDPA_SRW(8, 4) QSDPA_SRW(8, 8) QSDPA_SRW(8, 16) QSDPA_SRW(8, 32)
-  QSDPA_SRW(16, 4) QSDPA_SRW(16, 8) QSDPA_SRW(16, 16) QSDPA_SRW(16, 32)
-#undef QSDPA_SRW
-  if (!k) return -1;
-  hipExtLaunchKernelGGL(k, dim3(blocks), dim3(512), 0, static_cast<hipStream_t>(stream),
-                        static_cast<hipEvent_t>(ev_begin), static_cast<hipEvent_t>(ev_end), 0,
-                        static_cast<const uint8_t*>(src), static_cast<uint64_t>(bytes / width),
-                        static_cast<uint32_t*>(sink));
-  return hipGetLastError() == hipSuccess ? 0 : -1;
-}
-
-// Launch the streaming probe over `bytes` (a multiple of 16) with `blocks`
-// workgroups of 512 threads; ev_begin / ev_end (hipEvent_t) ride on the dispatch.
-extern "C" int qsdpa_debug_stream_read(const void* src, uint64_t bytes, void* sink, int blocks, void* stream,
-                                       void* ev_begin, void* ev_end) {
-  if (!src || !sink || blocks < 1 || bytes % 16) return -1;
-  hipExtLaunchKernelGGL(qsdpa::stream_read_kernel, dim3(blocks), dim3(512), 0, static_cast<hipStream_t>(stream),
-                        static_cast<hipEvent_t>(ev_begin), static_cast<hipEvent_t>(ev_end), 0,
-                        static_cast<const qsdpa::u4*>(src), static_cast<uint64_t>(bytes / 16),
-                        static_cast<uint32_t*>(sink));
-  return hipGetLastError() == hipSuccess ? 0 : -1;
-}
-
-// Copy the timeline stamps (uint64 [2048 workgroups][8 waves][18 slots]).
-extern "C" int qsdpa_debug_timeline(void* dst, size_t bytes) {
-  if (bytes > sizeof(g_timeline)) bytes = sizeof(g_timeline);
-  return hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_timeline), bytes) == hipSuccess ? 0 : -1;
-}
-#endif

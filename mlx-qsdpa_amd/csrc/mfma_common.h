@@ -50,6 +50,11 @@ struct MfmaParams {
   float* part_ml;
   int units;   // > 0: stream-K schedule of a left-padded batch over this many units per kv head
   int* sched;  // (first partial column, count) per sequence, for the merge when units > 0
+  // Split merge inside the launch (uniform splits, at most kFusedSplits):
+  // null = the merge kernel combines the partials; otherwise kTicketWords
+  // counters per block (batch, kv head, row block), zero between calls, and
+  // the last workgroup of a block merges its partials.
+  unsigned* tickets;
   // Query positions: the G * qL rows of a kv head are (position v / G, head
   // v % G); a block takes 16 consecutive rows.
   int qL, causal;
@@ -305,6 +310,7 @@ inline MfmaParams mfma_params(const qsdpa_decode_args* a, int num_splits, float*
   p.part_ml = part_ml;
   p.units = 0;
   p.sched = nullptr;
+  p.tickets = nullptr;
   return p;
 }
 

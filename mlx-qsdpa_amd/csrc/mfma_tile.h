@@ -360,12 +360,58 @@ struct Kernel {
   }
 };
 
+// Cache policy (the aux operand of buffer loads and stores) of the partials
+// that workgroups of one launch hand to each other: sc1, coherent across
+// the device's XCDs without a write-back of the whole L2 (what the compiler
+// emits for relaxed agent-scope atomic loads and stores on gfx950).
+constexpr int kCoherent = 16;
+
+// A normalised output row piece: out[b, hh, iq, d .. d + 8) = v / L (0 when
+// L = 0: every key of the row was masked or absent).  Output rows are only
+// 2-byte aligned in general: stores of 16-bit halves.
+template <typename Tag>
+__device__ __forceinline__ void store_out8(const MfmaParams& p, int b, int hh, int iq, int d, const float (&v)[8],
+                                           float L) {
+  const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+  uint32_t pk[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) pk[e] = pack_T2<Tag>(v[2 * e] * inv, v[2 * e + 1] * inv);
+  uint16_t* dst = p.out + static_cast<int64_t>(b) * p.o_sb + static_cast<int64_t>(hh) * p.o_sh +
+                  static_cast<int64_t>(iq) * p.o_sq + d;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    dst[2 * e] = static_cast<uint16_t>(pk[e]);
+    dst[2 * e + 1] = static_cast<uint16_t>(pk[e] >> 16);
+  }
+}
+
+// The partial rows of one block (batch b, kv head kvh) of a uniform-split
+// launch: rows (head, position) of the kv head, `num_splits` slots each,
+// addressed through buffer descriptors from the block's first slot (the
+// launcher keeps the span below 2^31 bytes).  Slot of query row v (position
+// v / G of head kvh * G + v % G) and split x: local(v) + x.
+template <typename Tag, int D>
+struct PartRows {
+  static constexpr int kEsz = Tag::kId == QSDPA_F16 ? 2 : 4;  // float16 normalised rows, or float32 sums
+  rsrc_t acc, ml;
+  int64_t first;
+  __device__ __forceinline__ PartRows(const MfmaParams& p, int b, int kvh) {
+    first = (static_cast<int64_t>(b) * p.Hq + static_cast<int64_t>(kvh) * p.G) * p.qL * p.num_splits;
+    const uint32_t rows = static_cast<uint32_t>(p.G * p.qL * p.num_splits);
+    acc = make_rsrc(reinterpret_cast<const uint8_t*>(p.part_acc) + first * D * kEsz, rows * D * kEsz);
+    ml = make_rsrc(p.part_ml + first * 2, rows * 8);
+  }
+  static __device__ __forceinline__ uint32_t local(const MfmaParams& p, int v) {
+    return static_cast<uint32_t>(((v % p.G) * p.qL + v / p.G) * p.num_splits);
+  }
+};
+
 // Merge the NWV waves' running (m, l, acc) of a block's 16 query rows and
 // store the result: the normalised output (one split) or the split's partial
 // at column `col`.  row_of(w, h): wave w's accumulator row of query row h
 // (D floats, dims in order); ml_of(w, h): its (m, l).  Rows >= nh are
 // padding.  Called by all `nthreads` threads after a barrier.
-template <typename Tag, int D, int NWV, typename RowF, typename MlF>
+template <typename Tag, int D, int NWV, bool FUSED, typename RowF, typename MlF>
 __device__ __forceinline__ void merge_store(const MfmaParams& p, RowF&& row_of, MlF&& ml_of, int nh, int v0,
                                             int kvh, int b, int col, int nthreads) {
   // 16 heads x D dims; thread -> (head, 8 consecutive dims).
@@ -400,17 +446,31 @@ __device__ __forceinline__ void merge_store(const MfmaParams& p, RowF&& row_of, 
     const int hh = kvh * p.G + vh % p.G;  // head and query position of the row
     const int iq = vh / p.G;
     if (p.num_splits == 1) {
-      const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-      uint32_t pk[kPer / 2];
+      store_out8<Tag>(p, b, hh, iq, d, v, L);
+    } else if (FUSED) {
+      // Partials merged inside this launch (split_merge): agent-coherent
+      // stores through the block's descriptors.
+      if constexpr (FUSED) {
+      const PartRows<Tag, D> pr(p, b, kvh);
+      const uint32_t slot = PartRows<Tag, D>::local(p, vh) + col;
+      if constexpr (Tag::kId == QSDPA_F16) {
+        const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+        const u4 w = u4{pack_T2<Tag>(v[0] * inv, v[1] * inv), pack_T2<Tag>(v[2] * inv, v[3] * inv),
+                        pack_T2<Tag>(v[4] * inv, v[5] * inv), pack_T2<Tag>(v[6] * inv, v[7] * inv)};
+        __builtin_amdgcn_raw_buffer_store_b128(w, pr.acc, (slot * D + d) * 2, 0, kCoherent);
+      } else {
 #pragma unroll
-      for (int e = 0; e < kPer / 2; ++e) pk[e] = pack_T2<Tag>(v[2 * e] * inv, v[2 * e + 1] * inv);
-      uint16_t* dst = p.out + static_cast<int64_t>(b) * p.o_sb + static_cast<int64_t>(hh) * p.o_sh +
-                      static_cast<int64_t>(iq) * p.o_sq + d;
-      // out rows are only 2-byte aligned in general: store pairs.
-#pragma unroll
-      for (int e = 0; e < kPer / 2; ++e) {
-        dst[2 * e] = static_cast<uint16_t>(pk[e]);
-        dst[2 * e + 1] = static_cast<uint16_t>(pk[e] >> 16);
+        for (int e = 0; e < 2; ++e)
+          __builtin_amdgcn_raw_buffer_store_b128(
+              u4{__builtin_bit_cast(uint32_t, v[4 * e]), __builtin_bit_cast(uint32_t, v[4 * e + 1]),
+                 __builtin_bit_cast(uint32_t, v[4 * e + 2]), __builtin_bit_cast(uint32_t, v[4 * e + 3])},
+              pr.acc, (slot * D + d + 4 * e) * 4, 0, kCoherent);
+      }
+      if (d == 0) {
+        typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+        __builtin_amdgcn_raw_buffer_store_b64(u2{__builtin_bit_cast(uint32_t, Mh), __builtin_bit_cast(uint32_t, L)},
+                                              pr.ml, slot * 8, 0, kCoherent);
+      }
       }
     } else {
       // Partial rows: (b, head, position) rows, each with its splits.

@@ -65,26 +65,6 @@
 
 #include "mfma_common.h"
 
-// Phase probe (a build with -DQSDPA_TIMELINE only; the default build has
-// none of it): every wave sums, over its tiles, the shader-clock cycles
-// (s_memtime) from the tile's start to its row maxima (QK, scores; waves 4-7
-// also their dequantization), from there to the tile's end (softmax, P.V;
-// waves 0-3 also their dequantization), and at the barrier, into a device
-// array that qsdpa_debug_prefill_phases() copies out.  Each stamp waits for
-// its own result, which lengthens the kernel by about a sixth.
-#ifdef QSDPA_TIMELINE
-constexpr int kPhWgs = 4096;
-__device__ unsigned long long g_pf_phases[kPhWgs * 8 * 4];
-__device__ __forceinline__ unsigned long long pf_stamp() {
-  unsigned long long t;
-  asm volatile("s_memtime %0\n\ts_waitcnt lgkmcnt(0)" : "=s"(t)::"memory");
-  return t;
-}
-#define QSDPA_PF_PROBE 1
-#else
-#define QSDPA_PF_PROBE 0
-#endif
-
 namespace qsdpa {
 namespace {
 
@@ -454,17 +434,10 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(MfmaParams p, i
   // dequantization from the register set `Rn` into `nxt` and that set's
   // reload from row `nrow`, the softmax, then P.V from `cur`.
   // two_c: P as two float16 terms (std::true_type) or one.
-#if QSDPA_PF_PROBE
-  unsigned long long ph_qk = 0, ph_pv = 0, ph_bar = 0, ph_t3 = 0, ph_n = 0;
-#endif
   auto tile = [&](auto two_c, const uint8_t* cur, uint8_t* nxt, typename P::Raw& Rn, int nrow,
                   int tb0) __attribute__((always_inline)) {
     constexpr bool kTwo = decltype(two_c)::value;
     const int tb = s0 + tb0;
-#if QSDPA_PF_PROBE
-    const unsigned long long ts1 = pf_stamp();
-    if (ph_t3) ph_bar += ts1 - ph_t3;
-#endif
     float mv[16];
     if constexpr (MASK)  // keys tb + 16 t + 4 quad + i of the lane's mask row
       mask_tile<16>(p, mrow, tb + 4 * quad, tb + kPTile <= p.N, [](int e) { return 16 * (e >> 2) + (e & 3); }, mv);
@@ -528,10 +501,6 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(MfmaParams p, i
 #pragma unroll
     for (int e = 1; e < 16; ++e) tmax = fmaxf(tmax, sc[e]);
     tmax = max_over_rows(tmax) * ea;
-#if QSDPA_PF_PROBE
-    const unsigned long long ts2 = pf_stamp();
-    ph_qk += ts2 - ts1;
-#endif
     const bool grow = tmax > mrun + kRescale;
     if (__builtin_amdgcn_ballot_w64(grow)) {
       const float mnew = grow ? tmax : mrun;
@@ -583,11 +552,6 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(MfmaParams p, i
     } else {
       __builtin_amdgcn_s_setprio(0);
     }
-#if QSDPA_PF_PROBE
-    ph_t3 = pf_stamp();
-    ph_pv += ph_t3 - ts2;
-    ++ph_n;
-#endif
   };
 
   // ---- the tile pipeline: four LDS buffers, tile j in buffer j % 4,
@@ -673,12 +637,6 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(MfmaParams p, i
     }
   }
 
-#if QSDPA_PF_PROBE
-  if (blockIdx.x < kPhWgs && lane == 0) {
-    unsigned long long* g = g_pf_phases + (blockIdx.x * 8 + wave) * 4;
-    g[0] = ph_qk; g[1] = ph_pv; g[2] = ph_bar; g[3] = ph_n;
-  }
-#endif
   // ---- normalise and store: lane (quad, r) holds dims 16 db + 4 quad + i of row r ----
   float l = lrun;
   l += shfl_xor_f32(l, 16);
@@ -804,59 +762,3 @@ int launch_prefill_mfma(const qsdpa_decode_args* a, int splits, float* part_acc,
 
 }  // namespace qsdpa
 
-#if QSDPA_PF_PROBE
-namespace qsdpa {
-namespace {
-// LDS read probe (probe build only): every wave of a 512-thread workgroup
-// reads the prefill kernel's K and V^T operand pattern (16-byte reads, rows
-// padded by 32 bytes) from one of two buffers, `iters` times, and workgroup
-// 0's wave 0 writes its s_memtime cycles: LDS bytes per cycle per CU.
-__global__ __launch_bounds__(kPThreads) void lds_read_kernel(int iters, uint32_t* sink, unsigned long long* cycles) {
-  using PG = PGeo<128>;
-  __shared__ __attribute__((aligned(16))) uint8_t s[2 * PG::BufBytes];
-  for (int i = threadIdx.x * 4; i < 2 * PG::BufBytes; i += kPThreads * 4)
-    *reinterpret_cast<uint32_t*>(s + i) = static_cast<uint32_t>(i) * 2654435761u;
-  __syncthreads();
-  const int lane = threadIdx.x & 63, quad = lane >> 4, r = lane & 15;
-  u4 acc = u4{0u, 0u, 0u, 0u};
-  const unsigned long long t0 = pf_stamp();
-  for (int it = 0; it < iters; ++it) {
-    const uint8_t* cur = s + (it & 1) * PG::BufBytes;
-    asm volatile("" ::: "memory");
-#pragma unroll
-    for (int m = 0; m < PG::NM; ++m)
-#pragma unroll
-      for (int tk = 0; tk < 4; ++tk) acc ^= *reinterpret_cast<const u4*>(cur + (16 * tk + r) * PG::KPitch + (32 * m + 8 * quad) * 2);
-#pragma unroll
-    for (int u = 0; u < 2; ++u)
-#pragma unroll
-      for (int db = 0; db < PG::NB; ++db)
-        acc ^= *reinterpret_cast<const u4*>(cur + PG::KBytes + (16 * db + r) * kVPitch + (32 * u + 8 * quad) * 2);
-  }
-  const unsigned long long t1 = pf_stamp();
-  if ((acc[0] ^ acc[1] ^ acc[2] ^ acc[3]) == 0x9e3779b9u) sink[blockIdx.x] = acc[0];
-  if (blockIdx.x == 0 && threadIdx.x == 0) cycles[0] = t1 - t0;
-}
-}  // namespace
-}  // namespace qsdpa
-
-// Launch the LDS read probe: `blocks` workgroups of 512 threads (one per CU:
-// 77,824 B of LDS each), `iters` reads of 32 KB per wave; cycles[0] gets
-// workgroup 0's s_memtime cycles.
-extern "C" int qsdpa_debug_lds_read(int blocks, int iters, void* sink, void* cycles, void* stream, void* ev_begin,
-                                    void* ev_end) {
-  if (blocks < 1 || iters < 1 || !sink || !cycles) return -1;
-  hipExtLaunchKernelGGL(qsdpa::lds_read_kernel, dim3(blocks), dim3(qsdpa::kPThreads), 0,
-                        static_cast<hipStream_t>(stream), static_cast<hipEvent_t>(ev_begin),
-                        static_cast<hipEvent_t>(ev_end), 0, iters, static_cast<uint32_t*>(sink),
-                        static_cast<unsigned long long*>(cycles));
-  return hipGetLastError() == hipSuccess ? 0 : -1;
-}
-
-// Copy the prefill phase sums (uint64 [4096 workgroups][8 waves][4]: QK
-// cycles, P.V cycles, barrier cycles, tiles).
-extern "C" int qsdpa_debug_prefill_phases(void* dst, size_t bytes) {
-  if (bytes > sizeof(g_pf_phases)) bytes = sizeof(g_pf_phases);
-  return hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_pf_phases), bytes) == hipSuccess ? 0 : -1;
-}
-#endif

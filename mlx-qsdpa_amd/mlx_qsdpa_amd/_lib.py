@@ -23,7 +23,7 @@ QSDPA_BF16 = 1
 QSDPA_F32 = 2
 QSDPA_BOOL = 3
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 NOALLOC_SCRATCH_BYTES = 16 << 20
 
 # Every symbol include/qsdpa.h declares.

@@ -390,7 +390,9 @@ class DecodePlan:
         self.num_splits = int(n.value)
         self.workspace = None
         if ws > 0:
-            self.workspace = torch.empty(ws, dtype=torch.uint8, device=q.device)
+            # Zero-filled: the split merge's counters at its start must be
+            # zero before the first call (each call leaves them zero).
+            self.workspace = torch.zeros(ws, dtype=torch.uint8, device=q.device)
             self.args.workspace = self.workspace.data_ptr()
             self.args.workspace_bytes = ws
         self._args_ref = ctypes.byref(self.args)
@@ -469,7 +471,7 @@ def _cached_decode(q, pk, pv, ks, vs, kb, vb, scale, bits, group_size, kv_start,
         a.N = N
         ws = _lib.check(lib.qsdpa_decode_workspace_size(ctypes.byref(a), None))
         if ws > a.workspace_bytes:
-            hit[1] = torch.empty(ws, dtype=torch.uint8, device=q.device)
+            hit[1] = torch.zeros(ws, dtype=torch.uint8, device=q.device)
             a.workspace, a.workspace_bytes = hit[1].data_ptr(), ws
         hit[2] = N
     out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
@@ -491,6 +493,21 @@ def decode_repeat(q, pk, pv, ks, vs, kb, vb, *, scale, bits, group_size):
     return None
 
 
+# Split-K workspaces of uncached decode calls, one per (device, stream): the
+# calls of a stream run in order, so they can share one buffer, zero-filled
+# once (the split merge's counters at its start are zero between calls).
+_WORKSPACES = {}
+
+
+def _stream_workspace(device, stream, nbytes):
+    key = (device.index, stream)
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+        _WORKSPACES[key] = ws
+    return ws
+
+
 def decode(q, pk, pv, ks, vs, kb, vb, *, scale, bits, group_size, mask=None, kv_start=None,
            num_splits=0, out=None, workspace=None, prof_events=None, causal=False):
     """Fused quantized attention; returns out [B, H_q, qL, D] (dtype of q).
@@ -503,7 +520,10 @@ def decode(q, pk, pv, ks, vs, kb, vb, *, scale, bits, group_size, mask=None, kv_
     around the main decode kernel (see qsdpa_decode_args.prof_begin).
 
     Without a mask, ``out`` or ``workspace``, a call that repeats an earlier
-    call's tensor geometry re-launches that call's argument block.
+    call's tensor geometry re-launches that call's argument block.  A
+    caller's ``workspace`` (uint8, at least qsdpa_decode_workspace_size
+    bytes) must be zero-filled before its first use; the library leaves the
+    counters at its start zero after every call, so it can be re-used.
     """
     _require_device(q, pk, pv, ks, vs, kb, vb, mask, kv_start)
     slot = None
@@ -528,7 +548,7 @@ def decode(q, pk, pv, ks, vs, kb, vb, *, scale, bits, group_size, mask=None, kv_
     ws = _lib.check(lib.qsdpa_decode_workspace_size(ctypes.byref(a), ctypes.byref(n)))
     if ws > 0:
         if workspace is None or workspace.numel() < ws:
-            workspace = torch.empty(ws, dtype=torch.uint8, device=q.device)
+            workspace = _stream_workspace(q.device, _stream(q), ws)
         a.workspace = workspace.data_ptr()
         a.workspace_bytes = ws
     if prof_events is not None:

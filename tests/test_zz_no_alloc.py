@@ -51,7 +51,7 @@ def _run_both(host, devt, bits, gs, dt, kv_start=None, num_splits=0, causal=Fals
         if noalloc:
             _lib.check(lib.qsdpa_decode_noalloc(ctypes.byref(a), stream))
         else:
-            wsbuf = torch.empty(max(ws, 1), dtype=torch.uint8, device=q.device)
+            wsbuf = torch.zeros(max(ws, 1), dtype=torch.uint8, device=q.device)  # zero-filled before first use
             a.workspace, a.workspace_bytes = wsbuf.data_ptr(), ws
             _lib.check(lib.qsdpa_decode(ctypes.byref(a), stream))
         torch.cuda.synchronize()
