@@ -233,7 +233,7 @@ int run_decode(const qsdpa_decode_args* args, int splits, void* workspace, hipSt
                             fused ? static_cast<unsigned*>(workspace) : nullptr, s);
   else rc = launch_decode_valu(args, splits, part_acc, part_ml, s);
   if (rc) return rc;
-  // The MFMA kernel stores float16 inputs' partials as normalised float16
+  // The MFMA kernels store float16 inputs' partials as normalised float16
   // rows (in the first half of the float32 area).
   if (splits > 1 && !fused)
     rc = launch_merge(args, splits, part_acc, part_ml, mfma && args->dtype == QSDPA_F16, units ? sched : nullptr,

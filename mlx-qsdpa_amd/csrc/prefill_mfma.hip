@@ -618,7 +618,10 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(MfmaParams p, i
       two = !(bound <= kPVSingle);
       if (bound > kVBound) {
         // k = 1 + floor(log2(bound / kVBound)), so that bound 2^-k < kVBound.
-        const float x = fminf(bound * (1.0f / kVBound), 0x1p100f);
+        // A finite bfloat16 bound (< 2^128) needs k <= 113; the clamp keeps
+        // k <= 126 when the scan overflowed to Inf, so that 2^-k and 2^k
+        // stay normal floats.
+        const float x = fminf(bound * (1.0f / kVBound), 0x1p125f);
         const int k = static_cast<int>((__builtin_bit_cast(uint32_t, x) >> 23) & 0xFFu) - 126;
         vsc = __builtin_bit_cast(float, static_cast<uint32_t>(127 - k) << 23);
         osc = __builtin_bit_cast(float, static_cast<uint32_t>(127 + k) << 23);
@@ -660,9 +663,13 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(MfmaParams p, i
       o[3] = static_cast<uint16_t>(hi >> 16);
     }
   } else {
-    // The split's partial of row (b, hq, iq), column `split`, as the decode
-    // kernel stores it: float16 inputs the normalised row acc / l as
-    // float16, bfloat16 inputs the float32 row; then (m, l).
+    // The split's partial of row (b, hq, iq), column `split`, then (m, l):
+    // float16 inputs store the normalised row acc / l as float16 (as the
+    // decode kernel does); bfloat16 inputs store it as float32, with
+    // (m + log2 l, 1) -- the same partial to the merge, whose weight for it
+    // is l 2^(m - M) either way, but a sum that stays below max |V| where
+    // acc itself would overflow float32 (rows of V near the bfloat16
+    // maximum).
     const int64_t slot = ((static_cast<int64_t>(b) * p.Hq + hq) * p.qL + iq) * S + split;
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
 #pragma unroll
@@ -673,12 +680,13 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(MfmaParams p, i
         *reinterpret_cast<u2*>(reinterpret_cast<uint16_t*>(p.part_acc) + slot * D + d) =
             u2{pack_T2<Tag>(acc[db][0] * inv, acc[db][1] * inv), pack_T2<Tag>(acc[db][2] * inv, acc[db][3] * inv)};
       } else {
-        __builtin_nontemporal_store(acc[db] * osc, reinterpret_cast<f4*>(p.part_acc + slot * D + d));
+        __builtin_nontemporal_store(acc[db] * (inv * osc), reinterpret_cast<f4*>(p.part_acc + slot * D + d));
       }
     }
     if (quad == 0) {
-      p.part_ml[slot * 2] = mrun;
-      p.part_ml[slot * 2 + 1] = l;
+      const bool norm = Tag::kId != QSDPA_F16 && l > 0.0f;
+      p.part_ml[slot * 2] = norm ? mrun + __log2f(l) : mrun;
+      p.part_ml[slot * 2 + 1] = norm ? 1.0f : l;
     }
   }
 }

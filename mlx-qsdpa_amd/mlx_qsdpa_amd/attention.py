@@ -24,35 +24,7 @@ import torch
 from torch import nn
 
 from . import cache_sdpa, kernels
-
-
-def _plain_sdpa(q, k, v, scale, mask, kv_start=None):
-    """softmax(scale * q k^T + mask) v in float32, grouped-query heads, mask
-    None / "causal" (lower-right aligned) / bool keep-mask / additive; keys
-    before kv_start[b] are skipped.  Rows with every key masked give zeros."""
-    B, Hq, L, D = q.shape
-    Hkv, N = k.shape[1], k.shape[2]
-    qf = q.float().reshape(B, Hkv, (Hq // Hkv) * L, D)
-    kt = k.float().transpose(-1, -2).contiguous()
-    s = torch.matmul(qf, kt).reshape(B, Hq, L, N) * float(scale)
-    cols = torch.arange(N, device=q.device)
-    if isinstance(mask, str):
-        if mask != "causal":
-            raise ValueError(f"unknown mask {mask!r}")
-        rows = torch.arange(L, device=q.device)[:, None] + (N - L)
-        s = s.masked_fill(cols[None, :] > rows, float("-inf"))
-    elif mask is not None:
-        m = mask.to(q.device)
-        s = s.masked_fill(~m, float("-inf")) if m.dtype == torch.bool else s + m.float()
-    if kv_start is not None:
-        ks = kv_start.to(q.device, torch.int64)
-        s = s.masked_fill(cols[None, None, None, :] < ks[:, None, None, None], float("-inf"))
-    mx = s.amax(dim=-1, keepdim=True)
-    e = torch.exp(s - torch.where(torch.isfinite(mx), mx, torch.zeros_like(mx)))
-    den = e.sum(dim=-1, keepdim=True)
-    p = e / torch.where(den > 0, den, torch.ones_like(den))
-    out = torch.matmul(p.reshape(B, Hkv, (Hq // Hkv) * L, N), v.float().contiguous())
-    return out.reshape(B, Hq, L, D).to(q.dtype)
+from .dispatch import attention_fp32
 
 
 def scaled_dot_product_attention(queries, keys, values, cache=None, scale=None, mask=None, *,
@@ -69,7 +41,7 @@ def scaled_dot_product_attention(queries, keys, values, cache=None, scale=None, 
         return cache_sdpa(queries, keys, values, cache, scale=scale, mask=mask, kv_start=kv_start)
     if isinstance(keys, tuple):
         raise TypeError("quantized keys need a cache marked _use_fused_sdpa")
-    return _plain_sdpa(queries, keys, values, scale, mask, kv_start)
+    return attention_fp32(queries, keys, values, scale, mask, kv_start)
 
 
 class KVCache:

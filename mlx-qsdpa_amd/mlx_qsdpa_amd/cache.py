@@ -164,17 +164,14 @@ class _Relayout:
         return self.kv
 
 
-def _spare_for(cache):
-    """The rotating cache's second buffer set (the target of a prefill's
-    requantization, which may not overwrite the window it reads), allocated
-    on first use and whenever the window's buffers changed shape.  It is
-    working memory, not cache state: nbytes does not count it."""
-    spare = getattr(cache, "_spare", None)
-    if spare is None or any(a.shape != b.shape or a.dtype != b.dtype or a.device != b.device
-                            for a, b in zip(spare[0] + spare[1], cache._keys + cache._values)):
-        spare = (tuple(torch.zeros_like(t) for t in cache._keys),
-                 tuple(torch.zeros_like(t) for t in cache._values))
-    return spare
+def _prefill_target(cache):
+    """Fresh buffers shaped like the rotating cache's window, the target of a
+    prefill's requantization (which may not overwrite the window it reads).
+    The old window is dropped once the launch is queued: the allocator
+    reuses its memory in stream order, so a cache holds one window between
+    prefills, as the reference's does."""
+    return (tuple(torch.zeros_like(t) for t in cache._keys),
+            tuple(torch.zeros_like(t) for t in cache._values))
 
 
 def _nbytes(tup):
@@ -604,11 +601,10 @@ class QuantizedRotatingSDPACache:
         S = keys.shape[2]
         n_old = min(self.offset, self.max_size)
         rot = self._ring_rot(n_old) if n_old else 0
-        spare = _spare_for(self)
-        total = kernels.requant_window((self._keys, self._values), (keys, values), spare, n_old, self.keep,
+        dst = _prefill_target(self)
+        total = kernels.requant_window((self._keys, self._values), (keys, values), dst, n_old, self.keep,
                                        rot, self.max_size, self.bits, self.group_size)
-        self._spare = (self._keys, self._values)
-        self._keys, self._values = spare
+        self._keys, self._values = dst
         self.offset += S
         self._idx = total if total < self.max_size else self.keep
         n_visible = min(self.offset, self.max_size)
@@ -781,11 +777,10 @@ class BatchQuantizedRotatingSDPACache:
         S = keys.shape[2]
         n_old = min(self._idx, self.max_size)
         rot = self._ring_rot() if n_old else 0
-        spare = _spare_for(self)
-        total = kernels.requant_window((self._keys, self._values), (keys, values), spare, n_old, self.keep,
+        dst = _prefill_target(self)
+        total = kernels.requant_window((self._keys, self._values), (keys, values), dst, n_old, self.keep,
                                        rot, self.max_size, self.bits, self.group_size)
-        self._spare = (self._keys, self._values)
-        self._keys, self._values = spare
+        self._keys, self._values = dst
         self.offset = self.offset + S
         self._idx = total
         return _sl(self._keys, 0, total), _sl(self._values, 0, total)
@@ -863,7 +858,6 @@ class BatchQuantizedRotatingSDPACache:
             for j, b in enumerate(keep):
                 rl.row(j, 0, kv, b, [(0, width)])
             self._keys, self._values = rl.run()
-            self._spare = None
         self.offset = self.offset[keep]
         self.left_padding = self.left_padding[keep]
 
@@ -896,7 +890,6 @@ class BatchQuantizedRotatingSDPACache:
                         rl.row(row)
                     row += 1
             self._keys, self._values = rl.run()
-            self._spare = None
         self.offset = torch.cat([self.offset, other.offset])
         self.left_padding = torch.cat([self.left_padding + (n - vis[0]), other.left_padding + (n - vis[1])])
         self._idx = n

@@ -18,6 +18,10 @@ choices:
   Shapes that kernel does not take (D = 64, unaligned views) keep the
   reference's path: HIP dequantize, then float32 attention with torch on
   the GPU (dispatch.py:68-83).
+
+Head dims the library does not compile (any other multiple of 32, e.g. 32
+or 512, which the reference's validation accepts: dispatch.py:48-49) take
+that same dequantize + attention path at every qL.
 """
 
 from __future__ import annotations
@@ -50,69 +54,55 @@ def _validate(q, packed_k, packed_v, bits, group_size):
     return B, H_q, qL, D, H_kv, N
 
 
-def attention_fp32(q, k, v, scale, mask=None):
+def attention_fp32(q, k, v, scale, mask=None, kv_start=None):
     """float32 SDPA on the GPU with MLX mask conventions.
 
-    q [B,Hq,L,D], k/v [B,Hkv,N,D] (dequantized T).  Bool masks keep True,
-    float masks are added, "causal" is lower-right aligned; rows with every
-    key masked return 0.  Output has q's dtype.
+    q [B,Hq,L,D], k/v [B,Hkv,N,D] (dequantized T), grouped-query heads.
+    Bool masks keep True, float masks are added, "causal" is lower-right
+    aligned; keys before kv_start[b] are skipped; rows with every key masked
+    return 0.  Output has q's dtype.
     """
     B, Hq, L, D = q.shape
     Hkv, N = k.shape[1], k.shape[2]
     G = Hq // Hkv
     qf = q.float().reshape(B, Hkv, G * L, D)
     kt = k.float().transpose(-1, -2).contiguous()
-    s = torch.matmul(qf, kt).reshape(B, Hkv, G, L, N) * float(scale)
-    s = s.reshape(B, Hq, L, N)
+    s = torch.matmul(qf, kt).reshape(B, Hq, L, N) * float(scale)
+    cols = torch.arange(N, device=q.device)
     if isinstance(mask, str):
         if mask != "causal":
             raise ValueError(f"unknown mask {mask!r}")
-        qi = torch.arange(L, device=q.device)[:, None] + (N - L)
-        kj = torch.arange(N, device=q.device)[None, :]
-        s = s.masked_fill(qi < kj, float("-inf"))
+        rows = torch.arange(L, device=q.device)[:, None] + (N - L)
+        s = s.masked_fill(cols[None, :] > rows, float("-inf"))
     elif mask is not None:
         m = mask.to(q.device)
-        if m.dtype == torch.bool:
-            s = s.masked_fill(~m, float("-inf"))
-        else:
-            s = s + m.float()
-    p = torch.softmax(s, dim=-1)
-    p = torch.nan_to_num(p, nan=0.0)
+        s = s.masked_fill(~m, float("-inf")) if m.dtype == torch.bool else s + m.float()
+    if kv_start is not None:
+        ks = kv_start.to(q.device, torch.int64)
+        s = s.masked_fill(cols[None, None, None, :] < ks[:, None, None, None], float("-inf"))
+    p = torch.nan_to_num(torch.softmax(s, dim=-1), nan=0.0)
     o = torch.matmul(p.reshape(B, Hkv, G * L, N), v.float().contiguous())
     return o.reshape(B, Hq, L, D).to(q.dtype)
 
 
-def dequantize_attention(q, k_quant, v_quant, *, bits, group_size, scale, mask):
+def dequantize_attention(q, k_quant, v_quant, *, bits, group_size, scale, mask, kv_start=None):
     """The reference's dequantize + SDPA path (dispatch.py:68-83)."""
     k = kernels.dequantize(*k_quant, group_size=group_size, bits=bits)
     v = kernels.dequantize(*v_quant, group_size=group_size, bits=bits)
-    return attention_fp32(q, k, v, scale, mask)
+    return attention_fp32(q, k, v, scale, mask, kv_start)
 
 
 def fallback_sdpa(q, k_quant, v_quant, *, bits, group_size, scale, mask=None, kv_start=None):
     """Dequantize (HIP) + float32 attention: the path of dispatch.py:68-83.
 
-    Missing biases are zeros (dispatch.py:71, 76); ``kv_start`` is folded
-    into the mask as "keys before kv_start[b] are masked".
+    Missing biases are zeros (dispatch.py:71, 76); keys before kv_start[b]
+    are masked.
     """
-    B, _, qL, _ = q.shape
-    N = k_quant[0].shape[2]
-    if kv_start is not None:
-        keep = torch.arange(N, device=q.device)[None, :] >= kv_start.to(q.device)[:, None]
-        keep = keep[:, None, None, :]
-        if mask is None:
-            mask = keep
-        elif isinstance(mask, str):
-            qi = torch.arange(qL, device=q.device)[:, None] + (N - qL)
-            mask = keep & (qi >= torch.arange(N, device=q.device)[None, :])
-        elif mask.dtype == torch.bool:
-            mask = mask.to(q.device) & keep
-        else:
-            mask = mask.to(q.device).masked_fill(~keep, float("-inf"))
     kb = k_quant[2] if k_quant[2] is not None else torch.zeros_like(k_quant[1])
     vb = v_quant[2] if v_quant[2] is not None else torch.zeros_like(v_quant[1])
     return dequantize_attention(q, (k_quant[0], k_quant[1], kb), (v_quant[0], v_quant[1], vb),
-                                bits=bits, group_size=group_size, scale=scale, mask=mask)
+                                bits=bits, group_size=group_size, scale=scale, mask=mask,
+                                kv_start=kv_start)
 
 
 def quantized_sdpa(
@@ -153,7 +143,7 @@ def quantized_sdpa(
     # call's argument block (the checks below held for it; its shapes and
     # strides are the block's key).
     if mask is None and kv_start is None and threshold is None and num_splits is None and q.dim() == 4 \
-            and q.shape[2] == 1 and bits in (4, 8):
+            and q.shape[2] == 1 and q.shape[3] in kernels.HEAD_DIMS and bits in (4, 8):
         both = k_biases is not None and v_biases is not None
         out = kernels.decode_repeat(q, packed_k, packed_v, k_scales, v_scales, k_biases if both else None,
                                     v_biases if both else None,
@@ -175,8 +165,8 @@ def quantized_sdpa(
     if isinstance(kv_start, torch.Tensor) and q.device.type == "cuda":
         kv_start = kernels.to_device(kv_start, q.device)
 
-    if qL > 1 and not _fused_takes(q, packed_k, packed_v, k_scales, v_scales, k_biases,
-                                   v_biases, scale, bits, group_size):
+    if D not in kernels.HEAD_DIMS or (qL > 1 and not _fused_takes(
+            q, packed_k, packed_v, k_scales, v_scales, k_biases, v_biases, scale, bits, group_size)):
         return fallback_sdpa(q, (packed_k, k_scales, k_biases),    # dispatch.py:68-83
                              (packed_v, v_scales, v_biases), bits=bits, group_size=group_size,
                              scale=scale, mask=mask, kv_start=kv_start)

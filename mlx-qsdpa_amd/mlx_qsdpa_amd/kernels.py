@@ -16,6 +16,9 @@ import torch
 from . import _lib
 
 _DTYPE_CODE = {torch.float16: _lib.QSDPA_F16, torch.bfloat16: _lib.QSDPA_BF16}
+# Head dims the decode kernels are compiled for (qsdpa_decode returns
+# QSDPA_ERR_UNSUPPORTED for any other D).
+HEAD_DIMS = (64, 128, 256)
 _MASK_CODE = {torch.float16: _lib.QSDPA_F16, torch.bfloat16: _lib.QSDPA_BF16,
               torch.float32: _lib.QSDPA_F32, torch.bool: _lib.QSDPA_BOOL}
 
@@ -417,7 +420,7 @@ class DecodePlan:
 
 # Argument blocks of recent decode calls, per thread: a call whose tensors
 # have the geometry of an earlier one -- shapes except the key count, strides,
-# dtypes, the same scalars and stream -- re-uses that call's validated
+# dtypes, pointer alignments, the same scalars and stream -- re-uses that call's validated
 # argument block and workspace, rewriting only the data pointers and the key
 # count (a decode loop over a growing cache hits every step).  The workspace
 # is re-used in the order of the stream it was cached for, so it never races.
@@ -427,7 +430,8 @@ _ARGS_MAX = 32
 
 def _cache_key(q, pk, pv, ks, vs, kb, vb, kv_start, scale, bits, group_size, num_splits, causal, stream):
     """The argument block's key: everything the block encodes except the key
-    count N and the data pointers, plus the device and stream, or None when
+    count N and the data pointers (but with each pointer's offset from a
+    16-byte boundary), plus the device and stream, or None when
     the tensors disagree with one another (the full path then raises).  pv
     must have pk's shape, the scales and biases one shape with pk's (B, H,
     N)."""
@@ -435,10 +439,14 @@ def _cache_key(q, pk, pv, ks, vs, kb, vb, kv_start, scale, bits, group_size, num
     if pv.shape != sk or vs.shape != ss or ss[:3] != sk[:3] or (kb is not None and kb.shape != ss) \
             or (vb is not None and vb.shape != ss):
         return None
+    # The plan (kernel, split count, workspace size) also depends on each
+    # pointer's alignment: a view 2 bytes off its allocation's start can
+    # take another kernel.
+    align = tuple(None if t is None else t.data_ptr() % 16 for t in (q, pk, pv, ks, vs, kb, vb))
     return (q.shape, q.stride(), q.dtype, sk[0], sk[1], sk[3], pk.dtype, pv.dtype, pk.stride(), pv.stride(), ss[3],
             ks.dtype, vs.dtype, ks.stride(), vs.stride(), None if kb is None else (kb.dtype, kb.stride()),
             None if vb is None else (vb.dtype, vb.stride()), None if kv_start is None else kv_start.shape,
-            float(scale), bits, group_size, int(num_splits), bool(causal), q.get_device(), stream)
+            float(scale), bits, group_size, int(num_splits), bool(causal), q.get_device(), stream, align)
 
 
 def _cached_decode(q, pk, pv, ks, vs, kb, vb, scale, bits, group_size, kv_start, num_splits,

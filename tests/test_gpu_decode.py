@@ -8,6 +8,7 @@ import numpy as np
 import pytest
 import torch
 
+import torch_oracle
 from conftest import from_np, to_np, torch_dtype
 from oracle import affine, attention
 
@@ -364,21 +365,11 @@ def test_multi_query_through_quantized_sdpa(device):
         assert_close(to_np(out), oracle_out(inp8, mask=mask), f"prefill {mask}")
 
 
-def _torch_dequant(p, s, b, bits, gs, T):
-    """Independent float32 dequantize with torch integer ops (shift / mask)."""
-    per = 32 // bits
-    shifts = torch.arange(per, device=p.device, dtype=torch.int64) * bits
-    codes = ((p.view(torch.int32).to(torch.int64) & 0xFFFFFFFF)[..., None] >> shifts) & ((1 << bits) - 1)
-    codes = codes.reshape(*p.shape[:-1], -1).float()
-    sf = s.float().repeat_interleave(gs, dim=-1)
-    bf = b.float().repeat_interleave(gs, dim=-1)
-    return torch.addcmul(bf, codes, sf).to(T)
-
-
 @pytest.mark.parametrize("N", [65536, 131072])
 def test_headline_full_size_properties(device, N):
-    """C3 at full N: vs an independent torch float32 reference, split-K vs single
-    pass, and invariance to a token permutation."""
+    """C3 at full N: vs the float64 oracle restated in torch (pinned to the
+    numpy oracle in test_gpu_parity_full.py), split-K vs single pass, and
+    invariance to a token permutation."""
     torch.manual_seed(0)
     B, Hq, Hkv, D, bits, gs = 1, 32, 2, 256, 4, 32
     T = torch.float16
@@ -388,11 +379,8 @@ def test_headline_full_size_properties(device, N):
     kq = kernels.quantize(kw, gs, bits)
     vq = kernels.quantize(vw, gs, bits)
     out = mq.quantized_sdpa(q, kq[0], vq[0], kq[1], vq[1], kq[2], vq[2], bits=bits, group_size=gs)
-    k = _torch_dequant(*kq, bits, gs, T)
-    v = _torch_dequant(*vq, bits, gs, T)
-    from mlx_qsdpa_amd.dispatch import attention_fp32
-    ref = attention_fp32(q, k, v, D ** -0.5).float()
-    err = (out.float() - ref).abs()
+    ref = torch_oracle.quantized_sdpa(q, kq, vq, bits=bits, group_size=gs)
+    err = (out.double() - ref).abs()
     assert bool((err <= ATOL + RTOL * ref.abs()).all()), f"max err {err.max().item():.3e}"
     single = mq.quantized_sdpa(q, kq[0], vq[0], kq[1], vq[1], kq[2], vq[2], bits=bits,
                                group_size=gs, num_splits=1)
@@ -412,8 +400,8 @@ def test_headline_full_size_properties(device, N):
 
 def test_c4_full_size_batched(device):
     """C4 at its full shape (B=16, H_q=32, H_kv=8, D=128, 4-bit gs64, lengths
-    U[1K, 32K] left-padded): the stream-K decode vs an independent torch
-    float32 reference with the padding masked, across split counts, and vs
+    U[1K, 32K] left-padded): the stream-K decode vs the float64 oracle
+    restated in torch with the padding masked, across split counts, and vs
     the same left padding given as a bool mask (uniform splits)."""
     torch.manual_seed(0)
     gen = torch.Generator(device="cpu")
@@ -427,18 +415,16 @@ def test_c4_full_size_batched(device):
     q = torch.randn((B, Hq, 1, D), device=device).to(T)
     ks = (N - lengths).to(device=device, dtype=torch.int32)
     keep = torch.arange(N, device=device)[None, :] >= ks[:, None].long()
-    from mlx_qsdpa_amd.dispatch import attention_fp32
-    ref = attention_fp32(q, _torch_dequant(*kq, bits, gs, T), _torch_dequant(*vq, bits, gs, T), D ** -0.5,
-                         keep[:, None, None, :]).float()
+    ref = torch_oracle.quantized_sdpa(q, kq, vq, bits=bits, group_size=gs, mask=keep[:, None, None, :])
     outs = {}
     for splits in (None, 2, 4):
         out = mq.quantized_sdpa(q, kq[0], vq[0], kq[1], vq[1], kq[2], vq[2], bits=bits, group_size=gs,
-                                kv_start=ks, num_splits=splits).float()
+                                kv_start=ks, num_splits=splits).double()
         err = (out - ref).abs()
         assert bool((err <= ATOL + RTOL * ref.abs()).all()), f"splits={splits}: max err {err.max().item():.3e}"
         outs[splits] = out
     masked = mq.quantized_sdpa(q, kq[0], vq[0], kq[1], vq[1], kq[2], vq[2], bits=bits, group_size=gs,
-                               mask=keep[:, None, None, :]).float()
+                               mask=keep[:, None, None, :]).double()
     assert (masked - outs[None]).abs().max().item() < 2e-3
 
 
@@ -538,3 +524,37 @@ def test_decode_argument_cache(device):
                 if min(n + 1, cap) <= 37:
                     continue  # sequence 1 has no keys: its row is all-masked
             assert_close(to_np(nxt), oracle_out(ref_in, mask=mask), f"n={n + 1} cached")
+
+
+def test_argument_cache_keys_on_alignment(device):
+    """A cached argument block is re-used only for views with the same
+    pointer alignment: the same geometry with q, or the K scales, one
+    element (2 bytes) off a 4-byte boundary takes another plan (the
+    matrix-core kernel reads them as 32-bit words), and each call still
+    matches the oracle, before and after the aligned block is cached."""
+    rng = np.random.default_rng(62)
+    B, Hq, Hkv, N, D, bits, gs = 1, 16, 2, 4000, 256, 4, 32
+    inp = make_inputs(rng, B, Hq, Hkv, N, D, bits, gs)
+    g = to_dev(inp, device)
+    want = oracle_out(inp)
+
+    def shifted(t):
+        """t's values in a view with t's strides, 2 bytes past a 4-byte boundary."""
+        wide = torch.empty(t.numel() + 1, dtype=t.dtype, device=device)
+        wide[1:] = t.reshape(-1)
+        v = wide[1:].view(t.shape)
+        assert v.stride() == t.stride() and v.data_ptr() % 4 == 2
+        return v
+
+    kernels._ARGS.d = {}
+    for name in ("q", "ks"):
+        for order in ("aligned first", "shifted first"):
+            print(f"alignment key: {name} {order}", flush=True)
+            kernels._ARGS.d = {}
+            alt = dict(g, **{name: shifted(g[name])})
+            seq = (g, alt, g, alt) if order == "aligned first" else (alt, g, alt, g)
+            for t in seq:
+                out = mq.quantized_sdpa(t["q"], t["kp"], t["vp"], t["ks"], t["vs"], t["kb"], t["vb"],
+                                        bits=bits, group_size=gs)
+                torch.cuda.synchronize()
+                assert_close(to_np(out), want, f"{name} {order}")

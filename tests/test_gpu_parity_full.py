@@ -5,6 +5,8 @@ patterns that smaller cases do not exercise.
   C2 (H_q = H_kv = 2, D=256, 8-bit gs64, bf16, 1% outlier channels x8) at
   N = 64K and 128K: the fused kernel (through the C ABI) against the float64
   oracle (tests/torch_oracle.py, pinned here to oracle/attention.py).
+* C4 at full shape through BatchQuantizedSDPACache.update_and_fetch and
+  cache_sdpa (left padding as kv_start and as an additive mask).
 * C5 end to end through BatchQuantizedRotatingSDPACache (B=4, H_q=16,
   H_kv=4, D=128, 8-bit gs128, bf16, window 4096, keep=4): advanced past the
   wrap, a qL=512 causal chunk, then 64 decode steps; every step's cache
@@ -18,6 +20,8 @@ patterns that smaller cases do not exercise.
   HIP quantize / dequantize kernels.
 * qL > 1 calls the fused kernel does not take (D = 64, a K view whose rows
   are not 16-byte aligned) through the dequantize + attention path.
+* Head dims the library does not compile (D = 32, 512) at qL = 1 and > 1
+  through the same path.
 
 Tolerance (north star): |out - ref| <= 2e-3 + 1e-2 |ref|.
 """
@@ -177,6 +181,77 @@ def test_c5_rotating_pipeline(device):
 
 
 # ---------------------------------------------------------------------------
+# C4 at full shape through the batch cache
+# ---------------------------------------------------------------------------
+def test_c4_batch_cache_full_shape(device):
+    """C4 (B=16, H_q=32, H_kv=8, D=128, 4-bit gs64, f16, lengths U[1K, 32K]
+    left-padded) through the API: BatchQuantizedSDPACache.update_and_fetch
+    (a left-padded prompt, then one appended token per sequence and step)
+    and cache_sdpa, with the padding as kv_start and as an additive -inf
+    mask (reference anchor: tests/test_cache_sdpa.py:177-344 of mlx-qsdpa).
+
+    Cache state: a seeded sample of 4096 prompt rows and every appended
+    column are bit-exact against the numpy quantizer; the prompt part is
+    unchanged by each append (also across the growth by 256 slots); offsets,
+    left padding and the key count follow the oracle cache (run on
+    one-head D=32 stand-ins of the same token counts, which is all they
+    depend on).  Attention: within tolerance of the float64 oracle over the
+    cache's contents with the padding masked."""
+    B, Hq, Hkv, D, bits, gs, dt, T = 16, 32, 8, 128, 4, 64, "f16", torch.float16
+    gen = torch.Generator(device="cpu")
+    gen.manual_seed(4)
+    lengths = torch.randint(1024, 32769, (B,), generator=gen).numpy()
+    lmax = int(lengths.max())
+    lp = (lmax - lengths).tolist()
+    cache = mq.BatchQuantizedSDPACache(lp, bits=bits, group_size=gs)
+    meta = oc.BatchQuantizedSDPACache(lp, bits=bits, group_size=32, dtype=dt)
+    g = torch.Generator(device=device)
+    g.manual_seed(4)
+    k = torch.randn((B, Hkv, lmax, D), generator=g, device=device).to(T)
+    v = torch.randn((B, Hkv, lmax, D), generator=g, device=device).to(T)
+    kq, vq = cache.update_and_fetch(k, v)
+    meta.update_and_fetch(np.zeros((B, 1, lmax, 32), np.float32), np.zeros((B, 1, lmax, 32), np.float32))
+    rng = np.random.default_rng(4)
+    bs, hs, ts = rng.integers(0, B, 4096), rng.integers(0, Hkv, 4096), rng.integers(0, lmax, 4096)
+    for src, got in ((k, kq), (v, vq)):
+        want = affine.quantize(to_np(src[bs, hs, ts]), gs, bits, dt)
+        assert np.array_equal(got[0].view(torch.int32)[bs, hs, ts].cpu().numpy().view(np.uint32), want[0]), \
+            "prompt rows: packed words differ"
+        for i in (1, 2):
+            assert np.array_equal(affine.T_bits(to_np(got[i][bs, hs, ts]), dt), affine.T_bits(want[i], dt)), \
+                "prompt rows: scales / biases differ"
+    del k, v
+    for step in range(4):
+        prev = tuple(t.clone() for t in kq + vq)
+        kn = affine.random_T(rng, (B, Hkv, 1, D), dt)
+        vn = affine.random_T(rng, (B, Hkv, 1, D), dt)
+        kq, vq = cache.update_and_fetch(from_np(kn, T, device), from_np(vn, T, device))
+        meta.update_and_fetch(np.zeros((B, 1, 1, 32), np.float32), np.zeros((B, 1, 1, 32), np.float32))
+        N = lmax + step + 1
+        assert cache.size() == meta.size() == N and kq[0].shape[2] == N
+        assert np.array_equal(cache.offset.numpy(), meta.offset)
+        assert np.array_equal(cache.left_padding.numpy(), meta.left_padding)
+        for old, new in zip(prev, kq + vq):
+            assert torch.equal(new[:, :, :N - 1].view(torch.int32) if new.dtype == torch.uint32 else new[:, :, :N - 1],
+                               old.view(torch.int32) if old.dtype == torch.uint32 else old), \
+                f"step {step}: an append changed earlier columns"
+        for src, got in ((kn, kq), (vn, vq)):
+            want = affine.quantize(src, gs, bits, dt)
+            assert np.array_equal(to_np(got[0][:, :, N - 1:]), want[0]), f"step {step}: appended words differ"
+            for i in (1, 2):
+                assert np.array_equal(affine.T_bits(to_np(got[i][:, :, N - 1:]), dt), affine.T_bits(want[i], dt)), \
+                    f"step {step}: appended scales / biases differ"
+        q = from_np(affine.random_T(rng, (B, Hq, 1, D), dt), T, device)
+        keep = torch.arange(N, device=device)[None, :] >= torch.tensor(lp, device=device)[:, None]
+        want = torch_oracle.quantized_sdpa(q, kq, vq, bits=bits, group_size=gs, mask=keep[:, None, None, :])
+        out = mq.cache_sdpa(q, kq, vq, cache, kv_start=cache.kv_start(device))
+        assert_close(out, want, f"C4 step {step} kv_start")
+        add = torch.zeros((B, 1, 1, N), dtype=T, device=device).masked_fill(~keep[:, None, None, :], float("-inf"))
+        out = mq.cache_sdpa(q, kq, vq, cache, mask=add)
+        assert_close(out, want, f"C4 step {step} additive mask")
+
+
+# ---------------------------------------------------------------------------
 # one DecodePlan, inputs overwritten in place between calls
 # ---------------------------------------------------------------------------
 @pytest.mark.parametrize("case", [(1, 32, 2, 8192, 256, 4, 32, "f16"), (3, 16, 4, 3000, 128, 8, 64, "bf16")],
@@ -290,6 +365,66 @@ def test_multi_query_fallback_path(device, monkeypatch, layout):
         want = attention.quantized_sdpa_reference(q, kq[0], vq[0], kq[1], vq[1], kq[2], vq[2], bits=bits,
                                                   group_size=gs, dtype=dt, mask=full)
         assert_close(got, torch.from_numpy(want).to(device), f"{layout} mask={mask}")
+
+
+@pytest.mark.parametrize("D,bits,gs,dt", [(32, 4, 32, "f16"), (512, 8, 64, "bf16"), (512, 4, 128, "f16")],
+                         ids=["D32-4b", "D512-8b", "D512-4b-gs128"])
+def test_uncompiled_head_dims(device, monkeypatch, D, bits, gs, dt):
+    """Head dims the library does not compile (the reference's validation
+    accepts any D % 32 == 0: dispatch.py:48-49, kernels templated on D:
+    kernels.py:44-50) return the attention through dequantize + attention,
+    for one query position and for several, unmasked, bool-masked, additive
+    and causal, with and without kv_start.  The fused kernel is made to
+    fail, so passing proves the fallback ran."""
+    B, Hq, Hkv, N = 2, 8, 2, 150
+    T = torch_dtype(dt)
+    rng = np.random.default_rng(D + bits)
+    kq = affine.quantize(affine.random_T(rng, (B, Hkv, N, D), dt), gs, bits, dt)
+    vq = affine.quantize(affine.random_T(rng, (B, Hkv, N, D), dt), gs, bits, dt)
+    dk = tuple(from_np(x, T, device) for x in kq)
+    dv = tuple(from_np(x, T, device) for x in vq)
+
+    def no_fused(*a, **k):
+        raise AssertionError("the fused kernel ran")
+
+    monkeypatch.setattr(kernels, "decode", no_fused)
+    monkeypatch.setattr(kernels, "decode_repeat", no_fused)
+    for L in (1, 3):
+        q = affine.random_T(rng, (B, Hq, L, D), dt)
+        for mask in (None, "bool", "additive", "causal"):
+            for starts in (None, np.array([0, 41])):
+                m_t = m_np = None
+                if mask == "causal":
+                    m_t = m_np = "causal"
+                elif mask == "bool":
+                    m_np = rng.random((B, 1, L, N)) > 0.4
+                    m_np[..., -1] = True
+                    m_t = torch.from_numpy(m_np).to(device)
+                elif mask == "additive":
+                    m_np = affine.random_T(rng, (B, 1, L, N), dt)
+                    m_np[rng.random((B, 1, L, N)) < 0.3] = -np.inf
+                    m_np[..., -1] = 0.0
+                    m_t = from_np(m_np, T, device)
+                ks = None if starts is None else torch.tensor(starts, dtype=torch.int32, device=device)
+                got = mq.quantized_sdpa(from_np(q, T, device), dk[0], dv[0], dk[1], dv[1], dk[2], dv[2],
+                                        bits=bits, group_size=gs, mask=m_t, kv_start=ks)
+                full = m_np
+                if starts is not None:
+                    keep = np.arange(N)[None, None, None, :] >= starts[:, None, None, None]
+                    if mask is None:
+                        full = np.broadcast_to(keep, (B, 1, L, N))
+                    elif mask == "causal":
+                        qi = np.arange(L)[:, None] + (N - L)
+                        full = keep & (qi >= np.arange(N)[None, :])[None, None]
+                    elif mask == "bool":
+                        full = keep & m_np
+                    else:
+                        full = np.where(keep, m_np, -np.inf).astype(np.float32)
+                want = attention.quantized_sdpa_reference(q, kq[0], vq[0], kq[1], vq[1], kq[2], vq[2],
+                                                          bits=bits, group_size=gs, dtype=dt, mask=full)
+                assert got.shape == (B, Hq, L, D) and got.dtype == T
+                assert_close(got, torch.from_numpy(want).to(device),
+                             f"D={D} L={L} mask={mask} kv_start={starts is not None}")
 
 
 def test_misaligned_packed_rows_are_copied(device):

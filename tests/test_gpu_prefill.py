@@ -146,12 +146,14 @@ def test_prefill_kv_start_and_masks(device):
     ((2, 32, 8, 900, 256), 1.0, 8.0, "parity"),          # max |V| ~ 40: P in two float16 terms
     ((2, 32, 8, 900, 256), 2.0e4, 40.0, "scaled"),       # max |V| ~ 3e6: V staged at 2^-6
     ((1, 16, 4, 3000, 128), 2.0e4, 40.0, "scaled"),      # the same through key splits
-], ids=["outliers", "beyond_f16", "beyond_f16_splits"])
+    ((2, 32, 8, 900, 256), 2.0e36, 4.0, "scaled"),       # max |V| ~ 4e37: V staged at 2^-119
+], ids=["outliers", "beyond_f16", "beyond_f16_splits", "near_bf16_max"])
 def test_prefill_bf16_large_values(device, case):
     """bfloat16 V with large values.  Past max |V| = 8 the kernel feeds P to
     the P.V MFMAs as two float16 terms (22 significant bits), and past
     64000 it stages V in float16 scaled by 2^-k and scales the output (or the
-    float32 partials) back by 2^k.  With outlier channels the parity bar
+    float32 partials) back by 2^k (k up to 113 for any finite bfloat16 V,
+    exercised near the bfloat16 maximum).  With outlier channels the parity bar
     holds; at |V| ~ 1e6 no float P meets an absolute 2e-3 where outputs
     cancel, so the bar there is 2^-20 max|V| (22-bit P moves an output by up to
     2^-22 max|V|) plus the relative 1e-2: a wrong scale would miss it by
