@@ -78,6 +78,10 @@ def parse_args(argv=None):
     ap.add_argument("--rotating-prefill", action="store_true",
                     help="time C5's prefill chunk (--qlen, default 512) through the batched rotating "
                          "cache: requant + attention")
+    ap.add_argument("--crossover-sweep", action="store_true",
+                    help="time one decode (qL = 1) through the fused kernel (library split count and "
+                         "single pass) and through dequantize + attention (cache_sdpa's branch below "
+                         "its crossover) over N, for the c1 / c3 / c5 shapes: one JSON line per point")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="time budget of the CPU baseline sample (0 = skip)")
     ap.add_argument("--seed", type=int, default=0)
@@ -555,12 +559,62 @@ def run_rotating_prefill(args) -> int:
     return 0
 
 
+def run_crossover_sweep(args) -> int:
+    """qL = 1 over N at the c1, c3 and c5 shapes: wall µs per call of
+    quantized_sdpa (the fused kernel with the library's split count, and
+    with num_splits=1: the reference's single pass, its choice for N <=
+    threshold = 4096) and of fallback_sdpa (HIP dequantize + float32
+    attention: cache_sdpa's branch for N < crossover).  Up to 32 KV sets are
+    cycled (fewer bytes than the MALL holds at small N, as a decode loop over
+    layers would see them); every point also reports the largest difference
+    between the fused and the fallback outputs."""
+    import torch
+
+    import mlx_qsdpa_amd as mq
+    from mlx_qsdpa_amd import metric
+
+    device = torch.device("cuda:0")
+    for name in ("c1", "c3", "c5"):
+        cfg = CONFIGS[name]
+        B, Hq, Hkv, D, bits, gs, dt, _, _ = cfg
+        for N in (256, 1024, 4096, 16384, 65536):
+            set_bytes = B * N * metric.kv_bytes_per_token(Hkv, D, bits, gs)
+            n_sets = max(2, min(32, math.ceil(args.kv_bytes / set_bytes)))
+            sets = make_sets(cfg, N, n_sets, device, args.seed)
+
+            def call(i, how):
+                q, kq, vq = sets[i % n_sets]
+                if how == "fallback":
+                    return mq.fallback_sdpa(q, kq, vq, bits=bits, group_size=gs, scale=D ** -0.5)
+                return mq.quantized_sdpa(q, kq[0], vq[0], kq[1], vq[1], kq[2], vq[2], bits=bits, group_size=gs,
+                                         num_splits=1 if how == "single_pass" else None)
+
+            us = {}
+            for how in ("fused", "single_pass", "fallback"):
+                for i in range(args.warmup):
+                    call(i, how)
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                for i in range(args.steps):
+                    call(i, how)
+                torch.cuda.synchronize()
+                us[how] = round((time.perf_counter() - t0) / args.steps * 1e6, 2)
+            diff = float((call(0, "fused").float() - call(0, "fallback").float()).abs().max())
+            print(json.dumps({"sweep": "crossover", "config": name, "N": N, "kv_sets": n_sets,
+                              "us_per_call": us, "max_abs_diff_fused_vs_fallback": diff}), flush=True)
+            del sets
+            torch.cuda.empty_cache()
+    return 0
+
+
 def main(argv=None) -> int:
     args = parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the decode path is "
               "single-GPU in this build, see DESIGN.md for how it would shard.", file=sys.stderr)
         return 2
+    if args.crossover_sweep:
+        return run_crossover_sweep(args)
     if args.rotating_prefill:
         return run_rotating_prefill(args)
     if args.config == "c4":
