@@ -165,17 +165,25 @@ int streamk_units(const qsdpa_decode_args* a, int splits) {
   return static_cast<int>(units);
 }
 
-// A split-K decode on the matrix-core kernel with uniform splits merges its
-// partials inside the launch (decode_mfma.hip::split_merge) when it has at
-// most kFusedSplits splits, its blocks of 16 query rows have counters (at
-// most kTicketBlocks) and a block's partial rows span less than 2^31 bytes;
-// otherwise the merge kernel combines them.
+// A split-K decode on the matrix-core kernel merges its partials inside the
+// launch (decode_mfma.hip::split_merge) when its (sequence, kv head, row
+// block) units have counters (at most kTicketBlocks of them) and a kv head's
+// (stream-K) or a block's (uniform) partial rows span less than 2^31 bytes;
+// with uniform splits only up to kFusedSplits of them (above that the merge
+// kernel is faster: the last workgroup would read every split alone).  The
+// stream-K schedule merges per sequence, over the few segments that cover
+// it.  Otherwise the merge kernel combines the partials.
 bool fused_merge(const qsdpa_decode_args* a, int splits, bool prefill, bool mfma, int units) {
-  if (prefill || !mfma || units > 0 || splits < 2 || splits > kFusedSplits) return false;
+  if (prefill || !mfma || splits < 2) return false;
+  if (units == 0 && splits > kFusedSplits) return false;
+  // D = 256 with 8-bit codes under the stream-K schedule has no such kernel
+  // (its registers spilled to scratch).
+  if (units > 0 && a->D == 256 && a->bits == 8) return false;
   const int64_t qL = std::max(a->q_len, 1);
   const int64_t G = a->H_q / a->H_kv;
   const int64_t blocks = static_cast<int64_t>(a->B) * a->H_kv * ((G * qL + 15) / 16);
-  return blocks <= kTicketBlocks && G * qL * splits * a->D * 4 < (int64_t(1) << 31);
+  const int64_t cols = units > 0 ? static_cast<int64_t>(units) + a->B : splits;
+  return blocks <= kTicketBlocks && G * qL * cols * a->D * 4 < (int64_t(1) << 31);
 }
 
 // Split count: enough workgroups to cover every CU twice, but never fewer

@@ -68,7 +68,8 @@ namespace {
 template <typename Tag, int D, int BITS, int GS, bool MASK, bool SK, bool FUSED>
 __device__ __forceinline__ void decode_segment(const MfmaParams& p, float* s_acc, float (*s_ml)[16][2],
                                                uint8_t* s_q, int lane, int wave, int quad, int r, int hblk,
-                                               int kvh, int b, int t_lo, int stride, int jmax, int col) {
+                                               int kvh, int b, int t_lo, int stride, int jmax, int col,
+                                               bool direct = false) {
   using G = Geo<D, BITS, GS>;
   using K = Kernel<Tag, D, BITS, GS>;
   constexpr int kRowF = D + 4;       // LDS floats per (wave, head) row
@@ -246,41 +247,50 @@ __device__ __forceinline__ void decode_segment(const MfmaParams& p, float* s_acc
 
   merge_store<Tag, D, kWaves, FUSED>(
       p, [&](int w, int h) { return s_acc + (w * 16 + h) * kRowF; },
-      [&](int w, int h) { return f32x2{s_ml[w][h][0], s_ml[w][h][1]}; }, nh, v0, kvh, b, col, kThreads);
+      [&](int w, int h) { return f32x2{s_ml[w][h][0], s_ml[w][h][1]}; }, nh, v0, kvh, b, col, kThreads, direct);
 }
 
-// The split merge inside the launch (the FUSED instantiation: uniform
-// splits, at most kFusedSplits of them), after decode_segment stored this
-// split's partial rows.  Every workgroup waits until its partial stores are
-// complete, then takes a ticket of its block (batch, kv head, row block): an
-// agent-scope atomic increment that wraps to zero at the split count, so the
-// counter is zero again after every call.  The workgroup that draws the last
-// ticket merges the block's partials in split order and writes the output;
-// the others exit.  No workgroup waits for another, and the order of every
-// sum is fixed, so repeated calls give identical bits whichever workgroup
-// merges.  The partials cross XCDs through agent-coherent loads and stores
+// The split merge inside the launch (the FUSED instantiations), after
+// decode_segment stored this workgroup's partial rows of sequence b at
+// column `col` of the block's rows.  The sequence's partials are the
+// `count` consecutive columns from `first` (uniform splits: the block's
+// num_splits columns; the stream-K schedule: the columns of the segments
+// that cover sequence b).  Every workgroup waits until its partial stores
+// are complete, then takes a ticket of its (sequence, kv head, row block):
+// an agent-scope atomic increment that wraps to zero at `count`, so the
+// counter is zero again after every call.  The workgroup that draws the
+// last ticket merges the partials in column order, CHUNK at a time with the
+// running rescale of the merge kernel, and writes the output; the others
+// go on.  No workgroup waits for another, and the order of every sum is
+// fixed, so repeated calls give identical bits whichever workgroup merges.
+// The partials cross XCDs through agent-coherent loads and stores
 // (kCoherent).  Thread t merges dims [8 (t % (D / 8)), +8) of row t / (D / 8).
 //
 // One level only: with more splits, a second level (the last of a group of
 // 16 merging into a group sum, the last group merging the sums) puts two
 // rounds of store, ticket and load on the path of the last workgroup, about
-// 2.9 us each on MI355X; measured at C3 (128 splits) that made the step
-// 30.2 us against 25.2 us with the merge kernel, so larger split counts keep
-// the merge kernel.
-template <typename Tag, int D>
-__device__ __forceinline__ void split_merge(const MfmaParams& p, int* s_flag, int b, int kvh, int hblk) {
+// 2.9 us each on MI355X; measured at C3 (128 uniform splits) that made the
+// step 30.2 us against 25.2 us with the merge kernel, so uniform splits
+// above kFusedSplits keep the merge kernel.
+//
+// CHUNK: partials in flight at once, 16 for uniform splits (count <= 16: one
+// round trip), 8 under the stream-K schedule, whose sequences span few
+// segments and whose kernels have less register room (16 spilled to
+// scratch there).
+template <typename Tag, int D, int CHUNK>
+__device__ __forceinline__ void split_merge(const MfmaParams& p, int* s_flag, int b, int kvh, int hblk, int first,
+                                            int count) {
   constexpr bool kHalf = Tag::kId == QSDPA_F16;  // float16 normalised partial rows
   constexpr int kPer = 8, kRowT = D / kPer;
   constexpr uint32_t kPast = 0x80000000u;  // an offset past every descriptor: reads zero
   typedef uint32_t u2 __attribute__((ext_vector_type(2)));
-  const int S = p.num_splits;
-  unsigned* tk = p.tickets + static_cast<int64_t>(blockIdx.z * gridDim.y + blockIdx.y) * kTicketWords;
+  unsigned* tk = p.tickets + static_cast<int64_t>(b * gridDim.y + blockIdx.y) * kTicketWords;
   // Every partial store of this workgroup is complete before its ticket.
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0)
-    *s_flag = __builtin_amdgcn_atomic_inc32(tk, static_cast<unsigned>(S - 1), __ATOMIC_RELAXED, "agent") ==
-              static_cast<unsigned>(S - 1);
+    *s_flag = __builtin_amdgcn_atomic_inc32(tk, static_cast<unsigned>(count - 1), __ATOMIC_RELAXED, "agent") ==
+              static_cast<unsigned>(count - 1);
   __syncthreads();
   if (!*s_flag) return;
 
@@ -290,61 +300,86 @@ __device__ __forceinline__ void split_merge(const MfmaParams& p, int* s_flag, in
   const int v = v0 + h;
   const int hh = kvh * p.G + v % p.G, iq = v / p.G;
   const PartRows<Tag, D> pr(p, b, kvh);
-  const uint32_t row0 = PartRows<Tag, D>::local(p, v);  // slot of split 0 of the row
-  // All S partials' loads are issued before the first wait (S <= 16;
-  // slots past S read zero through an offset past the descriptor).
-  u2 m2[kFusedSplits];
-  u4 w[kFusedSplits][kHalf ? 1 : 2];
-#pragma unroll
-  for (int k = 0; k < kFusedSplits; ++k) {
-    const bool ok = k < S;
-    const uint32_t slot = row0 + static_cast<uint32_t>(k);
-    m2[k] = __builtin_amdgcn_raw_buffer_load_b64(pr.ml, ok ? slot * 8 : kPast, 0, kCoherent);
-#pragma unroll
-    for (int q = 0; q < (kHalf ? 1 : 2); ++q)
-      w[k][q] = __builtin_amdgcn_raw_buffer_load_b128(
-          pr.acc, ok ? (slot * D + d + 4 * q) * PartRows<Tag, D>::kEsz : kPast, 0, kCoherent);
-  }
-  // Whole-vector bit casts: this compiler reads element 0 for a bit cast of
-  // any single element of a vector.
-  f32x2 ml[kFusedSplits];
-  float M = kNegBig;
-#pragma unroll
-  for (int k = 0; k < kFusedSplits; ++k) {
-    ml[k] = k < S ? __builtin_bit_cast(f32x2, m2[k]) : f32x2{kNegBig, 0.0f};
-    M = fmaxf(M, ml[k][0]);
-  }
-  // out = sum_s w_s x_s / sum_s l_s 2^(m_s - M), w_s = l_s 2^(m_s - M) for
-  // normalised rows, 2^(m_s - M) for float32 sums (the merge kernel's
-  // equations, merge.hip).
-  float L = 0.0f, acc[kPer];
+  const uint32_t row0 = PartRows<Tag, D>::local(p, v) + static_cast<uint32_t>(first);
+  float M = kNegBig, L = 0.0f, acc[kPer];
 #pragma unroll
   for (int e = 0; e < kPer; ++e) acc[e] = 0.0f;
+  for (int c0 = 0; c0 < count; c0 += CHUNK) {
+    // The chunk's loads are issued before its first wait (columns past
+    // `count` read zero through an offset past the descriptor).
+    u2 m2[CHUNK];
+    u4 w[CHUNK][kHalf ? 1 : 2];
 #pragma unroll
-  for (int k = 0; k < kFusedSplits; ++k) {
-    const float wk = fast_exp2(ml[k][0] - M);
-    L = fmaf(ml[k][1], wk, L);
-    const float we = kHalf ? ml[k][1] * wk : wk;
-    float xv[kPer];
-    if constexpr (kHalf) {
+    for (int k = 0; k < CHUNK; ++k) {
+      const bool ok = c0 + k < count;
+      const uint32_t slot = row0 + static_cast<uint32_t>(c0 + k);
+      m2[k] = __builtin_amdgcn_raw_buffer_load_b64(pr.ml, ok ? slot * 8 : kPast, 0, kCoherent);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t u = w[k][0][e];
-        xv[2 * e] = f16_bits_to_f32(static_cast<uint16_t>(u));
-        xv[2 * e + 1] = f16_bits_to_f32(static_cast<uint16_t>(u >> 16));
-      }
-    } else {
-#pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        const f4 f = __builtin_bit_cast(f4, w[k][q]);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) xv[4 * q + e] = f[e];
-      }
+      for (int q = 0; q < (kHalf ? 1 : 2); ++q)
+        w[k][q] = __builtin_amdgcn_raw_buffer_load_b128(
+            pr.acc, ok ? (slot * D + d + 4 * q) * PartRows<Tag, D>::kEsz : kPast, 0, kCoherent);
     }
+    // Whole-vector bit casts: this compiler reads element 0 for a bit cast
+    // of any single element of a vector.
+    f32x2 ml[CHUNK];
+    float Mc = M;
 #pragma unroll
-    for (int e = 0; e < kPer; ++e) acc[e] = fmaf(xv[e], we, acc[e]);
+    for (int k = 0; k < CHUNK; ++k) {
+      ml[k] = c0 + k < count ? __builtin_bit_cast(f32x2, m2[k]) : f32x2{kNegBig, 0.0f};
+      Mc = fmaxf(Mc, ml[k][0]);
+    }
+    // out = sum_s w_s x_s / sum_s l_s 2^(m_s - M), w_s = l_s 2^(m_s - M)
+    // for normalised rows, 2^(m_s - M) for float32 sums (the merge kernel's
+    // equations, merge.hip); earlier chunks rescaled to the new maximum.
+    const float f = fast_exp2(M - Mc);
+    L *= f;
+#pragma unroll
+    for (int e = 0; e < kPer; ++e) acc[e] *= f;
+    M = Mc;
+#pragma unroll
+    for (int k = 0; k < CHUNK; ++k) {
+      const float wk = fast_exp2(ml[k][0] - M);
+      L = fmaf(ml[k][1], wk, L);
+      const float we = kHalf ? ml[k][1] * wk : wk;
+      float xv[kPer];
+      if constexpr (kHalf) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t u = w[k][0][e];
+          xv[2 * e] = f16_bits_to_f32(static_cast<uint16_t>(u));
+          xv[2 * e + 1] = f16_bits_to_f32(static_cast<uint16_t>(u >> 16));
+        }
+      } else {
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const f4 fv = __builtin_bit_cast(f4, w[k][q]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) xv[4 * q + e] = fv[e];
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < kPer; ++e) acc[e] = fmaf(xv[e], we, acc[e]);
+    }
   }
   store_out8<Tag>(p, b, hh, iq, d, acc, L);
+}
+
+// Zero output rows of the block's 16 query rows for every sequence of the
+// stream-K schedule without keys (no segment covers them, so no merge
+// writes them).  One workgroup per block.
+template <typename Tag, int D>
+__device__ __forceinline__ void zero_empty_sequences(const MfmaParams& p, int kvh, int hblk) {
+  constexpr int kPer = 8, kRowT = D / kPer;
+  const int v0 = hblk * 16, nh = min(16, p.G * p.qL - v0);
+  const int t = threadIdx.x, h = t / kRowT, d = (t % kRowT) * kPer;
+  if (t >= 16 * kRowT || h >= nh) return;
+  const int v = v0 + h;
+  const int hh = kvh * p.G + v % p.G, iq = v / p.G;
+  float zero[kPer];
+#pragma unroll
+  for (int e = 0; e < kPer; ++e) zero[e] = 0.0f;
+  for (int b = 0; b < p.B; ++b)
+    if (seq_tiles(p.kv_start, b, p.N) == 0) store_out8<Tag>(p, b, hh, iq, d, zero, 0.0f);
 }
 
 // SK: the stream-K schedule of a left-padded batch (a loop over segments);
@@ -370,14 +405,20 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     // Uniform splits: grid (S, H_kv * row blocks, B); split x of sequence z.
     decode_segment<Tag, D, BITS, GS, MASK, false, FUSED>(p, s_acc, s_ml, s_q, lane, wave, quad, r, hblk, kvh, blockIdx.z, blockIdx.x,
                                      p.num_splits, 0x7FFFFFFF, blockIdx.x);
-    if constexpr (FUSED) split_merge<Tag, D>(p, &s_flag, blockIdx.z, kvh, hblk);
+    if constexpr (FUSED) split_merge<Tag, D, kFusedSplits>(p, &s_flag, blockIdx.z, kvh, hblk, 0, p.num_splits);
   } else {
     // Left-padded batch: grid (U, H_kv * row blocks, 1), unit x of the
     // stream-K schedule (common.h) owns global tiles [x * C, (x + 1) * C) of
     // the sequences laid end to end, one segment per sequence it touches.
     const int total = streamk_total(p.kv_start, p.B, p.N);
     const int C = max(1, (total + p.units - 1) / p.units);
-    if (blockIdx.x == 0 && blockIdx.y == 0 && wave == 0) streamk_write_sched(p.kv_start, p.B, p.N, C, p.sched);
+    if constexpr (FUSED) {
+      // Sequences without keys get zero rows here (the merge kernel's job
+      // otherwise).
+      if (blockIdx.x == 0) zero_empty_sequences<Tag, D>(p, kvh, hblk);
+    } else {
+      if (blockIdx.x == 0 && blockIdx.y == 0 && wave == 0) streamk_write_sched(p.kv_start, p.B, p.N, C, p.sched);
+    }
     int g = static_cast<int>(blockIdx.x) * C;
     const int g_end = min(g + C, total);
     if (g >= g_end) return;  // the whole workgroup: no work, nothing to store
@@ -387,8 +428,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       const int Tb = seq_tiles(p.kv_start, b, p.N);
       const int hi = min(g_end, P + Tb);
       if (hi > g) {
-        decode_segment<Tag, D, BITS, GS, MASK, true, false>(p, s_acc, s_ml, s_q, lane, wave, quad, r, hblk, kvh, b, g - P, 1, hi - g,
-                                         static_cast<int>(blockIdx.x) + b);
+        // Sequence b's tiles [P, P + Tb) lie in units P / C .. (P + Tb - 1) / C:
+        // its partials are those units' columns (unit + b).
+        const int uf = P / C, count = (P + Tb - 1) / C - uf + 1;
+        decode_segment<Tag, D, BITS, GS, MASK, true, FUSED>(p, s_acc, s_ml, s_q, lane, wave, quad, r, hblk, kvh, b, g - P, 1, hi - g,
+                                         static_cast<int>(blockIdx.x) + b, FUSED && count == 1);
+        if constexpr (FUSED) {
+          if (count > 1) split_merge<Tag, D, 8>(p, &s_flag, b, kvh, hblk, uf + b, count);
+        }
         __syncthreads();  // the next segment reuses the LDS
         g = hi;
       }
@@ -405,11 +452,26 @@ void launch_mask(const MfmaParams& p, int gs, hipStream_t stream, const qsdpa_de
   // No stream-K instantiation for D = 256, 8-bit codes with a mask tensor
   // (the launcher gives such calls uniform splits: abi.hip streamk_units).
   constexpr bool kStreamK = !(MASK && D == 256 && BITS == 8);
+  // Nor with the split merge inside the launch at D = 256, 8-bit codes
+  // (its registers spilled to scratch): such batches keep the merge kernel
+  // (abi.hip fused_merge).
+  constexpr bool kStreamKFused = kStreamK && !(D == 256 && BITS == 8);
   if (p.units) {
-    if constexpr (kStreamK)
-      k = gs == 32 ? decode_mfma_kernel<Tag, D, BITS, 32, true, MASK, false>
-        : gs == 64 ? decode_mfma_kernel<Tag, D, BITS, 64, true, MASK, false>
-                   : decode_mfma_kernel<Tag, D, BITS, 128, true, MASK, false>;
+    if constexpr (kStreamKFused) {
+      if (p.tickets)
+        k = gs == 32 ? decode_mfma_kernel<Tag, D, BITS, 32, true, MASK, true>
+          : gs == 64 ? decode_mfma_kernel<Tag, D, BITS, 64, true, MASK, true>
+                     : decode_mfma_kernel<Tag, D, BITS, 128, true, MASK, true>;
+      else
+        k = gs == 32 ? decode_mfma_kernel<Tag, D, BITS, 32, true, MASK, false>
+          : gs == 64 ? decode_mfma_kernel<Tag, D, BITS, 64, true, MASK, false>
+                     : decode_mfma_kernel<Tag, D, BITS, 128, true, MASK, false>;
+    } else if constexpr (kStreamK) {
+      if (!p.tickets)
+        k = gs == 32 ? decode_mfma_kernel<Tag, D, BITS, 32, true, MASK, false>
+          : gs == 64 ? decode_mfma_kernel<Tag, D, BITS, 64, true, MASK, false>
+                     : decode_mfma_kernel<Tag, D, BITS, 128, true, MASK, false>;
+    }
   } else if (p.tickets)
     k = gs == 32 ? decode_mfma_kernel<Tag, D, BITS, 32, false, MASK, true>
       : gs == 64 ? decode_mfma_kernel<Tag, D, BITS, 64, false, MASK, true>
@@ -497,6 +559,8 @@ int launch_decode_mfma(const qsdpa_decode_args* a, int num_splits, float* part_a
   p.tickets = tickets;
   if (units && a->mask.ptr && a->D == 256 && a->bits == 8)
     return fail(QSDPA_ERR_UNSUPPORTED, "decode_mfma: no stream-K kernel for D=256 8-bit codes with a mask");
+  if (units && tickets && a->D == 256 && a->bits == 8)
+    return fail(QSDPA_ERR_UNSUPPORTED, "decode_mfma: no stream-K kernel with the merge inside for D=256 8-bit codes");
   const bool f16 = a->dtype == QSDPA_F16;
   if (a->D == 128) {
     if (f16) launch_bits<F16, 128>(p, a->bits, a->group_size, stream, a);

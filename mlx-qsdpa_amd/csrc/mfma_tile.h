@@ -385,35 +385,45 @@ __device__ __forceinline__ void store_out8(const MfmaParams& p, int b, int hh, i
   }
 }
 
-// The partial rows of one block (batch b, kv head kvh) of a uniform-split
-// launch: rows (head, position) of the kv head, `num_splits` slots each,
-// addressed through buffer descriptors from the block's first slot (the
-// launcher keeps the span below 2^31 bytes).  Slot of query row v (position
-// v / G of head kvh * G + v % G) and split x: local(v) + x.
+// The partial rows of one block (batch b, kv head kvh) for the split merge
+// inside the launch: rows (head, position) of the kv head, `cols` slots
+// each, addressed through buffer descriptors from the block's first slot
+// (the launcher keeps the span below 2^31 bytes).  Uniform splits: the
+// block's own rows, cols = num_splits; the stream-K schedule: kv head kvh's
+// rows of every sequence, cols = units + B (sequence b's partials are its
+// consecutive columns).  Slot of query row v (position v / G of head
+// kvh * G + v % G) and column x: local(v) + x.
 template <typename Tag, int D>
 struct PartRows {
   static constexpr int kEsz = Tag::kId == QSDPA_F16 ? 2 : 4;  // float16 normalised rows, or float32 sums
   rsrc_t acc, ml;
   int64_t first;
   __device__ __forceinline__ PartRows(const MfmaParams& p, int b, int kvh) {
-    first = (static_cast<int64_t>(b) * p.Hq + static_cast<int64_t>(kvh) * p.G) * p.qL * p.num_splits;
-    const uint32_t rows = static_cast<uint32_t>(p.G * p.qL * p.num_splits);
+    const int64_t cols = cols_of(p);
+    const int64_t head0 = p.units ? static_cast<int64_t>(kvh) * p.G
+                                  : static_cast<int64_t>(b) * p.Hq + static_cast<int64_t>(kvh) * p.G;
+    first = head0 * p.qL * cols;
+    const uint32_t rows = static_cast<uint32_t>(p.G * p.qL * cols);
     acc = make_rsrc(reinterpret_cast<const uint8_t*>(p.part_acc) + first * D * kEsz, rows * D * kEsz);
     ml = make_rsrc(p.part_ml + first * 2, rows * 8);
   }
+  static __device__ __forceinline__ int64_t cols_of(const MfmaParams& p) {
+    return p.units ? static_cast<int64_t>(p.units) + p.B : p.num_splits;
+  }
   static __device__ __forceinline__ uint32_t local(const MfmaParams& p, int v) {
-    return static_cast<uint32_t>(((v % p.G) * p.qL + v / p.G) * p.num_splits);
+    return static_cast<uint32_t>(((v % p.G) * p.qL + v / p.G) * cols_of(p));
   }
 };
 
 // Merge the NWV waves' running (m, l, acc) of a block's 16 query rows and
-// store the result: the normalised output (one split) or the split's partial
-// at column `col`.  row_of(w, h): wave w's accumulator row of query row h
+// store the result: the normalised output (one split, or `direct`: a
+// sequence whose keys one segment covers, merged inside the launch) or the
+// split's partial at column `col`.  row_of(w, h): wave w's accumulator row of query row h
 // (D floats, dims in order); ml_of(w, h): its (m, l).  Rows >= nh are
 // padding.  Called by all `nthreads` threads after a barrier.
 template <typename Tag, int D, int NWV, bool FUSED, typename RowF, typename MlF>
 __device__ __forceinline__ void merge_store(const MfmaParams& p, RowF&& row_of, MlF&& ml_of, int nh, int v0,
-                                            int kvh, int b, int col, int nthreads) {
+                                            int kvh, int b, int col, int nthreads, bool direct = false) {
   // 16 heads x D dims; thread -> (head, 8 consecutive dims).
   constexpr int kPer = 8;
   for (int idx = threadIdx.x; idx < 16 * (D / kPer); idx += nthreads) {
@@ -445,7 +455,7 @@ __device__ __forceinline__ void merge_store(const MfmaParams& p, RowF&& row_of, 
     const int vh = v0 + h;
     const int hh = kvh * p.G + vh % p.G;  // head and query position of the row
     const int iq = vh / p.G;
-    if (p.num_splits == 1) {
+    if (p.num_splits == 1 || (FUSED && direct)) {
       store_out8<Tag>(p, b, hh, iq, d, v, L);
     } else if (FUSED) {
       // Partials merged inside this launch (split_merge): agent-coherent
