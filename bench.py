@@ -226,7 +226,7 @@ def run_c4(args) -> int:
     import numpy as np
     import torch
 
-    from mlx_qsdpa_amd import _lib, kernels, metric
+    from mlx_qsdpa_amd import kernels, metric
 
     c = C4
     B, Hq, Hkv, D, bits, gs = c["B"], c["H_q"], c["H_kv"], c["D"], c["bits"], c["group_size"]
@@ -257,23 +257,18 @@ def run_c4(args) -> int:
     kv_start = (lmax - lengths).to(device=device, dtype=torch.int32)
     torch.cuda.synchronize()
 
-    # Launch arguments built once: each step only moves the append column
-    # and the decode's key count (the caches grow in place).
-    lib = _lib.load()
-    qjobs = (_lib.QuantizeArgs * 2)(*[
-        _lib.QuantizeArgs(B, Hkv, 1, D, bits, gs, kernels.dtype_code(T), 0, kernels._view(x),
-                          kernels._view(kv[0]), kernels._view(kv[1]), kernels._view(kv[2]))
-        for kv, x in zip(bufs, new)])
+    # Launch arguments built once: each step only moves the decode's key
+    # count (the caches grow in place).  The one-token append of K and V
+    # rides in the decode launch (append=): the workgroup that reads a
+    # sequence's new key quantizes it into column n first.
     v0 = [t[:, :, :lmax + 1] for kv in bufs for t in kv]  # the split count is chosen for the first step
     plan = kernels.DecodePlan(q, v0[0], v0[3], v0[1], v0[4], v0[2], v0[5], scale=D ** -0.5, bits=bits,
-                              group_size=gs, kv_start=kv_start, num_splits=args.splits, capacity=cap)
+                              group_size=gs, kv_start=kv_start, num_splits=args.splits, capacity=cap,
+                              append=(new[0], new[1]))
     splits = plan.num_splits
-    stream = torch.cuda.current_stream(device).cuda_stream
 
     def step(n, ev=None):
-        qjobs[0].t0 = qjobs[1].t0 = n  # the appended column, K and V in one launch
-        _lib.check(lib.qsdpa_quantize_batch(qjobs, 2, stream))
-        plan.set_keys(n + 1)
+        plan.set_keys(n + 1)  # key n is the appended one
         plan(ev)
 
     n = lmax
@@ -341,7 +336,7 @@ def run_c4(args) -> int:
           f"({kern_gbps:.0f} GB/s), splits={splits}; API path {api_us:.2f} us/step", file=sys.stderr,
           flush=True)
     workload = (f"c4: batched decode B={B} H_q={Hq} H_kv={Hkv} D={D} {bits}-bit gs={gs} f16, lengths "
-                f"U[{c['len_lo']},{c['len_hi']}] left-padded, append + decode per step")
+                f"U[{c['len_lo']},{c['len_hi']}] left-padded, append + decode per step (one launch)")
     line = {
         "metric": "µs/decode step (append + decode) + effective HBM GB/s (% peak), C4 batched",
         "value": round(us_step, 3), "unit": "us/step", "n_gpus": 1, "steps": args.steps,

@@ -45,7 +45,7 @@
 extern "C" {
 #endif
 
-#define QSDPA_ABI_VERSION 5
+#define QSDPA_ABI_VERSION 6
 
 enum {
   QSDPA_OK = 0,
@@ -142,6 +142,21 @@ typedef struct {
    * and kv_start.                                                         */
   int32_t causal;
   int64_t mask_stride_q; /* mask stride over query positions (0 = broadcast) */
+
+  /* Optional quantize-on-append folded into the decode: the one-token
+   * update of a cache (update_and_fetch, mlx_qsdpa/cache.py:279-322, whose
+   * mx.quantize + slice assignment qsdpa_quantize replaces) and the decode
+   * over the updated cache in one call.  k_new / v_new: [B, H_kv, 1, D]
+   * dtype.  When set (both), the call first quantizes k_new[b, h, 0] and
+   * v_new[b, h, 0] into key N - 1 of the K / V views -- codes, scales and
+   * biases, exactly as qsdpa_quantize with t0 = N - 1 would; the views must
+   * be writable and carry biases -- then attends over all N keys.  On the
+   * matrix-core path with one block of query rows per kv head (H_q / H_kv *
+   * q_len <= 16) the workgroup that reads key N - 1 writes it first (no
+   * extra launch); otherwise a quantize launch precedes the decode.  ptr
+   * NULL (both) = no append.                                              */
+  qsdpa_view k_new;
+  qsdpa_view v_new;
 } qsdpa_decode_args;
 
 /* Bytes of workspace qsdpa_decode needs for these args (0 for a single

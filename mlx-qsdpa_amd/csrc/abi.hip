@@ -41,7 +41,7 @@ int launch_merge(const qsdpa_decode_args* a, int num_splits, const float* part_a
 bool mfma_supports(const qsdpa_decode_args* a);
 int mfma_num_splits(const qsdpa_decode_args* a, int cus);
 int launch_decode_mfma(const qsdpa_decode_args* a, int num_splits, float* part_acc, float* part_ml,
-                       int units, int* sched, unsigned* tickets, hipStream_t stream);
+                       int units, int* sched, unsigned* tickets, bool append, hipStream_t stream);
 // Defined in prefill_mfma.hip.
 bool prefill_supports(const qsdpa_decode_args* a);
 int prefill_num_splits(const qsdpa_decode_args* a, int cus);
@@ -124,6 +124,13 @@ int validate_decode(const qsdpa_decode_args* a) {
     const int al = md == QSDPA_F32 ? 4 : (md == QSDPA_BOOL ? 1 : 2);
     if ((rc = check_view(a->mask, "mask", al, 1, true))) return rc;
   }
+  if ((a->k_new.ptr == nullptr) != (a->v_new.ptr == nullptr))
+    return fail(QSDPA_ERR_INVALID, "k_new and v_new must both be given or both be NULL");
+  if (a->k_new.ptr) {
+    if (!a->k_biases.ptr) return fail(QSDPA_ERR_INVALID, "an append writes biases: k_biases / v_biases needed");
+    if ((rc = check_view(a->k_new, "k_new", 2, 1, true))) return rc;
+    if ((rc = check_view(a->v_new, "v_new", 2, 1, true))) return rc;
+  }
   return QSDPA_OK;
 }
 
@@ -163,6 +170,34 @@ int streamk_units(const qsdpa_decode_args* a, int splits) {
   if (units >= (int64_t(1) << 31) / 2) return 0;
   if (static_cast<int64_t>(a->B) * (a->N / kSchedTile + 1) >= (int64_t(1) << 31)) return 0;
   return static_cast<int>(units);
+}
+
+// The folded append (k_new / v_new) runs inside the matrix-core decode when
+// one block of query rows covers a kv head (so one workgroup reads a
+// sequence's key N - 1), the new rows are 16-byte aligned, D = 128 and
+// there is no mask tensor (the instantiations built with it); otherwise
+// the two rows are quantized by a launch of their own before the decode.
+bool fused_append(const qsdpa_decode_args* a, bool prefill, bool mfma) {
+  if (!a->k_new.ptr || prefill || !mfma || a->D != 128 || a->mask.ptr) return false;
+  const int64_t G = a->H_q / a->H_kv, qL = std::max(a->q_len, 1);
+  if (G * qL > 16) return false;
+  for (const qsdpa_view* v : {&a->k_new, &a->v_new})
+    if (!aligned(v->ptr, 16) || v->stride_b % 8 != 0 || v->stride_h % 8 != 0) return false;
+  return true;
+}
+
+int launch_append_quantize(const qsdpa_decode_args* a, hipStream_t s) {
+  qsdpa_quantize_args j[2] = {};
+  for (int i = 0; i < 2; ++i) {
+    j[i].B = a->B; j[i].H = a->H_kv; j[i].S = 1; j[i].D = a->D;
+    j[i].bits = a->bits; j[i].group_size = a->group_size; j[i].dtype = a->dtype; j[i].t0 = a->N - 1;
+    j[i].src = i ? a->v_new : a->k_new;
+    j[i].dst_packed = i ? a->v_packed : a->k_packed;
+    j[i].dst_scales = i ? a->v_scales : a->k_scales;
+    j[i].dst_biases = i ? a->v_biases : a->k_biases;
+  }
+  const qsdpa_quantize_args* ptrs[2] = {&j[0], &j[1]};
+  return launch_quantize(ptrs, 2, s);
 }
 
 // A split-K decode on the matrix-core kernel merges its partials inside the
@@ -235,10 +270,12 @@ int run_decode(const qsdpa_decode_args* args, int splits, void* workspace, hipSt
     sched = reinterpret_cast<int*>(base + w.sched);
   }
   int rc;
+  const bool append_inside = fused_append(args, prefill, mfma);
+  if (args->k_new.ptr && !append_inside && (rc = launch_append_quantize(args, s))) return rc;
   if (prefill) rc = launch_prefill_mfma(args, splits, part_acc, part_ml, s);
   else if (mfma)
     rc = launch_decode_mfma(args, splits, part_acc, part_ml, units, sched,
-                            fused ? static_cast<unsigned*>(workspace) : nullptr, s);
+                            fused ? static_cast<unsigned*>(workspace) : nullptr, append_inside, s);
   else rc = launch_decode_valu(args, splits, part_acc, part_ml, s);
   if (rc) return rc;
   // The MFMA kernels store float16 inputs' partials as normalised float16

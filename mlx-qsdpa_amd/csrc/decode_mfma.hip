@@ -55,17 +55,69 @@
 // partials for the merge kernel (merge.hip): float16 inputs store the
 // normalised row acc / l as float16 (half the bytes), bfloat16 float32 rows.
 #include "mfma_tile.h"
+#include "quant_group.h"
 #include "wave_split.h"
 
 namespace qsdpa {
 
 namespace {
 
+// The folded append of sequence b, kv head kvh (one wave): K and V rows of
+// p.knew / p.vnew quantized into key N - 1 of the caches, by the quantizer
+// of qsdpa_quantize (quant_group.h) with its one-row layout -- GS / 8 lanes
+// per group, 8 values each: lanes [0, D / 8) the K row, [D / 8, D / 4) the
+// V row -- so the cache holds the same bits either way.  append_load
+// issues the lane's 16-byte load of the new row; append_store quantizes
+// and stores.
+template <int D>
+__device__ __forceinline__ uint4 append_load(const MfmaParams& p, int b, int kvh, int lane) {
+  constexpr int kRowLanes = D / 8;
+  if (lane >= 2 * kRowLanes) return uint4{0u, 0u, 0u, 0u};
+  const bool isv = lane >= kRowLanes;
+  const int l = isv ? lane - kRowLanes : lane;
+  const uint16_t* src = isv ? p.vnew + b * p.vnew_sb + kvh * p.vnew_sh : p.knew + b * p.knew_sb + kvh * p.knew_sh;
+  return *reinterpret_cast<const uint4*>(src + 8 * l);
+}
+
+template <typename Tag, int D, int BITS, int GS>
+__device__ __forceinline__ void append_store(const MfmaParams& p, int b, int kvh, int lane, uint4 w) {
+  constexpr int L = GS / 8;         // lanes per group
+  constexpr int kRowLanes = D / 8;  // lanes per row
+  constexpr int PER = 32 / BITS;
+  if (lane >= 2 * kRowLanes) return;
+  const bool isv = lane >= kRowLanes;
+  const int l = isv ? lane - kRowLanes : lane;
+  const int g = l / L, part = l % L;
+  const int64_t t = p.N - 1;
+  const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+  uint16_t raw[8];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    raw[2 * k] = static_cast<uint16_t>(wv[k]);
+    raw[2 * k + 1] = static_cast<uint16_t>(wv[k] >> 16);
+  }
+  auto val = [&](int i) { return to_f32<Tag>(raw[i]); };
+  float lo, hi;
+  lane_minmax<8>(val, lo, hi);
+  uint32_t* dp = const_cast<uint32_t*>(isv ? p.vp + b * p.vp_sb + kvh * p.vp_sh + t * p.vp_sn
+                                           : p.kp + b * p.kp_sb + kvh * p.kp_sh + t * p.kp_sn);
+  uint16_t* ds = const_cast<uint16_t*>(isv ? p.vs + b * p.vs_sb + kvh * p.vs_sh + t * p.vs_sn
+                                           : p.ks + b * p.ks_sb + kvh * p.ks_sh + t * p.ks_sn);
+  uint16_t* db = const_cast<uint16_t*>(isv ? p.vb + b * p.vb_sb + kvh * p.vb_sh + t * p.vb_sn
+                                           : p.kb + b * p.kb_sb + kvh * p.kb_sh + t * p.kb_sn);
+  quantize_group<Tag, BITS, GS, L>(val, lo, hi, part, dp + 8 * l / PER, ds + g, db + g);
+}
+
+template <typename Tag, int D, int BITS, int GS>
+__device__ __forceinline__ void append_row(const MfmaParams& p, int b, int kvh, int lane) {
+  append_store<Tag, D, BITS, GS>(p, b, kvh, lane, append_load<D>(p, b, kvh, lane));
+}
+
 // One segment of a workgroup's work: tiles t_lo, t_lo + stride, ... (at
 // most jmax of them) of sequence b for the block's 16 query rows.  Writes the
 // normalised output (one split) or the partials at column `col` of the rows'
 // partial slots.  Called by the whole workgroup.
-template <typename Tag, int D, int BITS, int GS, bool MASK, bool SK, bool FUSED>
+template <typename Tag, int D, int BITS, int GS, bool MASK, bool SK, bool FUSED, bool APPEND>
 __device__ __forceinline__ void decode_segment(const MfmaParams& p, float* s_acc, float (*s_ml)[16][2],
                                                uint8_t* s_q, int lane, int wave, int quad, int r, int hblk,
                                                int kvh, int b, int t_lo, int stride, int jmax, int col,
@@ -183,10 +235,37 @@ __device__ __forceinline__ void decode_segment(const MfmaParams& p, float* s_acc
   __syncthreads();
   typename K::Regs R;
   int j = wave;
+  // The folded append: the wave that visits the sequence's last tile (wave
+  // 0 of split 0 when the sequence has no keys in range) writes key N - 1.
+  // Its new-row loads go first; unless the last tile is its first, its
+  // first tile's loads follow at once and the quantization and stores run
+  // while they are in flight.  Either way the stores are complete (a wait
+  // for every counter) before the wave issues another load, so before the
+  // last tile's.
+  bool appender = false;
+  uint4 nw = uint4{0u, 0u, 0u, 0u};
+  if constexpr (APPEND) {
+    appender = J > 0 ? t_lo + (J - 1) * stride == T - 1 && wave == wave_split_last_owner(J, D)
+                     : t_lo == 0 && wave == 0;
+    if (appender) {
+      nw = append_load<D>(p, b, kvh, lane);
+      if (J == 0 || j == J - 1) {
+        append_store<Tag, D, BITS, GS>(p, b, kvh, lane, nw);
+        __builtin_amdgcn_s_waitcnt(0);
+        appender = false;
+      }
+    }
+  }
   K::load_k(R, rs, L, row_of(j));
   __builtin_amdgcn_sched_barrier(0);
   K::load_v(R, rs, L, row_of(j));
   __builtin_amdgcn_sched_barrier(0);
+  if constexpr (APPEND) {
+    if (appender) {
+      append_store<Tag, D, BITS, GS>(p, b, kvh, lane, nw);
+      __builtin_amdgcn_s_waitcnt(0);
+    }
+  }
 
   // Q^T B operands, one 16-byte piece per lane and QK step m: head r, dims
   // quad*QD + 8m + j, in the order the K dequantizer produces them (float16
@@ -382,12 +461,15 @@ __device__ __forceinline__ void zero_empty_sequences(const MfmaParams& p, int kv
     if (seq_tiles(p.kv_start, b, p.N) == 0) store_out8<Tag>(p, b, hh, iq, d, zero, 0.0f);
 }
 
+// APPEND: the folded append (p.knew / p.vnew; its own instantiations, so the
+// others carry none of its registers: with it as a run-time branch the C3
+// kernel's SGPR spills doubled and the C5 kernel spilled to scratch).
 // SK: the stream-K schedule of a left-padded batch (a loop over segments);
 // otherwise one uniform split (a separate instantiation, so the loop's
 // register pressure stays out of the common case).  MASK: a mask tensor
 // (its own instantiation: with the mask code in the unmasked kernel, C3
 // took 23.2 instead of 22.3 us).
-template <typename Tag, int D, int BITS, int GS, bool SK, bool MASK, bool FUSED>
+template <typename Tag, int D, int BITS, int GS, bool SK, bool MASK, bool FUSED, bool APPEND>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_mfma_kernel(MfmaParams p) {
   constexpr int kRowF = D + 4;  // LDS floats per (wave, head) row
   __shared__ __attribute__((aligned(16))) float s_acc[kWaves * 16 * kRowF];
@@ -403,7 +485,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int kvh = blockIdx.y / p.hb_count;
   if constexpr (!SK) {
     // Uniform splits: grid (S, H_kv * row blocks, B); split x of sequence z.
-    decode_segment<Tag, D, BITS, GS, MASK, false, FUSED>(p, s_acc, s_ml, s_q, lane, wave, quad, r, hblk, kvh, blockIdx.z, blockIdx.x,
+    decode_segment<Tag, D, BITS, GS, MASK, false, FUSED, APPEND>(p, s_acc, s_ml, s_q, lane, wave, quad, r, hblk, kvh, blockIdx.z, blockIdx.x,
                                      p.num_splits, 0x7FFFFFFF, blockIdx.x);
     if constexpr (FUSED) split_merge<Tag, D, kFusedSplits>(p, &s_flag, blockIdx.z, kvh, hblk, 0, p.num_splits);
   } else {
@@ -412,6 +494,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     // the sequences laid end to end, one segment per sequence it touches.
     const int total = streamk_total(p.kv_start, p.B, p.N);
     const int C = max(1, (total + p.units - 1) / p.units);
+    // Sequences without keys: no segment reads their key N - 1, so unit 0
+    // writes the folded append's row for them.
+    if constexpr (APPEND) {
+      if (blockIdx.x == 0 && wave == 0)
+        for (int b = 0; b < p.B; ++b)
+          if (seq_tiles(p.kv_start, b, p.N) == 0) append_row<Tag, D, BITS, GS>(p, b, kvh, lane);
+    }
     if constexpr (FUSED) {
       // Sequences without keys get zero rows here (the merge kernel's job
       // otherwise).
@@ -431,7 +520,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         // Sequence b's tiles [P, P + Tb) lie in units P / C .. (P + Tb - 1) / C:
         // its partials are those units' columns (unit + b).
         const int uf = P / C, count = (P + Tb - 1) / C - uf + 1;
-        decode_segment<Tag, D, BITS, GS, MASK, true, FUSED>(p, s_acc, s_ml, s_q, lane, wave, quad, r, hblk, kvh, b, g - P, 1, hi - g,
+        decode_segment<Tag, D, BITS, GS, MASK, true, FUSED, APPEND>(p, s_acc, s_ml, s_q, lane, wave, quad, r, hblk, kvh, b, g - P, 1, hi - g,
                                          static_cast<int>(blockIdx.x) + b, FUSED && count == 1);
         if constexpr (FUSED) {
           if (count > 1) split_merge<Tag, D, 8>(p, &s_flag, b, kvh, hblk, uf + b, count);
@@ -445,41 +534,48 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   }
 }
 
+using DecodeKernel = void (*)(MfmaParams);
+
+template <typename Tag, int D, int BITS, bool SK, bool MASK, bool FUSED, bool APPEND>
+DecodeKernel by_gs(int gs) {
+  return gs == 32 ? decode_mfma_kernel<Tag, D, BITS, 32, SK, MASK, FUSED, APPEND>
+       : gs == 64 ? decode_mfma_kernel<Tag, D, BITS, 64, SK, MASK, FUSED, APPEND>
+                  : decode_mfma_kernel<Tag, D, BITS, 128, SK, MASK, FUSED, APPEND>;
+}
+
+// The instantiation for a launch; null where none is built (the launcher
+// never asks for those: abi.hip streamk_units, fused_merge, fused_append).
+template <typename Tag, int D, int BITS, bool MASK, bool APPEND>
+DecodeKernel pick_kernel(const MfmaParams& p, int gs) {
+  // No stream-K instantiation for D = 256, 8-bit codes with a mask tensor
+  // (the launcher gives such calls uniform splits: abi.hip streamk_units),
+  // nor with the split merge inside the launch at D = 256, 8-bit codes (its
+  // registers spilled to scratch): such batches keep the merge kernel.
+  constexpr bool kStreamK = !(MASK && D == 256 && BITS == 8);
+  constexpr bool kStreamKFused = kStreamK && !(D == 256 && BITS == 8);
+  if (p.units) {
+    if constexpr (kStreamKFused)
+      return p.tickets ? by_gs<Tag, D, BITS, true, MASK, true, APPEND>(gs)
+                       : by_gs<Tag, D, BITS, true, MASK, false, APPEND>(gs);
+    else if constexpr (kStreamK)
+      return p.tickets ? nullptr : by_gs<Tag, D, BITS, true, MASK, false, APPEND>(gs);
+    else
+      return nullptr;
+  }
+  return p.tickets ? by_gs<Tag, D, BITS, false, MASK, true, APPEND>(gs)
+                   : by_gs<Tag, D, BITS, false, MASK, false, APPEND>(gs);
+}
+
 template <typename Tag, int D, int BITS, bool MASK>
 void launch_mask(const MfmaParams& p, int gs, hipStream_t stream, const qsdpa_decode_args* a) {
   const dim3 grid(p.units ? p.units : p.num_splits, p.Hkv * p.hb_count, p.units ? 1 : p.B);
-  void (*k)(MfmaParams) = nullptr;
-  // No stream-K instantiation for D = 256, 8-bit codes with a mask tensor
-  // (the launcher gives such calls uniform splits: abi.hip streamk_units).
-  constexpr bool kStreamK = !(MASK && D == 256 && BITS == 8);
-  // Nor with the split merge inside the launch at D = 256, 8-bit codes
-  // (its registers spilled to scratch): such batches keep the merge kernel
-  // (abi.hip fused_merge).
-  constexpr bool kStreamKFused = kStreamK && !(D == 256 && BITS == 8);
-  if (p.units) {
-    if constexpr (kStreamKFused) {
-      if (p.tickets)
-        k = gs == 32 ? decode_mfma_kernel<Tag, D, BITS, 32, true, MASK, true>
-          : gs == 64 ? decode_mfma_kernel<Tag, D, BITS, 64, true, MASK, true>
-                     : decode_mfma_kernel<Tag, D, BITS, 128, true, MASK, true>;
-      else
-        k = gs == 32 ? decode_mfma_kernel<Tag, D, BITS, 32, true, MASK, false>
-          : gs == 64 ? decode_mfma_kernel<Tag, D, BITS, 64, true, MASK, false>
-                     : decode_mfma_kernel<Tag, D, BITS, 128, true, MASK, false>;
-    } else if constexpr (kStreamK) {
-      if (!p.tickets)
-        k = gs == 32 ? decode_mfma_kernel<Tag, D, BITS, 32, true, MASK, false>
-          : gs == 64 ? decode_mfma_kernel<Tag, D, BITS, 64, true, MASK, false>
-                     : decode_mfma_kernel<Tag, D, BITS, 128, true, MASK, false>;
-    }
-  } else if (p.tickets)
-    k = gs == 32 ? decode_mfma_kernel<Tag, D, BITS, 32, false, MASK, true>
-      : gs == 64 ? decode_mfma_kernel<Tag, D, BITS, 64, false, MASK, true>
-                 : decode_mfma_kernel<Tag, D, BITS, 128, false, MASK, true>;
-  else
-    k = gs == 32 ? decode_mfma_kernel<Tag, D, BITS, 32, false, MASK, false>
-      : gs == 64 ? decode_mfma_kernel<Tag, D, BITS, 64, false, MASK, false>
-                 : decode_mfma_kernel<Tag, D, BITS, 128, false, MASK, false>;
+  DecodeKernel k = nullptr;
+  // The folded append is built for D = 128 without a mask tensor.
+  if constexpr (D == 128 && !MASK) {
+    k = p.knew ? pick_kernel<Tag, D, BITS, MASK, true>(p, gs) : pick_kernel<Tag, D, BITS, MASK, false>(p, gs);
+  } else {
+    k = p.knew ? nullptr : pick_kernel<Tag, D, BITS, MASK, false>(p, gs);
+  }
   if (k) launch_profiled(k, grid, dim3(kThreads), stream, a->prof_begin, a->prof_end, p);
 }
 
@@ -552,15 +648,23 @@ int mfma_num_splits(const qsdpa_decode_args* a, int cus) {
 }
 
 int launch_decode_mfma(const qsdpa_decode_args* a, int num_splits, float* part_acc, float* part_ml,
-                       int units, int* sched, unsigned* tickets, hipStream_t stream) {
+                       int units, int* sched, unsigned* tickets, bool append, hipStream_t stream) {
   MfmaParams p = mfma_params(a, num_splits, part_acc, part_ml);
   p.units = units;
   p.sched = sched;
   p.tickets = tickets;
+  if (append) {
+    p.knew = static_cast<const uint16_t*>(a->k_new.ptr);
+    p.knew_sb = a->k_new.stride_b; p.knew_sh = a->k_new.stride_h;
+    p.vnew = static_cast<const uint16_t*>(a->v_new.ptr);
+    p.vnew_sb = a->v_new.stride_b; p.vnew_sh = a->v_new.stride_h;
+  }
   if (units && a->mask.ptr && a->D == 256 && a->bits == 8)
     return fail(QSDPA_ERR_UNSUPPORTED, "decode_mfma: no stream-K kernel for D=256 8-bit codes with a mask");
   if (units && tickets && a->D == 256 && a->bits == 8)
     return fail(QSDPA_ERR_UNSUPPORTED, "decode_mfma: no stream-K kernel with the merge inside for D=256 8-bit codes");
+  if (append && (a->D != 128 || a->mask.ptr))
+    return fail(QSDPA_ERR_UNSUPPORTED, "decode_mfma: the folded append is built for D=128 without a mask");
   const bool f16 = a->dtype == QSDPA_F16;
   if (a->D == 128) {
     if (f16) launch_bits<F16, 128>(p, a->bits, a->group_size, stream, a);

@@ -59,6 +59,12 @@ struct MfmaParams {
   // v % G); a block takes 16 consecutive rows.
   int qL, causal;
   int64_t q_sq, o_sq, m_sq;  // position strides of q, out and the mask
+  // Folded append (null = none): the new K / V rows [B, H_kv, 1, D], which
+  // the workgroup that reads key N - 1 quantizes into that key first.
+  const uint16_t* knew;
+  int64_t knew_sb, knew_sh;
+  const uint16_t* vnew;
+  int64_t vnew_sb, vnew_sh;
 };
 
 static_assert(kTile == kSchedTile, "the stream-K schedule counts the decode's key tiles");
@@ -311,6 +317,8 @@ inline MfmaParams mfma_params(const qsdpa_decode_args* a, int num_splits, float*
   p.units = 0;
   p.sched = nullptr;
   p.tickets = nullptr;
+  p.knew = p.vnew = nullptr;
+  p.knew_sb = p.knew_sh = p.vnew_sb = p.vnew_sh = 0;
   return p;
 }
 

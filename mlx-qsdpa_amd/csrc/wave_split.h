@@ -38,4 +38,10 @@ QSDPA_HD int wave_split_next(int j, int J, int J8, int wave) {
   return j < J8 ? J8 + wave : j + 4;
 }
 
+// The wave that visits the last position J - 1 (J >= 1).
+QSDPA_HD int wave_split_last_owner(int J, int D) {
+  const int J8 = wave_split_rr_end(J, D);
+  return J8 < J ? (J - 1 - J8) % 4 : (J - 1) % kSplitWaves;
+}
+
 }  // namespace qsdpa

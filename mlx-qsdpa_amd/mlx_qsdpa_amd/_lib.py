@@ -23,7 +23,7 @@ QSDPA_BF16 = 1
 QSDPA_F32 = 2
 QSDPA_BOOL = 3
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 NOALLOC_SCRATCH_BYTES = 16 << 20
 
 # Every symbol include/qsdpa.h declares.
@@ -65,6 +65,7 @@ class DecodeArgs(ctypes.Structure):
         ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
         ("prof_begin", ctypes.c_void_p), ("prof_end", ctypes.c_void_p),
         ("q_len", ctypes.c_int32), ("causal", ctypes.c_int32), ("mask_stride_q", ctypes.c_int64),
+        ("k_new", View), ("v_new", View),
     ]
 
 

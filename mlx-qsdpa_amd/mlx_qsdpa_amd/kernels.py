@@ -275,7 +275,7 @@ def dequantize(packed: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor 
 # decode
 # ---------------------------------------------------------------------------
 def _decode_args(q, pk, pv, ks, vs, kb, vb, out, scale, bits, group_size, mask, kv_start,
-                 num_splits, causal=False):
+                 num_splits, causal=False, append=None):
     B, Hq, qL, D = q.shape
     _, Hkv, N, _ = pk.shape
     if qL < 1:
@@ -335,6 +335,15 @@ def _decode_args(q, pk, pv, ks, vs, kb, vb, out, scale, bits, group_size, mask, 
     a.num_splits = int(num_splits)
     a.q_len = qL
     a.causal = int(bool(causal))
+    if append is not None:
+        k_new, v_new = append
+        if kb is None or vb is None:
+            raise ValueError("an append writes biases: the cache views must carry k / v biases")
+        for name, t in (("k_new", k_new), ("v_new", v_new)):
+            _expect_shape(name, t, (B, Hkv, 1, D))
+            if t.dtype != q.dtype or t.device != q.device or t.stride(-1) != 1:
+                raise ValueError(f"{name}: expected a {q.dtype} tensor on {q.device} with contiguous rows")
+        a.k_new, a.v_new = _view(k_new), _view(v_new)
     a.mask_stride_q = mask_sq
     return a, mask
 
@@ -361,7 +370,13 @@ class DecodePlan:
     """
 
     def __init__(self, q, pk, pv, ks, vs, kb, vb, *, scale, bits, group_size, mask=None,
-                 kv_start=None, num_splits=0, capacity=None, causal=False):
+                 kv_start=None, num_splits=0, capacity=None, causal=False, append=None):
+        """append: optional (k_new, v_new), [B, H_kv, 1, D] tensors of q's
+        dtype, whose rows every call first quantizes into key N - 1 of the
+        caches (the one-token update of a decode step, in the same launch
+        where the kernel takes it: qsdpa_decode_args.k_new).  The caller
+        writes the new token into them and moves N past it (set_keys) before
+        each call."""
         # Rows set_keys may reach: the views' own length unless the caller
         # states how many rows the underlying buffers hold, never more than
         # every buffer's storage holds, and never past a mask's last key.
@@ -378,14 +393,14 @@ class DecodePlan:
                 if t is not None and _rows_in_storage(t) < self.capacity:
                     raise ValueError(f"{name}: its storage holds {_rows_in_storage(t)} rows, "
                                      f"fewer than capacity {self.capacity}")
-        _require_device(q, pk, pv, ks, vs, kb, vb, mask, kv_start)
+        _require_device(q, pk, pv, ks, vs, kb, vb, mask, kv_start, *(append or ()))
         self.q = _inner_contig(q)
         self.out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
         if kv_start is not None:
             kv_start = kv_start.to(device=q.device, dtype=torch.int32).contiguous()
-        self._refs = (pk, pv, ks, vs, kb, vb, kv_start)
+        self._refs = (pk, pv, ks, vs, kb, vb, kv_start, append)
         self.args, self._mask = _decode_args(self.q, pk, pv, ks, vs, kb, vb, self.out, scale, bits,
-                                             group_size, mask, kv_start, num_splits, causal)
+                                             group_size, mask, kv_start, num_splits, causal, append)
         self.lib = _lib.load()
         n = ctypes.c_int32(0)
         ws = _lib.check(self.lib.qsdpa_decode_workspace_size(ctypes.byref(self.args),
@@ -517,7 +532,7 @@ def _stream_workspace(device, stream, nbytes):
 
 
 def decode(q, pk, pv, ks, vs, kb, vb, *, scale, bits, group_size, mask=None, kv_start=None,
-           num_splits=0, out=None, workspace=None, prof_events=None, causal=False):
+           num_splits=0, out=None, workspace=None, prof_events=None, causal=False, append=None):
     """Fused quantized attention; returns out [B, H_q, qL, D] (dtype of q).
 
     qL > 1 query positions (speculative or chunked decoding, prefill) run on
@@ -532,10 +547,13 @@ def decode(q, pk, pv, ks, vs, kb, vb, *, scale, bits, group_size, mask=None, kv_
     caller's ``workspace`` (uint8, at least qsdpa_decode_workspace_size
     bytes) must be zero-filled before its first use; the library leaves the
     counters at its start zero after every call, so it can be re-used.
+
+    ``append``: optional (k_new, v_new) [B, H_kv, 1, D] rows quantized into
+    key N - 1 of the caches before the attention (see DecodePlan).
     """
-    _require_device(q, pk, pv, ks, vs, kb, vb, mask, kv_start)
+    _require_device(q, pk, pv, ks, vs, kb, vb, mask, kv_start, *(append or ()))
     slot = None
-    if mask is None and out is None and workspace is None:
+    if mask is None and out is None and workspace is None and append is None:
         q = _inner_contig(q)
         if kv_start is not None and (kv_start.dtype != torch.int32 or kv_start.device != q.device
                                      or not kv_start.is_contiguous()):
@@ -550,7 +568,7 @@ def decode(q, pk, pv, ks, vs, kb, vb, *, scale, bits, group_size, mask=None, kv_
     if kv_start is not None:
         kv_start = kv_start.to(device=q.device, dtype=torch.int32).contiguous()
     a, keep_alive = _decode_args(q, pk, pv, ks, vs, kb, vb, out, scale, bits, group_size, mask,
-                                 kv_start, num_splits, causal)
+                                 kv_start, num_splits, causal, append)
     lib = _lib.load()
     n = ctypes.c_int32(0)
     ws = _lib.check(lib.qsdpa_decode_workspace_size(ctypes.byref(a), ctypes.byref(n)))

@@ -182,7 +182,8 @@ def test_wave_split_covers_every_position_once(tmp_path):
     """The decode kernel's share of a split's tile positions among its 8
     waves (csrc/wave_split.h, compiled here for the host): for every J up
     to 1024 and both ratios, each position in [0, J) is visited by exactly
-    one wave, and waves 4-7 take no positions of the tail."""
+    one wave, waves 4-7 take no positions of the tail, and
+    wave_split_last_owner names the wave that visits position J - 1."""
     header = HEADER.parent.parent / "mlx-qsdpa_amd" / "csrc" / "wave_split.h"
     src = tmp_path / "split.cc"
     src.write_text(f"""
@@ -195,11 +196,18 @@ int main() {{
       const int J8 = qsdpa::wave_split_rr_end(J, D);
       if (J8 < 0 || J8 > J) {{ std::printf("J8 %d of %d\\n", J8, J); return 1; }}
       std::vector<int> seen(J, 0);
+      int last = -1;
       for (int w = 0; w < 8; ++w)
         for (int j = w; j < J; j = qsdpa::wave_split_next(j, J, J8, w)) {{
           seen[j]++;
+          if (j == J - 1) last = w;
           if (w >= 4 && j >= J8) {{ std::printf("wave %d in the tail at %d (J=%d)\\n", w, j, J); return 1; }}
         }}
+      if (J > 0 && last != qsdpa::wave_split_last_owner(J, D)) {{
+        std::printf("D=%d J=%d last position visited by wave %d, owner %d\\n", D, J, last,
+                    qsdpa::wave_split_last_owner(J, D));
+        return 1;
+      }}
       for (int j = 0; j < J; ++j)
         if (seen[j] != 1) {{ std::printf("D=%d J=%d position %d seen %d times\\n", D, J, j, seen[j]); return 1; }}
     }}
