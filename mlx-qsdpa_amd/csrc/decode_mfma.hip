@@ -14,9 +14,11 @@
 // each block's keys at its last row's limit and each lane's at its own.
 //
 // Workgroup = 8 waves = one split of a (batch, kv head, block of 16 query
-// rows).  The sequence is cut into 32-token tiles; split s of S owns tiles
-// s, s + S, s + 2S, ..., so the whole grid streams one compact window of the
-// cache at a time.  Each wave streams its share of the split's tiles with
+// rows).  The sequence is cut into 32-token tiles, grouped in super-tiles of
+// up to 8 consecutive tiles; split s of S owns super-tiles s, s + S, s + 2S,
+// ..., so the whole grid streams one compact window of the cache at a time
+// and a workgroup's waves start on consecutive tiles.  Each wave streams its
+// share of the split's tiles with
 // one register set: the next tile's K loads are issued as soon as the
 // current K has been consumed, its V loads once the current V has been
 // re-arranged for the PV operands.  All K / V / scale / bias reads are raw
@@ -140,14 +142,23 @@ __device__ __forceinline__ void decode_segment(const MfmaParams& p, float* s_acc
   const int n_end = p.causal ? min(p.N, max(0, p.N - p.qL + (v0 + nh - 1) / p.G + 1)) : p.N;
   const int n_lane = p.causal ? min(n_end, max(0, p.N - p.qL + iq_lane + 1)) : n_end;
 
-  // Keys [s0, n_end) of this sequence, in 32-token tiles from s0.  The
-  // segment owns tiles t_lo, t_lo + stride, ... (positions j = 0, 1, ...,
-  // J - 1).  Uniform splits: split s of S owns tiles s, s + S, ..., so at any
-  // moment the grid streams one compact window of the cache.
+  // Keys [s0, n_end) of this sequence, in 32-token tiles from s0, taken in
+  // super-tiles of 2^sh consecutive tiles (wave_split.h): the segment owns
+  // super-tiles t_lo, t_lo + stride, ... (positions j = 0, 1, ..., J - 1).
+  // Uniform splits: split s of S owns super-tiles s, s + S, ..., so at any
+  // moment the grid streams one compact window of the cache, and each
+  // workgroup's first loads cover 8 consecutive tiles (its waves' first
+  // positions).  Measured on MI355X at C3 (128 splits): 21.2-21.4 us per
+  // decode kernel against 22.2-22.5 with single tiles round-robin (4 tiles
+  // per super-tile: 21.2).
   const int s0 = p.kv_start ? min(max(p.kv_start[b], 0), p.N) : 0;
   const int len = max(n_end - s0, 0);
   const int T = (len + kTile - 1) / kTile;
-  const int J = T > t_lo ? min(jmax, (T - t_lo + stride - 1) / stride) : 0;
+  // (Not for D = 256 with 8-bit codes, whose lanes read 64 contiguous bytes of
+  // a K row: C2 took 30.4-30.7 us against 30.1-30.2 with super-tiles.)
+  const int sh = D == 256 && BITS == 8 ? 0 : super_tile_shift(T, stride);
+  const int J = super_tile_positions(T, t_lo, stride, jmax, sh);
+  auto tile_of = [&](int j) -> int { return super_tile_tile(j, t_lo, stride, sh); };
   // The waves' shares of the J positions (wave_split.h).
   static_assert(kWaves == kSplitWaves, "the tile split is for 8 waves");
   const int J8 = wave_split_rr_end(J, D);
@@ -156,7 +167,7 @@ __device__ __forceinline__ void decode_segment(const MfmaParams& p, float* s_acc
   // descriptor (the loads read zero without touching memory).  Every tile
   // issues the same loads, so the compiler's vmcnt waits stay exact.
   const int oob = len + kTile;
-  auto row_of = [&](int j) -> int { return j < J ? (t_lo + j * stride) * kTile : oob; };
+  auto row_of = [&](int j) -> int { return j < J ? tile_of(j) * kTile : oob; };
 
   // Buffer descriptors over rows [s0, N) of this (batch, kv head).
   Rsrcs rs;
@@ -245,7 +256,7 @@ __device__ __forceinline__ void decode_segment(const MfmaParams& p, float* s_acc
   bool appender = false;
   uint4 nw = uint4{0u, 0u, 0u, 0u};
   if constexpr (APPEND) {
-    appender = J > 0 ? t_lo + (J - 1) * stride == T - 1 && wave == wave_split_last_owner(J, D)
+    appender = J > 0 ? tile_of(J - 1) == T - 1 && wave == wave_split_last_owner(J, D)
                      : t_lo == 0 && wave == 0;
     if (appender) {
       nw = append_load<D>(p, b, kvh, lane);

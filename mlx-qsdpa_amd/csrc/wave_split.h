@@ -1,6 +1,8 @@
-// How the 8 waves of a decode workgroup share the J tile positions of their
-// split (decode_mfma.hip).  Plain C++ as well as device code, so that a host
-// program can check the invariant the kernel relies on: every position in
+// How a decode split's key tiles are laid out (super-tiles) and how the 8
+// waves of a decode workgroup share the split's J tile positions
+// (decode_mfma.hip).  Plain C++ as well as device code, so that a host
+// program can check the invariants the kernel relies on: every tile of a
+// sequence belongs to exactly one split position, and every position in
 // [0, J) is visited by exactly one wave.
 //
 // Positions below J - E go round-robin to the 8 waves; the last E go to
@@ -42,6 +44,31 @@ QSDPA_HD int wave_split_next(int j, int J, int J8, int wave) {
 QSDPA_HD int wave_split_last_owner(int J, int D) {
   const int J8 = wave_split_rr_end(J, D);
   return J8 < J ? (J - 1 - J8) % 4 : (J - 1) % kSplitWaves;
+}
+
+// Super-tiles: a segment of a sequence's T key tiles owns super-tiles of
+// 2^sh consecutive tiles, t_lo, t_lo + stride, ... (at most jmax of them).
+// Uniform splits (stride = S > 1) use 8-tile super-tiles where every split
+// still gets one (T / S >= 8), else 4, 2 or 1; stream-K segments (stride 1)
+// take single tiles.
+QSDPA_HD int super_tile_shift(int T, int stride) {
+  const int per = stride > 1 ? T / stride : 0;
+  return per >= 8 ? 3 : per >= 4 ? 2 : per >= 2 ? 1 : 0;
+}
+
+// Positions of the segment: whole super-tiles, the sequence's last one
+// possibly short.
+QSDPA_HD int super_tile_positions(int T, int t_lo, int stride, int jmax, int sh) {
+  const int TS = (T + (1 << sh) - 1) >> sh;
+  const int cnt = TS > t_lo ? (jmax < (TS - t_lo + stride - 1) / stride ? jmax : (TS - t_lo + stride - 1) / stride) : 0;
+  if (cnt <= 0) return 0;
+  const int rest = T - ((t_lo + (cnt - 1) * stride) << sh);
+  return ((cnt - 1) << sh) + (rest < (1 << sh) ? rest : (1 << sh));
+}
+
+// The tile of position j.
+QSDPA_HD int super_tile_tile(int j, int t_lo, int stride, int sh) {
+  return ((t_lo + (j >> sh) * stride) << sh) + (j & ((1 << sh) - 1));
 }
 
 }  // namespace qsdpa

@@ -219,3 +219,56 @@ int main() {{
     subprocess.run(["g++", "-std=c++17", "-O1", "-Wall", "-Werror", str(src), "-o", str(exe)], check=True)
     out = subprocess.run([str(exe)], capture_output=True, text=True)
     assert out.returncode == 0 and out.stdout.strip() == "ok", out.stdout
+
+
+def test_super_tiles_cover_every_tile_once(tmp_path):
+    """The decode kernel's key-tile layout (csrc/wave_split.h, compiled here
+    for the host): for every tile count T up to 600 and split count S up to
+    160, uniform splits (super-tiles of up to 8 tiles, split s owning super-
+    tiles s, s + S, ...) cover each tile of [0, T) exactly once, positions of
+    a split visit increasing tiles, and every split keeps work whenever
+    T >= S.  Stream-K segments (stride 1, at most jmax tiles from t_lo) take
+    tiles t_lo, t_lo + 1, ... one by one."""
+    header = HEADER.parent.parent / "mlx-qsdpa_amd" / "csrc" / "wave_split.h"
+    src = tmp_path / "super.cc"
+    src.write_text(f"""
+#include <cstdio>
+#include <vector>
+#include "{header}"
+int main() {{
+  for (int T = 0; T <= 600; ++T)
+    for (int S = 2; S <= 160; ++S) {{
+      const int sh = qsdpa::super_tile_shift(T, S);
+      std::vector<int> seen(T, 0);
+      for (int s = 0; s < S; ++s) {{
+        const int J = qsdpa::super_tile_positions(T, s, S, 0x7FFFFFFF, sh);
+        if (T >= S && J == 0) {{ std::printf("T=%d S=%d split %d idle\\n", T, S, s); return 1; }}
+        int prev = -1;
+        for (int j = 0; j < J; ++j) {{
+          const int t = qsdpa::super_tile_tile(j, s, S, sh);
+          if (t < 0 || t >= T || t <= prev) {{ std::printf("T=%d S=%d split %d position %d tile %d\\n", T, S, s, j, t); return 1; }}
+          prev = t;
+          seen[t]++;
+        }}
+      }}
+      for (int t = 0; t < T; ++t)
+        if (seen[t] != 1) {{ std::printf("T=%d S=%d tile %d seen %d times\\n", T, S, t, seen[t]); return 1; }}
+    }}
+  for (int T = 0; T <= 200; ++T)
+    for (int lo = 0; lo <= T; ++lo)
+      for (int jmax = 1; jmax <= 40; ++jmax) {{
+        const int sh = qsdpa::super_tile_shift(T, 1);
+        const int J = qsdpa::super_tile_positions(T, lo, 1, jmax, sh);
+        const int want = T - lo < jmax ? T - lo : jmax;
+        if (sh != 0 || J != want) {{ std::printf("stream-K T=%d lo=%d jmax=%d: J %d\\n", T, lo, jmax, J); return 1; }}
+        for (int j = 0; j < J; ++j)
+          if (qsdpa::super_tile_tile(j, lo, 1, sh) != lo + j) {{ std::printf("stream-K tile\\n"); return 1; }}
+      }}
+  std::printf("ok\\n");
+  return 0;
+}}
+""")
+    exe = tmp_path / "super"
+    subprocess.run(["g++", "-std=c++17", "-O1", "-Wall", "-Werror", str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True)
+    assert out.returncode == 0 and out.stdout.strip() == "ok", out.stdout
