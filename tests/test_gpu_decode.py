@@ -287,6 +287,43 @@ def test_multi_query_matches_oracle(device, case):
         assert_close(got, want, f"qL={qL} splits={splits}")
 
 
+@pytest.mark.parametrize("case", [
+    # (B, Hq, Hkv, N, D, bits, gs, dtype, qL, causal, kv_start)
+    (2, 32, 2, 300, 256, 4, 32, "f16", 2, True, None),        # 32 rows: 2 blocks
+    (1, 16, 1, 1000, 256, 8, 64, "bf16", 3, False, None),     # 48 rows: 3 blocks, 8-bit
+    (2, 8, 2, 777, 256, 4, 128, "f16", 5, True, (0, 300)),    # 20 rows: a part-filled block, kv_start
+    (1, 32, 1, 500, 256, 4, 64, "bf16", 1, False, None),      # q_len 1, 32 heads per kv head
+    (1, 16, 2, 40, 256, 4, 32, "f16", 4, True, None),         # 64 rows over two tiles of keys
+    (3, 64, 2, 129, 256, 8, 32, "f16", 1, False, (5, 128, 129)),  # one key / no key left
+], ids=["G16-q2-causal", "G16-q3-bf16-8b", "G4-q5-kvstart", "G32-q1-bf16", "G16-q4-N40", "G32-q1-kvstart"])
+def test_row_blocks_match_oracle(device, case):
+    """Two to four blocks of 16 query rows per kv head at D = 256 (the decode
+    kernel's row blocks: several query positions, or more than 16 query
+    heads per kv head), with causal masks and kv_start, against the oracle,
+    at several split counts; repeated calls are bitwise identical."""
+    B, Hq, Hkv, N, D, bits, gs, dtype, qL, causal, starts = case
+    rng = np.random.default_rng(71 + qL + Hq)
+    inp = make_inputs(rng, B, Hq, Hkv, N, D, bits, gs, dtype=dtype)
+    inp["q"] = affine.random_T(rng, (B, Hq, qL, D), dtype)
+    qi = np.arange(qL)[:, None] + (N - qL)
+    keep = np.ones((B, 1, qL, N), dtype=bool)
+    if causal:
+        keep &= (qi >= np.arange(N)[None, :])[None, None]
+    kw = {"causal": True} if causal else {}
+    if starts is not None:
+        st = np.array(starts)
+        keep &= (np.arange(N)[None, :] >= np.clip(st, 0, N)[:, None])[:, None, None, :]
+        kw["kv_start"] = torch.tensor(st, dtype=torch.int32, device=device)
+    want = oracle_out(inp, mask=keep)
+    want[~keep.any(axis=-1, keepdims=True).repeat(Hq, axis=1).repeat(D, axis=-1)] = 0.0
+    for splits in (0, 1, 3, 7):
+        got = _fused(inp, device, num_splits=splits, **kw)
+        assert got.shape == (B, Hq, qL, D)
+        assert_close(got, want, f"{case} splits={splits}")
+        again = _fused(inp, device, num_splits=splits, **kw)
+        assert np.array_equal(got, again), f"splits={splits}: repeated call differs"
+
+
 @pytest.mark.parametrize("qL", [6, 40], ids=["q6", "q40-rows"])
 def test_multi_query_kv_start_causal(device, qL):
     """qL > 1 with left padding and causal together (stream-K schedule when
