@@ -75,9 +75,7 @@ namespace {
 // 172 us.
 constexpr int kPWaves = 8;
 constexpr int kPThreads = kPWaves * 64;
-constexpr int kPTile = 64;                   // tokens per tile
 constexpr int kPGroupRows = kPWaves * 16;    // query rows per workgroup
-constexpr int kVPitch = kPTile * 2 + 32;     // bytes per V^T row (dim) in LDS
 constexpr int kMaxPrefillSplits = 64;
 constexpr float kVBound = 64000.0f;          // largest |V| staged in float16 unscaled
 // bfloat16 inputs: the largest max |V| for which P enters the P.V MFMAs as
@@ -86,22 +84,45 @@ constexpr float kVBound = 64000.0f;          // largest |V| staged in float16 un
 // max|V| in the random tests), so one term keeps 2e-3 for |V| <= 8.
 constexpr float kPVSingle = 8.0f;
 
-// LDS rows are padded by 32 bytes.  Measured at the C5 chunk: with 16-byte
+// Tile geometry.  D = 128: 64-token tiles; D = 256: 32-token tiles, so that
+// a tile holds the same number of K / V values (and the four LDS buffers
+// still fit): the same MFMA, dequantization and LDS work per tile.
+//
+// LDS rows are padded.  Measured at the C5 chunk (D = 128): with 16-byte
 // padding (K 272 B, V^T 144 B per row) the 16-byte operand reads of the 16
 // rows of an MFMA block spend 1.8e7 bank-conflict cycles per call, with 32
 // bytes 2.0e6, and the kernel takes 121-123 us instead of 129-130; 48 and
-// 64 bytes conflict like 16.
+// 64 bytes conflict like 16.  D = 256 keeps K's row pitch modulo 256 bytes
+// (544 = 2 * 256 + 32) and pads V^T's 64-byte rows by 16 (80 B, 20 dwords:
+// the 16 rows of an operand read start on 16 distinct 4-dword bank groups),
+// which is what fits four buffers in the LDS.
 template <int D>
 struct PGeo {
+  static constexpr int Tile = D == 256 ? 32 : 64;  // tokens per tile
   static constexpr int KPitch = D * 2 + 32;        // bytes per K row (token) in LDS
-  static constexpr int KBytes = kPTile * KPitch;
-  static constexpr int VBytes = D * kVPitch;
+  static constexpr int VPitch = Tile * 2 + (D == 256 ? 16 : 32);  // bytes per V^T row (dim)
+  static constexpr int KBytes = Tile * KPitch;
+  static constexpr int VBytes = D * VPitch;
   static constexpr int BufBytes = KBytes + VBytes;
   static constexpr int NM = D / 32;                // QK k-steps
   static constexpr int NB = D / 16;                // PV dim blocks
+  static constexpr int NT = Tile / 16;             // S^T token blocks
+  static constexpr int NU = Tile / 32;             // P^T k-steps (32-token halves)
+  // QK accumulators per token block: with two token blocks, the k-steps
+  // alternate between two (summed after the last) so that four independent
+  // MFMA chains run, as with four token blocks.
+  static constexpr int KS = NT < 4 ? 2 : 1;
+  // The workgroup's threads split a tile: K token tid / KPT, dims
+  // [c D / KPT, (c + 1) D / KPT) with c = tid % KPT; V tokens 2 pr + e
+  // (pr = tid % Pairs, e = 0, 1), dims [cv D / VPT, (cv + 1) D / VPT) with
+  // cv = tid / Pairs.
+  static constexpr int KPT = kPThreads / Tile;
+  static constexpr int Pairs = Tile / 2;
+  static constexpr int VPT = kPThreads / Pairs;
+  static_assert(4 * BufBytes + 64 <= 160 * 1024, "four LDS buffers");
 };
 
-// Column of token t (0..63) of a tile in the V^T rows: within each 32-token
+// Column of token t (0..Tile-1) of a tile in the V^T rows: within each 32-token
 // half, the slot order of the S^T fragment (lane quad q holds tokens
 // 16 * (j >> 2) + 4 q + (j & 3), j = 0..7, as its k slots 8 q + j).
 __device__ __forceinline__ int vcol(int t) {
@@ -116,12 +137,6 @@ __device__ __forceinline__ int pair_dim(int i, int half) {
   if constexpr (Tag::kId == QSDPA_F16 && BITS == 4) return i + 4 * half;
   else return 2 * i + half;
 }
-
-// The workgroup's threads split a tile: K token tid / KPT, dims
-// [c D / KPT, (c + 1) D / KPT) with c = tid % KPT; V tokens 2 (tid % 32) + e
-// (e = 0, 1), dims [cv D / VPT, (cv + 1) D / VPT) with cv = tid / 32.
-constexpr int kKPT = kPThreads / kPTile;
-constexpr int kVPT = kPThreads / (kPTile / 2);
 
 // Loads at the thread's byte offset `voff` plus the uniform `soff` (the
 // buffer instruction's scalar offset, which the range check includes: words
@@ -149,9 +164,9 @@ __device__ __forceinline__ void load_words(rsrc_t rs, uint32_t voff, uint32_t so
 // them as soon as they arrive, and that mask waits for every load in flight.
 template <int D, int BITS, int GS>
 struct PRaw {
-  static constexpr int KW = D / kKPT * BITS / 32;
-  static constexpr int VW = D / kVPT * BITS / 32;
-  using KMeta = std::conditional_t<(D / kKPT > GS), uint32_t, uint16_t>;  // two groups: both half-words
+  static constexpr int KW = D / PGeo<D>::KPT * BITS / 32;
+  static constexpr int VW = D / PGeo<D>::VPT * BITS / 32;
+  using KMeta = std::conditional_t<(D / PGeo<D>::KPT > GS), uint32_t, uint16_t>;  // two groups: both half-words
   uint32_t k[KW];
   KMeta ks, kb;
   uint32_t v[2][VW];
@@ -167,9 +182,11 @@ template <typename Tag, int D, int BITS, int GS>
 struct Prefill {
   using PG = PGeo<D>;
   using Raw = PRaw<D, BITS, GS>;
+  static constexpr int kKPT = PG::KPT, kPairs = PG::Pairs;
+  static constexpr int kVPitch = PG::VPitch;
   static constexpr int kQD = D / kKPT;                    // K dims per thread
-  static constexpr int kKG = kQD > GS ? kQD / GS : 1;     // groups per K quarter (1 or 2)
-  static constexpr int kVD = D / kVPT;                    // V dims per thread and token
+  static constexpr int kKG = kQD > GS ? kQD / GS : 1;     // groups per K piece (1 or 2)
+  static constexpr int kVD = D / PG::VPT;                 // V dims per thread and token
   static_assert(kKG <= 2, "groups per K quarter");
   static_assert(kVD <= GS, "a V piece lies in one group");
 
@@ -191,7 +208,7 @@ struct Prefill {
     s.k_l = kt * s.k_sn + static_cast<uint32_t>(c * Raw::KW * 4);
     s.ks_l = kt * s.ks_sn + g0 * 2;
     s.kb_l = kt * s.kb_sn + g0 * 2;
-    const int pr = tid & 31, cv = tid >> 5;
+    const int pr = tid % kPairs, cv = tid / kPairs;
     const uint32_t gv = static_cast<uint32_t>(cv * kVD / GS);
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
@@ -268,7 +285,7 @@ struct Prefill {
     }
     // V: tokens 2 pr, 2 pr + 1, dims [cv D/VPT, (cv + 1) D/VPT), transposed.
     {
-      const int pr = tid & 31, cv = tid >> 5;
+      const int pr = tid % kPairs, cv = tid / kPairs;
       uint8_t* vt = buf + PG::KBytes + vcol(2 * pr) * 2;
       if constexpr (Tag::kId == QSDPA_F16) {
         uint32_t a[2][4];
@@ -352,7 +369,8 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(MfmaParams p, i
   const int s0 = p.kv_start ? min(max(p.kv_start[b], 0), p.N) : 0;
   const int n_end = p.causal ? min(p.N, max(0, p.N - p.qL + (v_first + nrows - 1) / p.G + 1)) : p.N;
   const int len = max(n_end - s0, 0);
-  const int T_all = (len + kPTile - 1) / kPTile;
+  constexpr int kTile = PG::Tile, NT = PG::NT, NU = PG::NU, KS = PG::KS;
+  const int T_all = (len + kTile - 1) / kTile;
   // This split's tiles: [j_base, j_base + T) of the group's T_all.
   const int j_base = static_cast<int>(static_cast<int64_t>(split) * T_all / S);
   const int T = static_cast<int>(static_cast<int64_t>(split + 1) * T_all / S) - j_base;
@@ -438,20 +456,22 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(MfmaParams p, i
                   int tb0) __attribute__((always_inline)) {
     constexpr bool kTwo = decltype(two_c)::value;
     const int tb = s0 + tb0;
-    float mv[16];
+    float mv[4 * NT];
     if constexpr (MASK)  // keys tb + 16 t + 4 quad + i of the lane's mask row
-      mask_tile<16>(p, mrow, tb + 4 * quad, tb + kPTile <= p.N, [](int e) { return 16 * (e >> 2) + (e & 3); }, mv);
+      mask_tile<4 * NT>(p, mrow, tb + 4 * quad, tb + kTile <= p.N, [](int e) { return 16 * (e >> 2) + (e & 3); }, mv);
     // ---- S^T = K Q^T ----
     // The A operands of step m + 1 are read while the MFMAs of step m run
     // (scheduling fences keep that order: left to itself the compiler
     // reuses one register set and waits for each read).
-    f4 S4[4];
+    f4 S4[NT][KS];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) S4[t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-    u4 ka[2][4];
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int k = 0; k < KS; ++k) S4[t][k] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    u4 ka[2][NT];
     auto read_k = [&](u4* x, int m) {
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
+      for (int t = 0; t < NT; ++t)
         x[t] = *reinterpret_cast<const u4*>(cur + (16 * t + r) * PG::KPitch + (32 * m + 8 * quad) * 2);
     };
     read_k(ka[0], 0);
@@ -460,10 +480,10 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(MfmaParams p, i
       __builtin_amdgcn_sched_barrier(0);
       if (m + 1 < PG::NM) read_k(ka[(m + 1) & 1], m + 1);
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
+      for (int t = 0; t < NT; ++t) {
         const u4 x = ka[m & 1][t];
         const uint32_t a[4] = {x[0], x[1], x[2], x[3]};
-        S4[t] = mfma<Tag>(a, qt[m], S4[t]);
+        S4[t][m % KS] = mfma<Tag>(a, qt[m], S4[t][m % KS]);
       }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -476,30 +496,31 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(MfmaParams p, i
       P::load(Rn, src, nrow);
     }
     // ---- scores: lane (quad, r) holds keys tb + 16 t + 4 quad + i of row r ----
-    float sc[16];
+    constexpr int NE = 4 * NT;
+    float sc[NE];
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+    for (int t = 0; t < NT; ++t)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) sc[4 * t + i] = S4[t][i];
+      for (int i = 0; i < 4; ++i) sc[4 * t + i] = KS == 2 ? S4[t][0][i] + S4[t][KS - 1][i] : S4[t][0][i];
     if (!fold) {
 #pragma unroll
-      for (int e = 0; e < 16; ++e) sc[e] *= p.qscale;
+      for (int e = 0; e < NE; ++e) sc[e] *= p.qscale;
       if constexpr (MASK) {
 #pragma unroll
-        for (int e = 0; e < 16; ++e) sc[e] += mv[e];
+        for (int e = 0; e < NE; ++e) sc[e] += mv[e];
       }
     }
-    if (tb + kPTile > n_wave) {  // keys past a row's limit (causal, or the sequence's end)
+    if (tb + kTile > n_wave) {  // keys past a row's limit (causal, or the sequence's end)
       const int lim = n_lane - tb - 4 * quad;  // key tb + 4 quad + k is past the limit when k >= lim
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
+      for (int t = 0; t < NT; ++t)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
           if (16 * t + i >= lim) sc[4 * t + i] = -__builtin_huge_valf();
     }
     float tmax = sc[0];
 #pragma unroll
-    for (int e = 1; e < 16; ++e) tmax = fmaxf(tmax, sc[e]);
+    for (int e = 1; e < NE; ++e) tmax = fmaxf(tmax, sc[e]);
     tmax = max_over_rows(tmax) * ea;
     const bool grow = tmax > mrun + kRescale;
     if (__builtin_amdgcn_ballot_w64(grow)) {
@@ -511,18 +532,19 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(MfmaParams p, i
       for (int i = 0; i < PG::NB; ++i) acc[i] *= f;
     }
     const float nm = -mrun;
-    float pr[16];
+    float pr[NE];
 #pragma unroll
-    for (int e = 0; e < 16; ++e) pr[e] = fast_exp2(fmaf(sc[e], ea, nm));
-    float s4[4];
+    for (int e = 0; e < NE; ++e) pr[e] = fast_exp2(fmaf(sc[e], ea, nm));
+    float s4[NT];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) s4[t] = (pr[4 * t] + pr[4 * t + 1]) + (pr[4 * t + 2] + pr[4 * t + 3]);
-    lrun += (s4[0] + s4[1]) + (s4[2] + s4[3]);
+    for (int t = 0; t < NT; ++t) s4[t] = (pr[4 * t] + pr[4 * t + 1]) + (pr[4 * t + 2] + pr[4 * t + 3]);
+    if constexpr (NT == 4) lrun += (s4[0] + s4[1]) + (s4[2] + s4[3]);
+    else lrun += s4[0] + s4[1];
     // P^T of half u: k slots 2i, 2i + 1 = tokens tau(quad, 2i), tau(quad, 2i + 1):
     // blocks 2u (i = 0, 1) and 2u + 1 (i = 2, 3).
-    uint32_t pb[2][4], pl[2][4];
+    uint32_t pb[NU][4], pl[NU][4];
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
+    for (int u = 0; u < NU; ++u)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int e = 4 * (2 * u + (i >> 1)) + 2 * (i & 1);
@@ -533,11 +555,11 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(MfmaParams p, i
     // ---- out^T += V^T P^T (two terms: the hi terms of all dim blocks, then the lo terms) ----
     const uint8_t* vt = cur + PG::KBytes;
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
+    for (int u = 0; u < NU; ++u) {
       uint32_t a[PG::NB][4];
 #pragma unroll
       for (int db = 0; db < PG::NB; ++db) {
-        const u4 x = *reinterpret_cast<const u4*>(vt + (16 * db + r) * kVPitch + (32 * u + 8 * quad) * 2);
+        const u4 x = *reinterpret_cast<const u4*>(vt + (16 * db + r) * PG::VPitch + (32 * u + 8 * quad) * 2);
         a[db][0] = x[0]; a[db][1] = x[1]; a[db][2] = x[2]; a[db][3] = x[3];
         acc[db] = mfma<F16>(a[db], pb[u], acc[db]);
       }
@@ -563,11 +585,11 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(MfmaParams p, i
   // to two tiles. ----
   typename P::Raw R0, R1;
   auto buf = [&](int j) { return s_buf + (j & 3) * PG::BufBytes; };
-  const int oob = len + 2 * kPTile;  // rows past every descriptor: the loads read zero
-  auto row_of = [&](int j) { return j < T ? (j_base + j) * kPTile : oob; };
+  const int oob = len + 2 * kTile;  // rows past every descriptor: the loads read zero
+  auto row_of = [&](int j) { return j < T ? (j_base + j) * kTile : oob; };
   // Keys of tile j; past the split's tiles, the sequence end (every score
   // masked: an odd tile count's last pair computes one empty tile).
-  auto keys_of = [&](int j) { return j < T ? (j_base + j) * kPTile : len; };
+  auto keys_of = [&](int j) { return j < T ? (j_base + j) * kTile : len; };
   auto run = [&](auto two_c) __attribute__((always_inline)) {
     for (int j = 0; j < T; j += 2) {
       // tiles j, j + 1 in buf(j), buf(j + 1); R0 holds tile j + 2, R1 tile j + 3.
@@ -589,7 +611,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(MfmaParams p, i
       // range's first row again: no effect on the maximum).
       constexpr int kRows = 8;
       float bound = 0.0f;
-      const int t_lo = j_base * kPTile, t_hi = min((j_base + T) * kPTile, len);
+      const int t_lo = j_base * kTile, t_hi = min((j_base + T) * kTile, len);
       for (int t0 = t_lo + tid; t0 < t_hi; t0 += kRows * kPThreads) {
         uint16_t sv[kRows][NG], bv[kRows][NG];
 #pragma unroll
@@ -714,39 +736,55 @@ void launch_prefill_gs(const MfmaParams& p, int gs, int groups, hipStream_t stre
 
 bool mfma_supports(const qsdpa_decode_args* a);
 
+// Tokens per tile (PGeo<D>::Tile) on the host.
+static int prefill_tile(int D) { return D == 256 ? PGeo<256>::Tile : PGeo<128>::Tile; }
+
 // The prefill kernel takes q_len > 1 calls on the MFMA path's layouts whose
-// kv heads have at least one full 128-row group (D = 128); others stay on
-// the decode kernel's 16-row blocks (a half-empty group would leave half its
-// waves computing padding rows).  K / V rows are read in 16-byte pieces (8-byte V
-// pieces at 4-bit), so the packed views must be aligned to the pieces.
+// kv heads have at least one full 128-row group (D = 128 or 256); others stay
+// on the decode kernel's 16-row blocks (a half-empty group would leave half
+// its waves computing padding rows).  K / V rows are read in 16-byte pieces
+// (8-byte V pieces at 4-bit), so the packed views must be aligned to the
+// pieces.  A thread's K piece (16 dims) always lies in one quantization group.
 bool prefill_supports(const qsdpa_decode_args* a) {
-  // D = 256 would need more than the 512 registers of a wave (its
-  // accumulators and Q rows double): those calls keep the decode kernel.
-  if (a->q_len <= 1 || a->D != 128 || !mfma_supports(a)) return false;
+  if (a->q_len <= 1 || (a->D != 128 && a->D != 256) || !mfma_supports(a)) return false;
   const int64_t rows = static_cast<int64_t>(a->H_q / a->H_kv) * a->q_len;
   if (rows < kPGroupRows) return false;
+  // D = 256 only for calls with two or more row groups per kv head and at
+  // least 2^24 (query row, key) pairs; smaller ones are faster on the decode
+  // kernel, whose 16-row blocks each stream the kv head (measured, wall time
+  // per call, decode kernel against this one: C3's heads at q_len = 8 over
+  // 32K / 128K keys 34.0 / 110.4 against 43.2 / 114.4 us, q_len = 16 over 4K
+  // 18.4 against 32.4; at q_len = 16 over 128K 206 against 144, q_len = 32
+  // over 32K 103 against 80; C2's heads at q_len = 512 over 4K 30.8 against
+  // 40.4, q_len = 256 over 32K 73.6 against 59.8).
+  if (a->D == 256 && (rows < 2 * kPGroupRows ||
+                      static_cast<int64_t>(a->B) * a->H_q * a->q_len * a->N < (int64_t(1) << 24)))
+    return false;
   const int64_t groups = (rows + kPGroupRows - 1) / kPGroupRows;
   if (groups * a->H_kv * a->B * kMaxPrefillSplits >= (int64_t(1) << 31)) return false;
   const int kq_bytes = a->D / 4 * a->bits / 8, vp_bytes = a->D / 8 * a->bits / 8;
   if (!aligned_view(a->k_packed, std::min(kq_bytes, 16), 4)) return false;
   if (!aligned_view(a->v_packed, std::min(vp_bytes, 16), 4)) return false;
-  if (a->D / 4 > a->group_size && !aligned_view(a->k_scales, 4, 2)) return false;
-  if (a->D / 4 > a->group_size && a->k_biases.ptr && !aligned_view(a->k_biases, 4, 2)) return false;
+  static_assert(128 / PGeo<128>::KPT == 16 && 256 / PGeo<256>::KPT == 16, "K pieces of 16 dims");
   // Row byte offsets up to 4 tiles past the last key stay within 32 bits.
   const int64_t max_sn = std::max({a->k_packed.stride_n * 4, a->v_packed.stride_n * 4, a->k_scales.stride_n * 2,
                                    a->v_scales.stride_n * 2, a->k_biases.stride_n * 2, a->v_biases.stride_n * 2});
-  if (max_sn < 0 || max_sn * (static_cast<int64_t>(a->N) + 4 * kPTile) >= (int64_t(1) << 31)) return false;
+  if (max_sn < 0 || max_sn * (static_cast<int64_t>(a->N) + 4 * prefill_tile(a->D)) >= (int64_t(1) << 31))
+    return false;
   return true;
 }
 
 // Key splits of the prefill kernel: enough workgroups for every CU, each
 // split at least 4 tiles (an explicit num_splits > 0 is kept, up to the
 // same bounds).  At the C5 chunk (256 row groups) one split; with
-// q_len = 128 (64 groups) 4 splits: 38 against 126 us in one.
+// q_len = 128 (64 groups) 4 splits: 38 against 126 us in one.  (At D = 256,
+// 8 tiles -- the same 256 keys -- made C3's heads at q_len = 16, N = 4096
+// 25.9 instead of 21.3 us.)
 int prefill_num_splits(const qsdpa_decode_args* a, int cus) {
   const int64_t rows = static_cast<int64_t>(a->H_q / a->H_kv) * a->q_len;
   const int64_t grid = (rows + kPGroupRows - 1) / kPGroupRows * a->H_kv * a->B;
-  const int64_t tiles = (static_cast<int64_t>(a->N) + kPTile - 1) / kPTile;
+  const int tile = prefill_tile(a->D);
+  const int64_t tiles = (static_cast<int64_t>(a->N) + tile - 1) / tile;
   int64_t s = a->num_splits > 0 ? a->num_splits : (cus + grid - 1) / grid;
   s = std::min<int64_t>(s, std::max<int64_t>(1, tiles / 4));
   s = std::min<int64_t>(s, kMaxPrefillSplits);
@@ -760,8 +798,13 @@ int launch_prefill_mfma(const qsdpa_decode_args* a, int splits, float* part_acc,
   const bool f16 = a->dtype == QSDPA_F16;
   auto bits = [&](auto tag) {
     using Tag = decltype(tag);
-    if (a->bits == 4) launch_prefill_gs<Tag, 128, 4>(p, a->group_size, groups, stream, a);
-    else launch_prefill_gs<Tag, 128, 8>(p, a->group_size, groups, stream, a);
+    if (a->D == 256) {
+      if (a->bits == 4) launch_prefill_gs<Tag, 256, 4>(p, a->group_size, groups, stream, a);
+      else launch_prefill_gs<Tag, 256, 8>(p, a->group_size, groups, stream, a);
+    } else {
+      if (a->bits == 4) launch_prefill_gs<Tag, 128, 4>(p, a->group_size, groups, stream, a);
+      else launch_prefill_gs<Tag, 128, 8>(p, a->group_size, groups, stream, a);
+    }
   };
   if (f16) bits(F16{});
   else bits(BF16{});

@@ -1,5 +1,6 @@
-"""The prefill kernel (many query positions per kv head, D = 128) against the
-float64 oracle (tests/torch_oracle.py, pinned to the numpy oracle by
+"""The prefill kernel (many query positions per kv head, D = 128 with 64-key
+tiles, D = 256 with 32-key tiles) against the float64 oracle
+(tests/torch_oracle.py, pinned to the numpy oracle by
 tests/test_gpu_parity_full.py).
 
 Shapes are chosen so the library routes them to the prefill kernel: at
@@ -216,3 +217,129 @@ def test_prefill_repeatable(device):
                            group_size=128, causal=True) for _ in range(3)]
     torch.cuda.synchronize()
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+
+
+# D = 256: 32-key tiles, the same 128-row groups.  The library sends a
+# D = 256 call here when its kv heads have two or more row groups (H_q /
+# H_kv x q_len >= 256) and it has at least 2^24 (query row, key) pairs
+# (B x H_q x q_len x N); the shapes below meet both.  (B, Hq, Hkv, N, L,
+# bits, gs, dtype, causal, symmetric)
+D256_PAIRS = 1 << 24
+D256_CASES = [
+    (1, 32, 2, 33000, 16, 4, 32, torch.float16, True, False),     # C3's heads, 2 groups: key splits
+    (2, 16, 4, 8300, 64, 8, 64, torch.bfloat16, True, False),     # partial last tile
+    (1, 2, 2, 16411, 512, 8, 64, torch.bfloat16, False, False),   # C2's heads (G = 1), full attention
+    (2, 8, 2, 2700, 400, 4, 128, torch.float16, True, True),      # 1600 rows: partial last group
+    (4, 16, 4, 2100, 128, 4, 64, torch.bfloat16, True, False),
+    (1, 32, 8, 8200, 64, 8, 32, torch.float16, False, False),
+]
+
+
+def _d256_routed(B, Hq, Hkv, N, L):
+    return Hq // Hkv * L >= 256 and B * Hq * L * N >= D256_PAIRS
+
+
+@pytest.mark.parametrize("case", D256_CASES, ids=lambda c: "B{}_H{}x{}_N{}_L{}_b{}_g{}_{}_{}{}".format(
+    *c[:7], str(c[7]).split(".")[-1], "causal" if c[8] else "full", "_sym" if c[9] else ""))
+def test_prefill_d256_matches_oracle(device, case):
+    B, Hq, Hkv, N, L, bits, gs, dtype, causal, sym = case
+    assert _d256_routed(B, Hq, Hkv, N, L)
+    print(f"prefill D=256 case {case}", flush=True)
+    q, kq, vq = _inputs(B, Hq, Hkv, N, L, bits, gs, dtype, seed=N + L + 256, symmetric=sym, D=256)
+    _check(q, kq, vq, bits, gs, f"D=256 case {case}", causal=causal)
+
+
+@pytest.mark.parametrize("keys", [1, 31, 32, 33, 65, 95])
+def test_prefill_d256_short_key_ranges(device, keys):
+    """One to three 32-key tiles at D = 256 (the pipeline's loads and stages
+    reach past the last tile): a long cache whose kv_start leaves `keys`
+    keys, with full attention and causal (where q_len > keys leaves the
+    first positions without keys: rows of zeros)."""
+    B, Hq, Hkv, N, L, bits, gs = 1, 16, 2, 33000, 32, 4, 64
+    assert _d256_routed(B, Hq, Hkv, N, L)
+    ks = torch.tensor([N - keys], dtype=torch.int32, device=device)
+    for dtype in (torch.bfloat16, torch.float16):
+        q, kq, vq = _inputs(B, Hq, Hkv, N, L, bits, gs, dtype, seed=keys + 256, D=256)
+        print(f"prefill D=256 short keys={keys} {dtype}", flush=True)
+        _check(q, kq, vq, bits, gs, f"D=256 short keys={keys} {dtype}", kv_start=ks)
+        _check(q, kq, vq, bits, gs, f"D=256 short keys={keys} {dtype} causal", kv_start=ks, causal=True)
+
+
+def test_prefill_d256_kv_start_and_masks(device):
+    B, Hq, Hkv, N, L, bits, gs = 2, 16, 2, 16500, 32, 8, 32
+    assert _d256_routed(B, Hq, Hkv, N, L)
+    for dtype in (torch.float16, torch.bfloat16):
+        q, kq, vq = _inputs(B, Hq, Hkv, N, L, bits, gs, dtype, seed=13, D=256)
+        ks = torch.tensor([19, 9000], dtype=torch.int32, device=device)  # starts inside a tile
+        print(f"prefill D=256 kv_start {dtype}", flush=True)
+        _check(q, kq, vq, bits, gs, f"D=256 kv_start {dtype}", kv_start=ks, causal=True)
+        g = torch.Generator(device="cpu").manual_seed(14)
+        keep = torch.rand(B, 1, L, N, generator=g) < 0.8
+        keep[..., -1] = True
+        print(f"prefill D=256 bool mask {dtype}", flush=True)
+        _check(q, kq, vq, bits, gs, f"D=256 bool mask {dtype}", mask=keep.to(device), causal=True)
+        add = (torch.randn(1, Hq, L, N, generator=g) * 3).to(dtype).to(device)
+        print(f"prefill D=256 additive mask {dtype}", flush=True)
+        _check(q, kq, vq, bits, gs, f"D=256 additive mask {dtype}", mask=add)
+
+
+@pytest.mark.parametrize("vmul,omul,tol", [(1.0, 8.0, "parity"), (2.0e4, 40.0, "scaled")],
+                         ids=["outliers", "beyond_f16"])
+def test_prefill_d256_bf16_large_values(device, vmul, omul, tol):
+    """bfloat16 V past max |V| = 8 (P as two float16 terms) and past 64000
+    (V staged at 2^-k) at D = 256; the bars as in the D = 128 test."""
+    B, Hq, Hkv, N, L = 2, 16, 2, 16500, 32
+    assert _d256_routed(B, Hq, Hkv, N, L)
+    g = torch.Generator(device="cpu").manual_seed(23)
+    q = torch.randn(B, Hq, L, 256, generator=g).bfloat16().to(device)
+    kw = torch.randn(B, Hkv, N, 256, generator=g)
+    vw = torch.randn(B, Hkv, N, 256, generator=g) * vmul
+    vw[..., :4] *= omul
+    kq = kernels.quantize(kw.bfloat16().to(device), 64, 8)
+    vq = kernels.quantize(vw.bfloat16().to(device), 64, 8)
+    print(f"prefill D=256 bf16 large V {vmul} {omul}", flush=True)
+    if tol == "parity":
+        _check(q, kq, vq, 8, 64, "D=256 large V", causal=True)
+        return
+    out = kernels.decode(q, kq[0], vq[0], kq[1], vq[1], kq[2], vq[2], scale=256 ** -0.5, bits=8, group_size=64,
+                         causal=True)
+    keep = torch.arange(N, device=device)[None, :] <= (N - L) + torch.arange(L, device=device)[:, None]
+    want = to.quantized_sdpa(q, kq, vq, bits=8, group_size=64, scale=256 ** -0.5, mask=keep[None, None])
+    vmax = float(kernels.dequantize(vq[0], vq[1], vq[2], 64, 8).float().abs().max())
+    err = (out.double() - want).abs()
+    bound = 2.0 ** -20 * vmax + RTOL * want.abs()
+    assert bool(torch.isfinite(out).all())
+    assert bool((err <= bound).all()), f"D=256 large V: max err {float(err.max()):.4g} (max |V| {vmax:.3g})"
+
+
+def test_prefill_d256_bf16_huge_k_scales(device):
+    """K groups with scales of 2^101 and more at D = 256 (the float32
+    dequantization path for the waves that hold them)."""
+    B, Hq, Hkv, N, L, bits, gs = 1, 16, 2, 33000, 32, 8, 64
+    assert _d256_routed(B, Hq, Hkv, N, L)
+    q, kq, vq = _inputs(B, Hq, Hkv, N, L, bits, gs, torch.bfloat16, seed=33, D=256)
+    q = (q.float() * 2.0 ** -108).bfloat16()
+    huge = torch.zeros(N, dtype=torch.bool)
+    huge[32:64] = True
+    huge[-64:-32] = True
+    huge[::7] = True
+    g = torch.Generator(device="cpu").manual_seed(34)
+    ks, kb = kq[1].clone(), kq[2].clone()
+    shape = (B, Hkv, int(huge.sum()), ks.shape[-1])
+    s = (2.0 ** 101 * (1.0 + torch.rand(shape, generator=g))).bfloat16().to(device)
+    ks[:, :, huge.to(device)] = s
+    kb[:, :, huge.to(device)] = (-(2 ** (bits - 1)) * s.float()).bfloat16()
+    kq = (kq[0], ks, kb)
+    print("prefill D=256 huge K scales", flush=True)
+    _check(q, kq, vq, bits, gs, "D=256 huge K scales", causal=True)
+
+
+def test_prefill_d256_repeatable(device):
+    """Repeated D = 256 calls (one pass and key splits) give bit-identical outputs."""
+    for (B, Hq, Hkv, N, L) in [(4, 16, 4, 2100, 128), (1, 32, 2, 33000, 16)]:
+        assert _d256_routed(B, Hq, Hkv, N, L)
+        q, kq, vq = _inputs(B, Hq, Hkv, N, L, 4, 32, torch.float16, seed=6, D=256)
+        outs = [kernels.decode(q, kq[0], vq[0], kq[1], vq[1], kq[2], vq[2], scale=256 ** -0.5, bits=4,
+                               group_size=32, causal=True) for _ in range(3)]
+        torch.cuda.synchronize()
+        assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
