@@ -120,3 +120,46 @@ def test_nan_past_the_end_decode(device, case):
 ], ids=["prefill-G4-q64-bf16", "prefill-G4-q40"])
 def test_nan_past_the_end_prefill(device, case, qL):
     _run(case, device, qL, True)
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+def test_nan_past_the_end_prefill_d256(device, dt):
+    """The D = 256 prefill kernel (32-key tiles; the call meets its routing
+    threshold: 256 rows per kv head, 2^24 row-key pairs), N = 32785 (17 keys
+    into the last tile), rows past N NaN / all-ones, with and without
+    kv_start; checked against the float64 torch oracle on the unpadded data
+    (the numpy oracle takes about 15 s at this size)."""
+    import torch_oracle as to
+    from mlx_qsdpa_amd import kernels
+
+    B, Hq, Hkv, N, D, bits, gs, qL = 1, 16, 2, 32785, 256, 4, 32, 32
+    assert Hq // Hkv * qL >= 256 and B * Hq * qL * N >= 1 << 24
+    T = torch_dtype(dt)
+    g = torch.Generator(device="cpu").manual_seed(41)
+    q = torch.randn(B, Hq, qL, D, generator=g).to(T).to(device)
+    kq = kernels.quantize(torch.randn(B, Hkv, N, D, generator=g).to(T).to(device), gs, bits)
+    vq = kernels.quantize(torch.randn(B, Hkv, N, D, generator=g).to(T).to(device), gs, bits)
+
+    def padded(x):
+        shape = (B, Hkv, N + 200, x.shape[-1])
+        if x.is_floating_point():
+            buf = torch.full(shape, float("nan"), dtype=x.dtype, device=device)
+            buf[:, :, :N] = x
+            return buf[:, :, :N]
+        buf = torch.full(shape, -1, dtype=torch.int32, device=device)  # all-ones codes
+        buf[:, :, :N] = x.view(torch.int32)
+        return buf.view(x.dtype)[:, :, :N]
+
+    dk, dv = [padded(x) for x in kq], [padded(x) for x in vq]
+    for kv_start in (None, torch.tensor([45], dtype=torch.int32, device=device)):
+        got = mq.quantized_sdpa(q, dk[0], dv[0], dk[1], dv[1], dk[2], dv[2], bits=bits, group_size=gs,
+                                mask="causal", kv_start=kv_start)
+        keep = torch.arange(N, device=device)[None, :] <= (N - qL) + torch.arange(qL, device=device)[:, None]
+        if kv_start is not None:
+            keep = keep & (torch.arange(N, device=device) >= int(kv_start[0]))[None, :]
+        want = to.quantized_sdpa(q, kq, vq, bits=bits, group_size=gs, scale=D ** -0.5, mask=keep[None, None])
+        torch.cuda.synchronize()
+        ctx = f"D=256 prefill {dt} kv_start={kv_start is not None}"
+        assert bool(torch.isfinite(got).all()), f"{ctx}: non-finite output (a row past N was read)"
+        err = (got.double() - want).abs()
+        assert bool((err <= ATOL + RTOL * want.abs()).all()), f"{ctx}: max err {float(err.max()):.3e}"
