@@ -93,7 +93,8 @@ def test_prefill_matches_oracle(device, case):
 SPLIT_CASES = [  # small grids: the planner gives each row group several key splits
     (1, 32, 8, 4000, 256, 4, 64, torch.float16, True, False),     # 64 groups: 4 splits
     (1, 16, 4, 3000, 128, 8, 128, torch.bfloat16, True, False),   # 16 groups: 11 splits
-    (2, 16, 4, 2500, 128, 4, 32, torch.float16, False, True),     # 32 groups, full attention
+    (2, 16, 4, 2500, 128, 4, 32, torch.float16, False, True),     # 32 groups, full attention: 8 splits
+    (2, 16, 4, 2500, 256, 8, 64, torch.bfloat16, True, False),    # 64 groups: 4 splits, bfloat16
 ]
 
 
@@ -146,9 +147,10 @@ def test_prefill_kv_start_and_masks(device):
     # (shape B, H_q, H_kv, N, L; V scale; scale of 4 outlier channels; tolerance)
     ((2, 32, 8, 900, 256), 1.0, 8.0, "parity"),          # max |V| ~ 40: P in two float16 terms
     ((2, 32, 8, 900, 256), 2.0e4, 40.0, "scaled"),       # max |V| ~ 3e6: V staged at 2^-6
-    ((1, 16, 4, 3000, 128), 2.0e4, 40.0, "scaled"),      # the same through key splits
+    ((1, 16, 4, 3000, 128), 2.0e4, 40.0, "scaled"),      # the same through 11 key splits (merge kernel)
+    ((2, 32, 8, 2500, 128), 2.0e4, 40.0, "scaled"),      # 4 key splits (merge_rows_kernel)
     ((2, 32, 8, 900, 256), 2.0e36, 4.0, "scaled"),       # max |V| ~ 4e37: V staged at 2^-119
-], ids=["outliers", "beyond_f16", "beyond_f16_splits", "near_bf16_max"])
+], ids=["outliers", "beyond_f16", "beyond_f16_splits", "beyond_f16_4_splits", "near_bf16_max"])
 def test_prefill_bf16_large_values(device, case):
     """bfloat16 V with large values.  Past max |V| = 8 the kernel feeds P to
     the P.V MFMAs as two float16 terms (22 significant bits), and past
