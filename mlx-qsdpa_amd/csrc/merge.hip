@@ -133,38 +133,52 @@ __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ pa
 }
 
 // Many rows with few splits each (prefill partials): one thread per (row,
-// 4 dims), the splits in order with the same online rescaling as above,
-// four splits' loads in flight at a time.  Rows numbered as above, no
-// stream-K schedule.
-template <typename Tag, bool HALF>
+// W dims), the splits in order with the same online rescaling as above,
+// four splits' loads in flight at a time, one 16-byte load per split: W = 8
+// for float16 rows (HALF), 4 for float32 rows.  (8 dims of float32 rows --
+// two loads per split, half the threads -- took C5's prefill at q_len = 256
+// 74.6-75.5 against 71.1-71.3 us per call; float16 rows with 8 dims took
+// C3's heads at q_len = 512 128.6 against 130.5-130.9.)  Rows numbered as
+// above, no stream-K schedule.  ALIGNED: every output row piece is
+// 2W-byte aligned (one store; otherwise 16-bit stores).
+template <typename Tag, bool HALF, bool ALIGNED>
 __global__ __launch_bounds__(256) void merge_rows_kernel(const float* __restrict__ part_acc,
                                                          const float* __restrict__ part_ml, int D, int splits,
                                                          int Hq, int qL, int64_t rows, uint16_t* __restrict__ out,
                                                          int64_t o_sb, int64_t o_sh, int64_t o_sq) {
-  const int quads = D / 4;
+  constexpr int W = HALF ? 8 : 4;
+  const int pieces = D / W;
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (idx >= rows * quads) return;
-  const int64_t bh = idx / quads;
-  const int d = static_cast<int>(idx % quads) * 4;
+  if (idx >= rows * pieces) return;
+  const int64_t bh = idx / pieces;
+  const int d = static_cast<int>(idx % pieces) * W;
   const int64_t first = bh * splits;
   const float2* ml = reinterpret_cast<const float2*>(part_ml) + first;
   const float* pa = part_acc + first * D + d;
   const uint16_t* ph = reinterpret_cast<const uint16_t*>(part_acc) + first * D + d;
   float m = kNegBig, l = 0.0f;
-  float4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  float acc[W];
+#pragma unroll
+  for (int e = 0; e < W; ++e) acc[e] = 0.0f;
   for (int s0 = 0; s0 < splits; s0 += kPer) {
-    float4 x[kPer];
+    float x[kPer][W];
     float2 w[kPer];
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
       const int s = s0 + k;
       const bool ok = s < splits;
       if constexpr (HALF) {
-        const uint2 hv = ok ? *reinterpret_cast<const uint2*>(ph + static_cast<int64_t>(s) * D) : uint2{0u, 0u};
-        x[k] = float4{f16_bits_to_f32(static_cast<uint16_t>(hv.x)), f16_bits_to_f32(static_cast<uint16_t>(hv.x >> 16)),
-                      f16_bits_to_f32(static_cast<uint16_t>(hv.y)), f16_bits_to_f32(static_cast<uint16_t>(hv.y >> 16))};
+        const uint4 hv = ok ? *reinterpret_cast<const uint4*>(ph + static_cast<int64_t>(s) * D) : uint4{0u, 0u, 0u, 0u};
+        const uint32_t u[4] = {hv.x, hv.y, hv.z, hv.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          x[k][2 * e] = f16_bits_to_f32(static_cast<uint16_t>(u[e]));
+          x[k][2 * e + 1] = f16_bits_to_f32(static_cast<uint16_t>(u[e] >> 16));
+        }
       } else {
-        x[k] = ok ? *reinterpret_cast<const float4*>(pa + static_cast<int64_t>(s) * D) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+        const float4 a0 = ok ? *reinterpret_cast<const float4*>(pa + static_cast<int64_t>(s) * D)
+                             : float4{0.0f, 0.0f, 0.0f, 0.0f};
+        x[k][0] = a0.x; x[k][1] = a0.y; x[k][2] = a0.z; x[k][3] = a0.w;
       }
       w[k] = ok ? ml[s] : float2{kNegBig, 0.0f};
     }
@@ -173,14 +187,15 @@ __global__ __launch_bounds__(256) void merge_rows_kernel(const float* __restrict
     for (int k = 0; k < kPer; ++k) mr = fmaxf(mr, w[k].x);
     const float f = fast_exp2(m - mr);
     l *= f;
-    acc.x *= f; acc.y *= f; acc.z *= f; acc.w *= f;
+#pragma unroll
+    for (int e = 0; e < W; ++e) acc[e] *= f;
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
-      const float e = fast_exp2(w[k].x - mr);
-      l = fmaf(w[k].y, e, l);
-      const float ex = HALF ? w[k].y * e : e;
-      acc.x = fmaf(x[k].x, ex, acc.x); acc.y = fmaf(x[k].y, ex, acc.y);
-      acc.z = fmaf(x[k].z, ex, acc.z); acc.w = fmaf(x[k].w, ex, acc.w);
+      const float ek = fast_exp2(w[k].x - mr);
+      l = fmaf(w[k].y, ek, l);
+      const float ex = HALF ? w[k].y * ek : ek;
+#pragma unroll
+      for (int e = 0; e < W; ++e) acc[e] = fmaf(x[k][e], ex, acc[e]);
     }
     m = mr;
   }
@@ -189,10 +204,35 @@ __global__ __launch_bounds__(256) void merge_rows_kernel(const float* __restrict
   const int64_t b = bh / rows_b;
   const int h = static_cast<int>((bh % rows_b) / qL), i = static_cast<int>(bh % qL);
   uint16_t* dst = out + b * o_sb + static_cast<int64_t>(h) * o_sh + static_cast<int64_t>(i) * o_sq + d;
-  dst[0] = from_f32<Tag>(acc.x * inv);
-  dst[1] = from_f32<Tag>(acc.y * inv);
-  dst[2] = from_f32<Tag>(acc.z * inv);
-  dst[3] = from_f32<Tag>(acc.w * inv);
+  uint32_t o[W / 2];
+#pragma unroll
+  for (int e = 0; e < W / 2; ++e)
+    o[e] = from_f32<Tag>(acc[2 * e] * inv) | (static_cast<uint32_t>(from_f32<Tag>(acc[2 * e + 1] * inv)) << 16);
+  if constexpr (ALIGNED && W == 8) {
+    *reinterpret_cast<uint4*>(dst) = uint4{o[0], o[1], o[2], o[3]};
+  } else if constexpr (ALIGNED) {
+    *reinterpret_cast<uint2*>(dst) = uint2{o[0], o[1]};
+  } else {
+#pragma unroll
+    for (int e = 0; e < W / 2; ++e) {
+      dst[2 * e] = static_cast<uint16_t>(o[e]);
+      dst[2 * e + 1] = static_cast<uint16_t>(o[e] >> 16);
+    }
+  }
+}
+
+template <typename Tag, bool HALF>
+void launch_merge_rows(dim3 g, const float* part_acc, const float* part_ml, const qsdpa_decode_args* a, int splits,
+                       int qL, int64_t rows, uint16_t* out, int64_t o_sq, hipStream_t stream) {
+  // Aligned pieces (W = 8 or 4 values): the base and every stride a multiple of W elements.
+  constexpr int W = HALF ? 8 : 4;
+  const bool al = aligned(out, 2 * W) && a->out.stride_b % W == 0 && a->out.stride_h % W == 0 && o_sq % W == 0;
+  if (al)
+    merge_rows_kernel<Tag, HALF, true><<<g, dim3(256), 0, stream>>>(part_acc, part_ml, a->D, splits, a->H_q, qL, rows,
+                                                                     out, a->out.stride_b, a->out.stride_h, o_sq);
+  else
+    merge_rows_kernel<Tag, HALF, false><<<g, dim3(256), 0, stream>>>(part_acc, part_ml, a->D, splits, a->H_q, qL, rows,
+                                                                      out, a->out.stride_b, a->out.stride_h, o_sq);
 }
 
 }  // namespace
@@ -206,17 +246,14 @@ int launch_merge(const qsdpa_decode_args* a, int num_splits, const float* part_a
   const int64_t o_sq = qL > 1 ? a->out.stride_n : 0;
   const int64_t rows = static_cast<int64_t>(a->B) * a->H_q * qL;
   if (!sched && num_splits <= 16 && rows >= 2048) {
-    const int64_t threads = rows * (a->D / 4);
+    const int64_t threads = rows * (a->D / (a->dtype == QSDPA_F16 && half_parts ? 8 : 4));
     const dim3 g(static_cast<unsigned>((threads + 255) / 256));
     if (a->dtype == QSDPA_F16 && half_parts)
-      merge_rows_kernel<F16, true><<<g, dim3(256), 0, stream>>>(part_acc, part_ml, a->D, num_splits, a->H_q, qL, rows,
-                                                                out, a->out.stride_b, a->out.stride_h, o_sq);
+      launch_merge_rows<F16, true>(g, part_acc, part_ml, a, num_splits, qL, rows, out, o_sq, stream);
     else if (a->dtype == QSDPA_F16)
-      merge_rows_kernel<F16, false><<<g, dim3(256), 0, stream>>>(part_acc, part_ml, a->D, num_splits, a->H_q, qL, rows,
-                                                                 out, a->out.stride_b, a->out.stride_h, o_sq);
+      launch_merge_rows<F16, false>(g, part_acc, part_ml, a, num_splits, qL, rows, out, o_sq, stream);
     else
-      merge_rows_kernel<BF16, false><<<g, dim3(256), 0, stream>>>(part_acc, part_ml, a->D, num_splits, a->H_q, qL,
-                                                                  rows, out, a->out.stride_b, a->out.stride_h, o_sq);
+      launch_merge_rows<BF16, false>(g, part_acc, part_ml, a, num_splits, qL, rows, out, o_sq, stream);
     return check_launch("merge_rows");
   }
   const dim3 grid(a->B * a->H_q * qL, a->D / 32);

@@ -345,3 +345,24 @@ def test_prefill_d256_repeatable(device):
                                group_size=32, causal=True) for _ in range(3)]
         torch.cuda.synchronize()
         assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_prefill_split_merge_unaligned_out(device, dtype):
+    """Key splits merged by the row merge into an output whose rows are not
+    aligned (a view one element into wider rows: 16-bit stores) give the
+    same bits as into a contiguous output (one store per 8 values of
+    float16 partial rows, per 4 of float32 ones)."""
+    B, Hq, Hkv, N, L, bits, gs = 1, 32, 8, 4000, 256, 4, 64   # 4 key splits, 8192 rows
+    q, kq, vq = _inputs(B, Hq, Hkv, N, L, bits, gs, dtype, seed=77)
+    args = dict(scale=128 ** -0.5, bits=bits, group_size=gs, causal=True)
+    splits, _ = kernels.decode_plan(q, kq[0], vq[0], kq[1], vq[1], kq[2], vq[2], scale=128 ** -0.5, bits=bits,
+                                    group_size=gs)
+    assert 1 < splits <= 16
+    ref = kernels.decode(q, kq[0], vq[0], kq[1], vq[1], kq[2], vq[2], **args)
+    wide = torch.zeros(B, Hq, L, 128 + 2, dtype=q.dtype, device=device)
+    out = wide[..., 1:129]
+    kernels.decode(q, kq[0], vq[0], kq[1], vq[1], kq[2], vq[2], out=out, **args)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    assert bool((wide[..., 0] == 0).all()) and bool((wide[..., 129] == 0).all())
