@@ -6,13 +6,16 @@
 // decode kernel (decode_mfma.hip) takes such calls in blocks of 16 query rows,
 // each of which loads and dequantizes the kv head's whole K / V again.  Here
 // one workgroup takes 128 rows of a kv head -- 8 waves x 16 rows -- and every
-// 64-token K / V tile is loaded once per workgroup, dequantized once into
-// LDS, and read from LDS by all eight waves.  Per tile j, in each wave:
+// K / V tile (64 tokens at D = 128, 32 at D = 256: the same number of
+// values) is loaded once per workgroup, dequantized once into LDS, and read
+// from LDS by all eight waves.  Per tile j, in each wave (described for
+// D = 128; PGeo gives the D = 256 shapes):
 //
 //   QK         S^T = K Q^T (A = K rows from LDS buffer j % 4, B = Q^T in
 //              registers): 4 token blocks x D/32 steps of v_mfma_f32_16x16x32
 //              in the input type T, steps outer so that consecutive MFMAs
-//              feed four independent accumulators;
+//              feed four independent accumulators (D = 256: 2 token blocks,
+//              each with two accumulators for alternate steps);
 //   dequant    every thread turns its piece of tile j + 2 (raw codes, scales
 //              and biases loaded two tiles ahead into one of two register
 //              sets) into values in LDS buffer (j + 2) % 4 -- K row-major
@@ -35,7 +38,8 @@
 //              tile maximum over a row's four lanes by row swaps (VALU)
 //              rather than LDS permutes;
 //   PV         out^T += V^T P^T in float16 (A = V^T rows from LDS, B = P^T);
-//   barrier    one per pair of tiles (four buffers, 155,648 B of LDS): a
+//   barrier    one per pair of tiles (four buffers, 155,648 B of LDS at
+//              D = 128, 151,552 B at D = 256): a
 //              buffer is rewritten two tiles after its last reads, and read
 //              two tiles after its writes, so one barrier after every odd
 //              tile orders both, and the waves drift by up to two tiles
