@@ -394,10 +394,7 @@ int launch_requant(const qsdpa_requant_args* const* jobs, int count, hipStream_t
   }
   const dim3 grid(static_cast<unsigned>((lanes + 255) / 256), static_cast<unsigned>(a0->B * a0->H * ng),
                   static_cast<unsigned>(count));
-#ifndef QSDPA_RQ_LDS
-#define QSDPA_RQ_LDS 0
-#endif
-  auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, dim3(256), QSDPA_RQ_LDS, stream, j); };
+  auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, dim3(256), 0, stream, j); };
   const bool f16 = a0->dtype == QSDPA_F16;
   const int gs = a0->group_size, bits = a0->bits;
 #define QSDPA_REQUANT_CASE(T, B_, G_)                \
