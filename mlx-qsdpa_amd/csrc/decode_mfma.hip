@@ -202,7 +202,8 @@ __device__ __forceinline__ void decode_segment(const MfmaParams& p, float* s_acc
   const int gv = (r * G::NB) / GS;      // group of the lane's V dims
   const int vword = G::NG >= 2 ? quad % G::ND : 0;  // V meta word this lane loads
   LaneOffsets L;
-  L.k_r = quad * G::KW * 4 + r * rs.k_sn;
+  constexpr bool kPairK = G::PairK && !MASK;  // whole-row K loads (Geo::PairK)
+  L.k_r = kPairK ? quad * G::KW * 4 + (r >> 3) * 16 + (r & 7) * rs.k_sn : quad * G::KW * 4 + r * rs.k_sn;
   L.ks_r = kg0 * 2 + r * rs.ks_sn;
   L.kb_r = kg0 * 2 + r * rs.kb_sn;
   L.v_r = r * G::VW * 4 + 4 * quad * rs.v_sn;
@@ -267,7 +268,7 @@ __device__ __forceinline__ void decode_segment(const MfmaParams& p, float* s_acc
       }
     }
   }
-  K::load_k(R, rs, L, row_of(j));
+  K::template load_k<kPairK>(R, rs, L, row_of(j));
   __builtin_amdgcn_sched_barrier(0);
   K::load_v(R, rs, L, row_of(j));
   __builtin_amdgcn_sched_barrier(0);
@@ -309,7 +310,7 @@ __device__ __forceinline__ void decode_segment(const MfmaParams& p, float* s_acc
   while (j < J) {
     const int nj = next_pos(j);
     const int nrow = row_of(nj);
-    auto ik = [&](typename K::Regs& X) { K::load_k(X, rs, L, nrow); };
+    auto ik = [&](typename K::Regs& X) { K::template load_k<kPairK>(X, rs, L, nrow); };
     auto iv = [&](typename K::Regs& X) { K::load_v(X, rs, L, nrow); };
     K::template compute_tile<MASK>(R, p, qt, acc, mrun, lrun, s0 + row_of(j), s0, n_lane, quad, mrow, vm, ik, iv);
     j = nj;

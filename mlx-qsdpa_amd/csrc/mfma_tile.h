@@ -33,6 +33,16 @@ struct Geo {
   static constexpr int RW = D * BITS / 32;      // words per row
   static constexpr int NG = D / GS;             // groups (scales) per row
   static constexpr int ND = NG >= 2 ? NG / 2 : 1;  // 32-bit meta words per row
+  // D = 256 4-bit: 32-byte K quarters of 128-byte rows.  Each 16-byte K
+  // load covers 8 whole rows (lanes r and r + 8 read the two halves of row
+  // r & 7 of its 8), and a DPP exchange between lanes r and r ^ 8 gives
+  // every lane its own row's quarter (load_k, qk_half; in the kernels
+  // without a mask tensor).  Loaded as quarters, every K line was requested
+  // by two loads of half a line.  Measured at C3 (three rounds on one box):
+  // kernel p50 21.0-21.3 against 21.7-22.4 us, 24.3-24.5 against 24.7-25.5
+  // us per step; C5 (D = 128 8-bit, the same quarter shape) was 0.1 us
+  // slower with it and keeps the quarter loads.
+  static constexpr bool PairK = D == 256 && BITS == 4;
   static_assert(KG == 1 || KG == 2, "groups per quarter");
   static_assert(VW >= 1, "V piece");
 };
@@ -111,11 +121,19 @@ struct Kernel {
   // `rel0` rows past the sequence's first key.  Rows past the end fall
   // outside the buffer descriptors and read as zero (only the sequence's
   // last tile has such rows; their scores are set to -inf).
+  // PK: the PairK load (and, in qk_half, exchange); G::PairK && !MASK.
+  template <bool PK>
   static __device__ __forceinline__ void load_k(Regs& R, const Rsrcs& rs, const LaneOffsets& L, int rel0) {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const uint32_t row = static_cast<uint32_t>(rel0 + 16 * u);
-      buffer_words<G::KW, kAux>(rs.k, L.k_r, row * rs.k_sn, R.kw[u]);
+      if constexpr (PK) {
+        // Rows row + (r & 7) and row + 8 + (r & 7), 16-byte piece 2 quad + (r >> 3).
+        buffer_words<4, kAux>(rs.k, L.k_r, row * rs.k_sn, R.kw[u]);
+        buffer_words<4, kAux>(rs.k, L.k_r, (row + 8) * rs.k_sn, R.kw[u] + 4);
+      } else {
+        buffer_words<G::KW, kAux>(rs.k, L.k_r, row * rs.k_sn, R.kw[u]);
+      }
       if constexpr (G::KG == 2)
         R.ks[u] = __builtin_amdgcn_raw_buffer_load_b32(rs.ks, L.ks_r, row * rs.ks_sn, kAux);
       else
@@ -149,6 +167,7 @@ struct Kernel {
 
   // S^T for one 16-token half u: K dequantized into the A operand (scale *
   // code + bias with the lane's group scales / biases), Q^T as B.
+  template <bool PK>
   static __device__ __forceinline__ f4 qk_half(const Regs& R, int u, const uint32_t (&qt)[G::NM][4]) {
     uint32_t s2[2], b2[2];
     float sf[2], bf[2];
@@ -161,12 +180,30 @@ struct Kernel {
       b2[g] = splat_lo(bw);
       bf[g] = to_f32<Tag>(static_cast<uint16_t>(bw));
     }
+    // PairK: lane r < 8 holds piece 2 quad of row r (words 0-3) and of row
+    // r + 8 (4-7), lane r >= 8 piece 2 quad + 1 of rows r - 8 and r; one
+    // exchange with lane r ^ 8 (DPP row_ror:8) leaves both pieces of row r.
+    uint32_t kw[G::KW];
+    if constexpr (PK) {
+      const bool lo8 = (threadIdx.x & 8) == 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t a0 = R.kw[u][i], a1 = R.kw[u][4 + i];
+        const uint32_t x0 = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(a0), 0x128, 0xF, 0xF, false));
+        const uint32_t x1 = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(a1), 0x128, 0xF, 0xF, false));
+        kw[i] = lo8 ? a0 : x1;
+        kw[4 + i] = lo8 ? x0 : a1;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < G::KW; ++i) kw[i] = R.kw[u][i];
+    }
     f4 S = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int m = 0; m < G::NM; ++m) {
       const int g = (G::KG == 2 && m >= G::NM / 2) ? 1 : 0;
       uint32_t a[4];
-      dequant_k<Tag, BITS>(R.kw[u] + m * G::WPS, s2[g], b2[g], sf[g], bf[g], a);
+      dequant_k<Tag, BITS>(kw + m * G::WPS, s2[g], b2[g], sf[g], bf[g], a);
       S = mfma<Tag>(a, qt[m], S);
     }
     return S;
@@ -243,7 +280,7 @@ struct Kernel {
     // ---- S^T = K Q^T (Q^T operand m: 16 B per lane, in registers) ----
     f4 S[2];
 #pragma unroll
-    for (int u = 0; u < 2; ++u) S[u] = qk_half(R, u, qt);
+    for (int u = 0; u < 2; ++u) S[u] = qk_half<G::PairK && !MASK>(R, u, qt);
     issue_k(R);
 
     // ---- scores of (the lane's row, tokens tau(quad, j)), online softmax ----
