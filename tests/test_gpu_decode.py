@@ -204,7 +204,8 @@ def test_kv_start_left_padding(device, heads):
     (70, 8, 2, 300, 128, 64, "f16", (None, 2, 3)),    # more sequences than a wave's 64 lanes
     (5, 32, 8, 1100, 128, 32, "f16", (2, 7, 64)),
     (6, 16, 1, 700, 256, 32, "bf16", (None, 4, 16)),
-], ids=["B70", "B5-G4", "B6-D256-bf16"])
+    (7, 32, 2, 650, 256, 32, "f16", (None, 3, 16)),   # C3's heads (G = 16), float16
+], ids=["B70", "B5-G4", "B6-D256-bf16", "B7-D256-G16-f16"])
 def test_kv_start_streamk_schedule(device, case):
     """A left-padded batch runs splits * B equal units over its sequences laid
     end to end (units cross sequences): ragged lengths, empty sequences (kv_start >= N, also past N),
