@@ -606,7 +606,8 @@ def main(argv=None) -> int:
     args = parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the decode path is "
-              "single-GPU in this build, see DESIGN.md for how it would shard.", file=sys.stderr)
+              "single-GPU in this build (sharding by kv head and by sequence is a design only).",
+              file=sys.stderr)
         return 2
     if args.crossover_sweep:
         return run_crossover_sweep(args)
