@@ -80,7 +80,10 @@ namespace {
 constexpr int kPWaves = 8;
 constexpr int kPThreads = kPWaves * 64;
 constexpr int kPGroupRows = kPWaves * 16;    // query rows per workgroup
-constexpr int kMaxPrefillSplits = 64;
+// Up to 256 key splits, so that one row group per kv head still covers every
+// CU (with 64, C3's heads at q_len = 8 over 128K keys left half the CUs idle:
+// 109-111 against 75-80 us per call).
+constexpr int kMaxPrefillSplits = 256;
 constexpr float kVBound = 64000.0f;          // largest |V| staged in float16 unscaled
 // bfloat16 inputs: the largest max |V| for which P enters the P.V MFMAs as
 // one float16 term (11 significant bits); above it, as two (hi + lo, 22
@@ -753,16 +756,18 @@ bool prefill_supports(const qsdpa_decode_args* a) {
   if (a->q_len <= 1 || (a->D != 128 && a->D != 256) || !mfma_supports(a)) return false;
   const int64_t rows = static_cast<int64_t>(a->H_q / a->H_kv) * a->q_len;
   if (rows < kPGroupRows) return false;
-  // D = 256 only for calls with two or more row groups per kv head and at
-  // least 2^24 (query row, key) pairs; smaller ones are faster on the decode
-  // kernel, whose 16-row blocks each stream the kv head (measured, wall time
-  // per call, decode kernel against this one: C3's heads at q_len = 8 over
-  // 32K / 128K keys 34.0 / 110.4 against 43.2 / 114.4 us, q_len = 16 over 4K
-  // 18.4 against 32.4; at q_len = 16 over 128K 206 against 144, q_len = 32
-  // over 32K 103 against 80; C2's heads at q_len = 512 over 4K 30.8 against
-  // 40.4, q_len = 256 over 32K 73.6 against 59.8).
-  if (a->D == 256 && (rows < 2 * kPGroupRows ||
-                      static_cast<int64_t>(a->B) * a->H_q * a->q_len * a->N < (int64_t(1) << 24)))
+  // D = 256 only for calls with at least 2^24 (query row, key) pairs; below
+  // that the decode kernel, whose 16-row blocks each stream the kv head, was
+  // as fast or faster in all but one case measured (wall time per call,
+  // decode kernel against this one with up to 256 key splits: C3's heads at
+  // q_len = 8 over 16K /
+  // 32K / 64K / 128K keys 23.1-23.2 / 34.0-34.3 / 57-59 / 109-111 against
+  // 28.2-28.4 / 34.4 / 47.6-49.2 / 75-84 us, q_len = 16 over 8K / 16K 23.6 /
+  // 34.0-34.2 against 29.4-29.7 / 35.8-35.9; C2's heads at q_len = 128 over
+  // 32K / 128K 45.8-46.6 / 145-148 against 43.3-43.4 / 101-105, q_len = 256
+  // over 8K 31.5 against 35.1-35.2).  A half-filled row group loses: C3's
+  // heads at q_len = 4 over 128K 58-59 against 73-75 us.
+  if (a->D == 256 && static_cast<int64_t>(a->B) * a->H_q * a->q_len * a->N < (int64_t(1) << 24))
     return false;
   const int64_t groups = (rows + kPGroupRows - 1) / kPGroupRows;
   if (groups * a->H_kv * a->B * kMaxPrefillSplits >= (int64_t(1) << 31)) return false;

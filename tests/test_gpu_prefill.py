@@ -95,6 +95,7 @@ SPLIT_CASES = [  # small grids: the planner gives each row group several key spl
     (1, 16, 4, 3000, 128, 8, 128, torch.bfloat16, True, False),   # 16 groups: 11 splits
     (2, 16, 4, 2500, 128, 4, 32, torch.float16, False, True),     # 32 groups, full attention: 8 splits
     (2, 16, 4, 2500, 256, 8, 64, torch.bfloat16, True, False),    # 64 groups: 4 splits, bfloat16
+    (1, 8, 2, 40010, 32, 4, 64, torch.float16, True, False),      # 2 groups: 128 splits, merge kernel
 ]
 
 
@@ -234,11 +235,13 @@ D256_CASES = [
     (2, 8, 2, 2700, 400, 4, 128, torch.float16, True, True),      # 1600 rows: partial last group
     (4, 16, 4, 2100, 128, 4, 64, torch.bfloat16, True, False),
     (1, 32, 8, 8200, 64, 8, 32, torch.float16, False, False),
+    (1, 32, 2, 65611, 8, 4, 32, torch.float16, True, False),      # one group per kv head: 128 key splits
+    (1, 2, 2, 65601, 128, 8, 64, torch.bfloat16, True, False),    # C2's heads, one group: 128 key splits
 ]
 
 
 def _d256_routed(B, Hq, Hkv, N, L):
-    return Hq // Hkv * L >= 256 and B * Hq * L * N >= D256_PAIRS
+    return Hq // Hkv * L >= 128 and B * Hq * L * N >= D256_PAIRS
 
 
 @pytest.mark.parametrize("case", D256_CASES, ids=lambda c: "B{}_H{}x{}_N{}_L{}_b{}_g{}_{}_{}{}".format(
