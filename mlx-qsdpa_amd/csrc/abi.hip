@@ -47,6 +47,11 @@ bool prefill_supports(const qsdpa_decode_args* a);
 int prefill_num_splits(const qsdpa_decode_args* a, int cus);
 int launch_prefill_mfma(const qsdpa_decode_args* a, int splits, float* part_acc, float* part_ml,
                         hipStream_t stream);
+// Defined in decode_rows32.hip.
+bool rows32_supports(const qsdpa_decode_args* a);
+int rows32_num_splits(const qsdpa_decode_args* a, int cus);
+int launch_decode_rows32(const qsdpa_decode_args* a, int num_splits, float* part_acc, float* part_ml,
+                         hipStream_t stream);
 
 
 namespace {
@@ -210,6 +215,7 @@ int launch_append_quantize(const qsdpa_decode_args* a, hipStream_t s) {
 // it.  Otherwise the merge kernel combines the partials.
 bool fused_merge(const qsdpa_decode_args* a, int splits, bool prefill, bool mfma, int units) {
   if (prefill || !mfma || splits < 2) return false;
+  if (rows32_supports(a)) return false;  // the 32-row kernel: the merge kernel
   if (units == 0 && splits > kFusedSplits) return false;
   // D = 256 with 8-bit codes under the stream-K schedule has no such kernel
   // (its registers spilled to scratch).
@@ -231,7 +237,7 @@ int decode_plan(const qsdpa_decode_args* a, int* num_splits, int64_t* workspace_
   const bool mfma = mfma_supports(a);
   if (splits == 0 && !prefill) {
     if (mfma) {
-      splits = mfma_num_splits(a, compute_units());
+      splits = rows32_supports(a) ? rows32_num_splits(a, compute_units()) : mfma_num_splits(a, compute_units());
     } else {
       const int G = a->H_q / a->H_kv;
       const int64_t units = static_cast<int64_t>(a->B) * a->H_kv * (G / valu_heads_per_block(G));
@@ -273,6 +279,7 @@ int run_decode(const qsdpa_decode_args* args, int splits, void* workspace, hipSt
   const bool append_inside = fused_append(args, prefill, mfma);
   if (args->k_new.ptr && !append_inside && (rc = launch_append_quantize(args, s))) return rc;
   if (prefill) rc = launch_prefill_mfma(args, splits, part_acc, part_ml, s);
+  else if (mfma && rows32_supports(args)) rc = launch_decode_rows32(args, splits, part_acc, part_ml, s);
   else if (mfma)
     rc = launch_decode_mfma(args, splits, part_acc, part_ml, units, sched,
                             fused ? static_cast<unsigned*>(workspace) : nullptr, append_inside, s);

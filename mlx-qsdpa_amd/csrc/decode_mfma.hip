@@ -641,8 +641,11 @@ bool mfma_supports(const qsdpa_decode_args* a) {
   return true;
 }
 
-// Splits per (batch, kv head, head block): one workgroup per CU in total
-// (LDS and registers allow one 8-wave group per CU), each split at least
+// Splits per (batch, kv head, head block): at most one workgroup per CU in
+// total (LDS and registers allow one 8-wave group per CU; rounded down, as a
+// few workgroups past the CU count run as a second round: C3's heads at
+// q_len = 3 and 7 over 128K keys, 6 and 14 units of 43 and 19 splits, took
+// 258 and 266 workgroups), each split at least
 // four tiles (half the waves busy: at C1, N=4096, 32 splits give 9.56 us per
 // step against 10.35 with 16; at C3, N=16K, 128 splits 13.6 against 14.95
 // with 64).  A left-padded batch (kv_start, B > 1) runs the stream-K
@@ -653,7 +656,7 @@ bool mfma_supports(const qsdpa_decode_args* a) {
 int mfma_num_splits(const qsdpa_decode_args* a, int cus) {
   const int hb = (a->H_q / a->H_kv * std::max(a->q_len, 1) + 15) / 16;
   const int64_t units = static_cast<int64_t>(a->B) * a->H_kv * hb;
-  int64_t s = (cus + units - 1) / units;
+  int64_t s = cus / units;
   s = std::min<int64_t>(s, std::max<int64_t>(1, a->N / (4 * kTile)));
   s = std::min<int64_t>(s, 1024);
   return static_cast<int>(std::max<int64_t>(s, 1));

@@ -1,0 +1,276 @@
+// Decode of more than 16 query rows per kv head at D = 256 with 4-bit codes
+// (speculative decoding windows, short chunks; the prefill kernel takes the
+// large calls): 32 query rows per workgroup, each wave computing both 16-row
+// halves from one dequantized K / V tile.
+//
+// Reference: the path these calls take there is the dequantize + SDPA
+// fallback (mlx_qsdpa/dispatch.py:68-83); the attention is the decode's
+// (kernels.py:224-318 per split, merged as kernels.py:342-418).
+//
+// The 16-row decode kernel (decode_mfma.hip) gives every block of 16 rows
+// its own workgroups, so each block streams the kv head and dequantizes it
+// again: at D = 256 the exact dequantization is about half of that kernel's
+// VALU work and the re-reads multiply its HBM bytes.  Here a block of 32
+// rows does both once.  The two halves' accumulators (128 VGPRs) leave no
+// room for Q^T in registers, so each QK step reads its B operands from the
+// staged Q rows in LDS (16 ds_read_b128 per wave and tile).  Everything else
+// -- tiles, super-tiles, the waves' shares, the whole-row K loads, the
+// transposed V loads, the online softmax, the LDS merge of the 8 waves and
+// the partial rows -- is the 16-row kernel's, with two running (m, l) per
+// lane (row r of each half).  Uniform key splits, the merge kernel for the
+// partials, no mask tensor (such calls keep the 16-row kernel).
+#include "abi_internal.h"
+#include "mfma_tile.h"
+#include "wave_split.h"
+
+namespace qsdpa {
+
+namespace {
+
+constexpr int kRows = 32;  // query rows per workgroup
+
+template <typename Tag, int GS>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_rows32_kernel(
+    MfmaParams p) {
+  constexpr int D = 256, BITS = 4;
+  using G = Geo<D, BITS, GS>;
+  using K = Kernel<Tag, D, BITS, GS>;
+  static_assert(G::PairK, "whole-row K loads");
+  constexpr int kRowF = D + 4;       // LDS floats per (wave, row) of the merge
+  constexpr int kQRow = D * 2 + 16;  // bytes per staged Q row
+  __shared__ __attribute__((aligned(16))) float s_acc[kWaves * 16 * kRowF];
+  __shared__ float s_ml[kWaves][16][2];
+  __shared__ __attribute__((aligned(16))) uint8_t s_q[kRows * kQRow];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int quad = lane >> 4;
+  const int r = lane & 15;
+  const int hblk = blockIdx.y % p.hb_count;
+  const int kvh = blockIdx.y / p.hb_count;
+  const int b = blockIdx.z;
+
+  // The block's rows v0 .. v0 + nh - 1 of the kv head's G * qL rows (row v:
+  // position v / G of head kvh * G + v % G); lane r computes row r of each
+  // half (clamped to the last real row).
+  const int v0 = hblk * kRows;
+  const int nh = min(kRows, p.G * p.qL - v0);
+  const int n_end = p.causal ? min(p.N, max(0, p.N - p.qL + (v0 + nh - 1) / p.G + 1)) : p.N;
+  int n_lane[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int iq = (v0 + min(16 * k + r, nh - 1)) / p.G;
+    n_lane[k] = p.causal ? min(n_end, max(0, p.N - p.qL + iq + 1)) : n_end;
+  }
+
+  // Keys [s0, n_end), 32-token tiles in super-tiles; split x of S owns
+  // super-tiles x, x + S, ... (as the 16-row kernel's uniform splits).
+  const int s0 = p.kv_start ? min(max(p.kv_start[b], 0), p.N) : 0;
+  const int len = max(n_end - s0, 0);
+  const int T = (len + kTile - 1) / kTile;
+  const int t_lo = blockIdx.x, stride = p.num_splits;
+  const int sh = super_tile_shift(T, stride);
+  const int J = super_tile_positions(T, t_lo, stride, 0x7FFFFFFF, sh);
+  auto tile_of = [&](int j) -> int { return super_tile_tile(j, t_lo, stride, sh); };
+  static_assert(kWaves == kSplitWaves, "the tile split is for 8 waves");
+  const int J8 = wave_split_rr_end(J, D);
+  auto next_pos = [&](int j) -> int { return wave_split_next(j, J, J8, wave); };
+  const int oob = len + kTile;  // rows outside every descriptor: the loads read zero
+  auto row_of = [&](int j) -> int { return j < J ? tile_of(j) * kTile : oob; };
+
+  Rsrcs rs;
+  {
+    const int64_t tok0 = s0;
+    auto rsrc = [&](const void* base, int64_t sb, int64_t shh, int64_t sn, int esz, int row_bytes, bool present) {
+      const uint8_t* p0 = static_cast<const uint8_t*>(base) +
+                          (static_cast<int64_t>(b) * sb + static_cast<int64_t>(kvh) * shh + tok0 * sn) * esz;
+      const uint32_t bytes =
+          (present && len > 0) ? static_cast<uint32_t>((len - 1) * sn * esz + row_bytes) : 0u;
+      return make_rsrc(p0, bytes);
+    };
+    constexpr int kRow = D * BITS / 8;
+    constexpr int kMeta = G::NG * 2;
+    rs.k = rsrc(p.kp, p.kp_sb, p.kp_sh, p.kp_sn, 4, kRow, true);
+    rs.v = rsrc(p.vp, p.vp_sb, p.vp_sh, p.vp_sn, 4, kRow, true);
+    rs.ks = rsrc(p.ks, p.ks_sb, p.ks_sh, p.ks_sn, 2, kMeta, true);
+    rs.vs = rsrc(p.vs, p.vs_sb, p.vs_sh, p.vs_sn, 2, kMeta, true);
+    rs.kb = rsrc(p.has_bias ? p.kb : p.ks, p.kb_sb, p.kb_sh, p.kb_sn, 2, kMeta, p.has_bias);
+    rs.vb = rsrc(p.has_bias ? p.vb : p.vs, p.vb_sb, p.vb_sh, p.vb_sn, 2, kMeta, p.has_bias);
+    rs.k_sn = static_cast<uint32_t>(p.kp_sn * 4);
+    rs.v_sn = static_cast<uint32_t>(p.vp_sn * 4);
+    rs.ks_sn = static_cast<uint32_t>(p.ks_sn * 2);
+    rs.vs_sn = static_cast<uint32_t>(p.vs_sn * 2);
+    rs.kb_sn = static_cast<uint32_t>(p.kb_sn * 2);
+    rs.vb_sn = static_cast<uint32_t>(p.vb_sn * 2);
+  }
+
+  // Per-lane byte offsets (the 16-row kernel's, whole-row K loads).
+  const int kg0 = (quad * G::QD) / GS;
+  const int gv = (r * G::NB) / GS;
+  const int vword = G::NG >= 2 ? quad % G::ND : 0;
+  LaneOffsets L;
+  L.k_r = quad * G::KW * 4 + (r >> 3) * 16 + (r & 7) * rs.k_sn;
+  L.ks_r = kg0 * 2 + r * rs.ks_sn;
+  L.kb_r = kg0 * 2 + r * rs.kb_sn;
+  L.v_r = r * G::VW * 4 + 4 * quad * rs.v_sn;
+  L.vs_r = vword * 4 + r * rs.vs_sn;
+  L.vb_r = vword * 4 + r * rs.vb_sn;
+  asm("" : "+v"(L.k_r), "+v"(L.ks_r), "+v"(L.kb_r), "+v"(L.v_r), "+v"(L.vs_r), "+v"(L.vb_r));
+  VMetaLane vm;
+  {
+    const int dw = G::NG >= 2 ? gv / 2 : 0;
+    const int half = G::NG >= 2 ? gv % 2 : 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) vm.src[k] = (16 * dw + 4 * quad + k) * 4;
+    vm.sel = half ? 0x07060302u : 0x05040100u;
+    vm.shift = half ? 0u : 16u;
+  }
+
+  // Stage the block's 32 Q rows (zero rows for padding), two rows per
+  // thread, each 16-byte piece already in the order the K dequantizer
+  // produces the dims (float16: 0, 4, 1, 5, 2, 6, 3, 7).
+  {
+    constexpr int kQChunks = D / 8;  // 16-byte pieces per row
+    const int qh = threadIdx.x / kQChunks, qc = threadIdx.x % kQChunks;
+    const uint8_t* q0 = reinterpret_cast<const uint8_t*>(p.q) +
+                        (static_cast<int64_t>(b) * p.q_sb + static_cast<int64_t>(kvh) * p.G * p.q_sh) * 2;
+    const rsrc_t rq = make_rsrc(
+        q0, static_cast<uint32_t>(((p.G - 1) * p.q_sh + static_cast<int64_t>(p.qL - 1) * p.q_sq) * 2 + D * 2));
+    static_assert(kThreads / kQChunks * 2 == kRows, "two staging rounds");
+    u4 qv[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int row = qh + 16 * k;
+      const int v = v0 + min(row, nh - 1);
+      const int64_t off = (static_cast<int64_t>(v % p.G) * p.q_sh + static_cast<int64_t>(v / p.G) * p.q_sq) * 2;
+      qv[k] = __builtin_amdgcn_raw_buffer_load_b128(rq, static_cast<uint32_t>(off + qc * 16), 0, 0);
+    }
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int row = qh + 16 * k;
+      u4 w = row < nh ? qv[k] : u4{0u, 0u, 0u, 0u};
+      if constexpr (Tag::kId == QSDPA_F16) {
+        w = u4{perm(w[2], w[0], 0x05040100u), perm(w[2], w[0], 0x07060302u), perm(w[3], w[1], 0x05040100u),
+               perm(w[3], w[1], 0x07060302u)};
+      }
+      *reinterpret_cast<u4*>(s_q + row * kQRow + qc * 16) = w;
+    }
+  }
+  __syncthreads();
+
+  typename K::Regs R;
+  int j = wave;
+  K::template load_k<true>(R, rs, L, row_of(j));
+  __builtin_amdgcn_sched_barrier(0);
+  K::load_v(R, rs, L, row_of(j));
+  __builtin_amdgcn_sched_barrier(0);
+
+  // The lane's Q^T pieces: row r of half 0, dims quad * QD + 8 m.
+  const uint8_t* qlds = s_q + r * kQRow + quad * G::QD * 2;
+  f4 acc[2][G::NB];
+#pragma unroll
+  for (int k = 0; k < 2; ++k)
+#pragma unroll
+    for (int i = 0; i < G::NB; ++i) acc[k][i] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  float mrun[2] = {kNegBig, kNegBig};
+  float lrun[2] = {0.0f, 0.0f};
+
+  while (j < J) {
+    const int nj = next_pos(j);
+    const int nrow = row_of(nj);
+    auto ik = [&](typename K::Regs& X) { K::template load_k<true>(X, rs, L, nrow); };
+    auto iv = [&](typename K::Regs& X) { K::load_v(X, rs, L, nrow); };
+    K::compute_tile2(R, p, qlds, 16 * kQRow, acc, mrun, lrun, s0 + row_of(j), s0, n_lane, quad, vm, ik, iv);
+    j = nj;
+  }
+
+  // Merge the 8 waves through LDS, one half at a time, and store each half's
+  // rows: the output (one split) or the split's partials (merge kernel).
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int nk = min(16, nh - 16 * k);  // real rows of the half (uniform)
+    if (nk <= 0) break;
+    float l = lrun[k];
+    l += shfl_xor_f32(l, 16);
+    l += shfl_xor_f32(l, 32);
+    if (k == 1) __syncthreads();  // half 0's merge has read the LDS
+    if (quad == 0) {
+      s_ml[wave][r][0] = mrun[k];
+      s_ml[wave][r][1] = l;
+    }
+    float* row = s_acc + (wave * 16 + r) * kRowF;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float* dst = row + (4 * quad + i) * G::NB;
+#pragma unroll
+      for (int nb = 0; nb < G::NB; nb += 4)
+        *reinterpret_cast<f4*>(dst + nb) =
+            f4{acc[k][nb][i], acc[k][nb + 1][i], acc[k][nb + 2][i], acc[k][nb + 3][i]};
+    }
+    __syncthreads();
+    merge_store<Tag, D, kWaves, false>(
+        p, [&](int w, int h) { return s_acc + (w * 16 + h) * kRowF; },
+        [&](int w, int h) { return f32x2{s_ml[w][h][0], s_ml[w][h][1]}; }, nk, v0 + 16 * k, kvh, b,
+        static_cast<int>(blockIdx.x), kThreads);
+  }
+}
+
+using Rows32Kernel = void (*)(MfmaParams);
+
+template <typename Tag>
+Rows32Kernel rows32_by_gs(int gs) {
+  return gs == 32 ? decode_rows32_kernel<Tag, 32> : gs == 64 ? decode_rows32_kernel<Tag, 64>
+                                                               : decode_rows32_kernel<Tag, 128>;
+}
+
+}  // namespace
+
+// Calls for the 32-row kernel (those the prefill kernel does not take):
+// D = 256, 4-bit codes, several query positions with more than 16 rows per
+// kv head, no mask tensor, no folded append, and uniform splits (kv_start
+// only with one sequence: a left-padded batch takes the stream-K schedule of
+// the 16-row kernel); and enough work per kv head: at least 16K keys and
+// 1.5 * 2^20 (row, key) pairs.  Measured against the 16-row kernel, C3's
+// heads, wall time per call on one box (both with splits rounded down to
+// one round of workgroups), 32-row kernel against 16-row kernel, in us:
+//   q_len = 2 over 16K / 32K / 64K keys   16.5 / 19.4-19.6 / 22.1-22.2
+//                                         against 15.4 / 17.9-18.1 / 23.2-23.3
+//   q_len = 3 over 16K / 32K / 64K / 128K 19.0-19.1 / 21.6 / 28.0-28.4 / 42.8-44.0
+//                                         against 18.3-18.5 / 24.2-24.3 / 33.0-33.2 / 53.8-55.1
+//   q_len = 4 over 16K / 32K / 64K        19.4-19.7 / 22.2-22.4 / 28.7-28.8
+//                                         against 18.2 / 23.6-23.8 / 34.2-34.3
+//   q_len = 6 over 16K / 32K / 64K        22.9 / 29.0-29.2 / 38.9-41.9
+//                                         against 24.7-24.8 / 35.0-35.2 / 57.0-57.5
+//   q_len = 7 over 128K                   80.1-81.6 against 118.8-119.3
+//   q_len = 8 over 32K                    29.7 against 33.9-34.1
+//   q_len = 12 / 16 over 16K              31.1 / 31.8-32.0 against 31.4 / 34.3-34.4
+//   q_len = 16 over 8K                    25.1-25.2 against 23.8
+bool rows32_supports(const qsdpa_decode_args* a) {
+  if (a->D != 256 || a->bits != 4 || a->q_len <= 1 || a->mask.ptr || a->k_new.ptr) return false;
+  if (a->kv_start && a->B > 1) return false;
+  const int64_t rows = static_cast<int64_t>(a->H_q / a->H_kv) * a->q_len;
+  return rows > 16 && a->N >= 16384 && rows * a->N >= (int64_t(3) << 19);
+}
+
+// Splits: as the 16-row kernel's (at most one workgroup per CU), over 32-row
+// blocks.
+int rows32_num_splits(const qsdpa_decode_args* a, int cus) {
+  const int hb = (a->H_q / a->H_kv * a->q_len + kRows - 1) / kRows;
+  const int64_t units = static_cast<int64_t>(a->B) * a->H_kv * hb;
+  int64_t s = cus / units;
+  s = std::min<int64_t>(s, std::max<int64_t>(1, a->N / (4 * kTile)));
+  s = std::min<int64_t>(s, 1024);
+  return static_cast<int>(std::max<int64_t>(s, 1));
+}
+
+int launch_decode_rows32(const qsdpa_decode_args* a, int num_splits, float* part_acc, float* part_ml,
+                         hipStream_t stream) {
+  MfmaParams p = mfma_params(a, num_splits, part_acc, part_ml);
+  p.hb_count = (p.G * p.qL + kRows - 1) / kRows;
+  const dim3 grid(num_splits, p.Hkv * p.hb_count, p.B);
+  Rows32Kernel k = a->dtype == QSDPA_F16 ? rows32_by_gs<F16>(a->group_size) : rows32_by_gs<BF16>(a->group_size);
+  launch_profiled(k, grid, dim3(kThreads), stream, a->prof_begin, a->prof_end, p);
+  return check_launch("decode_rows32");
+}
+
+}  // namespace qsdpa

@@ -397,6 +397,212 @@ struct Kernel {
       issue_v(R);
     }
   }
+
+  // ---- Two 16-row halves per wave (decode_rows32.hip; D = 256, 4-bit) ----
+  // One dequantized K / V tile feeds the MFMAs of both halves of a 32-row
+  // block.  Q^T does not fit in registers beside two accumulator sets, so
+  // each QK step reads its B operands from the staged Q rows in LDS: qlds is
+  // the lane's 16-byte piece of its row in half 0 (step m at +16 m), half 1
+  // lies half_bytes further.
+
+  // S^T of both token halves u (S[u][k]) for both row halves k.  Each QK
+  // step's two Q^T pieces are read once, one step ahead (the scheduling
+  // barrier keeps the compiler from hoisting every step's LDS reads, which
+  // ran the kernel out of registers), and feed four MFMAs.
+  static __device__ __forceinline__ void qk_tile2(const Regs& R, const uint8_t* qlds, int half_bytes,
+                                                  f4 (&S)[2][2]) {
+    static_assert(G::PairK, "the two-half kernel loads whole K rows");
+    uint32_t s2[2][2], b2[2][2];
+    float sf[2][2], bf[2][2];
+    uint32_t kw[2][G::KW];
+    const bool lo8 = (threadIdx.x & 8) == 0;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        const uint32_t sw = (G::KG == 2 && g == 1) ? (R.ks[u] >> 16) : R.ks[u];
+        const uint32_t bw = (G::KG == 2 && g == 1) ? (R.kb[u] >> 16) : R.kb[u];
+        s2[u][g] = splat_lo(sw);
+        sf[u][g] = to_f32<Tag>(static_cast<uint16_t>(sw));
+        b2[u][g] = splat_lo(bw);
+        bf[u][g] = to_f32<Tag>(static_cast<uint16_t>(bw));
+      }
+      // The whole-row exchange of qk_half (lanes r and r ^ 8).
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t a0 = R.kw[u][i], a1 = R.kw[u][4 + i];
+        const uint32_t x0 = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(a0), 0x128, 0xF, 0xF, false));
+        const uint32_t x1 = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(a1), 0x128, 0xF, 0xF, false));
+        kw[u][i] = lo8 ? a0 : x1;
+        kw[u][4 + i] = lo8 ? x0 : a1;
+      }
+#pragma unroll
+      for (int k = 0; k < 2; ++k) S[u][k] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    u4 q0 = *reinterpret_cast<const u4*>(qlds);
+    u4 q1 = *reinterpret_cast<const u4*>(qlds + half_bytes);
+#pragma unroll
+    for (int m = 0; m < G::NM; ++m) {
+      u4 n0 = q0, n1 = q1;
+      if (m + 1 < G::NM) {
+        n0 = *reinterpret_cast<const u4*>(qlds + 16 * (m + 1));
+        n1 = *reinterpret_cast<const u4*>(qlds + half_bytes + 16 * (m + 1));
+      }
+      __builtin_amdgcn_sched_barrier(0x67F);  // everything but LDS reads may cross
+      const uint32_t b0[4] = {q0[0], q0[1], q0[2], q0[3]};
+      const uint32_t b1[4] = {q1[0], q1[1], q1[2], q1[3]};
+      const int g = (G::KG == 2 && m >= G::NM / 2) ? 1 : 0;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        uint32_t a[4];
+        dequant_k<Tag, BITS>(kw[u] + m * G::WPS, s2[u][g], b2[u][g], sf[u][g], bf[u][g], a);
+        S[u][0] = mfma<Tag>(a, b0, S[u][0]);
+        S[u][1] = mfma<Tag>(a, b1, S[u][1]);
+      }
+      q0 = n0;
+      q1 = n1;
+    }
+  }
+
+  // Online softmax of one half's scores (sc: the lane's 8 tokens, scaled
+  // unless `fold`) into its running (m, l) and P^T operands (pb_lo: the
+  // bfloat16 low terms).
+  static __device__ __forceinline__ void softmax_half(float (&sc)[8], float ea, f4 (&acc)[G::NB], float& mrun,
+                                                      float& lrun, uint32_t (&pb)[4], uint32_t (&pb_lo)[4]) {
+    const float tmax = max_over_rows(max8(sc)) * ea;
+    const bool grow = tmax > mrun + kRescale;
+    if (__builtin_amdgcn_ballot_w64(grow)) {
+      const float mnew = grow ? tmax : mrun;
+      const float f = fast_exp2(mrun - mnew);
+      mrun = mnew;
+      lrun *= f;
+#pragma unroll
+      for (int i = 0; i < G::NB; ++i) acc[i] *= f;
+    }
+    float pr[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) pr[j] = fast_exp2(fmaf(sc[j], ea, -mrun));
+    lrun += ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pb[i] = pack_T2<Tag>(pr[2 * i], pr[2 * i + 1]);
+    if constexpr (Tag::kId == QSDPA_BF16) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        pb_lo[i] = pack_T2<Tag>(pr[2 * i] - unpack_T2_lo<Tag>(pb[i]), pr[2 * i + 1] - unpack_T2_hi<Tag>(pb[i]));
+    }
+  }
+
+  // One tile for a 32-row block: QK of both halves, their online softmax,
+  // PV of both halves from one dequantized V^T.  n1[k]: the lane's end of
+  // keys in half k.  No mask tensor.
+  template <typename IK, typename IV>
+  static __device__ __forceinline__ void compute_tile2(Regs& R, const MfmaParams& p, const uint8_t* qlds,
+                                                       int half_bytes, f4 (&acc)[2][G::NB], float (&mrun)[2],
+                                                       float (&lrun)[2], int tb, int n0, const int (&n1)[2], int quad,
+                                                       const VMetaLane& vm, IK&& issue_k, IV&& issue_v) {
+    static_assert(BITS == 4, "the two-half kernel is built for 4-bit codes");
+    f4 S[2][2];  // [token half u][row half k]
+    qk_tile2(R, qlds, half_bytes, S);
+    issue_k(R);
+
+    const bool fold = p.qscale > 0.0f;
+    const float ea = fold ? p.qscale : 1.0f;
+    const bool partial = tb + kTile > min(n1[0], n1[1]) || tb < n0;
+    uint32_t pb[2][4], pb_lo[2][4];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      float sc[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) sc[j] = S[j >> 2][k][j & 3];
+      if (!fold) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) sc[j] *= p.qscale;
+      }
+      if (__builtin_expect(partial, 0)) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int t = tb + tau(quad, j);
+          if (t >= n1[k] || t < n0) sc[j] = -__builtin_huge_valf();
+        }
+      }
+      softmax_half(sc, ea, acc[k], mrun[k], lrun[k], pb[k], pb_lo[k]);
+    }
+
+    // V scale / bias words of the lane's 8 tokens (as in compute_tile).
+    uint32_t dS[8], dB[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      dS[j] = __builtin_amdgcn_ds_bpermute(vm.src[j & 3], static_cast<int>(R.vs[j >> 2]));
+      dB[j] = __builtin_amdgcn_ds_bpermute(vm.src[j & 3], static_cast<int>(R.vb[j >> 2]));
+    }
+    if constexpr (Tag::kId == QSDPA_F16) {
+      uint32_t sv2[4], bv2[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sv2[i] = perm(dS[2 * i + 1], dS[2 * i], vm.sel);
+        bv2[i] = perm(dB[2 * i + 1], dB[2 * i], vm.sel);
+      }
+      // X: nibbles 0-3 of tokens (2i, 2i+1), Y: nibbles 4-7 (as pv_f16).
+      uint32_t X[4][G::VW], Y[4][G::VW];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int w = 0; w < G::VW; ++w) {
+          X[i][w] = perm(R.vw[2 * i + 1][w], R.vw[2 * i][w], 0x05040100u);
+          Y[i][w] = perm(R.vw[2 * i + 1][w], R.vw[2 * i][w], 0x07060302u);
+        }
+      issue_v(R);
+#pragma unroll
+      for (int nb = 0; nb < G::NB; ++nb) {
+        const int w = nb >> 3, k = nb & 7;
+        uint32_t a[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t src = k < 4 ? X[i][w] : Y[i][w];
+          a[i] = f16x2_fma(nib_codes(src, src >> 8, k & 3), sv2[i], bv2[i]);
+        }
+        acc[0][nb] = mfma<Tag>(a, pb[0], acc[0][nb]);
+        acc[1][nb] = mfma<Tag>(a, pb[1], acc[1][nb]);
+      }
+    } else {
+      float svf[8], bvf[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        svf[j] = __builtin_bit_cast(float, (dS[j] << vm.shift) & 0xFFFF0000u);
+        bvf[j] = __builtin_bit_cast(float, (dB[j] << vm.shift) & 0xFFFF0000u);
+      }
+      uint32_t lo[8][G::VW], hi[8][G::VW];
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int w = 0; w < G::VW; ++w) {
+          lo[j][w] = R.vw[j][w] & 0x0F0F0F0Fu;         // nibbles 0, 2, 4, 6 as bytes
+          hi[j][w] = (R.vw[j][w] >> 4) & 0x0F0F0F0Fu;  // nibbles 1, 3, 5, 7
+        }
+#pragma unroll
+      for (int nb = 0; nb < G::NB; ++nb) {
+        const int w = nb >> 3, k = nb & 7;
+        uint32_t a[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float c[2];
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            const int j = 2 * i + e;
+            const uint32_t src = (k & 1) ? hi[j][w] : lo[j][w];
+            c[e] = fmaf(svf[j], static_cast<float>((src >> (8 * (k >> 1))) & 0xFFu), bvf[j]);
+          }
+          a[i] = pack_T2<Tag>(c[0], c[1]);
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          acc[h][nb] = mfma<Tag>(a, pb[h], acc[h][nb]);
+          acc[h][nb] = mfma<Tag>(a, pb_lo[h], acc[h][nb]);
+        }
+      }
+      issue_v(R);
+    }
+  }
 };
 
 // Cache policy (the aux operand of buffer loads and stores) of the partials

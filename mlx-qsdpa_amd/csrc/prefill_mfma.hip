@@ -783,9 +783,10 @@ bool prefill_supports(const qsdpa_decode_args* a) {
   return true;
 }
 
-// Key splits of the prefill kernel: enough workgroups for every CU, each
-// split at least 4 tiles (an explicit num_splits > 0 is kept, up to the
-// same bounds).  At the C5 chunk (256 row groups) one split; with
+// Key splits of the prefill kernel: as many workgroups as CUs, rounded down
+// (one workgroup fits a CU, and a few past the CU count run as a second
+// round), each split at least 4 tiles (an explicit num_splits > 0 is kept,
+// up to the same bounds).  At the C5 chunk (256 row groups) one split; with
 // q_len = 128 (64 groups) 4 splits: 38 against 126 us in one.  (At D = 256,
 // 8 tiles -- the same 256 keys -- made C3's heads at q_len = 16, N = 4096
 // 25.9 instead of 21.3 us.)
@@ -794,7 +795,7 @@ int prefill_num_splits(const qsdpa_decode_args* a, int cus) {
   const int64_t grid = (rows + kPGroupRows - 1) / kPGroupRows * a->H_kv * a->B;
   const int tile = prefill_tile(a->D);
   const int64_t tiles = (static_cast<int64_t>(a->N) + tile - 1) / tile;
-  int64_t s = a->num_splits > 0 ? a->num_splits : (cus + grid - 1) / grid;
+  int64_t s = a->num_splits > 0 ? a->num_splits : cus / grid;  // one round of workgroups
   s = std::min<int64_t>(s, std::max<int64_t>(1, tiles / 4));
   s = std::min<int64_t>(s, kMaxPrefillSplits);
   return static_cast<int>(std::max<int64_t>(s, 1));

@@ -325,6 +325,58 @@ def test_row_blocks_match_oracle(device, case):
         assert np.array_equal(got, again), f"splits={splits}: repeated call differs"
 
 
+@pytest.mark.parametrize("case", [
+    # (B, Hq, Hkv, N, D, bits, gs, dtype, qL, causal, kv_start); calls with
+    # 16K+ keys and 1.5 * 2^20 (row, key) pairs per kv head take this kernel,
+    # kv_start shortens the key range
+    (1, 32, 2, 49200, 256, 4, 32, "f16", 2, True, None),        # 32 rows: one full block
+    (2, 32, 2, 32768, 256, 4, 64, "bf16", 3, True, None),       # 48 rows: a half-filled second block
+    (1, 16, 1, 33000, 256, 4, 128, "f16", 7, False, None),      # 112 rows, full attention
+    (1, 2, 2, 81920, 256, 4, 32, "bf16", 20, True, (81270,)),   # G = 1: 20 positions over 650 keys
+    (1, 8, 2, 45000, 256, 4, 64, "f16", 9, True, (333,)),       # 36 rows: 4 rows in block 2, kv_start
+    (1, 16, 2, 40000, 256, 4, 32, "f16", 5, True, (39871,)),    # 40 rows over 129 keys
+    (1, 32, 2, 32768, 256, 4, 32, "bf16", 4, True, (32765,)),   # 3 keys: the first rows see none
+    (1, 16, 1, 16400, 256, 4, 32, "f16", 8, True, None),        # 128 rows over 16K keys
+], ids=["G16-q2", "G16-q3-bf16", "G16-q7-full", "G1-q20-bf16", "G4-q9-kvstart", "G8-q5-129keys",
+        "G16-q4-3keys-bf16", "G16-q8-N16K"])
+def test_rows32_blocks_match_oracle(device, case):
+    """More than 16 query rows per kv head at D = 256 with 4-bit codes over
+    long caches: the 32-row kernel (both 16-row halves of a block from one
+    dequantized tile, Q^T read from LDS), against the oracle at several split
+    counts, with causal masks, kv_start and partial blocks; repeated calls
+    are bitwise identical."""
+    B, Hq, Hkv, N, D, bits, gs, dtype, qL, causal, starts = case
+    rows = Hq // Hkv * qL
+    assert rows > 16 and N >= 16384 and rows * N >= 3 << 19 and B * Hq * qL * N < 1 << 24
+    rng = np.random.default_rng(91 + qL + Hq + N)
+    inp = make_inputs(rng, B, Hq, Hkv, N, D, bits, gs, dtype=dtype)
+    inp["q"] = affine.random_T(rng, (B, Hq, qL, D), dtype)
+    qi = np.arange(qL)[:, None] + (N - qL)
+    keep = np.ones((B, 1, qL, N), dtype=bool)
+    if causal:
+        keep &= (qi >= np.arange(N)[None, :])[None, None]
+    kw = {"causal": True} if causal else {}
+    if starts is not None:
+        st = np.array(starts)
+        keep &= (np.arange(N)[None, :] >= np.clip(st, 0, N)[:, None])[:, None, None, :]
+        kw["kv_start"] = torch.tensor(st, dtype=torch.int32, device=device)
+    want = oracle_out(inp, mask=keep)
+    want[~keep.any(axis=-1, keepdims=True).repeat(Hq, axis=1).repeat(D, axis=-1)] = 0.0
+    # The plan counts 32-row blocks: one workgroup per CU over B * H_kv * blocks.
+    g = to_dev(inp, device)
+    splits, _ = kernels.decode_plan(g["q"], g["kp"], g["vp"], g["ks"], g["vs"], g["kb"], g["vb"], scale=D ** -0.5,
+                                    bits=bits, group_size=gs)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    units = B * Hkv * ((rows + 31) // 32)
+    assert splits == max(1, min(cus // units, max(1, N // 128))), splits
+    for s in (0, 1, 3, 7):
+        got = _fused(inp, device, num_splits=s, **kw)
+        assert got.shape == (B, Hq, qL, D)
+        assert_close(got, want, f"{case} splits={s}")
+        again = _fused(inp, device, num_splits=s, **kw)
+        assert np.array_equal(got, again), f"splits={s}: repeated call differs"
+
+
 @pytest.mark.parametrize("qL", [6, 40], ids=["q6", "q40-rows"])
 def test_multi_query_kv_start_causal(device, qL):
     """qL > 1 with left padding and causal together (stream-K schedule when
