@@ -78,53 +78,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int oob = len + kTile;  // rows outside every descriptor: the loads read zero
   auto row_of = [&](int j) -> int { return j < J ? tile_of(j) * kTile : oob; };
 
-  Rsrcs rs;
-  {
-    const int64_t tok0 = s0;
-    auto rsrc = [&](const void* base, int64_t sb, int64_t shh, int64_t sn, int esz, int row_bytes, bool present) {
-      const uint8_t* p0 = static_cast<const uint8_t*>(base) +
-                          (static_cast<int64_t>(b) * sb + static_cast<int64_t>(kvh) * shh + tok0 * sn) * esz;
-      const uint32_t bytes =
-          (present && len > 0) ? static_cast<uint32_t>((len - 1) * sn * esz + row_bytes) : 0u;
-      return make_rsrc(p0, bytes);
-    };
-    constexpr int kRow = D * BITS / 8;
-    constexpr int kMeta = G::NG * 2;
-    rs.k = rsrc(p.kp, p.kp_sb, p.kp_sh, p.kp_sn, 4, kRow, true);
-    rs.v = rsrc(p.vp, p.vp_sb, p.vp_sh, p.vp_sn, 4, kRow, true);
-    rs.ks = rsrc(p.ks, p.ks_sb, p.ks_sh, p.ks_sn, 2, kMeta, true);
-    rs.vs = rsrc(p.vs, p.vs_sb, p.vs_sh, p.vs_sn, 2, kMeta, true);
-    rs.kb = rsrc(p.has_bias ? p.kb : p.ks, p.kb_sb, p.kb_sh, p.kb_sn, 2, kMeta, p.has_bias);
-    rs.vb = rsrc(p.has_bias ? p.vb : p.vs, p.vb_sb, p.vb_sh, p.vb_sn, 2, kMeta, p.has_bias);
-    rs.k_sn = static_cast<uint32_t>(p.kp_sn * 4);
-    rs.v_sn = static_cast<uint32_t>(p.vp_sn * 4);
-    rs.ks_sn = static_cast<uint32_t>(p.ks_sn * 2);
-    rs.vs_sn = static_cast<uint32_t>(p.vs_sn * 2);
-    rs.kb_sn = static_cast<uint32_t>(p.kb_sn * 2);
-    rs.vb_sn = static_cast<uint32_t>(p.vb_sn * 2);
-  }
-
-  // Per-lane byte offsets (the 16-row kernel's, whole-row K loads).
-  const int kg0 = (quad * G::QD) / GS;
-  const int gv = (r * G::NB) / GS;
-  const int vword = G::NG >= 2 ? quad % G::ND : 0;
+  const Rsrcs rs = tile_rsrcs<D, BITS, GS>(p, b, kvh, s0, len);
   LaneOffsets L;
-  L.k_r = quad * G::KW * 4 + (r >> 3) * 16 + (r & 7) * rs.k_sn;
-  L.ks_r = kg0 * 2 + r * rs.ks_sn;
-  L.kb_r = kg0 * 2 + r * rs.kb_sn;
-  L.v_r = r * G::VW * 4 + 4 * quad * rs.v_sn;
-  L.vs_r = vword * 4 + r * rs.vs_sn;
-  L.vb_r = vword * 4 + r * rs.vb_sn;
-  asm("" : "+v"(L.k_r), "+v"(L.ks_r), "+v"(L.kb_r), "+v"(L.v_r), "+v"(L.vs_r), "+v"(L.vb_r));
   VMetaLane vm;
-  {
-    const int dw = G::NG >= 2 ? gv / 2 : 0;
-    const int half = G::NG >= 2 ? gv % 2 : 0;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) vm.src[k] = (16 * dw + 4 * quad + k) * 4;
-    vm.sel = half ? 0x07060302u : 0x05040100u;
-    vm.shift = half ? 0u : 16u;
-  }
+  lane_setup<D, BITS, GS, true>(rs, quad, r, L, vm);  // whole-row K loads
 
   // Stage the block's 32 Q rows (zero rows for padding), two rows per
   // thread, each 16-byte piece already in the order the K dequantizer

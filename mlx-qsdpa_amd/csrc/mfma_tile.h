@@ -104,6 +104,65 @@ struct VMetaLane {
   uint32_t shift;
 };
 
+// Buffer descriptors over rows [s0, s0 + len) of (batch b, kv head kvh) of
+// the six K / V tensors, and their token strides in bytes.  Rows past them
+// (and every row of an absent bias) read as zero.
+template <int D, int BITS, int GS>
+__device__ __forceinline__ Rsrcs tile_rsrcs(const MfmaParams& p, int b, int kvh, int s0, int len) {
+  using G = Geo<D, BITS, GS>;
+  const int64_t tok0 = s0;
+  auto rsrc = [&](const void* base, int64_t sb, int64_t sh, int64_t sn, int esz, int row_bytes, bool present) {
+    const uint8_t* p0 = static_cast<const uint8_t*>(base) +
+                        (static_cast<int64_t>(b) * sb + static_cast<int64_t>(kvh) * sh + tok0 * sn) * esz;
+    const uint32_t bytes = (present && len > 0) ? static_cast<uint32_t>((len - 1) * sn * esz + row_bytes) : 0u;
+    return make_rsrc(p0, bytes);
+  };
+  constexpr int kRow = D * BITS / 8;
+  constexpr int kMeta = G::NG * 2;
+  Rsrcs rs;
+  rs.k = rsrc(p.kp, p.kp_sb, p.kp_sh, p.kp_sn, 4, kRow, true);
+  rs.v = rsrc(p.vp, p.vp_sb, p.vp_sh, p.vp_sn, 4, kRow, true);
+  rs.ks = rsrc(p.ks, p.ks_sb, p.ks_sh, p.ks_sn, 2, kMeta, true);
+  rs.vs = rsrc(p.vs, p.vs_sb, p.vs_sh, p.vs_sn, 2, kMeta, true);
+  rs.kb = rsrc(p.has_bias ? p.kb : p.ks, p.kb_sb, p.kb_sh, p.kb_sn, 2, kMeta, p.has_bias);
+  rs.vb = rsrc(p.has_bias ? p.vb : p.vs, p.vb_sb, p.vb_sh, p.vb_sn, 2, kMeta, p.has_bias);
+  rs.k_sn = static_cast<uint32_t>(p.kp_sn * 4);
+  rs.v_sn = static_cast<uint32_t>(p.vp_sn * 4);
+  rs.ks_sn = static_cast<uint32_t>(p.ks_sn * 2);
+  rs.vs_sn = static_cast<uint32_t>(p.vs_sn * 2);
+  rs.kb_sn = static_cast<uint32_t>(p.kb_sn * 2);
+  rs.vb_sn = static_cast<uint32_t>(p.vb_sn * 2);
+  return rs;
+}
+
+// Lane (quad, r)'s byte offsets of its loads within a tile (PK: whole-row K
+// loads, Geo::PairK) and where it gathers its tokens' V scales / biases.
+template <int D, int BITS, int GS, bool PK>
+__device__ __forceinline__ void lane_setup(const Rsrcs& rs, int quad, int r, LaneOffsets& L, VMetaLane& vm) {
+  using G = Geo<D, BITS, GS>;
+  const int kg0 = (quad * G::QD) / GS;  // first group of the lane's K quarter
+  const int gv = (r * G::NB) / GS;      // group of the lane's V dims
+  const int vword = G::NG >= 2 ? quad % G::ND : 0;  // V meta word this lane loads
+  L.k_r = PK ? quad * G::KW * 4 + (r >> 3) * 16 + (r & 7) * rs.k_sn : quad * G::KW * 4 + r * rs.k_sn;
+  L.ks_r = kg0 * 2 + r * rs.ks_sn;
+  L.kb_r = kg0 * 2 + r * rs.kb_sn;
+  L.v_r = r * G::VW * 4 + 4 * quad * rs.v_sn;
+  L.vs_r = vword * 4 + r * rs.vs_sn;
+  L.vb_r = vword * 4 + r * rs.vb_sn;
+  // Opaque to the optimizer: seeing r * stride inside, it folds a load's
+  // uniform row * stride + L into a per-lane (row + r) * stride, one
+  // quarter-rate v_mul_lo_u32 per load and tile.
+  asm("" : "+v"(L.k_r), "+v"(L.ks_r), "+v"(L.kb_r), "+v"(L.v_r), "+v"(L.vs_r), "+v"(L.vb_r));
+  // Token tau(quad, j) of a half sits in row 4*quad + (j & 3); its meta word
+  // gv / 2 was loaded by quad gv / 2.
+  const int dw = G::NG >= 2 ? gv / 2 : 0;
+  const int half = G::NG >= 2 ? gv % 2 : 0;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) vm.src[k] = (16 * dw + 4 * quad + k) * 4;
+  vm.sel = half ? 0x07060302u : 0x05040100u;
+  vm.shift = half ? 0u : 16u;
+}
+
 template <typename Tag, int D, int BITS, int GS>
 struct Kernel {
   static constexpr int kAux = load_policy<D, BITS>();
