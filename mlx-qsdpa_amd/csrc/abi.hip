@@ -47,8 +47,7 @@ bool prefill_supports(const qsdpa_decode_args* a);
 int prefill_num_splits(const qsdpa_decode_args* a, int cus);
 int launch_prefill_mfma(const qsdpa_decode_args* a, int splits, float* part_acc, float* part_ml,
                         hipStream_t stream);
-// Defined in decode_rows32.hip.
-bool rows32_supports(const qsdpa_decode_args* a);
+// Defined in decode_rows32.hip (rows32_supports: abi_internal.h).
 int rows32_num_splits(const qsdpa_decode_args* a, int cus);
 int launch_decode_rows32(const qsdpa_decode_args* a, int num_splits, float* part_acc, float* part_ml,
                          hipStream_t stream);

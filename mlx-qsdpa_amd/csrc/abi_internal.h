@@ -52,5 +52,8 @@ int launch_requant(const qsdpa_requant_args* const* jobs, int count, hipStream_t
 int launch_move_rows(const qsdpa_row_move* moves, int count, hipStream_t stream);
 int launch_decode(const qsdpa_decode_args* a, int num_splits, hipStream_t stream);
 int decode_plan(const qsdpa_decode_args* a, int* num_splits, int64_t* workspace_bytes);
+// Whether the 32-row decode kernel (decode_rows32.hip) takes a call; the
+// prefill kernel's routing defers to it for single row groups.
+bool rows32_supports(const qsdpa_decode_args* a);
 
 }  // namespace qsdpa

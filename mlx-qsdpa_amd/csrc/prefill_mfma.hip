@@ -769,6 +769,15 @@ bool prefill_supports(const qsdpa_decode_args* a) {
   // heads at q_len = 4 over 128K 58-59 against 73-75 us.
   if (a->D == 256 && static_cast<int64_t>(a->B) * a->H_q * a->q_len * a->N < (int64_t(1) << 24))
     return false;
+  // One row group per kv head at D = 256 goes to the 32-row decode kernel
+  // where that takes the call (4-bit codes, no mask tensor, ...): C3's heads
+  // at q_len = 8 over 64K / 128K keys 44.3-44.7 / 72.2-77.0 against
+  // 47.9-48.0 / 78.1-79.3 us per call here, q_len = 12 over 64K 66.3-72.3
+  // against 75.5-80.9.  From two groups on this kernel is as fast or faster
+  // (q_len = 16 over 32K / 64K / 128K 46.4-47.3 / 77.9-78.5 / 145.3-147.8
+  // there against 48.9-49.3 / 76.8-80.6 / 140.4-143.6 here, q_len = 64 over
+  // 128K 486.6-487.7 against 444.6-447.0).
+  if (a->D == 256 && rows < 2 * kPGroupRows && rows32_supports(a)) return false;
   const int64_t groups = (rows + kPGroupRows - 1) / kPGroupRows;
   if (groups * a->H_kv * a->B * kMaxPrefillSplits >= (int64_t(1) << 31)) return false;
   const int kq_bytes = a->D / 4 * a->bits / 8, vp_bytes = a->D / 8 * a->bits / 8;

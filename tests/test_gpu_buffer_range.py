@@ -125,7 +125,7 @@ def test_nan_past_the_end_prefill(device, case, qL):
 @pytest.mark.parametrize("dt", ["f16", "bf16"])
 def test_nan_past_the_end_prefill_d256(device, dt):
     """The D = 256 prefill kernel (32-key tiles; the call meets its routing
-    threshold: 128 rows per kv head, 2^24 row-key pairs), N = 32785 (17 keys
+    threshold: 256 rows per kv head, 2^24 row-key pairs), N = 32785 (17 keys
     into the last tile), rows past N NaN / all-ones, with and without
     kv_start; checked against the float64 torch oracle on the unpadded data
     (the numpy oracle takes about 15 s at this size)."""
@@ -133,7 +133,7 @@ def test_nan_past_the_end_prefill_d256(device, dt):
     from mlx_qsdpa_amd import kernels
 
     B, Hq, Hkv, N, D, bits, gs, qL = 1, 16, 2, 32785, 256, 4, 32, 32
-    assert Hq // Hkv * qL >= 128 and B * Hq * qL * N >= 1 << 24
+    assert Hq // Hkv * qL >= 256 and B * Hq * qL * N >= 1 << 24
     T = torch_dtype(dt)
     g = torch.Generator(device="cpu").manual_seed(41)
     q = torch.randn(B, Hq, qL, D, generator=g).to(T).to(device)

@@ -235,20 +235,24 @@ D256_CASES = [
     (2, 8, 2, 2700, 400, 4, 128, torch.float16, True, True),      # 1600 rows: partial last group
     (4, 16, 4, 2100, 128, 4, 64, torch.bfloat16, True, False),
     (1, 32, 8, 8200, 64, 8, 32, torch.float16, False, False),
-    (1, 32, 2, 65611, 8, 4, 32, torch.float16, True, False),      # one group per kv head: 128 key splits
+    (1, 32, 2, 65611, 8, 8, 32, torch.float16, True, False),      # one group per kv head: 128 key splits
     (1, 2, 2, 65601, 128, 8, 64, torch.bfloat16, True, False),    # C2's heads, one group: 128 key splits
 ]
 
 
-def _d256_routed(B, Hq, Hkv, N, L):
-    return Hq // Hkv * L >= 128 and B * Hq * L * N >= D256_PAIRS
+def _d256_routed(B, Hq, Hkv, N, L, bits=4):
+    """The call meets the D = 256 prefill routing (unmasked): two row groups
+    per kv head, or one with 8-bit codes (4-bit single groups go to the
+    32-row decode kernel), and 2^24 (row, key) pairs."""
+    rows = Hq // Hkv * L
+    return (rows >= 256 or (rows >= 128 and bits == 8)) and B * Hq * L * N >= D256_PAIRS
 
 
 @pytest.mark.parametrize("case", D256_CASES, ids=lambda c: "B{}_H{}x{}_N{}_L{}_b{}_g{}_{}_{}{}".format(
     *c[:7], str(c[7]).split(".")[-1], "causal" if c[8] else "full", "_sym" if c[9] else ""))
 def test_prefill_d256_matches_oracle(device, case):
     B, Hq, Hkv, N, L, bits, gs, dtype, causal, sym = case
-    assert _d256_routed(B, Hq, Hkv, N, L)
+    assert _d256_routed(B, Hq, Hkv, N, L, bits)
     print(f"prefill D=256 case {case}", flush=True)
     q, kq, vq = _inputs(B, Hq, Hkv, N, L, bits, gs, dtype, seed=N + L + 256, symmetric=sym, D=256)
     _check(q, kq, vq, bits, gs, f"D=256 case {case}", causal=causal)
@@ -272,7 +276,7 @@ def test_prefill_d256_short_key_ranges(device, keys):
 
 def test_prefill_d256_kv_start_and_masks(device):
     B, Hq, Hkv, N, L, bits, gs = 2, 16, 2, 16500, 32, 8, 32
-    assert _d256_routed(B, Hq, Hkv, N, L)
+    assert _d256_routed(B, Hq, Hkv, N, L, bits)
     for dtype in (torch.float16, torch.bfloat16):
         q, kq, vq = _inputs(B, Hq, Hkv, N, L, bits, gs, dtype, seed=13, D=256)
         ks = torch.tensor([19, 9000], dtype=torch.int32, device=device)  # starts inside a tile
@@ -321,7 +325,7 @@ def test_prefill_d256_bf16_huge_k_scales(device):
     """K groups with scales of 2^101 and more at D = 256 (the float32
     dequantization path for the waves that hold them)."""
     B, Hq, Hkv, N, L, bits, gs = 1, 16, 2, 33000, 32, 8, 64
-    assert _d256_routed(B, Hq, Hkv, N, L)
+    assert _d256_routed(B, Hq, Hkv, N, L, bits)
     q, kq, vq = _inputs(B, Hq, Hkv, N, L, bits, gs, torch.bfloat16, seed=33, D=256)
     q = (q.float() * 2.0 ** -108).bfloat16()
     huge = torch.zeros(N, dtype=torch.bool)
