@@ -377,6 +377,41 @@ def test_rows32_blocks_match_oracle(device, case):
         assert np.array_equal(got, again), f"splits={s}: repeated call differs"
 
 
+def test_rows32_strided_views_and_symmetric(device):
+    """The 32-row kernel over strided views: q and out as (B, qL, H, D)
+    buffers seen as (B, H, qL, D), K / V in capacity-padded buffers, with
+    and without biases (the symmetric format); bitwise equal to the same
+    call on contiguous copies."""
+    rng = np.random.default_rng(93)
+    B, Hq, Hkv, N, cap, D, qL = 1, 32, 2, 49200, 49300, 256, 3
+    assert Hq // Hkv * qL * N >= 3 << 19
+    for symmetric in (False, True):
+        inp = make_inputs(rng, B, Hq, Hkv, N, D, 4, 32, symmetric=symmetric)
+        inp["q"] = affine.random_T(rng, (B, Hq, qL, D), "f16")
+        g = to_dev(inp, device)
+        views = {}
+        for k in ("kp", "vp", "ks", "vs", "kb", "vb"):
+            t = g[k]
+            if t is None:
+                views[k] = None
+                continue
+            buf = torch.zeros((B, Hkv, cap, t.shape[-1]), dtype=t.dtype, device=device)
+            buf[:, :, :N] = t
+            views[k] = buf[:, :, :N]
+        q_bshd = g["q"].transpose(1, 2).contiguous()
+        q_view = q_bshd.transpose(1, 2)
+        assert not q_view.is_contiguous()
+        out_buf = torch.full((B, qL, Hq, D), float("nan"), dtype=torch.float16, device=device)
+        out_view = out_buf.transpose(1, 2)
+        kernels.decode(q_view, views["kp"], views["vp"], views["ks"], views["vs"], views["kb"], views["vb"],
+                       scale=D ** -0.5, bits=4, group_size=32, causal=True, out=out_view)
+        dense = kernels.decode(g["q"], g["kp"], g["vp"], g["ks"], g["vs"], g["kb"], g["vb"],
+                               scale=D ** -0.5, bits=4, group_size=32, causal=True)
+        torch.cuda.synchronize()
+        assert torch.equal(out_view, dense), f"symmetric={symmetric}: strided call differs"
+        assert_close(to_np(dense), oracle_out(inp, mask="causal"), f"rows32 symmetric={symmetric}")
+
+
 @pytest.mark.parametrize("qL", [6, 40], ids=["q6", "q40-rows"])
 def test_multi_query_kv_start_causal(device, qL):
     """qL > 1 with left padding and causal together (stream-K schedule when
