@@ -63,7 +63,11 @@ def parse_args(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=300)
-    ap.add_argument("--warmup", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=None,
+                    help="untimed steps before the timed ones (default: 2000 for the decode "
+                         "configurations c1, c2, c3, c5, whose first tens of milliseconds run "
+                         "below the steady clock: C3 measured 25.8-26.1 us per step after 30 "
+                         "warmup steps, 23.2-23.5 after 1000 to 3000; 30 for the other modes)")
     ap.add_argument("--config", default="c3", choices=sorted(CONFIGS) + ["c4"])
     ap.add_argument("--n", type=int, default=None, help="override the key count N")
     ap.add_argument("--kv-bytes", type=float, default=1.2e9,
@@ -609,6 +613,11 @@ def main(argv=None) -> int:
               "single-GPU in this build (sharding by kv head and by sequence is a design only).",
               file=sys.stderr)
         return 2
+    other_mode = args.crossover_sweep or args.rotating_prefill or args.config == "c4" or args.qlen > 1
+    if args.warmup is None:
+        # C4 appends a token per step, warmup included, so its lengths would
+        # drift with a long warmup.
+        args.warmup = 30 if other_mode else 2000
     if args.crossover_sweep:
         return run_crossover_sweep(args)
     if args.rotating_prefill:
