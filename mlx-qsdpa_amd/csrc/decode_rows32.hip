@@ -1,7 +1,7 @@
 // Decode of more than 16 query rows per kv head at D = 256 with 4-bit codes
-// (speculative decoding windows, short chunks; the prefill kernel takes the
-// large calls): 32 query rows per workgroup, each wave computing both 16-row
-// halves from one dequantized K / V tile.
+// and at D = 128 (speculative decoding windows, short chunks; the prefill
+// kernel takes the large calls): 32 query rows per workgroup, each wave
+// computing both 16-row halves from one dequantized K / V tile.
 //
 // Reference: the path these calls take there is the dequantize + SDPA
 // fallback (mlx_qsdpa/dispatch.py:68-83); the attention is the decode's
@@ -9,11 +9,12 @@
 //
 // The 16-row decode kernel (decode_mfma.hip) gives every block of 16 rows
 // its own workgroups, so each block streams the kv head and dequantizes it
-// again: at D = 256 the exact dequantization is about half of that kernel's
-// VALU work and the re-reads multiply its HBM bytes.  Here a block of 32
-// rows does both once.  The two halves' accumulators (128 VGPRs) leave no
-// room for Q^T in registers, so each QK step reads its B operands from the
-// staged Q rows in LDS (16 ds_read_b128 per wave and tile).  Everything else
+// again: the exact dequantization is about half of that kernel's VALU work
+// at D = 256 and two thirds at D = 128.  Here a block of 32 rows does it
+// once.  At D = 256 the two halves' accumulators (128 VGPRs) leave no room
+// for Q^T in registers, so each QK step reads its B operands from the
+// staged Q rows in LDS (16 ds_read_b128 per wave and tile at D = 256, 8 at
+// D = 128, which does the same).  Everything else
 // -- tiles, super-tiles, the waves' shares, the whole-row K loads, the
 // transposed V loads, the online softmax, the LDS merge of the 8 waves and
 // the partial rows -- is the 16-row kernel's, with two running (m, l) per
@@ -29,13 +30,12 @@ namespace {
 
 constexpr int kRows = 32;  // query rows per workgroup
 
-template <typename Tag, int GS>
+template <typename Tag, int D, int BITS, int GS>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_rows32_kernel(
     MfmaParams p) {
-  constexpr int D = 256, BITS = 4;
   using G = Geo<D, BITS, GS>;
   using K = Kernel<Tag, D, BITS, GS>;
-  static_assert(G::PairK, "whole-row K loads");
+  static_assert(!(D == 256 && BITS == 8), "D = 256 with 8-bit codes: no register room for two halves");
   constexpr int kRowF = D + 4;       // LDS floats per (wave, row) of the merge
   constexpr int kQRow = D * 2 + 16;  // bytes per staged Q row
   __shared__ __attribute__((aligned(16))) float s_acc[kWaves * 16 * kRowF];
@@ -81,32 +81,33 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   const Rsrcs rs = tile_rsrcs<D, BITS, GS>(p, b, kvh, s0, len);
   LaneOffsets L;
   VMetaLane vm;
-  lane_setup<D, BITS, GS, true>(rs, quad, r, L, vm);  // whole-row K loads
+  lane_setup<D, BITS, GS, G::PairK>(rs, quad, r, L, vm);
 
-  // Stage the block's 32 Q rows (zero rows for padding), two rows per
-  // thread, each 16-byte piece already in the order the K dequantizer
-  // produces the dims (float16: 0, 4, 1, 5, 2, 6, 3, 7).
+  // Stage the block's 32 Q rows (zero rows for padding), kThreads / (D / 8)
+  // rows per round, each 16-byte piece already in the order the K
+  // dequantizer produces the dims (float16 4-bit: 0, 4, 1, 5, 2, 6, 3, 7).
   {
     constexpr int kQChunks = D / 8;  // 16-byte pieces per row
+    constexpr int kRounds = kRows * kQChunks / kThreads;
+    static_assert(kRounds * kThreads == kRows * kQChunks, "whole staging rounds");
     const int qh = threadIdx.x / kQChunks, qc = threadIdx.x % kQChunks;
     const uint8_t* q0 = reinterpret_cast<const uint8_t*>(p.q) +
                         (static_cast<int64_t>(b) * p.q_sb + static_cast<int64_t>(kvh) * p.G * p.q_sh) * 2;
     const rsrc_t rq = make_rsrc(
         q0, static_cast<uint32_t>(((p.G - 1) * p.q_sh + static_cast<int64_t>(p.qL - 1) * p.q_sq) * 2 + D * 2));
-    static_assert(kThreads / kQChunks * 2 == kRows, "two staging rounds");
-    u4 qv[2];
+    u4 qv[kRounds];
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      const int row = qh + 16 * k;
+    for (int k = 0; k < kRounds; ++k) {
+      const int row = qh + (kThreads / kQChunks) * k;
       const int v = v0 + min(row, nh - 1);
       const int64_t off = (static_cast<int64_t>(v % p.G) * p.q_sh + static_cast<int64_t>(v / p.G) * p.q_sq) * 2;
       qv[k] = __builtin_amdgcn_raw_buffer_load_b128(rq, static_cast<uint32_t>(off + qc * 16), 0, 0);
     }
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      const int row = qh + 16 * k;
+    for (int k = 0; k < kRounds; ++k) {
+      const int row = qh + (kThreads / kQChunks) * k;
       u4 w = row < nh ? qv[k] : u4{0u, 0u, 0u, 0u};
-      if constexpr (Tag::kId == QSDPA_F16) {
+      if constexpr (Tag::kId == QSDPA_F16 && BITS == 4) {
         w = u4{perm(w[2], w[0], 0x05040100u), perm(w[2], w[0], 0x07060302u), perm(w[3], w[1], 0x05040100u),
                perm(w[3], w[1], 0x07060302u)};
       }
@@ -117,7 +118,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 
   typename K::Regs R;
   int j = wave;
-  K::template load_k<true>(R, rs, L, row_of(j));
+  K::template load_k<G::PairK>(R, rs, L, row_of(j));
   __builtin_amdgcn_sched_barrier(0);
   K::load_v(R, rs, L, row_of(j));
   __builtin_amdgcn_sched_barrier(0);
@@ -135,7 +136,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   while (j < J) {
     const int nj = next_pos(j);
     const int nrow = row_of(nj);
-    auto ik = [&](typename K::Regs& X) { K::template load_k<true>(X, rs, L, nrow); };
+    auto ik = [&](typename K::Regs& X) { K::template load_k<G::PairK>(X, rs, L, nrow); };
     auto iv = [&](typename K::Regs& X) { K::load_v(X, rs, L, nrow); };
     K::compute_tile2(R, p, qlds, 16 * kQRow, acc, mrun, lrun, s0 + row_of(j), s0, n_lane, quad, vm, ik, iv);
     j = nj;
@@ -174,20 +175,28 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 
 using Rows32Kernel = void (*)(MfmaParams);
 
-template <typename Tag>
+template <typename Tag, int D, int BITS>
 Rows32Kernel rows32_by_gs(int gs) {
-  return gs == 32 ? decode_rows32_kernel<Tag, 32> : gs == 64 ? decode_rows32_kernel<Tag, 64>
-                                                               : decode_rows32_kernel<Tag, 128>;
+  return gs == 32 ? decode_rows32_kernel<Tag, D, BITS, 32>
+       : gs == 64 ? decode_rows32_kernel<Tag, D, BITS, 64>
+                  : decode_rows32_kernel<Tag, D, BITS, 128>;
+}
+
+template <typename Tag>
+Rows32Kernel rows32_pick(const qsdpa_decode_args* a) {
+  if (a->D == 256) return rows32_by_gs<Tag, 256, 4>(a->group_size);
+  return a->bits == 4 ? rows32_by_gs<Tag, 128, 4>(a->group_size) : rows32_by_gs<Tag, 128, 8>(a->group_size);
 }
 
 }  // namespace
 
 // Calls for the 32-row kernel (those the prefill kernel does not take):
-// D = 256, 4-bit codes, several query positions with more than 16 rows per
-// kv head, no mask tensor, no folded append, and uniform splits (kv_start
-// only with one sequence: a left-padded batch takes the stream-K schedule of
-// the 16-row kernel); and enough work per kv head: at least 16K keys and
-// 1.5 * 2^20 (row, key) pairs.  Measured against the 16-row kernel, C3's
+// D = 256 with 4-bit codes or D = 128, several query positions with more
+// than 16 rows per kv head, no mask tensor, no folded append, and uniform
+// splits (kv_start only with one sequence: a left-padded batch takes the
+// stream-K schedule of the 16-row kernel); and enough work.  At D = 256, per
+// kv head: at least 16K keys and 1.5 * 2^20 (row, key) pairs.  Measured
+// against the 16-row kernel, C3's
 // heads, wall time per call on one box (both with splits rounded down to
 // one round of workgroups), 32-row kernel against 16-row kernel, in us:
 //   q_len = 2 over 16K / 32K / 64K keys   16.5 / 19.4-19.6 / 22.1-22.2
@@ -202,11 +211,23 @@ Rows32Kernel rows32_by_gs(int gs) {
 //   q_len = 8 over 32K                    29.7 against 33.9-34.1
 //   q_len = 12 / 16 over 16K              31.1 / 31.8-32.0 against 31.4 / 34.3-34.4
 //   q_len = 16 over 8K                    25.1-25.2 against 23.8
+//
+// At D = 128 (4- or 8-bit codes) the call's (row, key) pairs in all decide:
+// at least 2^23, and 16K keys.  C5's heads (B = 4, 8-bit bf16) at q_len = 8
+// over 16K / 32K keys 28.3 / 42.2-43.1 against 31.1-31.3 / 49.7-49.8 us,
+// q_len = 16 over 16K 39.8-40.4 against 53.1-53.7, q_len = 31 over 32K
+// 129.5-133.3 against 204.8-206.3; C1's heads (B = 1, 4-bit f16) at
+// q_len = 16 over 128K 27.9-28.2 against 34.9-35.0; but C5's heads at
+// q_len = 8 / 16 over 4K 18.1 / 23.4-23.6 against 16.8 / 21.5, C1's heads at
+// q_len = 5 over 64K 16.6-16.8 against 16.3-16.4 and q_len = 16 over 32K
+// 16.9 against 16.6.
 bool rows32_supports(const qsdpa_decode_args* a) {
-  if (a->D != 256 || a->bits != 4 || a->q_len <= 1 || a->mask.ptr || a->k_new.ptr) return false;
+  if (!(a->D == 128 || (a->D == 256 && a->bits == 4)) || a->q_len <= 1 || a->mask.ptr || a->k_new.ptr) return false;
   if (a->kv_start && a->B > 1) return false;
   const int64_t rows = static_cast<int64_t>(a->H_q / a->H_kv) * a->q_len;
-  return rows > 16 && a->N >= 16384 && rows * a->N >= (int64_t(3) << 19);
+  if (rows <= 16 || a->N < 16384) return false;
+  if (a->D == 128) return static_cast<int64_t>(a->B) * a->H_q * a->q_len * a->N >= (int64_t(1) << 23);
+  return rows * a->N >= (int64_t(3) << 19);
 }
 
 // Splits: as the 16-row kernel's (at most one workgroup per CU), over 32-row
@@ -225,7 +246,7 @@ int launch_decode_rows32(const qsdpa_decode_args* a, int num_splits, float* part
   MfmaParams p = mfma_params(a, num_splits, part_acc, part_ml);
   p.hb_count = (p.G * p.qL + kRows - 1) / kRows;
   const dim3 grid(num_splits, p.Hkv * p.hb_count, p.B);
-  Rows32Kernel k = a->dtype == QSDPA_F16 ? rows32_by_gs<F16>(a->group_size) : rows32_by_gs<BF16>(a->group_size);
+  Rows32Kernel k = a->dtype == QSDPA_F16 ? rows32_pick<F16>(a) : rows32_pick<BF16>(a);
   launch_profiled(k, grid, dim3(kThreads), stream, a->prof_begin, a->prof_end, p);
   return check_launch("decode_rows32");
 }

@@ -457,7 +457,7 @@ struct Kernel {
     }
   }
 
-  // ---- Two 16-row halves per wave (decode_rows32.hip; D = 256, 4-bit) ----
+  // ---- Two 16-row halves per wave (decode_rows32.hip) ----
   // One dequantized K / V tile feeds the MFMAs of both halves of a 32-row
   // block.  Q^T does not fit in registers beside two accumulator sets, so
   // each QK step reads its B operands from the staged Q rows in LDS: qlds is
@@ -470,7 +470,6 @@ struct Kernel {
   // ran the kernel out of registers), and feed four MFMAs.
   static __device__ __forceinline__ void qk_tile2(const Regs& R, const uint8_t* qlds, int half_bytes,
                                                   f4 (&S)[2][2]) {
-    static_assert(G::PairK, "the two-half kernel loads whole K rows");
     uint32_t s2[2][2], b2[2][2];
     float sf[2][2], bf[2][2];
     uint32_t kw[2][G::KW];
@@ -486,14 +485,19 @@ struct Kernel {
         b2[u][g] = splat_lo(bw);
         bf[u][g] = to_f32<Tag>(static_cast<uint16_t>(bw));
       }
-      // The whole-row exchange of qk_half (lanes r and r ^ 8).
+      if constexpr (G::PairK) {
+        // The whole-row exchange of qk_half (lanes r and r ^ 8).
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t a0 = R.kw[u][i], a1 = R.kw[u][4 + i];
-        const uint32_t x0 = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(a0), 0x128, 0xF, 0xF, false));
-        const uint32_t x1 = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(a1), 0x128, 0xF, 0xF, false));
-        kw[u][i] = lo8 ? a0 : x1;
-        kw[u][4 + i] = lo8 ? x0 : a1;
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t a0 = R.kw[u][i], a1 = R.kw[u][4 + i];
+          const uint32_t x0 = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(a0), 0x128, 0xF, 0xF, false));
+          const uint32_t x1 = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(a1), 0x128, 0xF, 0xF, false));
+          kw[u][i] = lo8 ? a0 : x1;
+          kw[u][4 + i] = lo8 ? x0 : a1;
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < G::KW; ++i) kw[u][i] = R.kw[u][i];
       }
 #pragma unroll
       for (int k = 0; k < 2; ++k) S[u][k] = f4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -559,7 +563,6 @@ struct Kernel {
                                                        int half_bytes, f4 (&acc)[2][G::NB], float (&mrun)[2],
                                                        float (&lrun)[2], int tb, int n0, const int (&n1)[2], int quad,
                                                        const VMetaLane& vm, IK&& issue_k, IV&& issue_v) {
-    static_assert(BITS == 4, "the two-half kernel is built for 4-bit codes");
     f4 S[2][2];  // [token half u][row half k]
     qk_tile2(R, qlds, half_bytes, S);
     issue_k(R);
@@ -601,27 +604,52 @@ struct Kernel {
         sv2[i] = perm(dS[2 * i + 1], dS[2 * i], vm.sel);
         bv2[i] = perm(dB[2 * i + 1], dB[2 * i], vm.sel);
       }
-      // X: nibbles 0-3 of tokens (2i, 2i+1), Y: nibbles 4-7 (as pv_f16).
-      uint32_t X[4][G::VW], Y[4][G::VW];
+      if constexpr (BITS == 4) {
+        // X: nibbles 0-3 of tokens (2i, 2i+1), Y: nibbles 4-7 (as pv_f16).
+        uint32_t X[4][G::VW], Y[4][G::VW];
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int w = 0; w < G::VW; ++w) {
-          X[i][w] = perm(R.vw[2 * i + 1][w], R.vw[2 * i][w], 0x05040100u);
-          Y[i][w] = perm(R.vw[2 * i + 1][w], R.vw[2 * i][w], 0x07060302u);
+          for (int w = 0; w < G::VW; ++w) {
+            X[i][w] = perm(R.vw[2 * i + 1][w], R.vw[2 * i][w], 0x05040100u);
+            Y[i][w] = perm(R.vw[2 * i + 1][w], R.vw[2 * i][w], 0x07060302u);
+          }
+        issue_v(R);
+#pragma unroll
+        for (int nb = 0; nb < G::NB; ++nb) {
+          const int w = nb >> 3, k = nb & 7;
+          uint32_t a[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const uint32_t src = k < 4 ? X[i][w] : Y[i][w];
+            a[i] = f16x2_fma(nib_codes(src, src >> 8, k & 3), sv2[i], bv2[i]);
+          }
+          acc[0][nb] = mfma<Tag>(a, pb[0], acc[0][nb]);
+          acc[1][nb] = mfma<Tag>(a, pb[1], acc[1][nb]);
         }
-      issue_v(R);
+      } else {
+        // Z0: bytes 0-1 of tokens (2i, 2i+1) interleaved, Z1: bytes 2-3 (as pv_f16).
+        uint32_t Z[4][G::VW][2];
 #pragma unroll
-      for (int nb = 0; nb < G::NB; ++nb) {
-        const int w = nb >> 3, k = nb & 7;
-        uint32_t a[4];
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const uint32_t src = k < 4 ? X[i][w] : Y[i][w];
-          a[i] = f16x2_fma(nib_codes(src, src >> 8, k & 3), sv2[i], bv2[i]);
+          for (int w = 0; w < G::VW; ++w) {
+            Z[i][w][0] = perm(R.vw[2 * i + 1][w], R.vw[2 * i][w], 0x05010400u);
+            Z[i][w][1] = perm(R.vw[2 * i + 1][w], R.vw[2 * i][w], 0x07030602u);
+          }
+        issue_v(R);
+#pragma unroll
+        for (int nb = 0; nb < G::NB; ++nb) {
+          const int w = nb >> 2, k = nb & 3;
+          uint32_t a[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const uint32_t t = perm(kMagic8, Z[i][w][k >> 1], (k & 1) ? kSelB23 : kSelB01);
+            a[i] = f16x2_fma(f16x2_sub1024(t), sv2[i], bv2[i]);
+          }
+          acc[0][nb] = mfma<Tag>(a, pb[0], acc[0][nb]);
+          acc[1][nb] = mfma<Tag>(a, pb[1], acc[1][nb]);
         }
-        acc[0][nb] = mfma<Tag>(a, pb[0], acc[0][nb]);
-        acc[1][nb] = mfma<Tag>(a, pb[1], acc[1][nb]);
       }
     } else {
       float svf[8], bvf[8];
@@ -631,16 +659,17 @@ struct Kernel {
         bvf[j] = __builtin_bit_cast(float, (dB[j] << vm.shift) & 0xFFFF0000u);
       }
       uint32_t lo[8][G::VW], hi[8][G::VW];
+      if constexpr (BITS == 4) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
+        for (int j = 0; j < 8; ++j)
 #pragma unroll
-        for (int w = 0; w < G::VW; ++w) {
-          lo[j][w] = R.vw[j][w] & 0x0F0F0F0Fu;         // nibbles 0, 2, 4, 6 as bytes
-          hi[j][w] = (R.vw[j][w] >> 4) & 0x0F0F0F0Fu;  // nibbles 1, 3, 5, 7
-        }
+          for (int w = 0; w < G::VW; ++w) {
+            lo[j][w] = R.vw[j][w] & 0x0F0F0F0Fu;         // nibbles 0, 2, 4, 6 as bytes
+            hi[j][w] = (R.vw[j][w] >> 4) & 0x0F0F0F0Fu;  // nibbles 1, 3, 5, 7
+          }
+      }
 #pragma unroll
       for (int nb = 0; nb < G::NB; ++nb) {
-        const int w = nb >> 3, k = nb & 7;
         uint32_t a[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -648,8 +677,15 @@ struct Kernel {
 #pragma unroll
           for (int e = 0; e < 2; ++e) {
             const int j = 2 * i + e;
-            const uint32_t src = (k & 1) ? hi[j][w] : lo[j][w];
-            c[e] = fmaf(svf[j], static_cast<float>((src >> (8 * (k >> 1))) & 0xFFu), bvf[j]);
+            if constexpr (BITS == 4) {
+              const int w = nb >> 3, k = nb & 7;
+              const uint32_t src = (k & 1) ? hi[j][w] : lo[j][w];
+              c[e] = static_cast<float>((src >> (8 * (k >> 1))) & 0xFFu);
+            } else {
+              const int w = nb >> 2, k = nb & 3;
+              c[e] = static_cast<float>((R.vw[j][w] >> (8 * k)) & 0xFFu);
+            }
+            c[e] = fmaf(svf[j], c[e], bvf[j]);
           }
           a[i] = pack_T2<Tag>(c[0], c[1]);
         }

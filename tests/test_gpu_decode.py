@@ -337,17 +337,26 @@ def test_row_blocks_match_oracle(device, case):
     (1, 16, 2, 40000, 256, 4, 32, "f16", 5, True, (39871,)),    # 40 rows over 129 keys
     (1, 32, 2, 32768, 256, 4, 32, "bf16", 4, True, (32765,)),   # 3 keys: the first rows see none
     (1, 16, 1, 16400, 256, 4, 32, "f16", 8, True, None),        # 128 rows over 16K keys
+    # D = 128, 4- and 8-bit: 2^23 (row, key) pairs in all
+    (4, 16, 4, 16400, 128, 8, 128, "bf16", 8, True, None),      # C5's heads: 32 rows
+    (1, 8, 2, 131100, 128, 4, 64, "f16", 16, True, None),       # C1's heads: 64 rows over 128K keys
+    (2, 16, 4, 70000, 128, 4, 32, "f16", 5, False, None),       # 20 rows, full attention
+    (1, 4, 4, 140000, 128, 8, 64, "bf16", 20, True, (139300,)), # G = 1: 20 positions over 700 keys
+    (1, 32, 8, 40000, 128, 4, 128, "bf16", 9, True, None),      # 36 rows: 4 in block 2
 ], ids=["G16-q2", "G16-q3-bf16", "G16-q7-full", "G1-q20-bf16", "G4-q9-kvstart", "G8-q5-129keys",
-        "G16-q4-3keys-bf16", "G16-q8-N16K"])
+        "G16-q4-3keys-bf16", "G16-q8-N16K", "D128-c5-q8", "D128-c1-q16-128K", "D128-G4-q5-full",
+        "D128-G1-q20-kvstart", "D128-G4-q9-bf16"])
 def test_rows32_blocks_match_oracle(device, case):
-    """More than 16 query rows per kv head at D = 256 with 4-bit codes over
-    long caches: the 32-row kernel (both 16-row halves of a block from one
-    dequantized tile, Q^T read from LDS), against the oracle at several split
-    counts, with causal masks, kv_start and partial blocks; repeated calls
-    are bitwise identical."""
+    """More than 16 query rows per kv head over long caches, at D = 256
+    with 4-bit codes and at D = 128: the 32-row kernel (both 16-row halves
+    of a block from one dequantized tile, Q^T read from LDS), against the
+    oracle at several split counts, with causal masks, kv_start and partial
+    blocks; repeated calls are bitwise identical."""
     B, Hq, Hkv, N, D, bits, gs, dtype, qL, causal, starts = case
     rows = Hq // Hkv * qL
-    assert rows > 16 and N >= 16384 and rows * N >= 3 << 19 and B * Hq * qL * N < 1 << 24
+    enough = B * Hq * qL * N >= 1 << 23 if D == 128 else rows * N >= 3 << 19
+    assert 16 < rows < 128 or (D == 256 and B * Hq * qL * N < 1 << 24)  # not the prefill kernel's
+    assert rows > 16 and N >= 16384 and enough
     rng = np.random.default_rng(91 + qL + Hq + N)
     inp = make_inputs(rng, B, Hq, Hkv, N, D, bits, gs, dtype=dtype)
     inp["q"] = affine.random_T(rng, (B, Hq, qL, D), dtype)
