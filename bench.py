@@ -67,7 +67,8 @@ def parse_args(argv=None):
                     help="untimed steps before the timed ones (default: 2000 for the decode "
                          "configurations c1, c2, c3, c5, whose first tens of milliseconds run "
                          "below the steady clock: C3 measured 25.8-26.1 us per step after 30 "
-                         "warmup steps, 23.2-23.5 after 1000 to 3000; 30 for the other modes)")
+                         "warmup steps, 23.2-23.5 after 1000 to 3000; 300 for c4, 68.3-69.4 "
+                         "after 30 and 62.9-63.2 after 300; 30 for the other modes)")
     ap.add_argument("--config", default="c3", choices=sorted(CONFIGS) + ["c4"])
     ap.add_argument("--n", type=int, default=None, help="override the key count N")
     ap.add_argument("--kv-bytes", type=float, default=1.2e9,
@@ -240,6 +241,10 @@ def run_c4(args) -> int:
     gen.manual_seed(args.seed)
     lengths = torch.randint(c["len_lo"], c["len_hi"] + 1, (B,), generator=gen)
     lmax = int(lengths.max())
+    # Every step appends a key to each sequence, warmup included: the
+    # sequences start `warmup` keys shorter, so that the timed steps see the
+    # drawn lengths.
+    start = (lengths - args.warmup).clamp(min=1)
     total = args.warmup + 2 * args.steps
     cap = lmax + total
     W, G = D * bits // 32, D // gs
@@ -258,7 +263,7 @@ def run_c4(args) -> int:
             kernels.quantize_into(w, kv, t0, bits, gs)
     q = torch.randn((B, Hq, 1, D), generator=g, device=device, dtype=torch.float32).to(T)
     new = [torch.randn((B, Hkv, 1, D), generator=g, device=device, dtype=torch.float32).to(T) for _ in range(2)]
-    kv_start = (lmax - lengths).to(device=device, dtype=torch.int32)
+    kv_start = (lmax - start).to(device=device, dtype=torch.int32)
     torch.cuda.synchronize()
 
     # Launch arguments built once: each step only moves the decode's key
@@ -303,7 +308,7 @@ def run_c4(args) -> int:
     # then cache_sdpa with kv_start = the left padding, per step.
     import mlx_qsdpa_amd as mq
 
-    cache = mq.BatchQuantizedSDPACache((lmax - lengths).tolist(), bits=bits, group_size=gs)
+    cache = mq.BatchQuantizedSDPACache((lmax - start).tolist(), bits=bits, group_size=gs)
     for t0_ in range(0, lmax, chunk):
         n_ = min(chunk, lmax - t0_)
         kk = torch.randn((B, Hkv, n_, D), generator=g, device=device, dtype=torch.float32).to(T)
@@ -316,20 +321,42 @@ def run_c4(args) -> int:
         kq, vq = cache.update_and_fetch(new[0], new[1])
         return mq.cache_sdpa(q, kq, vq, cache, kv_start=cache.kv_start(device))
 
+    def cap_now():
+        return cache._keys[0].shape[2]
+
     for _ in range(args.warmup):
         api_step()
-    torch.cuda.synchronize()
-    cap0 = cache._keys[0].shape[2]
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
+    # The cache grows by 256 slots when full (a concatenation of every
+    # buffer, as the reference's cache does).  Time the steady steps between
+    # two growths, and one growing step on its own.
+    cap0 = cap_now()
+    for _ in range(cache.step + 1):
+        if cap_now() != cap0:
+            break
         api_step()
     torch.cuda.synchronize()
-    api_us = (time.perf_counter() - t0) / args.steps * 1e6
-    grew = cache._keys[0].shape[2] != cap0
+    api_steps = min(args.steps, cache.step - 2)
+    cap1 = cap_now()
+    t0 = time.perf_counter()
+    for _ in range(api_steps):
+        api_step()
+    torch.cuda.synchronize()
+    api_us = (time.perf_counter() - t0) / api_steps * 1e6
+    grew = cap_now() != cap1
+    growth_us = None
+    for _ in range(cache.step + 1):  # on to the next growth, each step timed alone
+        before = cap_now()
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        api_step()
+        torch.cuda.synchronize()
+        if cap_now() != before:
+            growth_us = (time.perf_counter() - t1) * 1e6
+            break
     del cache
 
     us_step = wall / args.steps * 1e6
-    valid = lambda n_: int((lengths + (n_ + 1 - lmax)).sum())  # noqa: E731 (keys per sequence after the append)
+    valid = lambda n_: int((start + (n_ + 1 - lmax)).sum())  # noqa: E731 (keys per sequence after the append)
     bytes_wall = np.mean([metric.decode_bytes(B, Hq, Hkv, D, bits, gs, valid(k))
                           for k in range(n_first, n_first + args.steps)])
     bytes_kern = np.mean([metric.decode_bytes(B, Hq, Hkv, D, bits, gs, valid(k))
@@ -337,7 +364,8 @@ def run_c4(args) -> int:
     step_gbps = bytes_wall / (us_step * 1e-6) / 1e9
     kern_gbps = bytes_kern / (kern_us * 1e-6) / 1e9
     print(f"bench: c4 {us_step:.2f} us/step wall (append + decode), decode kernel {kern_us:.2f} us "
-          f"({kern_gbps:.0f} GB/s), splits={splits}; API path {api_us:.2f} us/step", file=sys.stderr,
+          f"({kern_gbps:.0f} GB/s), splits={splits}; API path {api_us:.2f} us/step between cache growths, "
+          f"a growing step {growth_us or 0:.0f} us", file=sys.stderr,
           flush=True)
     workload = (f"c4: batched decode B={B} H_q={Hq} H_kv={Hkv} D={D} {bits}-bit gs={gs} f16, lengths "
                 f"U[{c['len_lo']},{c['len_hi']}] left-padded, append + decode per step (one launch)")
@@ -351,7 +379,8 @@ def run_c4(args) -> int:
                    "num_splits": splits},
         "effective_gbps": round(step_gbps, 1),
         "pct_hbm_peak": round(100.0 * step_gbps / HBM_PEAK_GBPS, 2),
-        "api_path": {"us_per_step": round(api_us, 3), "cache_grew_in_timed_steps": grew,
+        "api_path": {"us_per_step": round(api_us, 3), "steps": api_steps, "cache_grew_in_timed_steps": grew,
+                     "growth_step_us": None if growth_us is None else round(growth_us, 1),
                      "call": "BatchQuantizedSDPACache.update_and_fetch + cache_sdpa(kv_start=left padding)"},
         "roofline": {"bound": "hbm", "achieved": round(kern_gbps, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(kern_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
@@ -615,9 +644,10 @@ def main(argv=None) -> int:
         return 2
     other_mode = args.crossover_sweep or args.rotating_prefill or args.config == "c4" or args.qlen > 1
     if args.warmup is None:
-        # C4 appends a token per step, warmup included, so its lengths would
-        # drift with a long warmup.
-        args.warmup = 30 if other_mode else 2000
+        # C4 (20 ms at 300 steps) starts its sequences that many keys
+        # shorter, as it appends one per step.
+        args.warmup = 300 if args.config == "c4" and not (args.crossover_sweep or args.rotating_prefill) \
+            else 30 if other_mode else 2000
     if args.crossover_sweep:
         return run_crossover_sweep(args)
     if args.rotating_prefill:
