@@ -19,7 +19,7 @@
 // transposed V loads, the online softmax, the LDS merge of the 8 waves and
 // the partial rows -- is the 16-row kernel's, with two running (m, l) per
 // lane (row r of each half).  Uniform key splits, the merge kernel for the
-// partials, no mask tensor (such calls keep the 16-row kernel).
+// partials; a mask tensor (its own instantiation, MASK) only at D = 128.
 #include "abi_internal.h"
 #include "mfma_tile.h"
 #include "wave_split.h"
@@ -30,12 +30,13 @@ namespace {
 
 constexpr int kRows = 32;  // query rows per workgroup
 
-template <typename Tag, int D, int BITS, int GS>
+template <typename Tag, int D, int BITS, int GS, bool MASK>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_rows32_kernel(
     MfmaParams p) {
   using G = Geo<D, BITS, GS>;
   using K = Kernel<Tag, D, BITS, GS>;
   static_assert(!(D == 256 && BITS == 8), "D = 256 with 8-bit codes: no register room for two halves");
+  static_assert(!(D == 256 && MASK), "D = 256: no register room for the mask values");
   constexpr int kRowF = D + 4;       // LDS floats per (wave, row) of the merge
   constexpr int kQRow = D * 2 + 16;  // bytes per staged Q row
   __shared__ __attribute__((aligned(16))) float s_acc[kWaves * 16 * kRowF];
@@ -57,10 +58,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int nh = min(kRows, p.G * p.qL - v0);
   const int n_end = p.causal ? min(p.N, max(0, p.N - p.qL + (v0 + nh - 1) / p.G + 1)) : p.N;
   int n_lane[2];
+  int64_t mrow[2];  // the lane's mask rows (MASK)
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
-    const int iq = (v0 + min(16 * k + r, nh - 1)) / p.G;
+    const int v = v0 + min(16 * k + r, nh - 1);
+    const int iq = v / p.G;
     n_lane[k] = p.causal ? min(n_end, max(0, p.N - p.qL + iq + 1)) : n_end;
+    mrow[k] = static_cast<int64_t>(b) * p.m_sb + static_cast<int64_t>(kvh * p.G + v % p.G) * p.m_sh +
+              static_cast<int64_t>(iq) * p.m_sq;
   }
 
   // Keys [s0, n_end), 32-token tiles in super-tiles; split x of S owns
@@ -138,7 +143,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     const int nrow = row_of(nj);
     auto ik = [&](typename K::Regs& X) { K::template load_k<G::PairK>(X, rs, L, nrow); };
     auto iv = [&](typename K::Regs& X) { K::load_v(X, rs, L, nrow); };
-    K::compute_tile2(R, p, qlds, 16 * kQRow, acc, mrun, lrun, s0 + row_of(j), s0, n_lane, quad, vm, ik, iv);
+    K::template compute_tile2<MASK>(R, p, qlds, 16 * kQRow, acc, mrun, lrun, s0 + row_of(j), s0, n_lane, quad, mrow,
+                                    vm, ik, iv);
     j = nj;
   }
 
@@ -175,24 +181,33 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 
 using Rows32Kernel = void (*)(MfmaParams);
 
-template <typename Tag, int D, int BITS>
+template <typename Tag, int D, int BITS, bool MASK>
 Rows32Kernel rows32_by_gs(int gs) {
-  return gs == 32 ? decode_rows32_kernel<Tag, D, BITS, 32>
-       : gs == 64 ? decode_rows32_kernel<Tag, D, BITS, 64>
-                  : decode_rows32_kernel<Tag, D, BITS, 128>;
+  return gs == 32 ? decode_rows32_kernel<Tag, D, BITS, 32, MASK>
+       : gs == 64 ? decode_rows32_kernel<Tag, D, BITS, 64, MASK>
+                  : decode_rows32_kernel<Tag, D, BITS, 128, MASK>;
+}
+
+template <typename Tag, bool MASK>
+Rows32Kernel rows32_d128(const qsdpa_decode_args* a) {
+  return a->bits == 4 ? rows32_by_gs<Tag, 128, 4, MASK>(a->group_size) : rows32_by_gs<Tag, 128, 8, MASK>(a->group_size);
 }
 
 template <typename Tag>
 Rows32Kernel rows32_pick(const qsdpa_decode_args* a) {
-  if (a->D == 256) return rows32_by_gs<Tag, 256, 4>(a->group_size);
-  return a->bits == 4 ? rows32_by_gs<Tag, 128, 4>(a->group_size) : rows32_by_gs<Tag, 128, 8>(a->group_size);
+  if (a->D == 256) return rows32_by_gs<Tag, 256, 4, false>(a->group_size);
+  return a->mask.ptr ? rows32_d128<Tag, true>(a) : rows32_d128<Tag, false>(a);
 }
 
 }  // namespace
 
 // Calls for the 32-row kernel (those the prefill kernel does not take):
 // D = 256 with 4-bit codes or D = 128, several query positions with more
-// than 16 rows per kv head, no mask tensor, no folded append, and uniform
+// than 16 rows per kv head, a mask tensor only at D = 128 (C5's heads with
+// a bool mask at q_len = 8 over 16K / 64K keys 32.1-32.2 / 89.1-89.5
+// against 34.1-34.3 / 113.9-114.9 us, with an additive one at q_len = 16
+// over 32K 85.1-89.5 against 118.3-119.6; C1's heads with a bool mask at
+// q_len = 16 over 128K 35.7-35.8 against 43.1-43.5), no folded append, and uniform
 // splits (kv_start only with one sequence: a left-padded batch takes the
 // stream-K schedule of the 16-row kernel); and enough work.  At D = 256, per
 // kv head: at least 16K keys and 1.5 * 2^20 (row, key) pairs.  Measured
@@ -222,7 +237,8 @@ Rows32Kernel rows32_pick(const qsdpa_decode_args* a) {
 // q_len = 5 over 64K 16.6-16.8 against 16.3-16.4 and q_len = 16 over 32K
 // 16.9 against 16.6.
 bool rows32_supports(const qsdpa_decode_args* a) {
-  if (!(a->D == 128 || (a->D == 256 && a->bits == 4)) || a->q_len <= 1 || a->mask.ptr || a->k_new.ptr) return false;
+  if (!(a->D == 128 || (a->D == 256 && a->bits == 4)) || a->q_len <= 1 || a->k_new.ptr) return false;
+  if (a->mask.ptr && a->D != 128) return false;  // D = 256: no register room for the mask values
   if (a->kv_start && a->B > 1) return false;
   const int64_t rows = static_cast<int64_t>(a->H_q / a->H_kv) * a->q_len;
   if (rows <= 16 || a->N < 16384) return false;

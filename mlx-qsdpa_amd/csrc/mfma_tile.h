@@ -557,17 +557,25 @@ struct Kernel {
 
   // One tile for a 32-row block: QK of both halves, their online softmax,
   // PV of both halves from one dequantized V^T.  n1[k]: the lane's end of
-  // keys in half k.  No mask tensor.
-  template <typename IK, typename IV>
+  // keys in half k.  MASK: a mask tensor's values for the lane's rows mrow[k]
+  // (loaded before the next tile's K loads, as compute_tile does).
+  template <bool MASK, typename IK, typename IV>
   static __device__ __forceinline__ void compute_tile2(Regs& R, const MfmaParams& p, const uint8_t* qlds,
                                                        int half_bytes, f4 (&acc)[2][G::NB], float (&mrun)[2],
                                                        float (&lrun)[2], int tb, int n0, const int (&n1)[2], int quad,
-                                                       const VMetaLane& vm, IK&& issue_k, IV&& issue_v) {
+                                                       const int64_t (&mrow)[2], const VMetaLane& vm, IK&& issue_k,
+                                                       IV&& issue_v) {
+    float mv[2][8];
+    if constexpr (MASK) {
+#pragma unroll
+      for (int k = 0; k < 2; ++k)
+        mask_tile<8>(p, mrow[k], tb + 4 * quad, tb + kTile <= p.N, [](int j) { return tau(0, j); }, mv[k]);
+    }
     f4 S[2][2];  // [token half u][row half k]
     qk_tile2(R, qlds, half_bytes, S);
     issue_k(R);
 
-    const bool fold = p.qscale > 0.0f;
+    const bool fold = !MASK && p.qscale > 0.0f;
     const float ea = fold ? p.qscale : 1.0f;
     const bool partial = tb + kTile > min(n1[0], n1[1]) || tb < n0;
     uint32_t pb[2][4], pb_lo[2][4];
@@ -579,6 +587,10 @@ struct Kernel {
       if (!fold) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) sc[j] *= p.qscale;
+      }
+      if constexpr (MASK) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) sc[j] += mv[k][j];
       }
       if (__builtin_expect(partial, 0)) {
 #pragma unroll

@@ -386,6 +386,41 @@ def test_rows32_blocks_match_oracle(device, case):
         assert np.array_equal(got, again), f"splits={s}: repeated call differs"
 
 
+@pytest.mark.parametrize("case,mk", [
+    ((4, 16, 4, 16400, 128, 8, 128, "bf16", 8), "bool"),
+    ((2, 16, 4, 65600, 128, 4, 32, "f16", 8), "additive"),
+    ((1, 8, 2, 120000, 128, 4, 64, "f16", 9), "bool-causal"),
+], ids=["c5-q8-bool", "G4-q8-additive-per-head", "c1-q9-bool-causal"])
+def test_rows32_masked_d128(device, case, mk):
+    """Mask tensors on the 32-row kernel (D = 128): a bool mask broadcast
+    over heads, an additive per-(head, position) mask with -inf entries, and
+    a bool mask with the causal flag, against the oracle."""
+    B, Hq, Hkv, N, D, bits, gs, dtype, qL = case
+    assert Hq // Hkv * qL > 16 and N >= 16384 and B * Hq * qL * N >= 1 << 23
+    rng = np.random.default_rng(97 + qL + N)
+    inp = make_inputs(rng, B, Hq, Hkv, N, D, bits, gs, dtype=dtype)
+    inp["q"] = affine.random_T(rng, (B, Hq, qL, D), dtype)
+    kw = {}
+    if mk.startswith("bool"):
+        keep = rng.random((B, 1, qL, N)) < 0.7
+        keep[..., -1] = True
+        m_np, kw["mask"] = keep, torch.from_numpy(keep).to(device)
+        if mk == "bool-causal":
+            kw["causal"] = True
+            qi = np.arange(qL)[:, None] + (N - qL)
+            m_np = keep & (qi >= np.arange(N)[None, :])[None, None]
+    else:
+        add = (rng.standard_normal((1, Hq, qL, N)) * 2).astype(np.float32)
+        add[rng.random(add.shape) < 0.2] = -np.inf
+        add[..., -1] = 0.0
+        add = add.astype(np.float16).astype(np.float32)
+        m_np, kw["mask"] = add, torch.from_numpy(add).to(device, torch.float16)
+    want = oracle_out(inp, mask=m_np)
+    for s in (0, 1, 5):
+        got = _fused(inp, device, num_splits=s, **kw)
+        assert_close(got, want, f"{case} {mk} splits={s}")
+
+
 def test_rows32_strided_views_and_symmetric(device):
     """The 32-row kernel over strided views: q and out as (B, qL, H, D)
     buffers seen as (B, H, qL, D), K / V in capacity-padded buffers, with
