@@ -50,7 +50,7 @@ int launch_prefill_mfma(const qsdpa_decode_args* a, int splits, float* part_acc,
 // Defined in decode_rows32.hip (rows32_supports: abi_internal.h).
 int rows32_num_splits(const qsdpa_decode_args* a, int cus);
 int launch_decode_rows32(const qsdpa_decode_args* a, int num_splits, float* part_acc, float* part_ml,
-                         hipStream_t stream);
+                         int units, int* sched, hipStream_t stream);
 
 
 namespace {
@@ -278,7 +278,7 @@ int run_decode(const qsdpa_decode_args* args, int splits, void* workspace, hipSt
   const bool append_inside = fused_append(args, prefill, mfma);
   if (args->k_new.ptr && !append_inside && (rc = launch_append_quantize(args, s))) return rc;
   if (prefill) rc = launch_prefill_mfma(args, splits, part_acc, part_ml, s);
-  else if (mfma && rows32_supports(args)) rc = launch_decode_rows32(args, splits, part_acc, part_ml, s);
+  else if (mfma && rows32_supports(args)) rc = launch_decode_rows32(args, splits, part_acc, part_ml, units, sched, s);
   else if (mfma)
     rc = launch_decode_mfma(args, splits, part_acc, part_ml, units, sched,
                             fused ? static_cast<unsigned*>(workspace) : nullptr, append_inside, s);

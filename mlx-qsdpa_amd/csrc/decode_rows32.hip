@@ -18,8 +18,9 @@
 // -- tiles, super-tiles, the waves' shares, the whole-row K loads, the
 // transposed V loads, the online softmax, the LDS merge of the 8 waves and
 // the partial rows -- is the 16-row kernel's, with two running (m, l) per
-// lane (row r of each half).  Uniform key splits, the merge kernel for the
-// partials; a mask tensor (its own instantiation, MASK) only at D = 128.
+// lane (row r of each half).  Uniform key splits, or for left-padded
+// batches the 16-row kernel's stream-K schedule (SK); the merge kernel for
+// the partials; a mask tensor (its own instantiation, MASK) only at D = 128.
 #include "abi_internal.h"
 #include "mfma_tile.h"
 #include "wave_split.h"
@@ -30,26 +31,28 @@ namespace {
 
 constexpr int kRows = 32;  // query rows per workgroup
 
+template <int D>
+constexpr int kRowFloats = D + 4;  // LDS floats per (wave, row) of the merge
+template <int D>
+constexpr int kQRowBytes = D * 2 + 16;  // bytes per staged Q row
+
+// One segment of a block's keys (sequence b): the super-tiles t_lo,
+// t_lo + stride, ... up to jmax positions (uniform splits: split x of S from
+// x with stride S; the stream-K schedule: a unit's consecutive tiles of one
+// sequence), merged over the waves and stored as the output (one split) or
+// the partials at column `col`.  Called by the whole workgroup.
 template <typename Tag, int D, int BITS, int GS, bool MASK>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_rows32_kernel(
-    MfmaParams p) {
+__device__ __forceinline__ void rows32_segment(const MfmaParams& p, float* s_acc, float (*s_ml)[16][2],
+                                               uint8_t* s_q, int hblk, int kvh, int b, int t_lo, int stride,
+                                               int jmax, int col) {
   using G = Geo<D, BITS, GS>;
   using K = Kernel<Tag, D, BITS, GS>;
-  static_assert(!(D == 256 && BITS == 8), "D = 256 with 8-bit codes: no register room for two halves");
-  static_assert(!(D == 256 && MASK), "D = 256: no register room for the mask values");
-  constexpr int kRowF = D + 4;       // LDS floats per (wave, row) of the merge
-  constexpr int kQRow = D * 2 + 16;  // bytes per staged Q row
-  __shared__ __attribute__((aligned(16))) float s_acc[kWaves * 16 * kRowF];
-  __shared__ float s_ml[kWaves][16][2];
-  __shared__ __attribute__((aligned(16))) uint8_t s_q[kRows * kQRow];
-
+  constexpr int kRowF = kRowFloats<D>;
+  constexpr int kQRow = kQRowBytes<D>;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int quad = lane >> 4;
   const int r = lane & 15;
-  const int hblk = blockIdx.y % p.hb_count;
-  const int kvh = blockIdx.y / p.hb_count;
-  const int b = blockIdx.z;
 
   // The block's rows v0 .. v0 + nh - 1 of the kv head's G * qL rows (row v:
   // position v / G of head kvh * G + v % G); lane r computes row r of each
@@ -68,14 +71,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
               static_cast<int64_t>(iq) * p.m_sq;
   }
 
-  // Keys [s0, n_end), 32-token tiles in super-tiles; split x of S owns
-  // super-tiles x, x + S, ... (as the 16-row kernel's uniform splits).
+  // Keys [s0, n_end), 32-token tiles in super-tiles (the 16-row kernel's).
   const int s0 = p.kv_start ? min(max(p.kv_start[b], 0), p.N) : 0;
   const int len = max(n_end - s0, 0);
   const int T = (len + kTile - 1) / kTile;
-  const int t_lo = blockIdx.x, stride = p.num_splits;
   const int sh = super_tile_shift(T, stride);
-  const int J = super_tile_positions(T, t_lo, stride, 0x7FFFFFFF, sh);
+  const int J = super_tile_positions(T, t_lo, stride, jmax, sh);
   auto tile_of = [&](int j) -> int { return super_tile_tile(j, t_lo, stride, sh); };
   static_assert(kWaves == kSplitWaves, "the tile split is for 8 waves");
   const int J8 = wave_split_rr_end(J, D);
@@ -174,29 +175,83 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     __syncthreads();
     merge_store<Tag, D, kWaves, false>(
         p, [&](int w, int h) { return s_acc + (w * 16 + h) * kRowF; },
-        [&](int w, int h) { return f32x2{s_ml[w][h][0], s_ml[w][h][1]}; }, nk, v0 + 16 * k, kvh, b,
-        static_cast<int>(blockIdx.x), kThreads);
+        [&](int w, int h) { return f32x2{s_ml[w][h][0], s_ml[w][h][1]}; }, nk, v0 + 16 * k, kvh, b, col,
+        kThreads);
+  }
+}
+
+// SK: a left-padded batch on the stream-K schedule of the 16-row kernel
+// (common.h): grid (U, H_kv * row blocks, 1), unit x owning global tiles
+// [x C, (x + 1) C) of the sequences laid end to end, one segment per
+// sequence it touches, its partials at column x + b; workgroup (0, 0)
+// writes the (first column, count) table for the merge kernel.
+// Otherwise uniform splits: grid (S, H_kv * row blocks, B).
+template <typename Tag, int D, int BITS, int GS, bool MASK, bool SK>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_rows32_kernel(
+    MfmaParams p) {
+  static_assert(!(D == 256 && BITS == 8), "D = 256 with 8-bit codes: no register room for two halves");
+  static_assert(!(D == 256 && MASK), "D = 256: no register room for the mask values");
+  __shared__ __attribute__((aligned(16))) float s_acc[kWaves * 16 * kRowFloats<D>];
+  __shared__ float s_ml[kWaves][16][2];
+  __shared__ __attribute__((aligned(16))) uint8_t s_q[kRows * kQRowBytes<D>];
+  const int hblk = blockIdx.y % p.hb_count;
+  const int kvh = blockIdx.y / p.hb_count;
+  if constexpr (!SK) {
+    rows32_segment<Tag, D, BITS, GS, MASK>(p, s_acc, s_ml, s_q, hblk, kvh, blockIdx.z, blockIdx.x, p.num_splits,
+                                           0x7FFFFFFF, blockIdx.x);
+  } else {
+    const int total = streamk_total(p.kv_start, p.B, p.N);
+    const int C = max(1, (total + p.units - 1) / p.units);
+    if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x < 64) streamk_write_sched(p.kv_start, p.B, p.N, C, p.sched);
+    int g = static_cast<int>(blockIdx.x) * C;
+    const int g_end = min(g + C, total);
+    if (g >= g_end) return;  // the whole workgroup: no work, nothing to store
+    int b, P;
+    streamk_find(p.kv_start, p.B, p.N, g, b, P);
+    while (g < g_end && b < p.B) {
+      const int Tb = seq_tiles(p.kv_start, b, p.N);
+      const int hi = min(g_end, P + Tb);
+      if (hi > g) {
+        rows32_segment<Tag, D, BITS, GS, MASK>(p, s_acc, s_ml, s_q, hblk, kvh, b, g - P, 1, hi - g,
+                                               static_cast<int>(blockIdx.x) + b);
+        __syncthreads();  // the next segment reuses the LDS
+        g = hi;
+      }
+      P += Tb;
+      ++b;
+    }
   }
 }
 
 using Rows32Kernel = void (*)(MfmaParams);
 
-template <typename Tag, int D, int BITS, bool MASK>
+template <typename Tag, int D, int BITS, bool MASK, bool SK>
 Rows32Kernel rows32_by_gs(int gs) {
-  return gs == 32 ? decode_rows32_kernel<Tag, D, BITS, 32, MASK>
-       : gs == 64 ? decode_rows32_kernel<Tag, D, BITS, 64, MASK>
-                  : decode_rows32_kernel<Tag, D, BITS, 128, MASK>;
+  return gs == 32 ? decode_rows32_kernel<Tag, D, BITS, 32, MASK, SK>
+       : gs == 64 ? decode_rows32_kernel<Tag, D, BITS, 64, MASK, SK>
+                  : decode_rows32_kernel<Tag, D, BITS, 128, MASK, SK>;
 }
 
-template <typename Tag, bool MASK>
+template <typename Tag, bool MASK, bool SK>
 Rows32Kernel rows32_d128(const qsdpa_decode_args* a) {
-  return a->bits == 4 ? rows32_by_gs<Tag, 128, 4, MASK>(a->group_size) : rows32_by_gs<Tag, 128, 8, MASK>(a->group_size);
+  return a->bits == 4 ? rows32_by_gs<Tag, 128, 4, MASK, SK>(a->group_size)
+                      : rows32_by_gs<Tag, 128, 8, MASK, SK>(a->group_size);
+}
+
+// No stream-K instantiation at D = 256: it spilled (28-48 bytes of scratch
+// per lane); rows32_supports keeps such batches on the 16-row kernel.
+template <typename Tag, bool SK>
+Rows32Kernel rows32_pick_sk(const qsdpa_decode_args* a) {
+  if (a->D == 256) {
+    if constexpr (SK) return nullptr;
+    else return rows32_by_gs<Tag, 256, 4, false, false>(a->group_size);
+  }
+  return a->mask.ptr ? rows32_d128<Tag, true, SK>(a) : rows32_d128<Tag, false, SK>(a);
 }
 
 template <typename Tag>
-Rows32Kernel rows32_pick(const qsdpa_decode_args* a) {
-  if (a->D == 256) return rows32_by_gs<Tag, 256, 4, false>(a->group_size);
-  return a->mask.ptr ? rows32_d128<Tag, true>(a) : rows32_d128<Tag, false>(a);
+Rows32Kernel rows32_pick(const qsdpa_decode_args* a, bool sk) {
+  return sk ? rows32_pick_sk<Tag, true>(a) : rows32_pick_sk<Tag, false>(a);
 }
 
 }  // namespace
@@ -207,9 +262,9 @@ Rows32Kernel rows32_pick(const qsdpa_decode_args* a) {
 // a bool mask at q_len = 8 over 16K / 64K keys 32.1-32.2 / 89.1-89.5
 // against 34.1-34.3 / 113.9-114.9 us, with an additive one at q_len = 16
 // over 32K 85.1-89.5 against 118.3-119.6; C1's heads with a bool mask at
-// q_len = 16 over 128K 35.7-35.8 against 43.1-43.5), no folded append, and uniform
-// splits (kv_start only with one sequence: a left-padded batch takes the
-// stream-K schedule of the 16-row kernel); and enough work.  At D = 256, per
+// q_len = 16 over 128K 35.7-35.8 against 43.1-43.5), no folded append (a
+// left-padded batch runs the 16-row kernel's stream-K schedule, at D = 128
+// only; the others uniform splits); and enough work.  At D = 256, per
 // kv head: at least 16K keys and 1.5 * 2^20 (row, key) pairs.  Measured
 // against the 16-row kernel, C3's
 // heads, wall time per call on one box (both with splits rounded down to
@@ -239,7 +294,7 @@ Rows32Kernel rows32_pick(const qsdpa_decode_args* a) {
 bool rows32_supports(const qsdpa_decode_args* a) {
   if (!(a->D == 128 || (a->D == 256 && a->bits == 4)) || a->q_len <= 1 || a->k_new.ptr) return false;
   if (a->mask.ptr && a->D != 128) return false;  // D = 256: no register room for the mask values
-  if (a->kv_start && a->B > 1) return false;
+  if (a->kv_start && a->B > 1 && a->D != 128) return false;  // no stream-K instantiation at D = 256
   const int64_t rows = static_cast<int64_t>(a->H_q / a->H_kv) * a->q_len;
   if (rows <= 16 || a->N < 16384) return false;
   if (a->D == 128) return static_cast<int64_t>(a->B) * a->H_q * a->q_len * a->N >= (int64_t(1) << 23);
@@ -258,11 +313,15 @@ int rows32_num_splits(const qsdpa_decode_args* a, int cus) {
 }
 
 int launch_decode_rows32(const qsdpa_decode_args* a, int num_splits, float* part_acc, float* part_ml,
-                         hipStream_t stream) {
+                         int units, int* sched, hipStream_t stream) {
   MfmaParams p = mfma_params(a, num_splits, part_acc, part_ml);
   p.hb_count = (p.G * p.qL + kRows - 1) / kRows;
-  const dim3 grid(num_splits, p.Hkv * p.hb_count, p.B);
-  Rows32Kernel k = a->dtype == QSDPA_F16 ? rows32_pick<F16>(a) : rows32_pick<BF16>(a);
+  p.units = units;
+  p.sched = sched;
+  const dim3 grid(units ? units : num_splits, p.Hkv * p.hb_count, units ? 1 : p.B);
+  const bool sk = units > 0;
+  Rows32Kernel k = a->dtype == QSDPA_F16 ? rows32_pick<F16>(a, sk) : rows32_pick<BF16>(a, sk);
+  if (!k) return fail(QSDPA_ERR_UNSUPPORTED, "decode_rows32: no stream-K kernel at D=256");
   launch_profiled(k, grid, dim3(kThreads), stream, a->prof_begin, a->prof_end, p);
   return check_launch("decode_rows32");
 }

@@ -343,9 +343,12 @@ def test_row_blocks_match_oracle(device, case):
     (2, 16, 4, 70000, 128, 4, 32, "f16", 5, False, None),       # 20 rows, full attention
     (1, 4, 4, 140000, 128, 8, 64, "bf16", 20, True, (139300,)), # G = 1: 20 positions over 700 keys
     (1, 32, 8, 40000, 128, 4, 128, "bf16", 9, True, None),      # 36 rows: 4 in block 2
+    # D = 128 left-padded batches: the stream-K schedule, an empty sequence
+    (4, 16, 4, 32768, 128, 4, 64, "f16", 8, True, (0, 5000, 32000, 32768)),
+    (3, 32, 8, 20000, 128, 8, 128, "bf16", 6, False, (100, 19990, 7)),
 ], ids=["G16-q2", "G16-q3-bf16", "G16-q7-full", "G1-q20-bf16", "G4-q9-kvstart", "G8-q5-129keys",
         "G16-q4-3keys-bf16", "G16-q8-N16K", "D128-c5-q8", "D128-c1-q16-128K", "D128-G4-q5-full",
-        "D128-G1-q20-kvstart", "D128-G4-q9-bf16"])
+        "D128-G1-q20-kvstart", "D128-G4-q9-bf16", "D128-streamK-q8", "D128-streamK-q6-bf16"])
 def test_rows32_blocks_match_oracle(device, case):
     """More than 16 query rows per kv head over long caches, at D = 256
     with 4-bit codes and at D = 128: the 32-row kernel (both 16-row halves
