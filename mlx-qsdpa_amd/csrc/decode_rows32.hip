@@ -264,9 +264,10 @@ Rows32Kernel rows32_pick(const qsdpa_decode_args* a, bool sk) {
 // over 32K 85.1-89.5 against 118.3-119.6; C1's heads with a bool mask at
 // q_len = 16 over 128K 35.7-35.8 against 43.1-43.5), no folded append (a
 // left-padded batch runs the 16-row kernel's stream-K schedule, at D = 128
-// only; the others uniform splits); and enough work.  At D = 256, per
-// kv head: at least 16K keys and 1.5 * 2^20 (row, key) pairs.  Measured
-// against the 16-row kernel, C3's
+// only; the others uniform splits); and enough work: at least 16K keys
+// and, at D = 256, 3 * 2^20 (row, key) pairs in all (32 rows of one kv head
+// over 64K keys were still faster on the 16-row kernel, 16.5 against 19.1
+// us, over 128K the same).  Measured against the 16-row kernel, C3's
 // heads, wall time per call on one box (both with splits rounded down to
 // one round of workgroups), 32-row kernel against 16-row kernel, in us:
 //   q_len = 2 over 16K / 32K / 64K keys   16.5 / 19.4-19.6 / 22.1-22.2
@@ -297,8 +298,8 @@ bool rows32_supports(const qsdpa_decode_args* a) {
   if (a->kv_start && a->B > 1 && a->D != 128) return false;  // no stream-K instantiation at D = 256
   const int64_t rows = static_cast<int64_t>(a->H_q / a->H_kv) * a->q_len;
   if (rows <= 16 || a->N < 16384) return false;
-  if (a->D == 128) return static_cast<int64_t>(a->B) * a->H_q * a->q_len * a->N >= (int64_t(1) << 23);
-  return rows * a->N >= (int64_t(3) << 19);
+  const int64_t pairs = static_cast<int64_t>(a->B) * a->H_q * a->q_len * a->N;
+  return pairs >= (a->D == 128 ? int64_t(1) << 23 : int64_t(3) << 20);
 }
 
 // Splits: as the 16-row kernel's (at most one workgroup per CU), over 32-row

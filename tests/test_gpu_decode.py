@@ -327,8 +327,8 @@ def test_row_blocks_match_oracle(device, case):
 
 @pytest.mark.parametrize("case", [
     # (B, Hq, Hkv, N, D, bits, gs, dtype, qL, causal, kv_start); calls with
-    # 16K+ keys and 1.5 * 2^20 (row, key) pairs per kv head take this kernel,
-    # kv_start shortens the key range
+    # 16K+ keys and 3 * 2^20 (row, key) pairs in all take this kernel at
+    # D = 256, kv_start shortens the key range
     (1, 32, 2, 49200, 256, 4, 32, "f16", 2, True, None),        # 32 rows: one full block
     (2, 32, 2, 32768, 256, 4, 64, "bf16", 3, True, None),       # 48 rows: a half-filled second block
     (1, 16, 1, 33000, 256, 4, 128, "f16", 7, False, None),      # 112 rows, full attention
@@ -336,7 +336,7 @@ def test_row_blocks_match_oracle(device, case):
     (1, 8, 2, 45000, 256, 4, 64, "f16", 9, True, (333,)),       # 36 rows: 4 rows in block 2, kv_start
     (1, 16, 2, 40000, 256, 4, 32, "f16", 5, True, (39871,)),    # 40 rows over 129 keys
     (1, 32, 2, 32768, 256, 4, 32, "bf16", 4, True, (32765,)),   # 3 keys: the first rows see none
-    (1, 16, 1, 16400, 256, 4, 32, "f16", 8, True, None),        # 128 rows over 16K keys
+    (1, 16, 1, 24600, 256, 4, 32, "f16", 8, True, None),        # 128 rows over 24K keys
     # D = 128, 4- and 8-bit: 2^23 (row, key) pairs in all
     (4, 16, 4, 16400, 128, 8, 128, "bf16", 8, True, None),      # C5's heads: 32 rows
     (1, 8, 2, 131100, 128, 4, 64, "f16", 16, True, None),       # C1's heads: 64 rows over 128K keys
@@ -347,7 +347,7 @@ def test_row_blocks_match_oracle(device, case):
     (4, 16, 4, 32768, 128, 4, 64, "f16", 8, True, (0, 5000, 32000, 32768)),
     (3, 32, 8, 20000, 128, 8, 128, "bf16", 6, False, (100, 19990, 7)),
 ], ids=["G16-q2", "G16-q3-bf16", "G16-q7-full", "G1-q20-bf16", "G4-q9-kvstart", "G8-q5-129keys",
-        "G16-q4-3keys-bf16", "G16-q8-N16K", "D128-c5-q8", "D128-c1-q16-128K", "D128-G4-q5-full",
+        "G16-q4-3keys-bf16", "G16-q8-N24K", "D128-c5-q8", "D128-c1-q16-128K", "D128-G4-q5-full",
         "D128-G1-q20-kvstart", "D128-G4-q9-bf16", "D128-streamK-q8", "D128-streamK-q6-bf16"])
 def test_rows32_blocks_match_oracle(device, case):
     """More than 16 query rows per kv head over long caches, at D = 256
@@ -357,7 +357,7 @@ def test_rows32_blocks_match_oracle(device, case):
     blocks; repeated calls are bitwise identical."""
     B, Hq, Hkv, N, D, bits, gs, dtype, qL, causal, starts = case
     rows = Hq // Hkv * qL
-    enough = B * Hq * qL * N >= 1 << 23 if D == 128 else rows * N >= 3 << 19
+    enough = B * Hq * qL * N >= (1 << 23 if D == 128 else 3 << 20)
     assert 16 < rows < 128 or (D == 256 and B * Hq * qL * N < 1 << 24)  # not the prefill kernel's
     assert rows > 16 and N >= 16384 and enough
     rng = np.random.default_rng(91 + qL + Hq + N)
@@ -431,7 +431,7 @@ def test_rows32_strided_views_and_symmetric(device):
     call on contiguous copies."""
     rng = np.random.default_rng(93)
     B, Hq, Hkv, N, cap, D, qL = 1, 32, 2, 49200, 49300, 256, 3
-    assert Hq // Hkv * qL * N >= 3 << 19
+    assert B * Hq * qL * N >= 3 << 20
     for symmetric in (False, True):
         inp = make_inputs(rng, B, Hq, Hkv, N, D, 4, 32, symmetric=symmetric)
         inp["q"] = affine.random_T(rng, (B, Hq, qL, D), "f16")
